@@ -1,0 +1,221 @@
+"""Benchmark of the ConvRot QuantLinear + LoRA forward on one MI355X (BASELINE.json metric and configs).
+
+A step is one QuantLinear+LoRA forward over one batch of synthetic input resident in HBM: rotate+quantize
+(kernel 1), LoRA down-projection, int8 MFMA GEMM with the fused dequant/bias/LoRA epilogue (kernels 2+3).
+The default workload is BASELINE.json configs[2] (M=16384+512, K=3072, N=12288, r=32), the configuration the
+north_star's targets are stated on.  ``value`` is the forward's throughput in TOPS (2*M*N*K per step time).
+Rank 0 prints one JSON line; ``roofline`` covers the dominant kernel (the GEMM, int8-MFMA bound) with its
+average duration measured by HIP events on the stream the kernels run on; ``cpu_baseline`` times the CPU
+oracle (a port of the same arithmetic) on a bounded sample of rows.
+
+    python bench.py [--steps K] [--warmup W] [--config 2] [--all] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+INT8_PEAK_TOPS = 5000.0     # MI355X dense int8 MFMA (5.0 POP/s)
+BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+METRIC = "QuantLinear+LoRA fwd TOPS & % int8 MFMA peak; rotate/quant GB/s; block fwd ms"
+
+# BASELINE.json configs -> shapes
+CONFIGS = {
+    0: dict(M=4096, K=3072, N=3072, r=16, w4=False, bias=True,
+            name="cfg0: ConvRot W8A8 QuantLinear+LoRA fwd, M=4096 K=3072 N=3072 r=16, fp32 bias"),
+    1: dict(M=4096, K=3072, N=3072, r=16, w4=True, bias=True,
+            name="cfg1: ConvRot W4A8 (g64) QuantLinear+LoRA fwd, M=4096 K=3072 N=3072 r=16"),
+    2: dict(M=16896, K=3072, N=12288, r=32, w4=False, bias=False,
+            name="cfg2: ConvRot W8A8 QuantLinear+LoRA fwd (MLP up @2048^2), M=16384+512 K=3072 N=12288 r=32"),
+}
+
+
+def synth(M, K, N, r, bias, seed=0):
+    """BASELINE.json inputs, generated on the CPU in the fixed order x -> outlier idx -> W -> bias -> A -> B."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g)
+    idx = torch.randperm(K, generator=g)[: K // 100]
+    x[:, idx] *= 20
+    x = x.to(torch.bfloat16)
+    W = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    b = torch.randn(N, generator=g) * 0.02 if bias else None
+    A = torch.randn(r, K, generator=g) * 0.01
+    B = torch.randn(N, r, generator=g) * 0.01
+    return x, W, b, A, B
+
+
+def time_loop(fn, iters, warm=3):
+    for _ in range(warm):
+        fn()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(iters):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / iters   # ms
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(cfg, x, W, b, A, B, budget_s=12.0, rows=2048):
+    """The CPU oracle's forward (numpy FWHT + quant, exact int32 GEMM via torch._int_mm, f64 epilogue) on a
+    bounded sample: the first ``rows`` rows, repeated until ``budget_s`` of work; returns TOPS."""
+    import numpy as np
+    from oracle import convrot as orc
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    K, N = cfg["K"], cfg["N"]
+    if cfg["w4"]:
+        qw, sw = orc.quant_weight_i4(W.float().numpy())
+    else:
+        qw, sw = orc.quant_weight_i8(W.float().numpy())
+    xs = x[:rows].float().numpy()
+    bn = None if b is None else b.numpy()
+    An, Bn = A.numpy(), B.numpy()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while not times or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        orc.forward(xs, qw, sw, w4=cfg["w4"], bias=bn, lora_A=An, lora_B=Bn, lora_scale=1.0, fast=True)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    return {"value": 2.0 * rows * N * K / t / 1e12, "unit": "TOPS", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{rows} of {cfg['M']} rows of {cfg['name'].split(':')[0]}, median of {len(times)} runs "
+                      f"({t * 1e3:.0f} ms each) on {cpu_model()}"}
+
+
+def run_config(k2, cfg, steps, warmup, dev):
+    L = k2._lib
+    M, K, N, r = cfg["M"], cfg["K"], cfg["N"], cfg["r"]
+    x, W, b, A, B = synth(M, K, N, r, cfg["bias"])
+    xd, Ad, Bd = x.to(dev), A.to(dev), B.to(dev)
+    bd = None if b is None else b.to(dev)
+    if cfg["w4"]:
+        qw, sw = L.quant_weight_i4(W.to(dev))
+        gemm = L.gemm_w4a8
+    else:
+        qw, sw = L.quant_weight_i8(W.to(dev))
+        gemm = L.gemm_w8a8
+    torch.cuda.synchronize()
+
+    def step():
+        qx, sx, _ = L.rotquant(xd)
+        u = L.lora_down(xd, Ad)
+        return gemm(qx, sx, qw, sw, bd, u, Bd, 1.0)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ms_step = time_loop(step, steps, warm=0)
+    wall = time.perf_counter() - t0
+
+    # per-kernel averages (events on torch's current stream, which is the stream the kernels run on)
+    qx, sx, _ = L.rotquant(xd)
+    u = L.lora_down(xd, Ad)
+    iters = max(steps, 10)
+    ms_rot = time_loop(lambda: L.rotquant(xd), iters)
+    ms_lora = time_loop(lambda: L.lora_down(xd, Ad), iters)
+    ms_gemm = time_loop(lambda: gemm(qx, sx, qw, sw, bd, u, Bd, 1.0), iters)
+    ops = 2.0 * M * N * K
+    rot_bytes = 2 * M * K + M * K + 4 * M
+    return dict(ms_step=ms_step, wall=wall, ms_rot=ms_rot, ms_lora=ms_lora, ms_gemm=ms_gemm, ops=ops,
+                rot_bytes=rot_bytes, tops=ops / (ms_step * 1e-3) / 1e12, x=x, W=W, b=b, A=A, B=B)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
+    ap.add_argument("--all", action="store_true", help="also report configs 0 and 1 (stderr)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    a = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if a.gpus > 1 or world > 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path (per-token rows shard with no "
+              "communication; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+
+    import __graft_entry__ as ge
+    k2 = ge.load_package()
+    dev = torch.device("cuda:0")
+    cfg = CONFIGS[a.config]
+    res = run_config(k2, cfg, a.steps, a.warmup, dev)
+
+    gemm_tops = res["ops"] / (res["ms_gemm"] * 1e-3) / 1e12
+    rot_gbs = res["rot_bytes"] / (res["ms_rot"] * 1e-3) / 1e9
+    extra = {
+        "fwd_tops": round(res["tops"], 1),
+        "fwd_pct_int8_peak": round(100 * res["tops"] / INT8_PEAK_TOPS, 2),
+        "gemm_ms": round(res["ms_gemm"], 4), "gemm_tops": round(gemm_tops, 1),
+        "gemm_pct_int8_peak": round(100 * gemm_tops / INT8_PEAK_TOPS, 2),
+        "rotquant_ms": round(res["ms_rot"], 4), "rotquant_GBps": round(rot_gbs, 1),
+        "rotquant_pct_hbm": round(100 * rot_gbs / HBM_PEAK_GBS, 2),
+        "lora_down_ms": round(res["ms_lora"], 4),
+        "lora_ops": 2.0 * cfg["M"] * cfg["r"] * (cfg["K"] + cfg["N"]),
+    }
+    cpu = None
+    if not a.no_cpu:
+        cpu = cpu_baseline(cfg, res["x"], res["W"], res["b"], res["A"], res["B"])
+    line = {
+        "metric": METRIC,
+        "value": round(res["tops"], 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(res["ms_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic: BASELINE.json distributions (x~N(0,1) bf16 with 1% outlier channels x20, "
+                "W~N(0,0.02), LoRA A,B~N(0,0.01)), seed 0",
+        "config": {"workload": cfg["name"], "M": cfg["M"], "K": cfg["K"], "N": cfg["N"], "rank": cfg["r"],
+                   "weights": "int4 g64" if cfg["w4"] else "int8 per-channel", "hadamard_block": 128},
+        "roofline": {"bound": "mfma", "kernel": "gemm_nt_kernel<EPI_W8>" if not cfg["w4"] else "gemm_w4_kernel",
+                     "achieved": round(gemm_tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                     "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    if a.all:
+        for c in (0, 1):
+            if c == a.config:
+                continue
+            r2 = run_config(k2, CONFIGS[c], a.steps, a.warmup, dev)
+            print(json.dumps({"config": CONFIGS[c]["name"], "ms_step": round(r2["ms_step"], 4),
+                              "tops": round(r2["tops"], 1), "gemm_ms": round(r2["ms_gemm"], 4),
+                              "rotquant_ms": round(r2["ms_rot"], 4)}), file=sys.stderr, flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,93 @@
+/* k2q — C ABI of the MI355X (gfx950) ConvRot QuantLinear + LoRA kernels.
+ *
+ * Every entry point takes raw device pointers, int64 shapes and a HIP stream passed as `void*`
+ * (a hipStream_t; never the null stream in the module), launches asynchronously on that stream and
+ * returns an int status (K2Q_OK or a negative K2Q_E* code).  No C++ exception crosses this boundary.
+ * The caller (PyTorch's caching allocator) owns every buffer; the library keeps no device memory and
+ * no mutable global state between calls, so calls on different streams are re-entrant.
+ *
+ * Layouts (row-major, last index contiguous):
+ *   x      M x K   bf16 activations (or f32 / bf16 weights for the weight quantizers)
+ *   q      M x K   int8 codes, s M f32 per-row scales (s = absmax/127 of the rotated row)
+ *   qw     N x K   int8 per-channel codes, sw N f32
+ *   qw4    N x K/2 packed int4 codes (in every 16-wide K chunk, byte j = code j | code j+8 << 4),
+ *          sw4 K/64 x N bf16 group scales, group-major (scales of one group are contiguous over n)
+ *   u      M x r   f32 LoRA down-projection x A^T;  lora_a r x K f32, lora_b N x r f32
+ *   y      M x N   bf16,  dy M x N bf16,  dx M x K bf16
+ * Constraints checked before any launch: K % 128 == 0 (Hadamard block), r % 16 == 0 and r <= 128 when
+ * a LoRA term is present, pointers 16-byte aligned, M, N >= 1.
+ */
+#ifndef K2Q_H
+#define K2Q_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define K2Q_OK 0
+#define K2Q_EINVAL (-1)      /* bad shape, null or misaligned pointer */
+#define K2Q_EARCH (-2)       /* current device is not gfx950 */
+#define K2Q_ELAUNCH (-3)     /* kernel launch reported an error */
+#define K2Q_EUNSUPPORTED (-4)/* shape outside what the kernels implement (e.g. K too large) */
+
+#define K2Q_DTYPE_BF16 0
+#define K2Q_DTYPE_F32 1
+
+/* Library version string and device check (K2Q_OK when the current device is gfx950). */
+const char* k2q_version(void);
+int k2q_check_device(void);
+
+/* (1) Rotate + per-row int8 quantize.
+ * Replaces the point where Fp8Linear.forward receives x (reference quantize.py:48); the rotation and
+ * the activation quantization have no reference code (north_star kernel (1)).  Also the int8 weight
+ * quantizer of Fp8Linear.__init__'s ConvRot counterpart (quantize.py:34-37): call it on W's rows.
+ * x_rot (nullable) receives bf16(FWHT(x)/sqrt(128)). */
+int k2q_rotquant(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                 int8_t* q, float* s, uint16_t* x_rot, void* stream);
+
+/* int4 group-64 weight quantizer of W R (counterpart of Fp8Linear.__init__, quantize.py:34-39). */
+int k2q_quant_weight_i4(const void* w, int w_dtype, int64_t N, int64_t K,
+                        uint8_t* qw4, uint16_t* sw4, void* stream);
+
+/* LoRA down-projection u = x.f32 @ A^T (lora.py:47, first product).  ws: 2*r*K bf16 workspace. */
+int k2q_lora_down(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const float* lora_a, int64_t r,
+                  uint16_t* ws, float* u, void* stream);
+
+/* (2)+(3) W8A8 GEMM with the fused epilogue, replacing F.linear(x, W_deq, b) of quantize.py:49-51 and
+ * the LoRA add of lora.py:47-48:
+ *   y = bf16(2^-7 s_x[m] s_w[n] acc[m,n] + bias[n] + lora_scale * sum_j u[m,j] lora_b[n,j]).
+ * bias, u, lora_b nullable (r ignored when u is null). */
+int k2q_gemm_w8a8(const int8_t* qx, const float* sx, const int8_t* qw, const float* sw, const float* bias,
+                  const float* u, const float* lora_b, int64_t r, float lora_scale,
+                  int64_t M, int64_t N, int64_t K, uint16_t* y, void* stream);
+
+/* W4A8 variant: per-group int32 partials scaled by the bf16 group scales. */
+int k2q_gemm_w4a8(const int8_t* qx, const float* sx, const uint8_t* qw4, const uint16_t* sw4,
+                  const float* bias, const float* u, const float* lora_b, int64_t r, float lora_scale,
+                  int64_t M, int64_t N, int64_t K, uint16_t* y, void* stream);
+
+/* Debug entries: raw int32 accumulators acc[m,n] = sum_k qx[m,k] qw[n,k] (W8), and for W4 the f32
+ * value sum_g sw4[n,g] * acc_g[m,n] without s_x, 2^-7, bias or LoRA. */
+int k2q_gemm_w8a8_acc(const int8_t* qx, const int8_t* qw, int64_t M, int64_t N, int64_t K,
+                      int32_t* acc, void* stream);
+int k2q_gemm_w4a8_f32(const int8_t* qx, const uint8_t* qw4, const uint16_t* sw4,
+                      int64_t M, int64_t N, int64_t K, float* out, void* stream);
+
+/* (4) Input gradient through the frozen base (autograd of quantize.py:51 + lora.py:47-48):
+ *   dx = bf16(2^-7 (dy W_hat) R + g A),   W_hat[n,k] = s_w[n] q[n,k] (or s_w4[n,k/64] q4[n,k]).
+ * k2q_dx_prep writes wt = bf16(W_hat)^T (K x N) and at = A^T (K x r, f32) into caller workspaces;
+ * k2q_gemm_dx then runs the bf16 MFMA GEMM with the inverse rotation and the LoRA term fused.
+ * g = lora_scale * dy @ lora_b (M x r f32) is supplied by the caller; g/at nullable. */
+int k2q_dx_prep(const int8_t* qw, const float* sw, const uint8_t* qw4, const uint16_t* sw4,
+                int64_t N, int64_t K, const float* lora_a, int64_t r,
+                uint16_t* wt, float* at, void* stream);
+int k2q_gemm_dx(const uint16_t* dy, const uint16_t* wt, int64_t M, int64_t N, int64_t K,
+                const float* g, const float* at, int64_t r, uint16_t* dx, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* K2Q_H */

@@ -1,0 +1,18 @@
+"""krea-2_amd — MI355X (gfx950) ConvRot QuantLinear + LoRA for the Krea 2 DiT.
+
+Drop-in for the reference's quantized-base / LoRA module API (``quantize.py``, ``lora.py``):
+:class:`ConvRotLinear` replaces ``Fp8Linear``, :func:`quantize_dit_convrot` replaces ``quantize_dit_fp8``, and
+:mod:`.lora` mirrors the adapter API.  The arithmetic runs in hand-written gfx950 HIP kernels behind the C ABI
+of ``include/k2q.h`` (``libk2q.so``, built by ``build.py``), reached through :mod:`._lib`.
+
+The directory name is not a Python identifier; load it with ``__graft_entry__.load_package()``, which
+registers it as ``krea2_amd``.
+"""
+from . import _lib
+from .lora import (DEFAULT_TARGETS, LoRALinear, inject_lora, load_lora, load_lora_weights, lora_disabled,
+                   lora_parameters, lora_scaled, save_lora)
+from .quantize import MODES, ConvRotLinear, quantize_dit_convrot
+
+__all__ = ["ConvRotLinear", "quantize_dit_convrot", "MODES", "LoRALinear", "inject_lora", "lora_scaled",
+           "lora_disabled", "lora_parameters", "save_lora", "load_lora_weights", "load_lora", "DEFAULT_TARGETS",
+           "_lib"]

@@ -1,0 +1,334 @@
+"""ctypes binding of ``libk2q.so`` (declared in ``include/k2q.h``) plus host-side argument checks.
+
+Every wrapper validates shapes, dtypes, devices and contiguity on the host and raises ``ValueError`` /
+``RuntimeError`` before any launch; a nonzero status from the library becomes ``RuntimeError``.  Kernels
+run on ``torch.cuda.current_stream()`` of the tensors' device.  Outputs are allocated with ``torch.empty``
+(PyTorch's caching allocator owns all memory).  There is no fallback: if the library or a gfx950 GPU is
+missing, the call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libk2q.so"
+
+K2Q_OK = 0
+_STATUS = {-1: "K2Q_EINVAL (bad shape, null or misaligned pointer)", -2: "K2Q_EARCH (device is not gfx950)",
+           -3: "K2Q_ELAUNCH (kernel launch failed)", -4: "K2Q_EUNSUPPORTED (shape outside the kernels)"}
+DTYPE_BF16 = 0
+DTYPE_F32 = 1
+HADAMARD_BLOCK = 128
+INT4_GROUP = 64
+MAX_RANK = 128
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_f32 = ctypes.c_float
+
+_SIGNATURES = {
+    "k2q_version": ([], ctypes.c_char_p),
+    "k2q_check_device": ([], _int),
+    "k2q_rotquant": ([_p, _int, _i64, _i64, _i64, _p, _p, _p, _p], _int),
+    "k2q_quant_weight_i4": ([_p, _int, _i64, _i64, _p, _p, _p], _int),
+    "k2q_lora_down": ([_p, _i64, _i64, _i64, _p, _i64, _p, _p, _p], _int),
+    "k2q_gemm_w8a8": ([_p, _p, _p, _p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p], _int),
+    "k2q_gemm_w4a8": ([_p, _p, _p, _p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p], _int),
+    "k2q_gemm_w8a8_acc": ([_p, _p, _i64, _i64, _i64, _p, _p], _int),
+    "k2q_gemm_w4a8_f32": ([_p, _p, _p, _i64, _i64, _i64, _p, _p], _int),
+    "k2q_dx_prep": ([_p, _p, _p, _p, _i64, _i64, _p, _i64, _p, _p, _p], _int),
+    "k2q_gemm_dx": ([_p, _p, _i64, _i64, _i64, _p, _p, _i64, _p, _p], _int),
+}
+EXPORTS = tuple(_SIGNATURES)
+
+_lib = None
+_lock = threading.Lock()
+_device_ok: dict[int, bool] = {}
+
+
+def load() -> ctypes.CDLL:
+    """Load ``libk2q.so`` once and bind every entry point's signature.  Raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(f"{LIB_PATH} is not built; run krea-2_amd/build.py (hipcc, gfx950)")
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, (args, res) in _SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.argtypes = args
+                fn.restype = res
+            _lib = lib
+    return _lib
+
+
+def version() -> str:
+    return load().k2q_version().decode()
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _check(rc: int, name: str) -> None:
+    if rc != K2Q_OK:
+        raise RuntimeError(f"{name} failed: {_STATUS.get(rc, rc)}")
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _device_check(dev: torch.device) -> None:
+    if dev.type != "cuda":
+        raise RuntimeError(f"k2q kernels need a gfx950 GPU tensor, got device {dev}")
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    if idx not in _device_ok:
+        with torch.cuda.device(idx):
+            _device_ok[idx] = load().k2q_check_device() == K2Q_OK
+    if not _device_ok[idx]:
+        raise RuntimeError(f"device cuda:{idx} is not gfx950 (MI355X); the k2q kernels are built for gfx950 only")
+
+
+def _need(t: torch.Tensor, name: str, dtype, ndim: int | None = None, dev: torch.device | None = None):
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a tensor")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if ndim is not None and t.dim() != ndim:
+        raise ValueError(f"{name} must be {ndim}-D, got shape {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if dev is not None and t.device != dev:
+        raise ValueError(f"{name} is on {t.device}, expected {dev}")
+    if t.data_ptr() % 16:
+        raise ValueError(f"{name} must be 16-byte aligned")
+
+
+def _check_k(K: int) -> None:
+    if K < HADAMARD_BLOCK or K % HADAMARD_BLOCK:
+        raise ValueError(f"in_features={K} must be a positive multiple of the Hadamard block {HADAMARD_BLOCK}")
+    if K > 16384:
+        raise ValueError(f"in_features={K} exceeds the rotate/quant kernel's 16384 limit")
+
+
+def _check_rank(r: int) -> None:
+    if r < 16 or r > MAX_RANK or r % 16:
+        raise ValueError(f"LoRA rank {r} must be a multiple of 16 in [16, {MAX_RANK}] for the fused path")
+
+
+# ----------------------------------------------------------------------------------------------------------
+# (1) rotate + quantize
+# ----------------------------------------------------------------------------------------------------------
+def rotquant(x: torch.Tensor, want_xrot: bool = False):
+    """Per-row FWHT-128 rotation + int8 quantization.  ``x`` (M,K) bf16 or f32, contiguous.
+    Returns ``(q int8 (M,K), s f32 (M,), xrot bf16 (M,K) | None)``."""
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"x must be bf16 or f32, got {x.dtype}")
+    _need(x, "x", x.dtype, 2)
+    M, K = x.shape
+    _check_k(K)
+    if M < 1:
+        raise ValueError("x has no rows")
+    _device_check(x.device)
+    q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    s = torch.empty((M,), dtype=torch.float32, device=x.device)
+    xr = torch.empty((M, K), dtype=torch.bfloat16, device=x.device) if want_xrot else None
+    dt = DTYPE_BF16 if x.dtype == torch.bfloat16 else DTYPE_F32
+    _check(load().k2q_rotquant(_ptr(x), dt, M, K, K, _ptr(q), _ptr(s), _ptr(xr), _stream(x.device)),
+           "k2q_rotquant")
+    return q, s, xr
+
+
+def quant_weight_i8(w: torch.Tensor):
+    """int8 per-output-channel quantization of ``W R``: ``(q int8 (N,K), s f32 (N,))``."""
+    q, s, _ = rotquant(w)
+    return q, s
+
+
+def quant_weight_i4(w: torch.Tensor):
+    """int4 group-64 quantization of ``W R``: ``(q4 uint8 (N,K/2) packed, s4 bf16 (K/64,N) group-major)``."""
+    if w.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"w must be bf16 or f32, got {w.dtype}")
+    _need(w, "w", w.dtype, 2)
+    N, K = w.shape
+    _check_k(K)
+    _device_check(w.device)
+    q4 = torch.empty((N, K // 2), dtype=torch.uint8, device=w.device)
+    s4 = torch.empty((K // INT4_GROUP, N), dtype=torch.bfloat16, device=w.device)
+    dt = DTYPE_BF16 if w.dtype == torch.bfloat16 else DTYPE_F32
+    _check(load().k2q_quant_weight_i4(_ptr(w), dt, N, K, _ptr(q4), _ptr(s4), _stream(w.device)),
+           "k2q_quant_weight_i4")
+    return q4, s4
+
+
+# ----------------------------------------------------------------------------------------------------------
+# LoRA down-projection
+# ----------------------------------------------------------------------------------------------------------
+def lora_down(x: torch.Tensor, A: torch.Tensor) -> torch.Tensor:
+    """``u = x.f32 @ A^T`` (M, r) f32; ``x`` (M,K) bf16, ``A`` (r,K) f32."""
+    _need(x, "x", torch.bfloat16, 2)
+    dev = x.device
+    _need(A, "lora_A", torch.float32, 2, dev)
+    M, K = x.shape
+    r = A.shape[0]
+    if A.shape[1] != K:
+        raise ValueError(f"lora_A has in_features {A.shape[1]}, x has {K}")
+    _check_rank(r)
+    _device_check(dev)
+    ws = torch.empty((2 * r * K,), dtype=torch.bfloat16, device=dev)
+    u = torch.empty((M, r), dtype=torch.float32, device=dev)
+    _check(load().k2q_lora_down(_ptr(x), M, K, K, _ptr(A), r, _ptr(ws), _ptr(u), _stream(dev)), "k2q_lora_down")
+    return u
+
+
+# ----------------------------------------------------------------------------------------------------------
+# (2)+(3) GEMMs with fused epilogue
+# ----------------------------------------------------------------------------------------------------------
+def _gemm_common(qx, sx, N, bias, u, lora_b):
+    _need(qx, "q_x", torch.int8, 2)
+    dev = qx.device
+    M, K = qx.shape
+    _need(sx, "s_x", torch.float32, 1, dev)
+    if sx.shape[0] != M:
+        raise ValueError("s_x length != rows of q_x")
+    if N % 4:
+        raise ValueError(f"out_features={N} must be a multiple of 4")
+    if bias is not None:
+        _need(bias, "bias", torch.float32, 1, dev)
+        if bias.shape[0] != N:
+            raise ValueError("bias length != out_features")
+    r = 0
+    if u is not None:
+        _need(u, "u", torch.float32, 2, dev)
+        if lora_b is None:
+            raise ValueError("u given without lora_B")
+        _need(lora_b, "lora_B", torch.float32, 2, dev)
+        r = u.shape[1]
+        if u.shape[0] != M or lora_b.shape != (N, r):
+            raise ValueError(f"LoRA shapes u{tuple(u.shape)} lora_B{tuple(lora_b.shape)} do not match M={M}, N={N}")
+        _check_rank(r)
+    return dev, M, K, r
+
+
+def gemm_w8a8(qx, sx, qw, sw, bias=None, u=None, lora_b=None, lora_scale: float = 1.0) -> torch.Tensor:
+    """``y = bf16(2^-7 s_x s_w acc + bias + lora_scale u lora_B^T)`` (M,N)."""
+    _need(qw, "q_w", torch.int8, 2)
+    N = qw.shape[0]
+    dev, M, K, r = _gemm_common(qx, sx, N, bias, u, lora_b)
+    if qw.shape[1] != K or qw.device != dev:
+        raise ValueError("q_w shape/device mismatch")
+    _need(sw, "s_w", torch.float32, 1, dev)
+    if sw.shape[0] != N:
+        raise ValueError("s_w length != out_features")
+    _check_k(K)
+    _device_check(dev)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    _check(load().k2q_gemm_w8a8(_ptr(qx), _ptr(sx), _ptr(qw), _ptr(sw), _ptr(bias), _ptr(u), _ptr(lora_b), r,
+                                float(lora_scale), M, N, K, _ptr(y), _stream(dev)), "k2q_gemm_w8a8")
+    return y
+
+
+def gemm_w4a8(qx, sx, q4, s4, bias=None, u=None, lora_b=None, lora_scale: float = 1.0) -> torch.Tensor:
+    """W4A8 variant of :func:`gemm_w8a8` (packed int4 codes, group-major bf16 group scales)."""
+    _need(q4, "q_w4", torch.uint8, 2)
+    N = q4.shape[0]
+    dev, M, K, r = _gemm_common(qx, sx, N, bias, u, lora_b)
+    if q4.shape[1] * 2 != K or q4.device != dev:
+        raise ValueError("q_w4 shape/device mismatch")
+    _need(s4, "s_w4", torch.bfloat16, 2, dev)
+    if s4.shape != (K // INT4_GROUP, N):
+        raise ValueError(f"s_w4 must be (K/64, N) = {(K // INT4_GROUP, N)}, got {tuple(s4.shape)}")
+    _check_k(K)
+    _device_check(dev)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    _check(load().k2q_gemm_w4a8(_ptr(qx), _ptr(sx), _ptr(q4), _ptr(s4), _ptr(bias), _ptr(u), _ptr(lora_b), r,
+                                float(lora_scale), M, N, K, _ptr(y), _stream(dev)), "k2q_gemm_w4a8")
+    return y
+
+
+def gemm_w8a8_acc(qx, qw) -> torch.Tensor:
+    """Debug: raw int32 accumulators ``qx @ qw^T`` (M,N)."""
+    _need(qx, "q_x", torch.int8, 2)
+    dev = qx.device
+    _need(qw, "q_w", torch.int8, 2, dev)
+    M, K = qx.shape
+    N = qw.shape[0]
+    if qw.shape[1] != K or N % 4:
+        raise ValueError("shape mismatch")
+    _check_k(K)
+    _device_check(dev)
+    acc = torch.empty((M, N), dtype=torch.int32, device=dev)
+    _check(load().k2q_gemm_w8a8_acc(_ptr(qx), _ptr(qw), M, N, K, _ptr(acc), _stream(dev)), "k2q_gemm_w8a8_acc")
+    return acc
+
+
+def gemm_w4a8_f32(qx, q4, s4) -> torch.Tensor:
+    """Debug: ``sum_g s4[g,n] * acc_g[m,n]`` in f32 (M,N), no s_x / 2^-7 / bias / LoRA."""
+    _need(qx, "q_x", torch.int8, 2)
+    dev = qx.device
+    _need(q4, "q_w4", torch.uint8, 2, dev)
+    _need(s4, "s_w4", torch.bfloat16, 2, dev)
+    M, K = qx.shape
+    N = q4.shape[0]
+    if q4.shape[1] * 2 != K or s4.shape != (K // INT4_GROUP, N) or N % 4:
+        raise ValueError("shape mismatch")
+    _check_k(K)
+    _device_check(dev)
+    out = torch.empty((M, N), dtype=torch.float32, device=dev)
+    _check(load().k2q_gemm_w4a8_f32(_ptr(qx), _ptr(q4), _ptr(s4), M, N, K, _ptr(out), _stream(dev)),
+           "k2q_gemm_w4a8_f32")
+    return out
+
+
+# ----------------------------------------------------------------------------------------------------------
+# (4) input gradient
+# ----------------------------------------------------------------------------------------------------------
+def gemm_dx(dy, qw, sw, *, w4: bool = False, g=None, lora_a=None) -> torch.Tensor:
+    """``dx = bf16(2^-7 (dy W_hat) R + g lora_A)`` (M,K); ``dy`` (M,N) bf16, ``g`` (M,r) f32 already
+    scaled (``lora_scale * dy @ lora_B``), ``lora_a`` (r,K) f32."""
+    _need(dy, "dy", torch.bfloat16, 2)
+    dev = dy.device
+    M, N = dy.shape
+    if w4:
+        _need(qw, "q_w4", torch.uint8, 2, dev)
+        K = qw.shape[1] * 2
+        _need(sw, "s_w4", torch.bfloat16, 2, dev)
+        if sw.shape != (K // INT4_GROUP, N):
+            raise ValueError("s_w4 shape mismatch")
+    else:
+        _need(qw, "q_w", torch.int8, 2, dev)
+        K = qw.shape[1]
+        _need(sw, "s_w", torch.float32, 1, dev)
+        if sw.shape[0] != N:
+            raise ValueError("s_w length mismatch")
+    if qw.shape[0] != N:
+        raise ValueError(f"dy has {N} columns, weight has {qw.shape[0]} rows")
+    _check_k(K)
+    if N % 64:
+        raise ValueError(f"out_features={N} must be a multiple of 64 for the input-gradient GEMM")
+    r = 0
+    if g is not None:
+        _need(g, "g", torch.float32, 2, dev)
+        _need(lora_a, "lora_A", torch.float32, 2, dev)
+        r = g.shape[1]
+        if g.shape[0] != M or lora_a.shape != (r, K):
+            raise ValueError("LoRA gradient shapes mismatch")
+        _check_rank(r)
+    _device_check(dev)
+    st = _stream(dev)
+    wt = torch.empty((K, N), dtype=torch.bfloat16, device=dev)
+    at = torch.empty((K, r), dtype=torch.float32, device=dev) if r else None
+    lib = load()
+    _check(lib.k2q_dx_prep(None if w4 else _ptr(qw), None if w4 else _ptr(sw), _ptr(qw) if w4 else None,
+                           _ptr(sw) if w4 else None, N, K, _ptr(lora_a) if r else None, r, _ptr(wt), _ptr(at), st),
+           "k2q_dx_prep")
+    dx = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+    _check(lib.k2q_gemm_dx(_ptr(dy), _ptr(wt), M, N, K, _ptr(g), _ptr(at), r, _ptr(dx), st), "k2q_gemm_dx")
+    return dx

@@ -1,0 +1,58 @@
+"""Build ``libk2q.so`` (the gfx950 HIP kernels behind the C ABI of ``include/k2q.h``) in-tree.
+
+``python krea-2_amd/build.py`` or ``build()`` from Python.  hipcc cross-compiles for gfx950 without a GPU,
+so this runs in the CPU container; the resulting ``.so`` sits next to this file and travels with the tree.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+CSRC = HERE / "csrc"
+INCLUDE = HERE.parent / "include"
+LIB = HERE / "libk2q.so"
+SOURCES = ("api.hip", "rotquant.hip", "gemm.hip", "lora.hip")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+# -ffp-contract=off: the rotation/quantization arithmetic is specified op by op (bit-exact int8 codes);
+# deliberate fused multiply-adds are written as __builtin_fmaf.  packed-fp32-ops is disabled on purpose.
+CFLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{INCLUDE}", "-Wall", "-Wno-unused-function",
+]
+
+
+def _compile(src: Path, obj: Path) -> None:
+    cmd = [HIPCC, *CFLAGS, "-c", str(src), "-o", str(obj)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src.name}:\n{r.stderr}")
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every kernel source for gfx950 and link ``libk2q.so``.  Always recompiles."""
+    objdir = HERE / "_build"
+    objdir.mkdir(exist_ok=True)
+    objs = [objdir / (Path(s).stem + ".o") for s in SOURCES]
+    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as ex:
+        list(ex.map(lambda so: _compile(CSRC / so[0], so[1]), zip(SOURCES, objs)))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stderr}")
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"built {LIB} ({LIB.stat().st_size} bytes)")
+    return LIB
+
+
+if __name__ == "__main__":
+    build(verbose=True)
+    sys.exit(0)

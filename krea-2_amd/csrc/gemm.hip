@@ -1,0 +1,663 @@
+// Kernels (2)-(4): LDS-tiled MFMA GEMMs with fused epilogues for gfx950.
+//
+// All three GEMMs of the path have both operands contiguous along the reduction axis ("NT"):
+//   forward  acc[m,n] = sum_k qx[m,k] qw[n,k]          int8 x int8 -> int32 (v_mfma_i32_32x32x32_i8)
+//   dX       t[m,k]   = sum_n dy[m,n] wt[k,n]          bf16 x bf16 -> f32   (v_mfma_f32_32x32x16_bf16)
+// so one skeleton serves both: operand "A" supplies the rows of the MFMA output (n, or k for dX),
+// operand "B" its columns (m); out[b_row][a_row] is row-major over (m, n|k).
+//
+// Tiling: 256 x 256 output tile per 256-thread workgroup (4 waves, 2 x 2, 128 x 128 per wave as 4 x 4
+// MFMA 32x32 blocks), 128 bytes of reduction per stage (128 int8 or 64 bf16), LDS double-buffered
+// (2 x 2 x 32 KB).  LDS rows are 128 B; the 16-byte chunk c of row r lives at chunk c ^ f(r) with
+// f(r) = (r & 7) ^ ((r >> 3) & 1), which keeps both the 16-byte stores of the global->LDS copy and the
+// 16-byte MFMA fragment reads free of bank conflicts.  Workgroup ids are remapped so that consecutive
+// tiles land on the same XCD (ids are dealt round-robin over the 8 XCDs), then grouped 8 B-tiles at a
+// time so concurrently running tiles share operand strips in that XCD's L2.
+//
+// Epilogues (in registers, MFMA C layout: lane l owns output column l%32 and rows 8j+4(l/32)+i):
+//   EPI_W8   y = bf16(2^-7 s_x[m] s_w[n] acc + bias[n] + LoRA), LoRA = one bf16 MFMA per 16 of rank
+//            accumulating lora_scale*u[m,:] . lora_b[n,:] onto the dequantized f32 value.
+//   EPI_ACC  raw int32 acc (debug entry for bit-exact checks).
+//   EPI_DX   inverse rotation: FWHT over each 128-block of k (a wave's 128 A-rows are one block),
+//            times 2^-7, plus the LoRA term g[m,:] . at[k,:], stored bf16.
+#include "k2q_common.h"
+
+namespace {
+
+enum { EPI_W8 = 0, EPI_ACC = 1, EPI_DX = 2 };
+
+constexpr int BT = 256;     // tile rows (A) and columns (B)
+constexpr int BKB = 128;    // reduction bytes per stage
+constexpr int TILE_BYTES = BT * BKB;
+
+struct GemmArgs {
+  const uint8_t* a;   // A operand, rows_a x kbytes, row stride lda_b bytes
+  const uint8_t* b;   // B operand, rows_b x kbytes
+  int64_t rows_a, rows_b, kbytes, lda_b, ldb_b;
+  void* out;          // out[b_row][a_row], row stride ldo elements
+  int64_t ldo;
+  const float* sx;    // EPI_W8: per-B-row scale (already multiplied by nothing; 2^-7 applied here)
+  const float* sw;    // EPI_W8: per-A-row scale
+  const float* bias;  // EPI_W8: per-A-row bias (nullable)
+  const float* lora_rb;  // per-B-row LoRA factor rows (u or g), rows_b x r f32 (nullable)
+  const float* lora_ra;  // per-A-row LoRA factor rows (lora_b or A^T), rows_a x r f32
+  int r;
+  float lora_scale;
+};
+
+__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+__device__ __forceinline__ void tile_coords(int64_t tiles_a, int64_t tiles_b, int64_t& ta, int64_t& tb) {
+  const int nwg = gridDim.x;
+  const int bid = blockIdx.x;
+  const int xcd = bid & 7, idx = bid >> 3;
+  const int per = (nwg + 7) >> 3, rem = nwg & 7;
+  const int lid = (rem == 0 || xcd < rem) ? xcd * per + idx : rem * per + (xcd - rem) * (per - 1) + idx;
+  constexpr int GB = 8;
+  const int64_t in_group = (int64_t)GB * tiles_a;
+  const int64_t g = lid / in_group;
+  const int64_t first_b = g * GB;
+  const int64_t gsize = (tiles_b - first_b) < GB ? (tiles_b - first_b) : GB;
+  const int64_t r = lid % in_group;
+  tb = first_b + r % gsize;
+  ta = r / gsize;
+}
+
+// Global -> registers: thread t copies chunk (t & 7) of tile rows (t >> 3) + 32 i, i = 0..7.  `tile` is the
+// workgroup-uniform address of the tile's first row at the current stage; the per-thread offsets are
+// 32-bit (row-in-tile * ld + chunk), with rows past the end clamped onto the last row (in bounds; those
+// results are never stored).
+template <int NL>  // NL = tile rows / 32
+struct TileOffsets {
+  uint32_t o[NL];
+};
+
+template <int NL>
+__device__ __forceinline__ TileOffsets<NL> tile_offsets(int64_t row0, int64_t nrows, int64_t ld) {
+  const int t = threadIdx.x;
+  TileOffsets<NL> r;
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    int64_t rr = (t >> 3) + 32 * i;
+    rr = row0 + rr < nrows ? rr : nrows - 1 - row0;
+    r.o[i] = (uint32_t)(rr * ld) + 16u * (uint32_t)(t & 7);
+  }
+  return r;
+}
+
+template <int NL>
+__device__ __forceinline__ void g2r(const uint8_t* tile, const TileOffsets<NL>& off, v4i (&r)[NL]) {
+#pragma unroll
+  for (int i = 0; i < NL; ++i) r[i] = *reinterpret_cast<const v4i*>(tile + off.o[i]);
+}
+
+template <int NL>
+__device__ __forceinline__ void r2s(uint8_t* s, const v4i (&r)[NL]) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    const int row = (t >> 3) + 32 * i;
+    const int pc = (t & 7) ^ swz(row);
+    *reinterpret_cast<v4i*>(s + row * BKB + 16 * pc) = r[i];
+  }
+}
+
+__device__ __forceinline__ v4i frag(const uint8_t* s, int row, int chunk) {
+  return *reinterpret_cast<const v4i*>(s + row * BKB + 16 * (chunk ^ swz(row)));
+}
+
+template <bool BF16>
+__device__ __forceinline__ void mma(v4i a, v4i b, v16i& c) {
+  if constexpr (BF16) {
+    v16f cf = __builtin_bit_cast(v16f, c);
+    cf = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b),
+                                                cf, 0, 0, 0);
+    c = __builtin_bit_cast(v16i, cf);
+  } else {
+    c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+  }
+}
+
+// 8 consecutive f32 -> 8 bf16 (times s), as an MFMA fragment.
+__device__ __forceinline__ v8bf f32x8_to_bf16(const float* p, float s) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0];
+  const float4 b = reinterpret_cast<const float4*>(p)[1];
+  v4i w;
+  w[0] = (int)pack_bf16x2(a.x * s, a.y * s);
+  w[1] = (int)pack_bf16x2(a.z * s, a.w * s);
+  w[2] = (int)pack_bf16x2(b.x * s, b.y * s);
+  w[3] = (int)pack_bf16x2(b.z * s, b.w * s);
+  return __builtin_bit_cast(v8bf, w);
+}
+
+// LoRA term of one 32 x 32 output block, accumulated onto its f32 values with bf16 MFMAs (r/16 of them):
+// f[a_row][b_col] += lora_ra[a_row, :] . (scale * lora_rb[b_col, :]).
+__device__ __forceinline__ v16f lora_block(const float* lora_ra, const float* lora_rb, int r, float scale,
+                                           int64_t rows_a, int64_t rows_b, int64_t arow0, int64_t bcol0,
+                                           int lane, v16f f) {
+  const int h = lane >> 5, c = lane & 31;
+  int64_t ra = arow0 + c, rb = bcol0 + c;
+  ra = ra < rows_a ? ra : rows_a - 1;
+  rb = rb < rows_b ? rb : rows_b - 1;
+  for (int ks = 0; ks < r; ks += 16) {
+    const v8bf fa = f32x8_to_bf16(lora_ra + ra * r + ks + 8 * h, 1.f);
+    const v8bf fb = f32x8_to_bf16(lora_rb + rb * r + ks + 8 * h, scale);
+    f = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, fb, f, 0, 0, 0);
+  }
+  return f;
+}
+
+// bf16 store of one 32 x 32 block: out[m][n..n+3], m = bcol0 + lane%32, n = arow0 + 8 j + 4 (lane/32).
+__device__ __forceinline__ void store_block(uint16_t* out, int64_t ldo, int64_t rows_a, int64_t rows_b,
+                                            int64_t arow0, int64_t bcol0, int lane, const v16f& f) {
+  const int h = lane >> 5, c32 = lane & 31;
+  const int64_t m = bcol0 + c32;
+  if (m >= rows_b) return;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t n = arow0 + 8 * j + 4 * h;
+    if (n >= rows_a) continue;
+    const v2u v = v2u{pack_bf16x2(f[4 * j], f[4 * j + 1]), pack_bf16x2(f[4 * j + 2], f[4 * j + 3])};
+    *reinterpret_cast<v2u*>(out + m * ldo + n) = v;
+  }
+}
+
+// Inverse rotation of one column slice: FWHT over the wave's 128 A-rows (one Hadamard block), times
+// 2^-7.  Row-index bits: i -> 0-1 (register e bits 0-1), h -> 2 (partner lane l^32), j -> 3-4 (e bits
+// 2-3), ia -> 5-6.  The order of the stages is free here: the result is held to a tolerance.
+__device__ __forceinline__ void fwht128_rows(v16f (&f)[4], int h) {
+#pragma unroll
+  for (int st = 1; st <= 8; st <<= 1)
+#pragma unroll
+    for (int ia = 0; ia < 4; ++ia)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        if (e & st) continue;
+        const float a = f[ia][e], b = f[ia][e + st];
+        f[ia][e] = a + b;
+        f[ia][e + st] = a - b;
+      }
+#pragma unroll
+  for (int st = 1; st <= 2; st <<= 1)
+#pragma unroll
+    for (int ia = 0; ia < 4; ++ia) {
+      if (ia & st) continue;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float a = f[ia][e], b = f[ia + st][e];
+        f[ia][e] = a + b;
+        f[ia + st][e] = a - b;
+      }
+    }
+#pragma unroll
+  for (int ia = 0; ia < 4; ++ia)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float pv = __shfl_xor(f[ia][e], 32, 64);
+      f[ia][e] = (h ? (pv - f[ia][e]) : (f[ia][e] + pv)) * 0.0078125f;
+    }
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs p) {
+  constexpr bool BF16 = (EPI == EPI_DX);
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* sA = smem;                    // [2][TILE_BYTES]
+  uint8_t* sB = smem + 2 * TILE_BYTES;   // [2][TILE_BYTES]
+
+  const int64_t tiles_a = (p.rows_a + BT - 1) / BT;
+  const int64_t tiles_b = (p.rows_b + BT - 1) / BT;
+  int64_t ta, tb;
+  tile_coords(tiles_a, tiles_b, ta, tb);
+  const int64_t A0 = ta * BT, B0 = tb * BT;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wa = wave & 1, wb = wave >> 1;
+  const int h = lane >> 5, c32 = lane & 31;
+
+  v16i acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = v16i{0};
+
+  const int nk = (int)(p.kbytes / BKB);
+  const TileOffsets<8> offa = tile_offsets<8>(A0, p.rows_a, p.lda_b);
+  const TileOffsets<8> offb = tile_offsets<8>(B0, p.rows_b, p.ldb_b);
+  const uint8_t* gA = p.a + A0 * p.lda_b;
+  const uint8_t* gB = p.b + B0 * p.ldb_b;
+  v4i ra[8], rb[8];
+  g2r(gA, offa, ra);
+  g2r(gB, offb, rb);
+  r2s(sA, ra);
+  r2s(sB, rb);
+  __syncthreads();
+
+  auto compute = [&](int buf) {
+    const uint8_t* tA = sA + buf * TILE_BYTES;
+    const uint8_t* tB = sB + buf * TILE_BYTES;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      v4i fa[4], fb[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        fa[i] = frag(tA, 128 * wa + 32 * i + c32, 2 * kk + h);
+        fb[i] = frag(tB, 128 * wb + 32 * i + c32, 2 * kk + h);
+      }
+#pragma unroll
+      for (int ia = 0; ia < 4; ++ia)
+#pragma unroll
+        for (int ib = 0; ib < 4; ++ib) mma<BF16>(fa[ia], fb[ib], acc[ia][ib]);
+    }
+  };
+  // Steady state: prefetch stage kt+1 into registers, run stage kt from LDS, publish kt+1 to the other
+  // buffer, one barrier.  The last stage has nothing to prefetch.
+  for (int kt = 0; kt < nk - 1; ++kt) {
+    const int buf = kt & 1;
+    g2r(gA + (kt + 1) * BKB, offa, ra);
+    g2r(gB + (kt + 1) * BKB, offb, rb);
+    compute(buf);
+    r2s(sA + (buf ^ 1) * TILE_BYTES, ra);
+    r2s(sB + (buf ^ 1) * TILE_BYTES, rb);
+    __syncthreads();
+  }
+  compute((nk - 1) & 1);
+
+  const int64_t a0 = A0 + 128 * wa;   // first A-row of this wave
+  const int64_t b0 = B0 + 128 * wb;   // first B-row of this wave
+
+  if constexpr (EPI == EPI_ACC) {
+    int32_t* out = static_cast<int32_t*>(p.out);
+#pragma unroll
+    for (int ia = 0; ia < 4; ++ia)
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib) {
+        const int64_t m = b0 + 32 * ib + c32;
+        if (m >= p.rows_b) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t n = a0 + 32 * ia + 8 * j + 4 * h;
+          if (n >= p.rows_a) continue;
+          int4 v = make_int4(acc[ia][ib][4 * j], acc[ia][ib][4 * j + 1], acc[ia][ib][4 * j + 2],
+                             acc[ia][ib][4 * j + 3]);
+          *reinterpret_cast<int4*>(out + m * p.ldo + n) = v;
+        }
+      }
+    return;
+  } else if constexpr (EPI == EPI_W8) {
+    // One 32-row slice (ia) at a time: its 4 scale/bias vectors, its LoRA A-fragments, then the four
+    // 32 x 32 blocks one by one, so at most one block's 16 f32 values are live beyond the accumulators.
+    float sxm[4];
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) {
+      int64_t m = b0 + 32 * ib + c32;
+      m = m < p.rows_b ? m : p.rows_b - 1;
+      sxm[ib] = p.sx[m] * 0.0078125f;  // 2^-7: the two unnormalised rotations
+    }
+    uint16_t* out = static_cast<uint16_t*>(p.out);
+#pragma unroll
+    for (int ia = 0; ia < 4; ++ia) {
+      float4 sw[4], bi[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        int64_t n = a0 + 32 * ia + 8 * j + 4 * h;
+        n = n < p.rows_a ? n : p.rows_a - 4;
+        sw[j] = *reinterpret_cast<const float4*>(p.sw + n);
+        bi[j] = p.bias ? *reinterpret_cast<const float4*>(p.bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib) {
+        v16f f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          f[4 * j + 0] = (float)acc[ia][ib][4 * j + 0] * (sxm[ib] * sw[j].x) + bi[j].x;
+          f[4 * j + 1] = (float)acc[ia][ib][4 * j + 1] * (sxm[ib] * sw[j].y) + bi[j].y;
+          f[4 * j + 2] = (float)acc[ia][ib][4 * j + 2] * (sxm[ib] * sw[j].z) + bi[j].z;
+          f[4 * j + 3] = (float)acc[ia][ib][4 * j + 3] * (sxm[ib] * sw[j].w) + bi[j].w;
+        }
+        if (p.lora_rb && p.r > 0)
+          f = lora_block(p.lora_ra, p.lora_rb, p.r, p.lora_scale, p.rows_a, p.rows_b, a0 + 32 * ia,
+                         b0 + 32 * ib, lane, f);
+        store_block(out, p.ldo, p.rows_a, p.rows_b, a0 + 32 * ia, b0 + 32 * ib, lane, f);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // keep the next slice's scale/bias loads out of this one
+    }
+  } else {  // EPI_DX: one 32-column slice (ib) at a time; the FWHT needs all 4 row slices of it.
+    uint16_t* out = static_cast<uint16_t*>(p.out);
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) {
+      v16f f[4];
+#pragma unroll
+      for (int ia = 0; ia < 4; ++ia) f[ia] = __builtin_bit_cast(v16f, acc[ia][ib]);
+      fwht128_rows(f, h);
+#pragma unroll
+      for (int ia = 0; ia < 4; ++ia) {
+        if (p.lora_rb && p.r > 0)
+          f[ia] = lora_block(p.lora_ra, p.lora_rb, p.r, p.lora_scale, p.rows_a, p.rows_b, a0 + 32 * ia,
+                             b0 + 32 * ib, lane, f[ia]);
+        store_block(out, p.ldo, p.rows_a, p.rows_b, a0 + 32 * ia, b0 + 32 * ib, lane, f[ia]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// W4A8: A operand = packed int4 weights (rows n, K/2 bytes per row), bf16 group scales sw4[g][n].
+// Tile 128 (n) x 128 (m), 4 waves 2 x 2 of 64 x 64.  A row in LDS is 64 B = 8 units of 8 B, unit u of
+// row r stored at u ^ ((r >> 2) & 7) (conflict-free 8-byte fragment reads).  A lane's 8 packed bytes hold
+// the 16 codes of one 16-wide K chunk; `w << 4 & 0xF0F0F0F0` and `w & 0xF0F0F0F0` give them as int8
+// values 16*q in K order, so one v_mfma_i32_32x32x32_i8 per 32 of K sees 16x the true products (exact,
+// |16 acc_g| <= 16*64*127*7 < 2^20).  Each 64-wide group is accumulated in int32, converted once and
+// scaled: accf += float(acc_g) * s[g][n]; the 1/16 is folded into the final scale.  The per-group
+// convert + FMA (2 VALU ops per output per group) bounds this kernel, not the MFMAs.
+constexpr int W4_BA = 128;                // n rows per tile
+constexpr int W4_BB = 128;                // m rows per tile
+constexpr int W4_IA = 2, W4_IB = 2;       // 32x32 blocks per wave along n and m
+constexpr int W4_TILE_A = W4_BA * 64;     // bytes per stage (128 K codes per row, packed)
+constexpr int W4_TILE_B = W4_BB * BKB;
+constexpr int W4_SCALES = 2 * W4_BA * 2;  // 2 groups x 128 n x bf16
+
+struct W4Args {
+  const uint8_t* a;      // N x K/2 packed
+  const uint16_t* s4;    // K/64 x N bf16
+  const int8_t* b;       // M x K int8
+  int64_t N, M, K;
+  void* out;             // bf16 y (EPI_W8) or f32 (EPI_ACC: sum_g s acc_g)
+  const float* sx;
+  const float* bias;
+  const float* lora_rb;
+  const float* lora_ra;
+  int r;
+  float lora_scale;
+};
+
+__device__ __forceinline__ int swz4(int row) { return (row >> 2) & 7; }
+
+template <int EPI>
+__global__ __launch_bounds__(256, 1) void gemm_w4_kernel(W4Args p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint8_t* sA = smem;                                  // [2][W4_TILE_A]
+  uint8_t* sB = smem + 2 * W4_TILE_A;                  // [2][W4_TILE_B]
+  uint16_t* sS = reinterpret_cast<uint16_t*>(smem + 2 * W4_TILE_A + 2 * W4_TILE_B);  // [2][2][128]
+
+  const int64_t tiles_a = (p.N + W4_BA - 1) / W4_BA;
+  const int64_t tiles_b = (p.M + W4_BB - 1) / W4_BB;
+  int64_t ta, tb;
+  tile_coords(tiles_a, tiles_b, ta, tb);
+  const int64_t A0 = ta * W4_BA, B0 = tb * W4_BB;
+
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int wa = wave & 1, wb = wave >> 1;
+  const int h = lane >> 5, c32 = lane & 31;
+  const int64_t kb = p.K / 2;   // packed bytes per A row
+
+  v16f accf[W4_IA][W4_IB];
+#pragma unroll
+  for (int i = 0; i < W4_IA; ++i)
+#pragma unroll
+    for (int j = 0; j < W4_IB; ++j) accf[i][j] = v16f{0.f};
+
+  uint32_t offa4[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    int64_t rr = (t >> 2) + 64 * i;
+    rr = A0 + rr < p.N ? rr : p.N - 1 - A0;
+    offa4[i] = (uint32_t)(rr * kb) + 16u * (uint32_t)(t & 3);
+  }
+  const TileOffsets<4> offb = tile_offsets<4>(B0, p.M, p.K);
+  const uint8_t* gA = p.a + A0 * kb;
+  const uint8_t* gB = reinterpret_cast<const uint8_t*>(p.b) + B0 * p.K;
+  int64_t ns = A0 + 4 * (t & 31);
+  ns = ns < p.N ? ns : p.N - 4;
+  const uint16_t* gS = p.s4 + (int64_t)((t >> 5) & 1) * p.N + ns;   // read by t < 64 only
+  v4i ra[2], rb[4];
+  v2u rs = v2u{0u, 0u};
+  auto load_stage = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) ra[i] = *reinterpret_cast<const v4i*>(gA + kt * 64 + offa4[i]);
+    g2r<4>(gB + kt * BKB, offb, rb);
+    if (t < 64) rs = *reinterpret_cast<const v2u*>(gS + (int64_t)kt * 2 * p.N);
+  };
+  auto store_stage = [&](int buf) {
+    uint8_t* tA = sA + buf * W4_TILE_A;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int row = (t >> 2) + 64 * i;
+      const int u0 = 2 * (t & 3);
+      *reinterpret_cast<v2u*>(tA + row * 64 + 8 * (u0 ^ swz4(row))) = v2u{(uint32_t)ra[i][0], (uint32_t)ra[i][1]};
+      *reinterpret_cast<v2u*>(tA + row * 64 + 8 * ((u0 + 1) ^ swz4(row))) =
+          v2u{(uint32_t)ra[i][2], (uint32_t)ra[i][3]};
+    }
+    r2s<4>(sB + buf * W4_TILE_B, rb);
+    if (t < 64) *reinterpret_cast<v2u*>(sS + buf * 2 * W4_BA + (t >> 5) * W4_BA + 4 * (t & 31)) = rs;
+  };
+
+  auto compute = [&](int buf) {
+    const uint8_t* tA = sA + buf * W4_TILE_A;
+    const uint8_t* tB = sB + buf * W4_TILE_B;
+    const uint16_t* tS = sS + buf * 2 * W4_BA;
+#pragma unroll
+    for (int grp = 0; grp < 2; ++grp) {
+      v16i acc[W4_IA][W4_IB];
+#pragma unroll
+      for (int i = 0; i < W4_IA; ++i)
+#pragma unroll
+        for (int j = 0; j < W4_IB; ++j) acc[i][j] = v16i{0};
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2) {
+        const int kk = 2 * grp + k2;
+        v4i fa[W4_IA], fb[W4_IB];
+#pragma unroll
+        for (int i = 0; i < W4_IA; ++i) {
+          const int row = 32 * W4_IA * wa + 32 * i + c32;
+          const v2u w = *reinterpret_cast<const v2u*>(tA + row * 64 + 8 * ((2 * kk + h) ^ swz4(row)));
+          fa[i] = v4i{(int)((w[0] << 4) & 0xF0F0F0F0u), (int)((w[1] << 4) & 0xF0F0F0F0u),
+                      (int)(w[0] & 0xF0F0F0F0u), (int)(w[1] & 0xF0F0F0F0u)};
+        }
+#pragma unroll
+        for (int i = 0; i < W4_IB; ++i) fb[i] = frag(tB, 32 * W4_IB * wb + 32 * i + c32, 2 * kk + h);
+#pragma unroll
+        for (int ia = 0; ia < W4_IA; ++ia)
+#pragma unroll
+          for (int ib = 0; ib < W4_IB; ++ib)
+            acc[ia][ib] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[ia], fb[ib], acc[ia][ib], 0, 0, 0);
+      }
+#pragma unroll
+      for (int ia = 0; ia < W4_IA; ++ia)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const v2u sp =
+              *reinterpret_cast<const v2u*>(tS + grp * W4_BA + 32 * W4_IA * wa + 32 * ia + 8 * j + 4 * h);
+          const float sv[4] = {bf16_bits_to_f32(sp[0] & 0xffffu), bf16_bits_to_f32(sp[0] >> 16),
+                               bf16_bits_to_f32(sp[1] & 0xffffu), bf16_bits_to_f32(sp[1] >> 16)};
+#pragma unroll
+          for (int ib = 0; ib < W4_IB; ++ib)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              accf[ia][ib][4 * j + i] = __builtin_fmaf((float)acc[ia][ib][4 * j + i], sv[i],
+                                                       accf[ia][ib][4 * j + i]);
+        }
+    }
+  };
+
+  const int nk = (int)(p.K / BKB);
+  load_stage(0);
+  store_stage(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk - 1; ++kt) {
+    const int buf = kt & 1;
+    load_stage(kt + 1);
+    compute(buf);
+    store_stage(buf ^ 1);
+    __syncthreads();
+  }
+  compute((nk - 1) & 1);
+
+  const int64_t a0 = A0 + 32 * W4_IA * wa, b0 = B0 + 32 * W4_IB * wb;
+  if constexpr (EPI == EPI_ACC) {
+    float* out = static_cast<float*>(p.out);
+#pragma unroll
+    for (int ia = 0; ia < W4_IA; ++ia)
+#pragma unroll
+      for (int ib = 0; ib < W4_IB; ++ib) {
+        const int64_t m = b0 + 32 * ib + c32;
+        if (m >= p.M) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t n = a0 + 32 * ia + 8 * j + 4 * h;
+          if (n >= p.N) continue;
+          const v4f v = v4f{accf[ia][ib][4 * j] * 0.0625f, accf[ia][ib][4 * j + 1] * 0.0625f,
+                            accf[ia][ib][4 * j + 2] * 0.0625f, accf[ia][ib][4 * j + 3] * 0.0625f};
+          *reinterpret_cast<v4f*>(out + m * p.N + n) = v;
+        }
+      }
+  } else {
+    uint16_t* out = static_cast<uint16_t*>(p.out);
+#pragma unroll
+    for (int ib = 0; ib < W4_IB; ++ib) {
+      int64_t m = b0 + 32 * ib + c32;
+      m = m < p.M ? m : p.M - 1;
+      const float sxm = p.sx[m] * (0.0078125f * 0.0625f);  // 2^-7 rotations, 1/16 nibble placement
+#pragma unroll
+      for (int ia = 0; ia < W4_IA; ++ia) {
+        v16f f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          int64_t n = a0 + 32 * ia + 8 * j + 4 * h;
+          n = n < p.N ? n : p.N - 4;
+          const float4 bi =
+              p.bias ? *reinterpret_cast<const float4*>(p.bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
+          f[4 * j + 0] = accf[ia][ib][4 * j + 0] * sxm + bi.x;
+          f[4 * j + 1] = accf[ia][ib][4 * j + 1] * sxm + bi.y;
+          f[4 * j + 2] = accf[ia][ib][4 * j + 2] * sxm + bi.z;
+          f[4 * j + 3] = accf[ia][ib][4 * j + 3] * sxm + bi.w;
+        }
+        if (p.lora_rb && p.r > 0)
+          f = lora_block(p.lora_ra, p.lora_rb, p.r, p.lora_scale, p.N, p.M, a0 + 32 * ia, b0 + 32 * ib, lane,
+                         f);
+        store_block(out, p.N, p.N, p.M, a0 + 32 * ia, b0 + 32 * ib, lane, f);
+      }
+    }
+  }
+}
+
+template <int EPI>
+int launch_w4(const W4Args& p, hipStream_t st) {
+  constexpr int lds = 2 * W4_TILE_A + 2 * W4_TILE_B + 2 * W4_SCALES;
+  if (hipFuncSetAttribute((const void*)gemm_w4_kernel<EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          lds) != hipSuccess)
+    return K2Q_ELAUNCH;
+  const int64_t tiles = ((p.N + W4_BA - 1) / W4_BA) * ((p.M + W4_BB - 1) / W4_BB);
+  if (tiles > 0x7fffffff) return K2Q_EUNSUPPORTED;
+  hipLaunchKernelGGL(gemm_w4_kernel<EPI>, dim3((unsigned)tiles), dim3(256), lds, st, p);
+  return k2q_launch_status();
+}
+
+template <int EPI>
+int launch_gemm(const GemmArgs& p, hipStream_t st) {
+  constexpr int lds = 4 * TILE_BYTES;
+  if (hipFuncSetAttribute((const void*)gemm_nt_kernel<EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          lds) != hipSuccess)
+    return K2Q_ELAUNCH;
+  const int64_t tiles = ((p.rows_a + BT - 1) / BT) * ((p.rows_b + BT - 1) / BT);
+  if (tiles > 0x7fffffff) return K2Q_EUNSUPPORTED;
+  hipLaunchKernelGGL(gemm_nt_kernel<EPI>, dim3((unsigned)tiles), dim3(256), lds, st, p);
+  return k2q_launch_status();
+}
+
+int check_common(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || N < 1 || K < K2Q_HADAMARD || K % K2Q_HADAMARD) return K2Q_EINVAL;
+  if (N % 4) return K2Q_EINVAL;
+  return K2Q_OK;
+}
+
+int check_lora(const float* u, const float* lb, int64_t r) {
+  if (!u) return K2Q_OK;
+  if (!lb || r < 16 || r > 128 || r % 16) return K2Q_EINVAL;
+  if (!k2q_aligned(u, 16) || !k2q_aligned(lb, 16)) return K2Q_EINVAL;
+  return K2Q_OK;
+}
+
+}  // namespace
+
+extern "C" int k2q_gemm_w8a8(const int8_t* qx, const float* sx, const int8_t* qw, const float* sw,
+                             const float* bias, const float* u, const float* lora_b, int64_t r,
+                             float lora_scale, int64_t M, int64_t N, int64_t K, uint16_t* y,
+                             void* stream) {
+  int rc = check_common(M, N, K);
+  if (rc) return rc;
+  if (!qx || !sx || !qw || !sw || !y) return K2Q_EINVAL;
+  if (!k2q_aligned(qx, 16) || !k2q_aligned(qw, 16) || !k2q_aligned(sw, 16) || !k2q_aligned(y, 8))
+    return K2Q_EINVAL;
+  if (bias && !k2q_aligned(bias, 16)) return K2Q_EINVAL;
+  if ((rc = check_lora(u, lora_b, r))) return rc;
+  GemmArgs p{};
+  p.a = reinterpret_cast<const uint8_t*>(qw);
+  p.b = reinterpret_cast<const uint8_t*>(qx);
+  p.rows_a = N; p.rows_b = M; p.kbytes = K; p.lda_b = K; p.ldb_b = K;
+  p.out = y; p.ldo = N;
+  p.sx = sx; p.sw = sw; p.bias = bias;
+  p.lora_rb = u; p.lora_ra = lora_b; p.r = u ? (int)r : 0; p.lora_scale = lora_scale;
+  return launch_gemm<EPI_W8>(p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int k2q_gemm_w8a8_acc(const int8_t* qx, const int8_t* qw, int64_t M, int64_t N, int64_t K,
+                                 int32_t* acc, void* stream) {
+  int rc = check_common(M, N, K);
+  if (rc) return rc;
+  if (!qx || !qw || !acc || !k2q_aligned(qx, 16) || !k2q_aligned(qw, 16) || !k2q_aligned(acc, 16))
+    return K2Q_EINVAL;
+  GemmArgs p{};
+  p.a = reinterpret_cast<const uint8_t*>(qw);
+  p.b = reinterpret_cast<const uint8_t*>(qx);
+  p.rows_a = N; p.rows_b = M; p.kbytes = K; p.lda_b = K; p.ldb_b = K;
+  p.out = acc; p.ldo = N;
+  return launch_gemm<EPI_ACC>(p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int k2q_gemm_dx(const uint16_t* dy, const uint16_t* wt, int64_t M, int64_t N, int64_t K,
+                           const float* g, const float* at, int64_t r, uint16_t* dx, void* stream) {
+  if (M < 1 || K < K2Q_HADAMARD || K % K2Q_HADAMARD || N < 64 || N % 64) return K2Q_EINVAL;
+  if (!dy || !wt || !dx || !k2q_aligned(dy, 16) || !k2q_aligned(wt, 16) || !k2q_aligned(dx, 8))
+    return K2Q_EINVAL;
+  int rc = check_lora(g, at, r);
+  if (rc) return rc;
+  GemmArgs p{};
+  p.a = reinterpret_cast<const uint8_t*>(wt);
+  p.b = reinterpret_cast<const uint8_t*>(dy);
+  p.rows_a = K; p.rows_b = M; p.kbytes = 2 * N; p.lda_b = 2 * N; p.ldb_b = 2 * N;
+  p.out = dx; p.ldo = K;
+  p.lora_rb = g; p.lora_ra = at; p.r = g ? (int)r : 0; p.lora_scale = 1.f;
+  return launch_gemm<EPI_DX>(p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int k2q_gemm_w4a8(const int8_t* qx, const float* sx, const uint8_t* qw4, const uint16_t* sw4,
+                             const float* bias, const float* u, const float* lora_b, int64_t r,
+                             float lora_scale, int64_t M, int64_t N, int64_t K, uint16_t* y, void* stream) {
+  int rc = check_common(M, N, K);
+  if (rc) return rc;
+  if (!qx || !sx || !qw4 || !sw4 || !y) return K2Q_EINVAL;
+  if (!k2q_aligned(qx, 16) || !k2q_aligned(qw4, 16) || !k2q_aligned(sw4, 8) || !k2q_aligned(y, 8))
+    return K2Q_EINVAL;
+  if (bias && !k2q_aligned(bias, 16)) return K2Q_EINVAL;
+  if ((rc = check_lora(u, lora_b, r))) return rc;
+  W4Args p{};
+  p.a = qw4; p.s4 = sw4; p.b = qx; p.N = N; p.M = M; p.K = K;
+  p.out = y; p.sx = sx; p.bias = bias;
+  p.lora_rb = u; p.lora_ra = lora_b; p.r = u ? (int)r : 0; p.lora_scale = lora_scale;
+  return launch_w4<EPI_W8>(p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int k2q_gemm_w4a8_f32(const int8_t* qx, const uint8_t* qw4, const uint16_t* sw4, int64_t M,
+                                 int64_t N, int64_t K, float* out, void* stream) {
+  int rc = check_common(M, N, K);
+  if (rc) return rc;
+  if (!qx || !qw4 || !sw4 || !out || !k2q_aligned(qx, 16) || !k2q_aligned(qw4, 16) ||
+      !k2q_aligned(sw4, 8) || !k2q_aligned(out, 16))
+    return K2Q_EINVAL;
+  W4Args p{};
+  p.a = qw4; p.s4 = sw4; p.b = qx; p.N = N; p.M = M; p.K = K; p.out = out;
+  return launch_w4<EPI_ACC>(p, static_cast<hipStream_t>(stream));
+}

@@ -1,0 +1,186 @@
+"""ConvRot quantized frozen base: the drop-in counterpart of the reference's ``Fp8Linear``.
+
+Reference interface followed (``quantize.py:23-68``): built from an existing ``nn.Linear``
+(``quantize.py:33``), class attribute ``is_quant_linear = True`` (``:31``, checked by ``lora.py:100,107``),
+``in_features`` / ``out_features`` (``:42``), a ``weight`` property used only as a device probe (``:44-46``),
+``bias`` Parameter or None (``:40-41``), every tensor an ``nn.Parameter(requires_grad=False)`` so block swap
+pages it (``mmdit.py:409-414``), and a walker that replaces the Linears of ``dit.blocks`` and returns the count
+(``quantize.py:54-68``).
+
+What differs is the arithmetic: activations are rotated by a block Walsh-Hadamard
+transform and quantized per token to int8 on the fly; weights are stored rotated and quantized, int8 per output
+channel (``w8a8``) or packed int4 with one bf16 scale per 64-wide group (``w4a8``); the GEMM runs on int8
+MFMA with int32 accumulation.  All of it runs in the HIP library ``libk2q.so``; nothing here computes on the
+CPU.  Scales are stored as integer bit patterns (f32 bits in int32, bf16 bits in int16) so that
+``Module.to(dtype)`` — which casts floating Parameters — leaves them exact.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+
+MODES = ("w8a8", "w4a8")
+
+
+class _ConvRotLinearFn(torch.autograd.Function):
+    """Forward: rotate+quantize x, optional LoRA down-projection, fused GEMM + epilogue.
+    Backward (straight-through over both quantizers): ``dX = 2^-7 (dY W_hat) R + g A`` with
+    ``g = s dY B``; ``dA = g^T x``, ``dB = s dY^T u`` — the autograd of ``lora.py:47-48`` through a frozen base.
+    Deterministic (no atomics, fixed reduction order), so checkpoint recompute reproduces the forward."""
+
+    @staticmethod
+    def forward(ctx, x2, lora_A, lora_B, qweight, wscale, bias, w4, lora_scale):
+        qx, sx, _ = _lib.rotquant(x2)
+        u = _lib.lora_down(x2, lora_A) if lora_A is not None else None
+        gemm = _lib.gemm_w4a8 if w4 else _lib.gemm_w8a8
+        y = gemm(qx, sx, qweight, wscale, bias, u, lora_B, lora_scale)
+        ctx.w4 = w4
+        ctx.lora_scale = lora_scale
+        ctx.save_for_backward(x2 if lora_A is not None else None, u, lora_A, lora_B, qweight, wscale)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, u, A, B, qweight, wscale = ctx.saved_tensors
+        dy = dy.contiguous()
+        if dy.dtype != torch.bfloat16:
+            dy = dy.to(torch.bfloat16)
+        g = dA = dB = None
+        if A is not None:
+            dyf = dy.float()
+            g = (ctx.lora_scale * (dyf @ B)).contiguous()
+            if ctx.needs_input_grad[1]:
+                dA = g.t() @ x2.float()
+            if ctx.needs_input_grad[2]:
+                dB = ctx.lora_scale * (dyf.t() @ u)
+        dx = None
+        if ctx.needs_input_grad[0]:
+            dx = _lib.gemm_dx(dy, qweight, wscale, w4=ctx.w4, g=g, lora_a=A if g is not None else None)
+        return dx, dA, dB, None, None, None, None, None
+
+
+class ConvRotLinear(nn.Module):
+    """Frozen ``nn.Linear`` with the ConvRot W8A8 / W4A8 base, computed by gfx950 HIP kernels.
+
+    ``y = bf16(2^-7 s_x[m] s_w[n] (q_x q_w^T)[m,n] + bias[n])`` with ``q_x`` the per-token int8 codes of
+    ``x R`` and ``q_w`` the codes of ``W R`` (R = blockdiag of 128x128 +-1 Hadamards).  Exposes
+    ``in_features`` / ``out_features`` / ``weight`` / ``bias`` so it drops in as a ``LoRALinear`` base.
+    """
+
+    is_quant_linear = True
+
+    def __init__(self, lin: nn.Linear | None = None, mode: str = "w8a8"):
+        super().__init__()
+        if mode not in MODES:
+            raise ValueError(f"mode must be one of {MODES}, got {mode!r}")
+        self.mode = mode
+        if lin is None:  # filled by from_quantized
+            return
+        w = lin.weight.data
+        N, K = w.shape
+        _lib._check_k(K)
+        if N % 4:
+            raise ValueError(f"out_features={N} must be a multiple of 4")
+        home = w.device
+        if home.type != "cuda":
+            if not torch.cuda.is_available():
+                raise RuntimeError("ConvRotLinear quantizes on the GPU (libk2q, gfx950); no GPU is available")
+            w = w.to("cuda")
+        w = w.contiguous()
+        if w.dtype not in (torch.bfloat16, torch.float32):
+            w = w.float()
+        if mode == "w8a8":
+            q, s = _lib.quant_weight_i8(w)
+            s_bits = s.view(torch.int32)
+        else:
+            q, s4 = _lib.quant_weight_i4(w)
+            s_bits = s4.view(torch.int16)
+        self.qweight = nn.Parameter(q.to(home), requires_grad=False)
+        self.wscale = nn.Parameter(s_bits.to(home), requires_grad=False)
+        self.bias = (nn.Parameter(lin.bias.data.clone(), requires_grad=False)
+                     if lin.bias is not None else None)
+        self.in_features, self.out_features = K, N
+
+    @classmethod
+    def from_quantized(cls, qweight: torch.Tensor, wscale_bits: torch.Tensor, bias: torch.Tensor | None,
+                       mode: str = "w8a8") -> "ConvRotLinear":
+        """Wrap already-quantized tensors (e.g. loaded from disk): ``qweight`` int8 (N,K) with ``wscale_bits``
+        int32 (N,) f32 bits, or uint8 (N,K/2) packed int4 with int16 (K/64,N) bf16 bits."""
+        m = cls(None, mode)
+        if mode == "w8a8":
+            if qweight.dtype != torch.int8 or wscale_bits.dtype != torch.int32:
+                raise ValueError("w8a8 expects int8 codes and int32 scale bits")
+            N, K = qweight.shape
+            if wscale_bits.shape != (N,):
+                raise ValueError("w8a8 scale bits must be (N,)")
+        else:
+            if qweight.dtype != torch.uint8 or wscale_bits.dtype != torch.int16:
+                raise ValueError("w4a8 expects uint8 packed codes and int16 bf16 scale bits")
+            N, K = qweight.shape[0], qweight.shape[1] * 2
+            if wscale_bits.shape != (K // _lib.INT4_GROUP, N):
+                raise ValueError("w4a8 scale bits must be (K/64, N)")
+        _lib._check_k(K)
+        m.qweight = nn.Parameter(qweight, requires_grad=False)
+        m.wscale = nn.Parameter(wscale_bits, requires_grad=False)
+        m.bias = nn.Parameter(bias, requires_grad=False) if bias is not None else None
+        m.in_features, m.out_features = K, N
+        return m
+
+    @property
+    def weight(self) -> torch.Tensor:  # device probe for LoRALinear (quantize.py:44-46)
+        return self.qweight
+
+    @property
+    def weight_scale(self) -> torch.Tensor:
+        """The scales as floats: f32 (N,) for w8a8, bf16 (K/64, N) for w4a8 (views, no copy)."""
+        return self.wscale.view(torch.float32 if self.mode == "w8a8" else torch.bfloat16)
+
+    def extra_repr(self) -> str:
+        return f"in_features={self.in_features}, out_features={self.out_features}, mode={self.mode}, " \
+               f"bias={self.bias is not None}"
+
+    def _bias_f32(self):
+        if self.bias is None:
+            return None
+        b = self.bias
+        return b if b.dtype == torch.float32 and b.is_contiguous() else b.float().contiguous()
+
+    def forward_lora(self, x: torch.Tensor, lora_A: torch.Tensor | None, lora_B: torch.Tensor | None,
+                     lora_scale: float) -> torch.Tensor:
+        """``base(x) + lora_scale * (x.f32 @ A^T) @ B^T`` in one fused pass (``lora.py:47-48``)."""
+        if x.shape[-1] != self.in_features:
+            raise ValueError(f"x has {x.shape[-1]} features, layer expects {self.in_features}")
+        if x.dtype != torch.bfloat16:
+            raise NotImplementedError(f"ConvRotLinear runs bf16 activations (the DiT dtype); got {x.dtype}")
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, self.in_features)
+        if not x2.is_contiguous() or x2.data_ptr() % 16:
+            x2 = x2.contiguous()
+        if x2.shape[0] == 0:
+            return x.new_empty(*lead, self.out_features)
+        y = _ConvRotLinearFn.apply(x2, lora_A, lora_B, self.qweight, self.weight_scale, self._bias_f32(),
+                                   self.mode == "w4a8", float(lora_scale))
+        return y.reshape(*lead, self.out_features)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.forward_lora(x, None, None, 0.0)
+
+
+def quantize_dit_convrot(dit, mode: str = "w8a8") -> int:
+    """Replace the transformer blocks' ``nn.Linear`` with :class:`ConvRotLinear` in place.
+
+    Same walk as ``quantize_dit_fp8`` (``quantize.py:54-68``): collect every ``nn.Linear`` child of every
+    module in ``dit.blocks`` first, then ``setattr``; the stages outside the blocks stay bf16.  Returns the
+    number of layers quantized.  Call BEFORE ``inject_lora`` (the adapters then wrap the quantized bases).
+    """
+    targets = []
+    for block in dit.blocks:
+        for mod in block.modules():
+            for name, child in mod.named_children():
+                if isinstance(child, nn.Linear):
+                    targets.append((mod, name, child))
+    for mod, name, child in targets:
+        setattr(mod, name, ConvRotLinear(child, mode))
+    return len(targets)

@@ -1,0 +1,369 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle on the same seeded inputs.
+
+Bars: int8 activation codes, scales and int32 accumulators bit-exact; the
+rotated bf16 output within 2 bf16 ulp of the dense rotation (it is in fact bit-exact with the oracle);
+bf16 outputs (y, dX) within 1e-2 relative Frobenius error of the oracle's float64 result.
+At BASELINE.json's full sizes the oracle runs on sampled rows/columns (size-independent checks).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import convrot as orc
+
+pytestmark = pytest.mark.gpu
+
+REL_FROB_TOL = 1e-2
+
+
+def rel_frob(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def make_x(M, K, seed=0, outliers=True, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g)
+    if outliers:
+        idx = torch.randperm(K, generator=g)[: max(1, K // 100)]
+        x[:, idx] *= 20
+    return x.to(dtype)
+
+
+def make_w(N, K, seed=1):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+
+
+def bits16(t):
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+# ------------------------------------------------------------------------------------------- device
+def test_device_is_gfx950(k2, dev):
+    assert k2._lib.load().k2q_check_device() == 0
+    assert "gfx950" in torch.cuda.get_device_properties(dev).gcnArchName
+
+
+# ------------------------------------------------------------------------------------------- kernel (1)
+@pytest.mark.parametrize("M,K", [(1, 128), (5, 640), (512, 3072), (64, 6144), (33, 12288), (16, 16384)])
+def test_rotquant_bf16_bit_exact(k2, dev, M, K):
+    x = make_x(M, K, seed=K + M)
+    q, s, xr = k2._lib.rotquant(x.to(dev), want_xrot=True)
+    q0, s0, xr0 = orc.rotquant(x.float().numpy(), want_xrot=True)
+    assert np.array_equal(q.cpu().numpy(), q0)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s0.view(np.uint32))
+    assert np.array_equal(bits16(xr), xr0)
+
+
+@pytest.mark.parametrize("N,K", [(64, 256), (96, 3072), (8, 16384)])
+def test_rotquant_f32_weights_bit_exact(k2, dev, N, K):
+    w = torch.randn(N, K, generator=torch.Generator().manual_seed(N)) * 0.02
+    q, s = k2._lib.quant_weight_i8(w.to(dev))
+    q0, s0 = orc.quant_weight_i8(w.numpy())
+    assert np.array_equal(q.cpu().numpy(), q0)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s0.view(np.uint32))
+
+
+def test_rotquant_special_rows(k2, dev):
+    H = torch.from_numpy(np.kron(np.eye(2), __import__("scipy.linalg").linalg.hadamard(128)))
+    v = torch.zeros(4, 256, dtype=torch.float64)
+    v[0, :7] = torch.tensor([254, 1, 3, 5, -1, -3, 7], dtype=torch.float64)   # exact .5 ties
+    v[2, 200] = 1e30                                                          # one huge value
+    v[3] = torch.arange(256) - 127.5
+    x = (v @ H / 128).float()
+    x[1] = 0                                                                  # zero row -> floor
+    q, s, _ = k2._lib.rotquant(x.to(dev))
+    q0, s0, _ = orc.rotquant(x.numpy())
+    assert np.array_equal(q.cpu().numpy(), q0) and np.array_equal(s.cpu().numpy(), s0)
+    assert q[0, :7].tolist() == [127, 0, 2, 2, 0, -2, 4]
+    assert torch.all(q[1] == 0)
+
+
+def test_rotquant_xrot_within_two_ulp_of_dense(k2, dev):
+    x = make_x(128, 1024, seed=3)
+    _, _, xr = k2._lib.rotquant(x.to(dev), want_xrot=True)
+    H = np.kron(np.eye(8), __import__("scipy.linalg").linalg.hadamard(128))
+    dense = x.double().numpy() @ H / math.sqrt(128)
+    d = np.abs(bits16(xr).astype(np.int32) - orc.bf16_bits(dense.astype(np.float32)).astype(np.int32))
+    assert d.max() <= 2
+
+
+@pytest.mark.parametrize("N,K", [(64, 128), (256, 3072), (32, 12288)])
+def test_quant_weight_i4_bit_exact(k2, dev, N, K):
+    w = make_w(N, K, seed=N + K)
+    q4, s4 = k2._lib.quant_weight_i4(w.to(dev))
+    q0, sb0 = orc.quant_weight_i4(w.float().numpy())
+    assert np.array_equal(q4.cpu().numpy(), orc.pack_i4(q0))
+    assert np.array_equal(bits16(s4), np.ascontiguousarray(sb0.T))
+
+
+# ------------------------------------------------------------------------------------------- kernel (2)
+@pytest.mark.parametrize("M,N,K", [(256, 256, 128), (300, 260, 384), (1, 4, 128), (513, 1028, 1152)])
+def test_gemm_int32_acc_bit_exact(k2, dev, M, N, K):
+    rng = np.random.default_rng(M * N + K)
+    qx = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    qw = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    acc = k2._lib.gemm_w8a8_acc(torch.from_numpy(qx).to(dev), torch.from_numpy(qw).to(dev))
+    assert np.array_equal(acc.cpu().numpy(), orc.gemm_acc(qx, qw))
+
+
+def test_gemm_int32_acc_extreme_codes(k2, dev):
+    """All codes at +-127: the largest |acc| the path can produce at K=12288 (1.98e8) stays exact."""
+    K = 12288
+    qx = np.full((64, K), 127, np.int8)
+    qx[1::2] = -127
+    qw = np.full((64, K), -127, np.int8)
+    acc = k2._lib.gemm_w8a8_acc(torch.from_numpy(qx).to(dev), torch.from_numpy(qw).to(dev))
+    assert np.array_equal(acc.cpu().numpy(), orc.gemm_acc(qx, qw))
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 128, 128), (130, 132, 384)])
+def test_gemm_w4_group_partials_exact(k2, dev, M, N, K):
+    """With unit group scales the f32 sum of int32 group partials is an exact integer (< 2^24)."""
+    rng = np.random.default_rng(M + N + K)
+    qx = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    q4 = rng.integers(-7, 8, size=(N, K), dtype=np.int8)
+    ones = torch.ones(K // 64, N, dtype=torch.bfloat16)
+    out = k2._lib.gemm_w4a8_f32(torch.from_numpy(qx).to(dev), torch.from_numpy(orc.pack_i4(q4)).to(dev),
+                                ones.to(dev))
+    assert np.array_equal(out.cpu().numpy().astype(np.int64), orc.gemm_acc(qx, q4).astype(np.int64))
+    s = (torch.rand(K // 64, N, generator=torch.Generator().manual_seed(1)) + 0.5).to(torch.bfloat16)
+    out = k2._lib.gemm_w4a8_f32(torch.from_numpy(qx).to(dev), torch.from_numpy(orc.pack_i4(q4)).to(dev), s.to(dev))
+    ref = np.einsum("mng,gn->mn", orc.gemm_acc_groups(qx, q4).astype(np.float64), s.double().numpy())
+    assert rel_frob(out.cpu().numpy(), ref) < 1e-6
+
+
+# ------------------------------------------------------------------------------------------- kernel (3)
+def _forward_case(k2, dev, M, K, N, r, w4, bias, seed):
+    x = make_x(M, K, seed=seed)
+    w = make_w(N, K, seed=seed + 1)
+    g = torch.Generator().manual_seed(seed + 2)
+    b = torch.randn(N, generator=g) * 0.02 if bias else None
+    A = torch.randn(r, K, generator=g) * 0.01 if r else None
+    B = torch.randn(N, r, generator=g) * 0.01 if r else None
+    xd = x.to(dev)
+    qx, sx, _ = k2._lib.rotquant(xd)
+    if w4:
+        qw, sw = k2._lib.quant_weight_i4(w.to(dev))
+        q0, s0 = orc.quant_weight_i4(w.float().numpy())
+        qw_o, sw_o = q0, s0
+    else:
+        qw, sw = k2._lib.quant_weight_i8(w.to(dev))
+        qw_o, sw_o = orc.quant_weight_i8(w.float().numpy())
+    u = k2._lib.lora_down(xd, A.to(dev)) if r else None
+    gemm = k2._lib.gemm_w4a8 if w4 else k2._lib.gemm_w8a8
+    y = gemm(qx, sx, qw, sw, b.to(dev) if bias else None, u, B.to(dev) if r else None, 1.0)
+    ref = orc.forward(x.float().numpy(), qw_o, sw_o, w4=w4, bias=None if b is None else b.numpy(),
+                      lora_A=None if A is None else A.numpy(), lora_B=None if B is None else B.numpy(),
+                      lora_scale=1.0)
+    return y, u, ref
+
+
+@pytest.mark.parametrize("M,K,N,r,bias", [(256, 256, 256, 0, False), (300, 384, 260, 16, True),
+                                          (512, 3072, 1024, 32, True), (257, 1024, 512, 64, False),
+                                          (64, 512, 128, 128, True)])
+def test_forward_w8a8(k2, dev, M, K, N, r, bias):
+    y, u, ref = _forward_case(k2, dev, M, K, N, r, False, bias, seed=M + N)
+    assert rel_frob(y.float().cpu().numpy(), ref["y64"]) < REL_FROB_TOL
+    # the bf16 output is the once-rounded f32 epilogue: far inside the bar
+    assert rel_frob(y.float().cpu().numpy(), ref["y64"]) < 4e-3
+    if r:
+        assert rel_frob(u.cpu().numpy(), ref["u"]) < 1e-5
+
+
+@pytest.mark.parametrize("M,K,N,r,bias", [(256, 256, 128, 0, False), (300, 384, 260, 16, True),
+                                          (512, 3072, 1024, 32, False)])
+def test_forward_w4a8(k2, dev, M, K, N, r, bias):
+    y, _, ref = _forward_case(k2, dev, M, K, N, r, True, bias, seed=M + N + 7)
+    assert rel_frob(y.float().cpu().numpy(), ref["y64"]) < 4e-3
+
+
+# ------------------------------------------------------------------------------------------- kernel (4)
+@pytest.mark.parametrize("M,K,N,r,w4", [(256, 256, 256, 0, False), (200, 384, 320, 16, False),
+                                        (512, 1024, 512, 64, False), (256, 512, 256, 32, True)])
+def test_input_gradient(k2, dev, M, K, N, r, w4):
+    w = make_w(N, K, seed=M + K)
+    g = torch.Generator().manual_seed(5)
+    dy = (torch.randn(M, N, generator=g) * 1e-3).to(torch.bfloat16)
+    A = torch.randn(r, K, generator=g) * 0.01 if r else None
+    B = torch.randn(N, r, generator=g) * 0.01 if r else None
+    if w4:
+        qw, sw = k2._lib.quant_weight_i4(w.to(dev))
+        qo, so = orc.quant_weight_i4(w.float().numpy())
+    else:
+        qw, sw = k2._lib.quant_weight_i8(w.to(dev))
+        qo, so = orc.quant_weight_i8(w.float().numpy())
+    gd = (dy.float() @ B).contiguous() if r else None
+    dx = k2._lib.gemm_dx(dy.to(dev), qw, sw, w4=w4, g=gd.to(dev) if r else None, lora_a=A.to(dev) if r else None)
+    x_dummy = np.zeros((M, K))
+    ref = orc.backward(dy.float().numpy(), x_dummy, qo, so, w4=w4, lora_A=None if A is None else A.numpy(),
+                       lora_B=None if B is None else B.numpy(), lora_scale=1.0)
+    assert rel_frob(dx.float().cpu().numpy(), ref["dx64"]) < REL_FROB_TOL
+
+
+# ------------------------------------------------------------------------------------------- module
+def _layers(k2, dev, K=512, N=384, r=32, mode="w8a8", seed=0, bias=False):
+    lin = torch.nn.Linear(K, N, bias=bias, dtype=torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(make_w(N, K, seed=seed))
+        if bias:
+            lin.bias.copy_(torch.randn(N, generator=torch.Generator().manual_seed(seed)) * 0.02)
+    base = k2.ConvRotLinear(lin.to(dev), mode)
+    lora = k2.LoRALinear(base, r, float(r))
+    g = torch.Generator().manual_seed(seed + 9)
+    with torch.no_grad():
+        lora.lora_A.copy_(torch.randn(r, K, generator=g) * 0.01)
+        lora.lora_B.copy_(torch.randn(N, r, generator=g) * 0.01)
+    return lin, base, lora
+
+
+@pytest.mark.parametrize("mode", ["w8a8", "w4a8"])
+def test_module_fused_lora_matches_reference_formula(k2, dev, mode):
+    _, base, lora = _layers(k2, dev, mode=mode, bias=True)
+    x = make_x(3 * 100, 512, seed=11).reshape(3, 100, 512).to(dev)
+    with torch.no_grad():
+        y = lora(x)
+        out = base(x)
+        delta = (x.to(torch.float32) @ lora.lora_A.t()) @ lora.lora_B.t()       # lora.py:47-48
+        ref = out + (lora.scale * lora.scale_mul) * delta.to(out.dtype)
+        assert y.shape == (3, 100, 384) and y.dtype == torch.bfloat16
+        assert rel_frob(y.float().cpu(), ref.float().cpu()) < REL_FROB_TOL
+        with k2.lora_disabled(lora):
+            assert torch.equal(lora(x), out)                                     # scale_mul 0 == base
+        with k2.lora_scaled(lora, -2.0):
+            yneg = lora(x)
+        ref_neg = out + (-2.0 * lora.scale) * delta.to(out.dtype)
+        assert rel_frob(yneg.float().cpu(), ref_neg.float().cpu()) < REL_FROB_TOL
+
+
+def test_module_matches_oracle_and_unquantized_linear(k2, dev):
+    lin, base, _ = _layers(k2, dev, K=1024, N=512)
+    x = make_x(256, 1024, seed=12)
+    q0, s0 = orc.quant_weight_i8(lin.weight.float().cpu().numpy())
+    assert np.array_equal(base.qweight.cpu().numpy(), q0)
+    with torch.no_grad():
+        y = base(x.to(dev)).float().cpu().numpy()
+    ref = orc.forward(x.float().numpy(), q0, s0)
+    assert rel_frob(y, ref["y64"]) < 4e-3
+    dense = x.double().numpy() @ lin.weight.double().cpu().numpy().T
+    assert rel_frob(y, dense) < 0.03        # W8A8 quantization error on outlier-laden activations
+
+
+@pytest.mark.parametrize("mode", ["w8a8", "w4a8"])
+def test_module_backward_matches_oracle(k2, dev, mode):
+    lin, base, lora = _layers(k2, dev, K=512, N=256, r=16, mode=mode)
+    x = make_x(192, 512, seed=13)
+    dy = (torch.randn(192, 256, generator=torch.Generator().manual_seed(3)) * 1e-3).to(torch.bfloat16)
+    xd = x.to(dev).requires_grad_(True)
+    lora(xd).backward(dy.to(dev))
+    w = lin.weight.float().cpu().numpy()
+    qo, so = orc.quant_weight_i4(w) if mode == "w4a8" else orc.quant_weight_i8(w)
+    ref = orc.backward(dy.float().numpy(), x.float().numpy(), qo, so, w4=mode == "w4a8",
+                       lora_A=lora.lora_A.detach().cpu().numpy(), lora_B=lora.lora_B.detach().cpu().numpy(),
+                       lora_scale=1.0)
+    assert rel_frob(xd.grad.float().cpu().numpy(), ref["dx64"]) < REL_FROB_TOL
+    assert rel_frob(lora.lora_A.grad.cpu().numpy(), ref["dA"]) < 1e-3
+    assert rel_frob(lora.lora_B.grad.cpu().numpy(), ref["dB"]) < 1e-3
+    assert base.qweight.grad is None
+
+
+def test_deterministic_and_checkpoint_recompute(k2, dev):
+    _, _, lora = _layers(k2, dev)
+    x = make_x(512, 512, seed=14).to(dev)
+    with torch.no_grad():
+        a, b = lora(x), lora(x)
+    assert torch.equal(a, b)
+    xa = x.clone().requires_grad_(True)
+    xb = x.clone().requires_grad_(True)
+    dy = torch.randn(512, 384, device=dev).to(torch.bfloat16)
+    lora(xa).backward(dy)
+    ga = (xa.grad.clone(), lora.lora_A.grad.clone())
+    lora.lora_A.grad = None
+    lora.lora_B.grad = None
+    torch.utils.checkpoint.checkpoint(lora, xb, use_reentrant=False).backward(dy)
+    assert torch.equal(xb.grad, ga[0]) and torch.equal(lora.lora_A.grad, ga[1])
+
+
+def test_walker_and_block_swap_on_gpu(k2, dev):
+    import torch.nn as nn
+
+    class Blk(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.mlp = nn.Module()
+            self.mlp.up = nn.Linear(256, 512, bias=False, dtype=torch.bfloat16)
+            self.mlp.down = nn.Linear(512, 256, bias=False, dtype=torch.bfloat16)
+
+    class Dit(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.first = nn.Linear(8, 256, dtype=torch.bfloat16)
+            self.blocks = nn.ModuleList([Blk(), Blk()])
+
+    dit = Dit().to(dev)
+    assert k2.quantize_dit_convrot(dit, "w8a8") == 4
+    ad = k2.inject_lora(dit, 16, include_txtfusion=False, include_txtmlp=False)
+    assert len(ad) == 4
+    blk = dit.blocks[1]
+    x = make_x(64, 256, seed=15).to(dev)
+    with torch.no_grad():
+        ref = blk.mlp.down(blk.mlp.up(x))
+    for p in blk.parameters():          # page out and back in, as mmdit.py:409-418 does
+        if not p.requires_grad:
+            p.data = p.data.to("cpu")
+    for p in blk.parameters():
+        if not p.requires_grad:
+            p.data = p.data.to(dev, non_blocking=True)
+    with torch.no_grad():
+        assert torch.equal(blk.mlp.down(blk.mlp.up(x)), ref)
+
+
+# ------------------------------------------------------------------------------------------- full size
+def test_full_size_cfg2_sampled(k2, dev):
+    """BASELINE.json configs[2] shapes (M=16896, K=3072, N=12288, r=32): sampled rows of the codes, scales
+    and y against the oracle; sampled entries of the int32 accumulators exact."""
+    M, K, N, r = 16896, 3072, 12288, 32
+    x = make_x(M, K, seed=0)
+    w = make_w(N, K, seed=1)
+    g = torch.Generator().manual_seed(2)
+    A = torch.randn(r, K, generator=g) * 0.01
+    B = torch.randn(N, r, generator=g) * 0.01
+    xd = x.to(dev)
+    qx, sx, _ = k2._lib.rotquant(xd)
+    qw, sw = k2._lib.quant_weight_i8(w.to(dev))
+    u = k2._lib.lora_down(xd, A.to(dev))
+    y = k2._lib.gemm_w8a8(qx, sx, qw, sw, None, u, B.to(dev), 1.0)
+    acc = k2._lib.gemm_w8a8_acc(qx, qw)
+    rows = np.sort(np.random.default_rng(0).choice(M, 48, replace=False))
+    rows[-1] = M - 1
+    cols = np.sort(np.random.default_rng(1).choice(N, 64, replace=False))
+    xs = x[torch.from_numpy(rows)].float().numpy()
+    q0, s0, _ = orc.rotquant(xs)
+    assert np.array_equal(qx.cpu().numpy()[rows], q0) and np.array_equal(sx.cpu().numpy()[rows], s0)
+    qw0, sw0 = orc.quant_weight_i8(w[torch.from_numpy(cols)].float().numpy())
+    assert np.array_equal(qw.cpu().numpy()[cols], qw0)
+    assert np.array_equal(acc.cpu().numpy()[np.ix_(rows, cols)], orc.gemm_acc(q0, qw0))
+    qw_all, sw_all = qw.cpu().numpy(), sw.cpu().numpy()
+    ref = orc.forward(xs, qw_all, sw_all, lora_A=A.numpy(), lora_B=B.numpy(), lora_scale=1.0)
+    assert rel_frob(y.float().cpu().numpy()[rows], ref["y64"]) < 4e-3
+
+
+def test_full_size_cfg3_input_gradient_sampled(k2, dev):
+    """BASELINE.json configs[3] shapes (M=4608, K=12288, N=3072, r=64): dX on sampled rows."""
+    M, K, N, r = 4608, 12288, 3072, 64
+    w = make_w(N, K, seed=3)
+    g = torch.Generator().manual_seed(4)
+    dy = (torch.randn(M, N, generator=g) * 1e-3).to(torch.bfloat16)
+    A = torch.randn(r, K, generator=g) * 0.01
+    B = torch.randn(N, r, generator=g) * 0.01
+    qw, sw = k2._lib.quant_weight_i8(w.to(dev))
+    gd = (dy.float() @ B).contiguous()
+    dx = k2._lib.gemm_dx(dy.to(dev), qw, sw, g=gd.to(dev), lora_a=A.to(dev))
+    rows = np.sort(np.random.default_rng(2).choice(M, 16, replace=False))
+    ref = orc.backward(dy.float().numpy()[rows], np.zeros((16, K)), qw.cpu().numpy(), sw.cpu().numpy(),
+                       lora_A=A.numpy(), lora_B=B.numpy(), lora_scale=1.0)
+    assert rel_frob(dx.float().cpu().numpy()[rows], ref["dx64"]) < REL_FROB_TOL

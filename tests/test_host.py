@@ -1,0 +1,193 @@
+"""CPU tests of the boundary: the C-ABI library loads and exports every symbol ``include/k2q.h`` declares,
+host-side validation rejects bad arguments before any launch, and the module satisfies the reference's
+duck-typed contract (``quantize.py:31-46``, ``lora.py:27-116``, ``mmdit.py:409-414``).  No GPU needed."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+from oracle import convrot as orc
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def header_symbols():
+    text = (ROOT / "include" / "k2q.h").read_text()
+    return sorted(set(re.findall(r"^(?:const char\*|int)\s+(k2q_\w+)\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol(k2):
+    lib = k2._lib.load()
+    syms = header_symbols()
+    assert len(syms) >= 11
+    for name in syms:
+        assert hasattr(lib, name), name
+    assert sorted(k2._lib.EXPORTS) == syms
+    assert k2._lib.version().startswith("k2q")
+
+
+def test_library_is_gfx950_only():
+    out = (ROOT / "krea-2_amd" / "libk2q.so").read_bytes()
+    assert b"gfx950" in out
+    for other in (b"gfx942", b"gfx90a", b"sm_"):
+        assert other + b"\x00" not in out or other == b"sm_"
+
+
+def test_status_codes_for_bad_arguments_without_gpu(k2):
+    """Entry points reject invalid shapes/pointers with K2Q_EINVAL before touching the device."""
+    lib = k2._lib.load()
+    buf = ctypes.create_string_buffer(4096 + 16)
+    p = (ctypes.addressof(buf) + 15) // 16 * 16
+    assert lib.k2q_rotquant(p, 0, 4, 100, 100, p, p, None, None) == -1        # K % 128
+    assert lib.k2q_rotquant(p, 7, 4, 128, 128, p, p, None, None) == -1        # dtype
+    assert lib.k2q_rotquant(None, 0, 4, 128, 128, p, p, None, None) == -1     # null
+    assert lib.k2q_rotquant(p + 2, 0, 4, 128, 128, p, p, None, None) == -1    # misaligned
+    assert lib.k2q_rotquant(p, 0, 4, 32768, 32768, p, p, None, None) == -4    # K too large
+    assert lib.k2q_gemm_w8a8(p, p, p, p, None, p, p, 8, 1.0, 4, 4, 128, p, None) == -1   # rank 8
+    assert lib.k2q_gemm_w8a8(p, p, p, p, None, None, None, 0, 0.0, 4, 6, 128, p, None) == -1  # N % 4
+    assert lib.k2q_gemm_dx(p, p, 4, 96, 128, None, None, 0, p, None) == -1    # N % 64
+    assert lib.k2q_lora_down(p, 4, 128, 128, p, 200, p, p, None) == -1       # rank > 128
+
+
+def test_wrappers_validate_before_launch(k2):
+    L = k2._lib
+    with pytest.raises(ValueError):
+        L.rotquant(torch.zeros(4, 100, dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        L.rotquant(torch.zeros(4, 256, dtype=torch.float16))
+    with pytest.raises(ValueError):
+        L.rotquant(torch.zeros(256, 4, dtype=torch.bfloat16).t())
+    with pytest.raises(ValueError):
+        L.gemm_w8a8(torch.zeros(4, 128, dtype=torch.int8), torch.zeros(4), torch.zeros(8, 256, dtype=torch.int8),
+                    torch.zeros(8))
+    with pytest.raises(ValueError):
+        L.lora_down(torch.zeros(4, 128, dtype=torch.bfloat16), torch.zeros(12, 128))
+    with pytest.raises(RuntimeError):          # valid shapes, CPU tensors: refuses, never computes on CPU
+        L.rotquant(torch.zeros(4, 128, dtype=torch.bfloat16))
+
+
+def _cpu_quantized(N=64, K=256, mode="w8a8", bias=True, seed=0):
+    """A ConvRotLinear assembled from oracle-quantized tensors (CPU; no kernel runs)."""
+    import __graft_entry__ as ge
+    k2 = ge.load_package()
+    rng = np.random.default_rng(seed)
+    W = orc.bf16_round((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    b = torch.randn(N, dtype=torch.bfloat16) if bias else None
+    if mode == "w8a8":
+        q, s = orc.quant_weight_i8(W)
+        return k2.ConvRotLinear.from_quantized(torch.from_numpy(q), torch.from_numpy(s).view(torch.int32), b, mode)
+    q, s_bits = orc.quant_weight_i4(W)
+    return k2.ConvRotLinear.from_quantized(torch.from_numpy(orc.pack_i4(q)),
+                                           torch.from_numpy(np.ascontiguousarray(s_bits.T)).view(torch.int16), b,
+                                           mode)
+
+
+@pytest.mark.parametrize("mode", ["w8a8", "w4a8"])
+def test_module_contract(k2, mode):
+    m = _cpu_quantized(mode=mode)
+    assert m.is_quant_linear is True and type(m).is_quant_linear is True
+    assert (m.in_features, m.out_features) == (256, 64)
+    assert m.weight is m.qweight and m.weight.device.type == "cpu"
+    assert isinstance(m.bias, nn.Parameter)
+    params = dict(m.named_parameters())
+    assert set(params) == {"qweight", "wscale", "bias"}
+    assert all(not p.requires_grad for p in params.values())
+    # Module.to(dtype) casts floating parameters only: codes and scale bits stay exact
+    before = {k: v.clone() for k, v in params.items()}
+    m.to(torch.float16)
+    assert m.qweight.dtype == before["qweight"].dtype and torch.equal(m.qweight, before["qweight"])
+    assert torch.equal(m.wscale, before["wscale"])
+    assert m.bias.dtype == torch.float16
+    if mode == "w8a8":
+        assert m.weight_scale.dtype == torch.float32 and m.weight_scale.shape == (64,)
+    else:
+        assert m.weight_scale.dtype == torch.bfloat16 and m.weight_scale.shape == (4, 64)
+
+
+def test_block_swap_repoints_parameters(k2):
+    """mmdit.py:409-414 pages with ``p.data = p.data.to(device)``; the module reads pointers per call."""
+    m = _cpu_quantized()
+    ptr = m.qweight.data_ptr()
+    for p in m.parameters():
+        p.data = p.data.clone()
+    assert m.qweight.data_ptr() != ptr and m.weight is m.qweight
+
+
+class _Block(nn.Module):
+    """Block-shaped module with the reference's Linear names (mmdit.py:170-175, 188-194)."""
+
+    def __init__(self, d=256, h=512):
+        super().__init__()
+        self.attn = nn.Module()
+        for n, o in (("wq", d), ("wk", d // 4), ("wv", d // 4), ("gate", d), ("wo", d)):
+            setattr(self.attn, n, nn.Linear(d, o, bias=False))
+        self.mlp = nn.Module()
+        self.mlp.gate = nn.Linear(d, h, bias=False)
+        self.mlp.up = nn.Linear(d, h, bias=False)
+        self.mlp.down = nn.Linear(h, d, bias=False)
+
+
+class _Dit(nn.Module):
+    def __init__(self, n=2):
+        super().__init__()
+        self.first = nn.Linear(64, 256)
+        self.blocks = nn.ModuleList(_Block() for _ in range(n))
+
+
+def test_inject_lora_accepts_quantized_bases_by_duck_typing(k2):
+    dit = _Dit()
+    for blk in dit.blocks:   # swap in pre-quantized bases the way the walker would
+        for mod in list(blk.modules()):
+            for name, child in list(mod.named_children()):
+                if isinstance(child, nn.Linear):
+                    setattr(mod, name, _cpu_quantized(child.out_features, child.in_features, bias=False))
+    adapters = k2.inject_lora(dit, 16, include_txtfusion=False, include_txtmlp=False)
+    assert len(adapters) == 16
+    assert set(adapters) == {f"blocks.{i}.{t}" for i in range(2) for t in k2.DEFAULT_TARGETS}
+    a = adapters["blocks.0.mlp.down"]
+    assert isinstance(a.base, k2.ConvRotLinear) and a.lora_A.shape == (16, 512) and a.lora_B.shape == (256, 16)
+    assert a.scale == 1.0 and a.scale_mul == 1.0 and torch.all(a.lora_B == 0)
+    assert all(not p.requires_grad for p in a.base.parameters())
+    assert next(dit.parameters()).dtype == torch.float32     # dtype probe stays the first Linear's
+    with k2.lora_scaled(dit, -2.0):
+        assert all(m.scale_mul == -2.0 for m in adapters.values())
+    with k2.lora_disabled(dit):
+        assert all(m.scale_mul == 0.0 for m in adapters.values())
+    assert all(m.scale_mul == 1.0 for m in adapters.values())
+
+
+def test_inject_lora_raises_without_targets(k2):
+    dit = _Dit()
+    for blk in dit.blocks:
+        blk.attn = nn.Module()
+        blk.mlp = nn.Module()
+    with pytest.raises(RuntimeError):
+        k2.inject_lora(dit, 16, include_txtfusion=False, include_txtmlp=False)
+
+
+def test_save_load_lora_roundtrip(k2, tmp_path):
+    dit = _Dit()
+    adapters = k2.inject_lora(dit, 16, include_txtfusion=False, include_txtmlp=False)
+    for m in adapters.values():
+        nn.init.normal_(m.lora_B)
+    path = str(tmp_path / "a.safetensors")
+    k2.save_lora(adapters, path, rank=16, alpha=16.0)
+    from safetensors import safe_open
+    with safe_open(path, "pt") as f:
+        assert f.metadata()["format"] == "krea2-lora"
+        assert "diffusion_model.blocks.1.mlp.up.lora_A.weight" in f.keys()
+    dit2 = _Dit()
+    ad2 = k2.load_lora(dit2, path)
+    for n, m in adapters.items():
+        assert torch.equal(ad2[n].lora_B, m.lora_B.detach().to(torch.bfloat16).float())
+
+
+def test_walker_requires_gpu_and_says_so(k2):
+    if torch.cuda.is_available():
+        pytest.skip("GPU present")
+    with pytest.raises(RuntimeError, match="GPU"):
+        k2.quantize_dit_convrot(_Dit(), "w8a8")
