@@ -198,12 +198,120 @@ __device__ __forceinline__ void fwht128_rows(v16f (&f)[4], int h) {
     }
 }
 
+// ---------------------------------------------------------------------------------------------------------
+// Main-loop data movement: global -> LDS by the gfx950 LDS-DMA path (global_load_lds_dwordx4), no VGPR
+// staging.  The reduction axis is cut in 64-byte stages; NSTAGE stages rotate through LDS and loads run
+// NSTAGE-1 stages ahead of the MFMAs.  A stage holds 256 A-rows and 256 B-rows of 64 B (16 KB each); the
+// 16-byte chunk c of LDS row r sits at c ^ swz64(r), conflict-free for the fragment reads.  One DMA wave
+// instruction fills 16 consecutive LDS rows (1 KB: lane l -> row l/4, physical chunk l%4), so each lane
+// fetches the logical chunk (l%4) ^ swz64(row) of its row.  A stage is consumed after every wave's
+// `s_waitcnt vmcnt` for it plus one s_barrier (raw, without __syncthreads' full memory fence, which would
+// drain the prefetches).
+constexpr int SBK = 64;                   // reduction bytes per stage
+constexpr int NSTAGE = 4;
+constexpr int STAGE_TILE = BT * SBK;      // 16 KB per operand per stage
+constexpr int STAGE_BYTES = 2 * STAGE_TILE;
+
+__device__ __forceinline__ int swz64(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
+
+struct DmaOffsets {
+  uint32_t o[4];
+};
+
+// Per-lane source offsets (bytes from the tile's first row) of the 4 DMA instructions a wave issues per
+// operand and stage: LDS rows 64*wave + 16*i + lane/4; rows past the matrix end are clamped (never stored).
+__device__ __forceinline__ DmaOffsets dma_offsets(int64_t row0, int64_t nrows, int64_t ld) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  DmaOffsets d;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int lrow = 64 * wave + 16 * i + (lane >> 2);
+    int64_t rr = lrow;
+    rr = row0 + rr < nrows ? rr : nrows - 1 - row0;
+    d.o[i] = (uint32_t)(rr * ld) + 16u * (uint32_t)((lane & 3) ^ swz64(lrow));
+  }
+  return d;
+}
+
+#define K2Q_GPTR(p) ((__attribute__((address_space(1))) void*)(p))
+#define K2Q_LPTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+__device__ __forceinline__ void dma_tile(const uint8_t* src, const DmaOffsets& d, uint8_t* lds_wave) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    __builtin_amdgcn_global_load_lds(K2Q_GPTR(src + d.o[i]), K2Q_LPTR(lds_wave + 1024 * i), 16, 0, 0);
+}
+
+__device__ __forceinline__ v4i frag64(const uint8_t* s, int row, int chunk) {
+  return *reinterpret_cast<const v4i*>(s + row * SBK + 16 * (chunk ^ swz64(row)));
+}
+
+// Epilogue LDS use (after the main loop has drained the ring): LoRA factor rows at offset 0 (at most
+// 2 x 256 x (2*128+16) B), then 3 x 256 floats of scales at SCALE_OFF.
+constexpr int LORA_LDS_MAX = 2 * BT * (2 * 128 + 16);
+constexpr int SCALE_OFF = (NSTAGE * STAGE_BYTES > LORA_LDS_MAX ? NSTAGE * STAGE_BYTES : LORA_LDS_MAX);
+constexpr int GEMM_LDS_BYTES = SCALE_OFF + 3 * BT * 4;
+
+// Thread t copies row A0+t of lora_ra and row B0+t of (lora_scale * lora_rb) into LDS as bf16, 32 ranks
+// per pass (16 float4 loads in flight per thread).
+template <typename Args>
+__device__ __forceinline__ void stage_lora_rows(const Args& p, int64_t A0, int64_t B0, int lstride, uint8_t* l_a,
+                                                uint8_t* l_b) {
+  const int t = threadIdx.x;
+  const int64_t ra = A0 + t < p.rows_a ? A0 + t : p.rows_a - 1;
+  const int64_t rb = B0 + t < p.rows_b ? B0 + t : p.rows_b - 1;
+  const float* srca = p.lora_ra + ra * p.r;
+  const float* srcb = p.lora_rb + rb * p.r;
+  for (int c0 = 0; c0 < p.r; c0 += 32) {
+    v4f va[8], vb[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      if (c0 + 4 * q < p.r) {
+        va[q] = *reinterpret_cast<const v4f*>(srca + c0 + 4 * q);
+        vb[q] = *reinterpret_cast<const v4f*>(srcb + c0 + 4 * q);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 8; q += 2) {
+      if (c0 + 4 * q < p.r) {
+        const v4u wa4 = v4u{pack_bf16x2(va[q][0], va[q][1]), pack_bf16x2(va[q][2], va[q][3]),
+                            pack_bf16x2(va[q + 1][0], va[q + 1][1]), pack_bf16x2(va[q + 1][2], va[q + 1][3])};
+        const float s = p.lora_scale;
+        const v4u wb4 = v4u{pack_bf16x2(vb[q][0] * s, vb[q][1] * s), pack_bf16x2(vb[q][2] * s, vb[q][3] * s),
+                            pack_bf16x2(vb[q + 1][0] * s, vb[q + 1][1] * s),
+                            pack_bf16x2(vb[q + 1][2] * s, vb[q + 1][3] * s)};
+        *reinterpret_cast<v4u*>(l_a + t * lstride + 2 * (c0 + 4 * q)) = wa4;
+        *reinterpret_cast<v4u*>(l_b + t * lstride + 2 * (c0 + 4 * q)) = wb4;
+      }
+    }
+  }
+}
+
+// LoRA term of one 32 x 32 block from the staged bf16 rows: f += lora_ra[arow,:] . lora_rb'[bcol,:].
+__device__ __forceinline__ v16f lora_block_lds(const uint8_t* l_a, const uint8_t* l_b, int lstride, int r,
+                                               int arow0, int bcol0, int lane, v16f f) {
+  const int h = lane >> 5, c = lane & 31;
+  const uint8_t* pa = l_a + (arow0 + c) * lstride + 16 * h;
+  const uint8_t* pb = l_b + (bcol0 + c) * lstride + 16 * h;
+  for (int ks = 0; ks < r; ks += 16) {
+    const v8bf fa = __builtin_bit_cast(v8bf, *reinterpret_cast<const v4i*>(pa + 2 * ks));
+    const v8bf fb = __builtin_bit_cast(v8bf, *reinterpret_cast<const v4i*>(pb + 2 * ks));
+    f = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, fb, f, 0, 0, 0);
+  }
+  return f;
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
 template <int EPI>
-__global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs p) {
+__global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_nt_kernel(GemmArgs p) {
   constexpr bool BF16 = (EPI == EPI_DX);
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  uint8_t* sA = smem;                    // [2][TILE_BYTES]
-  uint8_t* sB = smem + 2 * TILE_BYTES;   // [2][TILE_BYTES]
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // [NSTAGE][A tile | B tile]
 
   const int64_t tiles_a = (p.rows_a + BT - 1) / BT;
   const int64_t tiles_b = (p.rows_b + BT - 1) / BT;
@@ -222,47 +330,84 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v16i{0};
 
-  const int nk = (int)(p.kbytes / BKB);
-  const TileOffsets<8> offa = tile_offsets<8>(A0, p.rows_a, p.lda_b);
-  const TileOffsets<8> offb = tile_offsets<8>(B0, p.rows_b, p.ldb_b);
+  // Epilogue operands of this tile, fetched now so their latency hides under the main loop:
+  // thread t holds s_x of B-row B0+t (times 2^-7), s_w and bias of A-row A0+t.
+  float pre_sx = 0.f, pre_sw = 0.f, pre_bi = 0.f;
+  if constexpr (EPI == EPI_W8) {
+    const int t = threadIdx.x;
+    const int64_t rb = B0 + t < p.rows_b ? B0 + t : p.rows_b - 1;
+    const int64_t ra = A0 + t < p.rows_a ? A0 + t : p.rows_a - 1;
+    pre_sx = p.sx[rb] * 0.0078125f;  // 2^-7: the two unnormalised rotations
+    pre_sw = p.sw[ra];
+    pre_bi = p.bias ? p.bias[ra] : 0.f;
+  }
+
+  const int nk = (int)(p.kbytes / SBK);
+  const DmaOffsets offa = dma_offsets(A0, p.rows_a, p.lda_b);
+  const DmaOffsets offb = dma_offsets(B0, p.rows_b, p.ldb_b);
   const uint8_t* gA = p.a + A0 * p.lda_b;
   const uint8_t* gB = p.b + B0 * p.ldb_b;
-  v4i ra[8], rb[8];
-  g2r(gA, offa, ra);
-  g2r(gB, offb, rb);
-  r2s(sA, ra);
-  r2s(sB, rb);
-  __syncthreads();
+  uint8_t* ldsw = smem + 4096 * wave;   // this wave's DMA region inside a tile
 
-  auto compute = [&](int buf) {
-    const uint8_t* tA = sA + buf * TILE_BYTES;
-    const uint8_t* tB = sB + buf * TILE_BYTES;
+  auto issue = [&](int st) {
+    uint8_t* buf = ldsw + (st % NSTAGE) * STAGE_BYTES;
+    dma_tile(gA + (int64_t)st * SBK, offa, buf);
+    dma_tile(gB + (int64_t)st * SBK, offb, buf + STAGE_TILE);
+  };
+  auto read_frags = [&](int st, int kk, v4i (&fa)[4], v4i (&fb)[4]) {
+    const uint8_t* tA = smem + (st % NSTAGE) * STAGE_BYTES;
+    const uint8_t* tB = tA + STAGE_TILE;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      v4i fa[4], fb[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        fa[i] = frag(tA, 128 * wa + 32 * i + c32, 2 * kk + h);
-        fb[i] = frag(tB, 128 * wb + 32 * i + c32, 2 * kk + h);
-      }
-#pragma unroll
-      for (int ia = 0; ia < 4; ++ia)
-#pragma unroll
-        for (int ib = 0; ib < 4; ++ib) mma<BF16>(fa[ia], fb[ib], acc[ia][ib]);
+    for (int i = 0; i < 4; ++i) {
+      fa[i] = frag64(tA, 128 * wa + 32 * i + c32, 2 * kk + h);
+      fb[i] = frag64(tB, 128 * wb + 32 * i + c32, 2 * kk + h);
     }
   };
-  // Steady state: prefetch stage kt+1 into registers, run stage kt from LDS, publish kt+1 to the other
-  // buffer, one barrier.  The last stage has nothing to prefetch.
-  for (int kt = 0; kt < nk - 1; ++kt) {
-    const int buf = kt & 1;
-    g2r(gA + (kt + 1) * BKB, offa, ra);
-    g2r(gB + (kt + 1) * BKB, offb, rb);
-    compute(buf);
-    r2s(sA + (buf ^ 1) * TILE_BYTES, ra);
-    r2s(sB + (buf ^ 1) * TILE_BYTES, rb);
-    __syncthreads();
+  auto mfmas = [&](const v4i (&fa)[4], const v4i (&fb)[4]) {
+#pragma unroll
+    for (int ia = 0; ia < 4; ++ia)
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib) mma<BF16>(fa[ia], fb[ib], acc[ia][ib]);
+  };
+
+  // Software pipeline (one wave per SIMD, so the wave itself must keep the matrix pipe fed):
+  //   iteration kt, first half : read stage kt substep-1 fragments | 16 MFMAs on substep 0
+  //   mid-stage                : wait for stage kt+1's DMA, s_barrier (stage kt-1's buffer now free)
+  //   second half              : DMA stage kt+3 into that buffer, read stage kt+1 substep-0 fragments |
+  //                              16 MFMAs on substep 1
+  // so fragments are always in registers before their MFMAs.  The body has no branches: past the last
+  // stage the DMA re-loads stage nk-1 into the free buffer (never one still in use) and the extra
+  // fragment reads are discarded, which keeps exactly one DMA group (8 per wave) outstanding at the wait.
+  v4i f0a[4], f0b[4], f1a[4], f1b[4];
+  issue(0);
+  issue(nk > 1 ? 1 : nk - 1);
+  issue(nk > 2 ? 2 : nk - 1);
+  wait_vmcnt<16>();
+  lds_barrier();
+  read_frags(0, 0, f0a, f0b);
+  for (int kt = 0; kt < nk; ++kt) {
+    read_frags(kt, 1, f1a, f1b);
+    mfmas(f0a, f0b);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    wait_vmcnt<8>();
+    lds_barrier();
+    issue(kt + 3 < nk ? kt + 3 : nk - 1);
+    read_frags(kt + 1, 0, f0a, f0b);
+    mfmas(f1a, f1b);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM (LDS-DMA)
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
   }
-  compute((nk - 1) & 1);
+  wait_vmcnt<0>();   // no LDS-DMA may still be in flight when the workgroup's LDS is released
 
   const int64_t a0 = A0 + 128 * wa;   // first A-row of this wave
   const int64_t b0 = B0 + 128 * wb;   // first B-row of this wave
@@ -285,58 +430,62 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_kernel(GemmArgs p) {
         }
       }
     return;
-  } else if constexpr (EPI == EPI_W8) {
-    // One 32-row slice (ia) at a time: its 4 scale/bias vectors, its LoRA A-fragments, then the four
-    // 32 x 32 blocks one by one, so at most one block's 16 f32 values are live beyond the accumulators.
-    float sxm[4];
-#pragma unroll
-    for (int ib = 0; ib < 4; ++ib) {
-      int64_t m = b0 + 32 * ib + c32;
-      m = m < p.rows_b ? m : p.rows_b - 1;
-      sxm[ib] = p.sx[m] * 0.0078125f;  // 2^-7: the two unnormalised rotations
+  } else {
+    // The LDS ring is free now.  Publish the prefetched scales, and stage the LoRA factor rows of this
+    // tile as bf16 (A side: lora_ra rows A0.., B side: lora_scale * lora_rb rows B0..), rows padded to
+    // 2r+16 bytes so the epilogue's 16-byte fragment reads are conflict-free.
+    lds_barrier();
+    float* s_sx = reinterpret_cast<float*>(smem + SCALE_OFF);
+    float* s_sw = s_sx + BT;
+    float* s_bi = s_sw + BT;
+    if constexpr (EPI == EPI_W8) {
+      s_sx[threadIdx.x] = pre_sx;
+      s_sw[threadIdx.x] = pre_sw;
+      s_bi[threadIdx.x] = pre_bi;
     }
+    const bool lora = p.lora_rb != nullptr && p.r > 0;
+    const int lstride = 2 * p.r + 16;
+    uint8_t* l_a = smem;
+    uint8_t* l_b = smem + BT * lstride;
+    if (lora) stage_lora_rows(p, A0, B0, lstride, l_a, l_b);
+    lds_barrier();
     uint16_t* out = static_cast<uint16_t*>(p.out);
-#pragma unroll
-    for (int ia = 0; ia < 4; ++ia) {
-      float4 sw[4], bi[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        int64_t n = a0 + 32 * ia + 8 * j + 4 * h;
-        n = n < p.rows_a ? n : p.rows_a - 4;
-        sw[j] = *reinterpret_cast<const float4*>(p.sw + n);
-        bi[j] = p.bias ? *reinterpret_cast<const float4*>(p.bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-#pragma unroll
-      for (int ib = 0; ib < 4; ++ib) {
-        v16f f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          f[4 * j + 0] = (float)acc[ia][ib][4 * j + 0] * (sxm[ib] * sw[j].x) + bi[j].x;
-          f[4 * j + 1] = (float)acc[ia][ib][4 * j + 1] * (sxm[ib] * sw[j].y) + bi[j].y;
-          f[4 * j + 2] = (float)acc[ia][ib][4 * j + 2] * (sxm[ib] * sw[j].z) + bi[j].z;
-          f[4 * j + 3] = (float)acc[ia][ib][4 * j + 3] * (sxm[ib] * sw[j].w) + bi[j].w;
-        }
-        if (p.lora_rb && p.r > 0)
-          f = lora_block(p.lora_ra, p.lora_rb, p.r, p.lora_scale, p.rows_a, p.rows_b, a0 + 32 * ia,
-                         b0 + 32 * ib, lane, f);
-        store_block(out, p.ldo, p.rows_a, p.rows_b, a0 + 32 * ia, b0 + 32 * ib, lane, f);
-      }
-      __builtin_amdgcn_sched_barrier(0);  // keep the next slice's scale/bias loads out of this one
-    }
-  } else {  // EPI_DX: one 32-column slice (ib) at a time; the FWHT needs all 4 row slices of it.
-    uint16_t* out = static_cast<uint16_t*>(p.out);
-#pragma unroll
-    for (int ib = 0; ib < 4; ++ib) {
-      v16f f[4];
-#pragma unroll
-      for (int ia = 0; ia < 4; ++ia) f[ia] = __builtin_bit_cast(v16f, acc[ia][ib]);
-      fwht128_rows(f, h);
+    if constexpr (EPI == EPI_W8) {
 #pragma unroll
       for (int ia = 0; ia < 4; ++ia) {
-        if (p.lora_rb && p.r > 0)
-          f[ia] = lora_block(p.lora_ra, p.lora_rb, p.r, p.lora_scale, p.rows_a, p.rows_b, a0 + 32 * ia,
-                             b0 + 32 * ib, lane, f[ia]);
-        store_block(out, p.ldo, p.rows_a, p.rows_b, a0 + 32 * ia, b0 + 32 * ib, lane, f[ia]);
+        v4f sw[4], bi[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int nl = 128 * wa + 32 * ia + 8 * j + 4 * h;
+          sw[j] = *reinterpret_cast<const v4f*>(s_sw + nl);
+          bi[j] = *reinterpret_cast<const v4f*>(s_bi + nl);
+        }
+#pragma unroll
+        for (int ib = 0; ib < 4; ++ib) {
+          const float sxm = s_sx[128 * wb + 32 * ib + c32];
+          v16f f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              f[4 * j + i] = (float)acc[ia][ib][4 * j + i] * (sxm * sw[j][i]) + bi[j][i];
+          if (lora) f = lora_block_lds(l_a, l_b, lstride, p.r, 128 * wa + 32 * ia, 128 * wb + 32 * ib, lane, f);
+          store_block(out, p.ldo, p.rows_a, p.rows_b, a0 + 32 * ia, b0 + 32 * ib, lane, f);
+        }
+      }
+    } else {  // EPI_DX: one 32-column slice (ib) at a time; the FWHT needs all 4 row slices of it.
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib) {
+        v16f f[4];
+#pragma unroll
+        for (int ia = 0; ia < 4; ++ia) f[ia] = __builtin_bit_cast(v16f, acc[ia][ib]);
+        fwht128_rows(f, h);
+#pragma unroll
+        for (int ia = 0; ia < 4; ++ia) {
+          if (lora)
+            f[ia] = lora_block_lds(l_a, l_b, lstride, p.r, 128 * wa + 32 * ia, 128 * wb + 32 * ib, lane, f[ia]);
+          store_block(out, p.ldo, p.rows_a, p.rows_b, a0 + 32 * ia, b0 + 32 * ib, lane, f[ia]);
+        }
       }
     }
   }
@@ -557,7 +706,7 @@ int launch_w4(const W4Args& p, hipStream_t st) {
 
 template <int EPI>
 int launch_gemm(const GemmArgs& p, hipStream_t st) {
-  constexpr int lds = 4 * TILE_BYTES;
+  constexpr int lds = GEMM_LDS_BYTES;
   if (hipFuncSetAttribute((const void*)gemm_nt_kernel<EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
                           lds) != hipSuccess)
     return K2Q_ELAUNCH;
