@@ -468,7 +468,7 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
           for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-              f[4 * j + i] = (float)acc[ia][ib][4 * j + i] * (sxm * sw[j][i]) + bi[j][i];
+              f[4 * j + i] = __builtin_fmaf((float)acc[ia][ib][4 * j + i], sxm * sw[j][i], bi[j][i]);
           if (lora) f = lora_block_lds(l_a, l_b, lstride, p.r, 128 * wa + 32 * ia, 128 * wb + 32 * ib, lane, f);
           store_block(out, p.ldo, p.rows_a, p.rows_b, a0 + 32 * ia, b0 + 32 * ib, lane, f);
         }

@@ -17,16 +17,16 @@ typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 #define K2Q_HADAMARD 128
 
-// float -> bf16 bits, round to nearest even (NaN kept quiet); the rounding of torch's .to(bfloat16).
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-}
+// float -> bf16, round to nearest even (NaN stays NaN): the rounding of torch's .to(bfloat16).  gfx950
+// converts two floats per v_cvt_pk_bf16_f32.
+typedef float k2q_v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 k2q_v2bf __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(k2q_v2f{lo, hi}, k2q_v2bf));
 }
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) { return pack_bf16x2(f, 0.f) & 0xffffu; }
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 

@@ -3,8 +3,7 @@
 //
 // u: A (r x K, f32) is split once per call into bf16 hi + lo parts (A = hi + lo to ~2^-16 relative), and
 // u = x hi^T + x lo^T runs on v_mfma_f32_16x16x32_bf16 with f32 accumulation; x is bf16 already, so the
-// only rounding is the f32 accumulation.  Each wave owns 16 rows of x and all r columns of u; x fragments
-// are read straight from HBM in MFMA layout (lane l: row l%16, 8 contiguous k at 8*(l/16)).
+// only roundings are A's split residue and the f32 accumulation.  HBM-bound on reading x once.
 #include "k2q_common.h"
 
 namespace {
@@ -23,57 +22,81 @@ __global__ __launch_bounds__(256) void split_bf16_kernel(const float* __restrict
   lo[i] = (uint16_t)f32_to_bf16_bits(v - bf16_bits_to_f32(h));
 }
 
-constexpr int LD_UNROLL = 4;
-
-template <int RT>  // RT = r / 16 column tiles of u
+// u = x A^T for 32 rows per workgroup: the 4 waves split K in quarters, each runs 2 row tiles x RT rank
+// tiles of v_mfma_f32_16x16x32_bf16 (x hi and x lo), and the partial sums meet in LDS where wave 0..3
+// are added in that fixed order (deterministic).  Fragments come straight from global memory in MFMA
+// layout: lane l holds row l%16 (of x, or of A) and 8 contiguous k at 8*(l/16) of each 32-wide step.
+template <int RT>
 __global__ __launch_bounds__(256) void lora_down_kernel(const uint16_t* __restrict__ x, int64_t M, int K,
                                                         int64_t ldx, const uint16_t* __restrict__ hi,
                                                         const uint16_t* __restrict__ lo,
                                                         float* __restrict__ u) {
+  constexpr int UNR = RT <= 2 ? 4 : (RT <= 4 ? 2 : 1);   // 32-wide k steps whose loads fly together
+  __shared__ float part[4][2][RT][4][64];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int64_t m0 = (int64_t)blockIdx.x * 64 + 16 * wave;
-  const int r = RT * 16;
-  int64_t mr = m0 + (lane & 15);
-  mr = mr < M ? mr : M - 1;
-  const uint16_t* xp = x + mr * ldx + 8 * (lane >> 4);
+  const int64_t m0 = (int64_t)blockIdx.x * 32;
+  const int kq = K / 4;                 // this wave's quarter of K (a multiple of 32)
+  const int kbeg = wave * kq;
   const int kofs = 8 * (lane >> 4);
+  const uint16_t* xp[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    int64_t mr = m0 + 16 * t + (lane & 15);
+    mr = mr < M ? mr : M - 1;
+    xp[t] = x + mr * ldx + kofs;
+  }
+  const int64_t arow = (int64_t)(lane & 15) * K + kofs;
 
-  v4f_t acc[RT];
+  v4f acc[2][RT];
 #pragma unroll
-  for (int j = 0; j < RT; ++j) acc[j] = v4f_t{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int j = 0; j < RT; ++j) acc[t][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  for (int k0 = 0; k0 < K; k0 += 32 * LD_UNROLL) {
-    v8bf_t fx[LD_UNROLL];
+  for (int k0 = kbeg; k0 < kbeg + kq; k0 += 32 * UNR) {
+    v4i fx[UNR][2], fh[UNR][RT], fl[UNR][RT];
 #pragma unroll
-    for (int q = 0; q < LD_UNROLL; ++q) {
+    for (int q = 0; q < UNR; ++q) {
       const int k = k0 + 32 * q;
-      v4i w = v4i{0, 0, 0, 0};
-      if (k < K) w = *reinterpret_cast<const v4i*>(xp + k);
-      fx[q] = __builtin_bit_cast(v8bf_t, w);
-    }
+      const bool ok = k < kbeg + kq;
 #pragma unroll
-    for (int q = 0; q < LD_UNROLL; ++q) {
-      const int k = k0 + 32 * q;
-      if (k >= K) break;
+      for (int t = 0; t < 2; ++t) fx[q][t] = ok ? *reinterpret_cast<const v4i*>(xp[t] + k) : v4i{0, 0, 0, 0};
 #pragma unroll
       for (int j = 0; j < RT; ++j) {
-        const int64_t ao = (int64_t)(16 * j + (lane & 15)) * K + k + kofs;
-        const v8bf_t fh = __builtin_bit_cast(v8bf_t, *reinterpret_cast<const v4i*>(hi + ao));
-        const v8bf_t fl = __builtin_bit_cast(v8bf_t, *reinterpret_cast<const v4i*>(lo + ao));
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fx[q], fh, acc[j], 0, 0, 0);
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fx[q], fl, acc[j], 0, 0, 0);
+        const int64_t ao = (int64_t)16 * j * K + arow + (ok ? k : kbeg);
+        fh[q][j] = *reinterpret_cast<const v4i*>(hi + ao);
+        fl[q][j] = *reinterpret_cast<const v4i*>(lo + ao);
       }
     }
-  }
-  // C layout (16x16): lane l owns column l%16 and rows 4*(l/16) + i.
 #pragma unroll
-  for (int j = 0; j < RT; ++j)
+    for (int q = 0; q < UNR; ++q)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int j = 0; j < RT; ++j) {
+          const v8bf xa = __builtin_bit_cast(v8bf, fx[q][t]);
+          acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, __builtin_bit_cast(v8bf, fh[q][j]), acc[t][j], 0, 0, 0);
+          acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, __builtin_bit_cast(v8bf, fl[q][j]), acc[t][j], 0, 0, 0);
+        }
+  }
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int j = 0; j < RT; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) part[wave][t][j][i][lane] = acc[t][j][i];
+  __syncthreads();
+  // C layout (16x16): lane l owns column l%16 and rows 4*(l/16) + i.  Thread = (t, j, lane) slot.
+  for (int slot = threadIdx.x; slot < 2 * RT * 64; slot += 256) {
+    const int ln = slot & 63, j = (slot >> 6) % RT, t = (slot >> 6) / RT;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t m = m0 + 4 * (lane >> 4) + i;
-      if (m < M) u[m * r + 16 * j + (lane & 15)] = acc[j][i];
+      const float v = ((part[0][t][j][i][ln] + part[1][t][j][i][ln]) + part[2][t][j][i][ln]) + part[3][t][j][i][ln];
+      const int64_t m = m0 + 16 * t + 4 * (ln >> 4) + i;
+      if (m < M) u[m * (16 * RT) + 16 * j + (ln & 15)] = v;
     }
+  }
 }
 
 // wt[k][n] = bf16(W_hat[n][k]) for a 64 x 64 tile; W_hat = s_w[n] q[n][k] (int8) or
@@ -149,7 +172,7 @@ __global__ __launch_bounds__(256) void transpose_f32_kernel(const float* __restr
 
 extern "C" int k2q_lora_down(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const float* lora_a,
                              int64_t r, uint16_t* ws, float* u, void* stream) {
-  if (!x || !lora_a || !ws || !u || M < 1 || K < 32 || K % 32 || ldx < K || ldx % 8) return K2Q_EINVAL;
+  if (!x || !lora_a || !ws || !u || M < 1 || K < 128 || K % 128 || ldx < K || ldx % 8) return K2Q_EINVAL;
   if (r < 16 || r > 128 || r % 16) return K2Q_EINVAL;
   if (!k2q_aligned(x, 16) || !k2q_aligned(ws, 16) || !k2q_aligned(u, 16)) return K2Q_EINVAL;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -158,7 +181,7 @@ extern "C" int k2q_lora_down(const uint16_t* x, int64_t M, int64_t K, int64_t ld
   uint16_t* lo = ws + n;
   hipLaunchKernelGGL(split_bf16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, lora_a, n, hi,
                      lo);
-  const dim3 grid((unsigned)((M + 63) / 64));
+  const dim3 grid((unsigned)((M + 31) / 32));
   switch (r / 16) {
 #define K2Q_LD_CASE(RT)                                                                                     \
   case RT:                                                                                                  \
