@@ -208,7 +208,10 @@ __device__ __forceinline__ void fwht128_rows(v16f (&f)[4], int h) {
 // `s_waitcnt vmcnt` for it plus one s_barrier (raw, without __syncthreads' full memory fence, which would
 // drain the prefetches).
 constexpr int SBK = 64;                   // reduction bytes per stage
-constexpr int NSTAGE = 4;
+#ifndef K2Q_NSTAGE
+#define K2Q_NSTAGE 4
+#endif
+constexpr int NSTAGE = K2Q_NSTAGE;        // LDS ring depth (4 or 5)
 constexpr int STAGE_TILE = BT * SBK;      // 16 KB per operand per stage
 constexpr int STAGE_BYTES = 2 * STAGE_TILE;
 
@@ -246,59 +249,74 @@ __device__ __forceinline__ v4i frag64(const uint8_t* s, int row, int chunk) {
   return *reinterpret_cast<const v4i*>(s + row * SBK + 16 * (chunk ^ swz64(row)));
 }
 
-// Epilogue LDS use (after the main loop has drained the ring): LoRA factor rows at offset 0 (at most
-// 2 x 256 x (2*128+16) B), then 3 x 256 floats of scales at SCALE_OFF.
-constexpr int LORA_LDS_MAX = 2 * BT * (2 * 128 + 16);
-constexpr int SCALE_OFF = (NSTAGE * STAGE_BYTES > LORA_LDS_MAX ? NSTAGE * STAGE_BYTES : LORA_LDS_MAX);
-constexpr int GEMM_LDS_BYTES = SCALE_OFF + 3 * BT * 4;
+// Epilogue LDS use (after the main loop has drained the ring): the bf16 output tile, 256 rows of CROW
+// bytes (256 values + 16 B of padding, which spreads a lane group's 8-byte writes over all banks), then
+// 3 x 256 floats of scales at SCALE_OFF.
+constexpr int CROW = 2 * BT + 16;
+constexpr int SCALE_OFF = BT * CROW;
+constexpr int GEMM_LDS_BYTES =
+    NSTAGE * STAGE_BYTES > SCALE_OFF + 3 * BT * 4 ? NSTAGE * STAGE_BYTES : SCALE_OFF + 3 * BT * 4;
+static_assert(GEMM_LDS_BYTES <= 160 * 1024, "gfx950 LDS is 160 KB per workgroup");
 
-// Thread t copies row A0+t of lora_ra and row B0+t of (lora_scale * lora_rb) into LDS as bf16, 32 ranks
-// per pass (16 float4 loads in flight per thread).
-template <typename Args>
-__device__ __forceinline__ void stage_lora_rows(const Args& p, int64_t A0, int64_t B0, int lstride, uint8_t* l_a,
-                                                uint8_t* l_b) {
-  const int t = threadIdx.x;
-  const int64_t ra = A0 + t < p.rows_a ? A0 + t : p.rows_a - 1;
-  const int64_t rb = B0 + t < p.rows_b ? B0 + t : p.rows_b - 1;
-  const float* srca = p.lora_ra + ra * p.r;
-  const float* srcb = p.lora_rb + rb * p.r;
-  for (int c0 = 0; c0 < p.r; c0 += 32) {
-    v4f va[8], vb[8];
+// One 32 x 32 block of f32 (MFMA C layout) into the LDS tile as bf16: lane l owns tile row mrow0 + l%32
+// and columns ncol0 + 8j + 4(l/32) .. +3.
+__device__ __forceinline__ void ctile_put(uint8_t* ct, int mrow0, int ncol0, int lane, const v16f& f) {
+  uint8_t* row = ct + (mrow0 + (lane & 31)) * CROW + 2 * (ncol0 + 4 * (lane >> 5));
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      if (c0 + 4 * q < p.r) {
-        va[q] = *reinterpret_cast<const v4f*>(srca + c0 + 4 * q);
-        vb[q] = *reinterpret_cast<const v4f*>(srcb + c0 + 4 * q);
+  for (int j = 0; j < 4; ++j)
+    *reinterpret_cast<v2u*>(row + 16 * j) = v2u{pack_bf16x2(f[4 * j], f[4 * j + 1]), pack_bf16x2(f[4 * j + 2], f[4 * j + 3])};
+}
+
+// Adds f onto the same positions (each lane touches only the values it wrote itself).
+__device__ __forceinline__ void ctile_add(uint8_t* ct, int mrow0, int ncol0, int lane, const v16f& f) {
+  uint8_t* row = ct + (mrow0 + (lane & 31)) * CROW + 2 * (ncol0 + 4 * (lane >> 5));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const v2u o = *reinterpret_cast<const v2u*>(row + 16 * j);
+    *reinterpret_cast<v2u*>(row + 16 * j) =
+        v2u{pack_bf16x2(bf16_bits_to_f32(o[0] & 0xffffu) + f[4 * j], bf16_bits_to_f32(o[0] >> 16) + f[4 * j + 1]),
+            pack_bf16x2(bf16_bits_to_f32(o[1] & 0xffffu) + f[4 * j + 2], bf16_bits_to_f32(o[1] >> 16) + f[4 * j + 3])};
+  }
+}
+
+// The wave's LoRA fragments for ranks c0 .. c0+31 (f32, converted later): la[i][kq] = lora_ra row
+// a0 + 32i + l%32, ranks c0 + 16kq + 8(l/32) .. +7; lb likewise from lora_rb rows b0 + 32i + l%32.
+template <int NB, typename Args>
+__device__ __forceinline__ void load_lora_frags(const Args& p, int64_t a0, int64_t b0, int c0, int lane,
+                                                v4f (&la)[4][2][2], v4f (&lb)[NB][2][2]) {
+  const int h = lane >> 5, c = lane & 31;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    int64_t ra = a0 + 32 * i + c;
+    ra = ra < p.rows_a ? ra : p.rows_a - 1;
+#pragma unroll
+    for (int kq = 0; kq < 2; ++kq) {
+      const int k = c0 + 16 * kq + 8 * h;
+      if (c0 + 16 * kq < p.r) {
+        la[i][kq][0] = *reinterpret_cast<const v4f*>(p.lora_ra + ra * p.r + k);
+        la[i][kq][1] = *reinterpret_cast<const v4f*>(p.lora_ra + ra * p.r + k + 4);
       }
     }
+  }
 #pragma unroll
-    for (int q = 0; q < 8; q += 2) {
-      if (c0 + 4 * q < p.r) {
-        const v4u wa4 = v4u{pack_bf16x2(va[q][0], va[q][1]), pack_bf16x2(va[q][2], va[q][3]),
-                            pack_bf16x2(va[q + 1][0], va[q + 1][1]), pack_bf16x2(va[q + 1][2], va[q + 1][3])};
-        const float s = p.lora_scale;
-        const v4u wb4 = v4u{pack_bf16x2(vb[q][0] * s, vb[q][1] * s), pack_bf16x2(vb[q][2] * s, vb[q][3] * s),
-                            pack_bf16x2(vb[q + 1][0] * s, vb[q + 1][1] * s),
-                            pack_bf16x2(vb[q + 1][2] * s, vb[q + 1][3] * s)};
-        *reinterpret_cast<v4u*>(l_a + t * lstride + 2 * (c0 + 4 * q)) = wa4;
-        *reinterpret_cast<v4u*>(l_b + t * lstride + 2 * (c0 + 4 * q)) = wb4;
+  for (int i = 0; i < NB; ++i) {
+    int64_t rb = b0 + 32 * i + c;
+    rb = rb < p.rows_b ? rb : p.rows_b - 1;
+#pragma unroll
+    for (int kq = 0; kq < 2; ++kq) {
+      const int k = c0 + 16 * kq + 8 * h;
+      if (c0 + 16 * kq < p.r) {
+        lb[i][kq][0] = *reinterpret_cast<const v4f*>(p.lora_rb + rb * p.r + k);
+        lb[i][kq][1] = *reinterpret_cast<const v4f*>(p.lora_rb + rb * p.r + k + 4);
       }
     }
   }
 }
 
-// LoRA term of one 32 x 32 block from the staged bf16 rows: f += lora_ra[arow,:] . lora_rb'[bcol,:].
-__device__ __forceinline__ v16f lora_block_lds(const uint8_t* l_a, const uint8_t* l_b, int lstride, int r,
-                                               int arow0, int bcol0, int lane, v16f f) {
-  const int h = lane >> 5, c = lane & 31;
-  const uint8_t* pa = l_a + (arow0 + c) * lstride + 16 * h;
-  const uint8_t* pb = l_b + (bcol0 + c) * lstride + 16 * h;
-  for (int ks = 0; ks < r; ks += 16) {
-    const v8bf fa = __builtin_bit_cast(v8bf, *reinterpret_cast<const v4i*>(pa + 2 * ks));
-    const v8bf fb = __builtin_bit_cast(v8bf, *reinterpret_cast<const v4i*>(pb + 2 * ks));
-    f = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, fb, f, 0, 0, 0);
-  }
-  return f;
+__device__ __forceinline__ v8bf f32x8_to_bf16v(v4f a, v4f b, float s) {
+  const v4u w = v4u{pack_bf16x2(a[0] * s, a[1] * s), pack_bf16x2(a[2] * s, a[3] * s), pack_bf16x2(b[0] * s, b[1] * s),
+                    pack_bf16x2(b[2] * s, b[3] * s)};
+  return __builtin_bit_cast(v8bf, w);
 }
 
 template <int N>
@@ -308,8 +326,16 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
+// Eight waves (two per SIMD) on a 256 x 256 tile: wave w covers A-rows 128*(w&1) .. +128 and B-rows
+// 64*(w>>1) .. +64 (4 x 2 MFMA blocks, 128 accumulator registers), so both waves of a SIMD issue LDS-DMA
+// and MFMAs and each can run while the other waits.
+constexpr int GW = 8;                   // waves per workgroup
+constexpr int GT = 64 * GW;             // threads per workgroup
+constexpr int WB = 2;                   // 32-wide B blocks per wave
+constexpr int DMA_PER_WAVE = STAGE_TILE / 1024 / GW;   // DMA instructions per wave, operand and stage
+
 template <int EPI>
-__global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_nt_kernel(GemmArgs p) {
+__global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_nt_kernel(GemmArgs p) {
   constexpr bool BF16 = (EPI == EPI_DX);
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // [NSTAGE][A tile | B tile]
 
@@ -324,17 +350,17 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
   const int wa = wave & 1, wb = wave >> 1;
   const int h = lane >> 5, c32 = lane & 31;
 
-  v16i acc[4][4];
+  v16i acc[4][WB];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = v16i{0};
+    for (int j = 0; j < WB; ++j) acc[i][j] = v16i{0};
 
   // Epilogue operands of this tile, fetched now so their latency hides under the main loop:
-  // thread t holds s_x of B-row B0+t (times 2^-7), s_w and bias of A-row A0+t.
+  // thread t < 256 holds s_x of B-row B0+t (times 2^-7), s_w and bias of A-row A0+t.
   float pre_sx = 0.f, pre_sw = 0.f, pre_bi = 0.f;
   if constexpr (EPI == EPI_W8) {
-    const int t = threadIdx.x;
+    const int t = threadIdx.x & (BT - 1);
     const int64_t rb = B0 + t < p.rows_b ? B0 + t : p.rows_b - 1;
     const int64_t ra = A0 + t < p.rows_a ? A0 + t : p.rows_a - 1;
     pre_sx = p.sx[rb] * 0.0078125f;  // 2^-7: the two unnormalised rotations
@@ -343,81 +369,98 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
   }
 
   const int nk = (int)(p.kbytes / SBK);
-  const DmaOffsets offa = dma_offsets(A0, p.rows_a, p.lda_b);
-  const DmaOffsets offb = dma_offsets(B0, p.rows_b, p.ldb_b);
+  uint32_t offa[DMA_PER_WAVE], offb[DMA_PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < DMA_PER_WAVE; ++i) {
+    const int lrow = 16 * (DMA_PER_WAVE * wave + i) + (lane >> 2);
+    int64_t ra = lrow, rb = lrow;
+    ra = A0 + ra < p.rows_a ? ra : p.rows_a - 1 - A0;
+    rb = B0 + rb < p.rows_b ? rb : p.rows_b - 1 - B0;
+    const uint32_t ch = 16u * (uint32_t)((lane & 3) ^ swz64(lrow));
+    offa[i] = (uint32_t)(ra * p.lda_b) + ch;
+    offb[i] = (uint32_t)(rb * p.ldb_b) + ch;
+  }
   const uint8_t* gA = p.a + A0 * p.lda_b;
   const uint8_t* gB = p.b + B0 * p.ldb_b;
-  uint8_t* ldsw = smem + 4096 * wave;   // this wave's DMA region inside a tile
+  uint8_t* ldsw = smem + 1024 * DMA_PER_WAVE * wave;   // this wave's DMA rows inside a tile
 
-  auto issue = [&](int st) {
-    uint8_t* buf = ldsw + (st % NSTAGE) * STAGE_BYTES;
-    dma_tile(gA + (int64_t)st * SBK, offa, buf);
-    dma_tile(gB + (int64_t)st * SBK, offb, buf + STAGE_TILE);
+  // DMA of reduction stage `src` into ring slot `slot`.
+  auto issue = [&](int src, int slot) {
+    uint8_t* buf = ldsw + slot * STAGE_BYTES;
+#pragma unroll
+    for (int i = 0; i < DMA_PER_WAVE; ++i)
+      __builtin_amdgcn_global_load_lds(K2Q_GPTR(gA + (int64_t)src * SBK + offa[i]), K2Q_LPTR(buf + 1024 * i), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < DMA_PER_WAVE; ++i)
+      __builtin_amdgcn_global_load_lds(K2Q_GPTR(gB + (int64_t)src * SBK + offb[i]), K2Q_LPTR(buf + STAGE_TILE + 1024 * i),
+                                       16, 0, 0);
   };
-  auto read_frags = [&](int st, int kk, v4i (&fa)[4], v4i (&fb)[4]) {
+  auto read_frags = [&](int st, int kk, v4i (&fa)[4], v4i (&fb)[WB]) {
     const uint8_t* tA = smem + (st % NSTAGE) * STAGE_BYTES;
     const uint8_t* tB = tA + STAGE_TILE;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      fa[i] = frag64(tA, 128 * wa + 32 * i + c32, 2 * kk + h);
-      fb[i] = frag64(tB, 128 * wb + 32 * i + c32, 2 * kk + h);
-    }
+    for (int i = 0; i < 4; ++i) fa[i] = frag64(tA, 128 * wa + 32 * i + c32, 2 * kk + h);
+#pragma unroll
+    for (int i = 0; i < WB; ++i) fb[i] = frag64(tB, 64 * wb + 32 * i + c32, 2 * kk + h);
   };
-  auto mfmas = [&](const v4i (&fa)[4], const v4i (&fb)[4]) {
+  auto mfmas = [&](const v4i (&fa)[4], const v4i (&fb)[WB]) {
 #pragma unroll
     for (int ia = 0; ia < 4; ++ia)
 #pragma unroll
-      for (int ib = 0; ib < 4; ++ib) mma<BF16>(fa[ia], fb[ib], acc[ia][ib]);
+      for (int ib = 0; ib < WB; ++ib) mma<BF16>(fa[ia], fb[ib], acc[ia][ib]);
   };
 
-  // Software pipeline (one wave per SIMD, so the wave itself must keep the matrix pipe fed):
-  //   iteration kt, first half : read stage kt substep-1 fragments | 16 MFMAs on substep 0
-  //   mid-stage                : wait for stage kt+1's DMA, s_barrier (stage kt-1's buffer now free)
-  //   second half              : DMA stage kt+3 into that buffer, read stage kt+1 substep-0 fragments |
-  //                              16 MFMAs on substep 1
+  // Software pipeline:
+  //   iteration kt, first half : read stage kt substep-1 fragments | 8 MFMAs on substep 0
+  //   mid-stage                : wait for stage kt+1's DMA, s_barrier (stage kt-1's slot now free)
+  //   second half              : DMA stage kt+NSTAGE-1 into that slot, read stage kt+1 substep-0
+  //                              fragments | 8 MFMAs on substep 1
   // so fragments are always in registers before their MFMAs.  The body has no branches: past the last
-  // stage the DMA re-loads stage nk-1 into the free buffer (never one still in use) and the extra
-  // fragment reads are discarded, which keeps exactly one DMA group (8 per wave) outstanding at the wait.
-  v4i f0a[4], f0b[4], f1a[4], f1b[4];
-  issue(0);
-  issue(nk > 1 ? 1 : nk - 1);
-  issue(nk > 2 ? 2 : nk - 1);
-  wait_vmcnt<16>();
+  // stage the DMA re-loads stage nk-1 into the freed slot (never one still in use) and the extra
+  // fragment reads are discarded, which keeps the count of outstanding DMA groups fixed at the wait.
+  constexpr int G = 2 * DMA_PER_WAVE;   // DMA instructions per wave per stage
+  v4i f0a[4], f0b[WB], f1a[4], f1b[WB];
+#pragma unroll
+  for (int st = 0; st < NSTAGE - 1; ++st) issue(st < nk ? st : nk - 1, st);
+  wait_vmcnt<G * (NSTAGE - 2)>();
   lds_barrier();
   read_frags(0, 0, f0a, f0b);
   for (int kt = 0; kt < nk; ++kt) {
     read_frags(kt, 1, f1a, f1b);
     mfmas(f0a, f0b);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 4 + WB; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-    wait_vmcnt<8>();
+    __builtin_amdgcn_sched_group_barrier(0x008, 4 * WB - (4 + WB), 0);
+    wait_vmcnt<G * (NSTAGE - 3)>();
     lds_barrier();
-    issue(kt + 3 < nk ? kt + 3 : nk - 1);
+    issue(kt + NSTAGE - 1 < nk ? kt + NSTAGE - 1 : nk - 1, (kt + NSTAGE - 1) % NSTAGE);
     read_frags(kt + 1, 0, f0a, f0b);
     mfmas(f1a, f1b);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < G; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM (LDS-DMA)
+    }
+#pragma unroll
+    for (int i = 0; i < 4 + WB; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 4 * WB - G, 0);
   }
   wait_vmcnt<0>();   // no LDS-DMA may still be in flight when the workgroup's LDS is released
 
   const int64_t a0 = A0 + 128 * wa;   // first A-row of this wave
-  const int64_t b0 = B0 + 128 * wb;   // first B-row of this wave
+  const int64_t b0 = B0 + 64 * wb;    // first B-row of this wave
 
   if constexpr (EPI == EPI_ACC) {
     int32_t* out = static_cast<int32_t*>(p.out);
 #pragma unroll
     for (int ia = 0; ia < 4; ++ia)
 #pragma unroll
-      for (int ib = 0; ib < 4; ++ib) {
+      for (int ib = 0; ib < WB; ++ib) {
         const int64_t m = b0 + 32 * ib + c32;
         if (m >= p.rows_b) continue;
 #pragma unroll
@@ -431,25 +474,25 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
       }
     return;
   } else {
-    // The LDS ring is free now.  Publish the prefetched scales, and stage the LoRA factor rows of this
-    // tile as bf16 (A side: lora_ra rows A0.., B side: lora_scale * lora_rb rows B0..), rows padded to
-    // 2r+16 bytes so the epilogue's 16-byte fragment reads are conflict-free.
-    lds_barrier();
+    // Epilogue in three passes over an LDS copy of the output tile (256 rows of CROW bytes, bf16):
+    //   A  dequantize (W8: f32 = 2^-7 s_x s_w acc + bias; DX: inverse FWHT, 2^-7) -> bf16 -> LDS
+    //   B  LoRA: fresh f32 accumulators (the integer ones are dead by now) over bf16 MFMAs, added onto
+    //      the staged values and re-rounded (the reference also adds a bf16 delta to a bf16 base)
+    //   C  coalesced 16-byte stores, 512 contiguous bytes per output row segment.
+    lds_barrier();   // every wave is done with the LDS ring
     float* s_sx = reinterpret_cast<float*>(smem + SCALE_OFF);
     float* s_sw = s_sx + BT;
     float* s_bi = s_sw + BT;
     if constexpr (EPI == EPI_W8) {
-      s_sx[threadIdx.x] = pre_sx;
-      s_sw[threadIdx.x] = pre_sw;
-      s_bi[threadIdx.x] = pre_bi;
+      if (threadIdx.x < BT) {
+        s_sx[threadIdx.x] = pre_sx;
+        s_sw[threadIdx.x] = pre_sw;
+        s_bi[threadIdx.x] = pre_bi;
+      }
     }
     const bool lora = p.lora_rb != nullptr && p.r > 0;
-    const int lstride = 2 * p.r + 16;
-    uint8_t* l_a = smem;
-    uint8_t* l_b = smem + BT * lstride;
-    if (lora) stage_lora_rows(p, A0, B0, lstride, l_a, l_b);
     lds_barrier();
-    uint16_t* out = static_cast<uint16_t*>(p.out);
+    uint8_t* ctile = smem;
     if constexpr (EPI == EPI_W8) {
 #pragma unroll
       for (int ia = 0; ia < 4; ++ia) {
@@ -461,31 +504,77 @@ __global__ __launch_bounds__(256, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) 
           bi[j] = *reinterpret_cast<const v4f*>(s_bi + nl);
         }
 #pragma unroll
-        for (int ib = 0; ib < 4; ++ib) {
-          const float sxm = s_sx[128 * wb + 32 * ib + c32];
+        for (int ib = 0; ib < WB; ++ib) {
+          const float sxm = s_sx[64 * wb + 32 * ib + c32];
           v16f f;
 #pragma unroll
           for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
               f[4 * j + i] = __builtin_fmaf((float)acc[ia][ib][4 * j + i], sxm * sw[j][i], bi[j][i]);
-          if (lora) f = lora_block_lds(l_a, l_b, lstride, p.r, 128 * wa + 32 * ia, 128 * wb + 32 * ib, lane, f);
-          store_block(out, p.ldo, p.rows_a, p.rows_b, a0 + 32 * ia, b0 + 32 * ib, lane, f);
+          ctile_put(ctile, 64 * wb + 32 * ib, 128 * wa + 32 * ia, lane, f);
         }
       }
     } else {  // EPI_DX: one 32-column slice (ib) at a time; the FWHT needs all 4 row slices of it.
 #pragma unroll
-      for (int ib = 0; ib < 4; ++ib) {
+      for (int ib = 0; ib < WB; ++ib) {
         v16f f[4];
 #pragma unroll
         for (int ia = 0; ia < 4; ++ia) f[ia] = __builtin_bit_cast(v16f, acc[ia][ib]);
         fwht128_rows(f, h);
 #pragma unroll
-        for (int ia = 0; ia < 4; ++ia) {
-          if (lora)
-            f[ia] = lora_block_lds(l_a, l_b, lstride, p.r, 128 * wa + 32 * ia, 128 * wb + 32 * ib, lane, f[ia]);
-          store_block(out, p.ldo, p.rows_a, p.rows_b, a0 + 32 * ia, b0 + 32 * ib, lane, f[ia]);
+        for (int ia = 0; ia < 4; ++ia) ctile_put(ctile, 64 * wb + 32 * ib, 128 * wa + 32 * ia, lane, f[ia]);
+      }
+    }
+    if (lora) {
+      v16f L[4][WB];
+#pragma unroll
+      for (int ia = 0; ia < 4; ++ia)
+#pragma unroll
+        for (int ib = 0; ib < WB; ++ib) L[ia][ib] = v16f{0.f};
+      for (int c0 = 0; c0 < p.r; c0 += 32) {
+        v4f la[4][2][2], lb[WB][2][2];
+        load_lora_frags<WB>(p, a0, b0, c0, lane, la, lb);
+#pragma unroll
+        for (int kq = 0; kq < 2; ++kq) {
+          if (c0 + 16 * kq >= p.r) break;
+          v8bf fa[4], fb[WB];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) fa[i] = f32x8_to_bf16v(la[i][kq][0], la[i][kq][1], 1.f);
+#pragma unroll
+          for (int i = 0; i < WB; ++i) fb[i] = f32x8_to_bf16v(lb[i][kq][0], lb[i][kq][1], p.lora_scale);
+#pragma unroll
+          for (int ia = 0; ia < 4; ++ia)
+#pragma unroll
+            for (int ib = 0; ib < WB; ++ib)
+              L[ia][ib] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ia], fb[ib], L[ia][ib], 0, 0, 0);
         }
+      }
+#pragma unroll
+      for (int ia = 0; ia < 4; ++ia)
+#pragma unroll
+        for (int ib = 0; ib < WB; ++ib) ctile_add(ctile, 64 * wb + 32 * ib, 128 * wa + 32 * ia, lane, L[ia][ib]);
+    }
+    lds_barrier();
+    // Pass C: wave w stores tile rows 32w .. 32w+31, two rows (2 x 512 B) per instruction.
+    uint16_t* out = static_cast<uint16_t*>(p.out);
+    const int chunk = lane & 31;
+    const int64_t col = A0 + 8 * chunk;
+    constexpr int RPW = BT / GW;   // rows per wave
+    if ((p.ldo & 7) == 0) {        // rows are 16-byte aligned: one 16-byte store per lane
+      const bool col_ok = col < p.rows_a;
+#pragma unroll 4
+      for (int i = 0; i < RPW / 2; ++i) {
+        const int row = RPW * wave + 2 * i + (lane >> 5);
+        const v4u v = *reinterpret_cast<const v4u*>(ctile + row * CROW + 16 * chunk);
+        if (col_ok && B0 + row < p.rows_b) *reinterpret_cast<v4u*>(out + (B0 + row) * p.ldo + col) = v;
+      }
+    } else {                       // ragged widths: element stores
+      for (int i = 0; i < RPW / 2; ++i) {
+        const int row = RPW * wave + 2 * i + (lane >> 5);
+        if (B0 + row >= p.rows_b) continue;
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(ctile + row * CROW + 16 * chunk);
+        for (int e = 0; e < 8 && col + e < p.rows_a; ++e) out[(B0 + row) * p.ldo + col + e] = src[e];
       }
     }
   }
@@ -712,7 +801,7 @@ int launch_gemm(const GemmArgs& p, hipStream_t st) {
     return K2Q_ELAUNCH;
   const int64_t tiles = ((p.rows_a + BT - 1) / BT) * ((p.rows_b + BT - 1) / BT);
   if (tiles > 0x7fffffff) return K2Q_EUNSUPPORTED;
-  hipLaunchKernelGGL(gemm_nt_kernel<EPI>, dim3((unsigned)tiles), dim3(256), lds, st, p);
+  hipLaunchKernelGGL(gemm_nt_kernel<EPI>, dim3((unsigned)tiles), dim3(GT), lds, st, p);
   return k2q_launch_status();
 }
 
@@ -737,6 +826,7 @@ extern "C" int k2q_gemm_w8a8(const int8_t* qx, const float* sx, const int8_t* qw
                              void* stream) {
   int rc = check_common(M, N, K);
   if (rc) return rc;
+  if (!k2q_aligned(y, 16)) return K2Q_EINVAL;
   if (!qx || !sx || !qw || !sw || !y) return K2Q_EINVAL;
   if (!k2q_aligned(qx, 16) || !k2q_aligned(qw, 16) || !k2q_aligned(sw, 16) || !k2q_aligned(y, 8))
     return K2Q_EINVAL;
@@ -769,7 +859,7 @@ extern "C" int k2q_gemm_w8a8_acc(const int8_t* qx, const int8_t* qw, int64_t M, 
 extern "C" int k2q_gemm_dx(const uint16_t* dy, const uint16_t* wt, int64_t M, int64_t N, int64_t K,
                            const float* g, const float* at, int64_t r, uint16_t* dx, void* stream) {
   if (M < 1 || K < K2Q_HADAMARD || K % K2Q_HADAMARD || N < 64 || N % 64) return K2Q_EINVAL;
-  if (!dy || !wt || !dx || !k2q_aligned(dy, 16) || !k2q_aligned(wt, 16) || !k2q_aligned(dx, 8))
+  if (!dy || !wt || !dx || !k2q_aligned(dy, 16) || !k2q_aligned(wt, 16) || !k2q_aligned(dx, 16))
     return K2Q_EINVAL;
   int rc = check_lora(g, at, r);
   if (rc) return rc;
