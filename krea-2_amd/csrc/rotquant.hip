@@ -20,7 +20,7 @@
 
 namespace {
 
-constexpr int kNCH = 4;  // max chunks of 16 elements per lane (K <= 1024 * WPR * 4)
+constexpr int kMaxNCH = 4;  // chunks of 16 elements per lane (K <= 1024 * WPR * 4)
 
 enum { MODE_ROW_I8 = 0, MODE_GROUP_I4 = 1 };
 
@@ -66,7 +66,7 @@ __device__ __forceinline__ float wave_max(float m) {
   return m;
 }
 
-template <typename Tin, int WPR, int MODE>
+template <typename Tin, int WPR, int MODE, int kNCH>
 __global__ __launch_bounds__(256) void rotquant_kernel(const Tin* __restrict__ x, int64_t M, int K,
                                                        int64_t ldx, int8_t* __restrict__ q,
                                                        float* __restrict__ s,
@@ -87,7 +87,7 @@ __global__ __launch_bounds__(256) void rotquant_kernel(const Tin* __restrict__ x
   const int pos = 16 * ((l & 1) | (((l >> 1) & 1) << 1) | (((l >> 3) & 1) << 2));
   const int off = blk * K2Q_HADAMARD + pos;
   const bool row_ok = row < M;
-  const int nch = (K + CW - 1) / CW;
+  constexpr int nch = kNCH;
 
   const Tin* xr = x + (row_ok ? row : 0) * ldx;
   float v[kNCH][16];
@@ -116,12 +116,21 @@ __global__ __launch_bounds__(256) void rotquant_kernel(const Tin* __restrict__ x
         v[c][i + st] = a - b;
       }
     }
+    // One v_fmac_f32_dpp per element and stage: v += partner(v) * c.  The 16 registers are visited
+    // round-robin, so a DPP read never follows the VALU write of its own source closer than 15
+    // instructions; the s_nop before each stage covers the in-lane stage's last writes.
+    asm volatile("s_nop 1" ::: "memory");
 #pragma unroll
-    for (int i = 0; i < 16; ++i) v[c][i] = __builtin_fmaf(dpp_f<0xB1>(v[c][i]), c1, v[c][i]);
+    for (int i = 0; i < 16; ++i)
+      asm volatile("v_fmac_f32_dpp %0, %0, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf" : "+v"(v[c][i]) : "v"(c1));
+    asm volatile("s_nop 1" ::: "memory");
 #pragma unroll
-    for (int i = 0; i < 16; ++i) v[c][i] = __builtin_fmaf(dpp_f<0x4E>(v[c][i]), c2, v[c][i]);
+    for (int i = 0; i < 16; ++i)
+      asm volatile("v_fmac_f32_dpp %0, %0, %1 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf" : "+v"(v[c][i]) : "v"(c2));
+    asm volatile("s_nop 1" ::: "memory");
 #pragma unroll
-    for (int i = 0; i < 16; ++i) v[c][i] = __builtin_fmaf(dpp_f<0x128>(v[c][i]), c8, v[c][i]);
+    for (int i = 0; i < 16; ++i)
+      asm volatile("v_fmac_f32_dpp %0, %0, %1 row_ror:8 row_mask:0xf bank_mask:0xf" : "+v"(v[c][i]) : "v"(c8));
     if (MODE == MODE_ROW_I8) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[c][i]));
@@ -203,22 +212,27 @@ __global__ __launch_bounds__(256) void rotquant_kernel(const Tin* __restrict__ x
   }
 }
 
-template <typename Tin, int MODE>
-int launch_rotquant(const void* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, float* s,
-                    uint16_t* xrot, uint8_t* q4, uint16_t* s4, hipStream_t st) {
-  const Tin* xp = static_cast<const Tin*>(x);
-  if (K <= 4096) {
-    hipLaunchKernelGGL((rotquant_kernel<Tin, 1, MODE>), dim3((M + 3) / 4), dim3(256), 0, st, xp, M,
-                       (int)K, ldx, q, s, xrot, q4, s4);
-  } else if (K <= 8192) {
-    hipLaunchKernelGGL((rotquant_kernel<Tin, 2, MODE>), dim3((M + 1) / 2), dim3(256), 0, st, xp, M,
-                       (int)K, ldx, q, s, xrot, q4, s4);
-  } else if (K <= 16384) {
-    hipLaunchKernelGGL((rotquant_kernel<Tin, 4, MODE>), dim3(M), dim3(256), 0, st, xp, M, (int)K, ldx,
-                       q, s, xrot, q4, s4);
-  } else {
-    return K2Q_EUNSUPPORTED;
+template <typename Tin, int WPR, int MODE>
+void launch_wpr(const Tin* xp, int64_t M, int64_t K, int64_t ldx, int8_t* q, float* s, uint16_t* xrot, uint8_t* q4,
+                uint16_t* s4, hipStream_t st) {
+  const dim3 grid((unsigned)((M + (4 / WPR) - 1) / (4 / WPR)));
+  const int nch = (int)((K + 1024 * WPR - 1) / (1024 * WPR));   // chunks of 16 elements per lane
+  switch (nch) {
+    case 1: hipLaunchKernelGGL((rotquant_kernel<Tin, WPR, MODE, 1>), grid, dim3(256), 0, st, xp, M, (int)K, ldx, q, s, xrot, q4, s4); break;
+    case 2: hipLaunchKernelGGL((rotquant_kernel<Tin, WPR, MODE, 2>), grid, dim3(256), 0, st, xp, M, (int)K, ldx, q, s, xrot, q4, s4); break;
+    case 3: hipLaunchKernelGGL((rotquant_kernel<Tin, WPR, MODE, 3>), grid, dim3(256), 0, st, xp, M, (int)K, ldx, q, s, xrot, q4, s4); break;
+    default: hipLaunchKernelGGL((rotquant_kernel<Tin, WPR, MODE, 4>), grid, dim3(256), 0, st, xp, M, (int)K, ldx, q, s, xrot, q4, s4); break;
   }
+}
+
+template <typename Tin, int MODE>
+int launch_rotquant(const void* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, float* s, uint16_t* xrot,
+                    uint8_t* q4, uint16_t* s4, hipStream_t st) {
+  const Tin* xp = static_cast<const Tin*>(x);
+  if (K <= 4096) launch_wpr<Tin, 1, MODE>(xp, M, K, ldx, q, s, xrot, q4, s4, st);
+  else if (K <= 8192) launch_wpr<Tin, 2, MODE>(xp, M, K, ldx, q, s, xrot, q4, s4, st);
+  else if (K <= 16384) launch_wpr<Tin, 4, MODE>(xp, M, K, ldx, q, s, xrot, q4, s4, st);
+  else return K2Q_EUNSUPPORTED;
   return k2q_launch_status();
 }
 
