@@ -51,9 +51,12 @@ int k2q_rotquant(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
 int k2q_quant_weight_i4(const void* w, int w_dtype, int64_t N, int64_t K,
                         uint8_t* qw4, uint16_t* sw4, void* stream);
 
-/* LoRA down-projection u = x.f32 @ A^T (lora.py:47, first product).  ws: 2*r*K bf16 workspace. */
+/* LoRA down-projection u = x.f32 @ A^T (lora.py:47, first product).  When the rows alone do not fill the
+ * GPU, K is cut into slices whose partials meet in ws (k2q_lora_down_ws_bytes(M, K, r) bytes; 0 means none
+ * is used) and are added in slice order; with ws == NULL or ws_bytes too small it runs unsliced. */
+int64_t k2q_lora_down_ws_bytes(int64_t M, int64_t K, int64_t r);
 int k2q_lora_down(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const float* lora_a, int64_t r,
-                  uint16_t* ws, float* u, void* stream);
+                  void* ws, int64_t ws_bytes, float* u, void* stream);
 
 /* (2)+(3) W8A8 GEMM with the fused epilogue, replacing F.linear(x, W_deq, b) of quantize.py:49-51 and
  * the LoRA add of lora.py:47-48:

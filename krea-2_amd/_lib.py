@@ -35,7 +35,8 @@ _SIGNATURES = {
     "k2q_check_device": ([], _int),
     "k2q_rotquant": ([_p, _int, _i64, _i64, _i64, _p, _p, _p, _p], _int),
     "k2q_quant_weight_i4": ([_p, _int, _i64, _i64, _p, _p, _p], _int),
-    "k2q_lora_down": ([_p, _i64, _i64, _i64, _p, _i64, _p, _p, _p], _int),
+    "k2q_lora_down_ws_bytes": ([_i64, _i64, _i64], _i64),
+    "k2q_lora_down": ([_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _p], _int),
     "k2q_gemm_w8a8": ([_p, _p, _p, _p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p], _int),
     "k2q_gemm_w4a8": ([_p, _p, _p, _p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p], _int),
     "k2q_gemm_w8a8_acc": ([_p, _p, _i64, _i64, _i64, _p, _p], _int),
@@ -182,9 +183,11 @@ def lora_down(x: torch.Tensor, A: torch.Tensor) -> torch.Tensor:
         raise ValueError(f"lora_A has in_features {A.shape[1]}, x has {K}")
     _check_rank(r)
     _device_check(dev)
-    ws = torch.empty((2 * r * K,), dtype=torch.bfloat16, device=dev)
+    lib = load()
+    nws = lib.k2q_lora_down_ws_bytes(M, K, r)
+    ws = torch.empty((nws // 4,), dtype=torch.float32, device=dev) if nws else None
     u = torch.empty((M, r), dtype=torch.float32, device=dev)
-    _check(load().k2q_lora_down(_ptr(x), M, K, K, _ptr(A), r, _ptr(ws), _ptr(u), _stream(dev)), "k2q_lora_down")
+    _check(lib.k2q_lora_down(_ptr(x), M, K, K, _ptr(A), r, _ptr(ws), nws, _ptr(u), _stream(dev)), "k2q_lora_down")
     return u
 
 

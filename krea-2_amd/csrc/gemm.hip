@@ -832,6 +832,9 @@ extern "C" int k2q_gemm_w8a8(const int8_t* qx, const float* sx, const int8_t* qw
     return K2Q_EINVAL;
   if (bias && !k2q_aligned(bias, 16)) return K2Q_EINVAL;
   if ((rc = check_lora(u, lora_b, r))) return rc;
+  if (M <= K2Q_GEMV_MAX_M)
+    return k2q_launch_gemv_w8a8(qx, sx, qw, sw, bias, u, lora_b, (int)r, lora_scale, M, N, K, y,
+                                static_cast<hipStream_t>(stream));
   GemmArgs p{};
   p.a = reinterpret_cast<const uint8_t*>(qw);
   p.b = reinterpret_cast<const uint8_t*>(qx);

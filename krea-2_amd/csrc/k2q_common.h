@@ -30,6 +30,12 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) { return pack_bf16
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
+// Skinny-M forward (gemv.hip), used by k2q_gemm_w8a8 for 1 <= M <= K2Q_GEMV_MAX_M.
+#define K2Q_GEMV_MAX_M 8
+int k2q_launch_gemv_w8a8(const int8_t* qx, const float* sx, const int8_t* qw, const float* sw, const float* bias,
+                         const float* u, const float* lora_b, int r, float lora_scale, int64_t M, int64_t N,
+                         int64_t K, uint16_t* y, hipStream_t st);
+
 // Status helpers for the C ABI.
 static inline int k2q_launch_status() {
   hipError_t e = hipGetLastError();
@@ -37,3 +43,12 @@ static inline int k2q_launch_status() {
 }
 
 static inline int k2q_aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+// Compute units of the current device (launch planning only; 256 on MI355X).
+static inline int k2q_cu_count() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      n < 1)
+    return 256;
+  return n;
+}

@@ -1,102 +1,170 @@
 // LoRA down-projection u = x A^T (reference lora.py:47, first product) and the operand preparation of
 // the input-gradient GEMM (transposed dequantized weight, transposed LoRA A).
 //
-// u: A (r x K, f32) is split once per call into bf16 hi + lo parts (A = hi + lo to ~2^-16 relative), and
+// u: every A fragment (f32) is split in registers into bf16 hi + lo (A = hi + lo to ~2^-16 relative) and
 // u = x hi^T + x lo^T runs on v_mfma_f32_16x16x32_bf16 with f32 accumulation; x is bf16 already, so the
-// only roundings are A's split residue and the f32 accumulation.  HBM-bound on reading x once.
+// only roundings are A's split residue and the f32 accumulation.  Bound by streaming x (once) and A (once
+// per workgroup) into the CUs.
 #include "k2q_common.h"
 
 namespace {
 
-typedef __bf16 v8bf_t __attribute__((ext_vector_type(8)));
-typedef float v4f_t __attribute__((ext_vector_type(4)));
-
-__global__ __launch_bounds__(256) void split_bf16_kernel(const float* __restrict__ a, int64_t n,
-                                                         uint16_t* __restrict__ hi,
-                                                         uint16_t* __restrict__ lo) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
-  const float v = a[i];
-  const uint32_t h = f32_to_bf16_bits(v);
-  hi[i] = (uint16_t)h;
-  lo[i] = (uint16_t)f32_to_bf16_bits(v - bf16_bits_to_f32(h));
+// hi = bf16(v), lo = bf16(v - hi) for 8 consecutive k (element e of the vectors = k + e).
+__device__ __forceinline__ void split8(v4f p, v4f q, v8bf& hi, v8bf& lo) {
+  const v4u h = v4u{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(q[0], q[1]), pack_bf16x2(q[2], q[3])};
+  const v4u l = v4u{pack_bf16x2(p[0] - __uint_as_float(h[0] << 16), p[1] - __uint_as_float(h[0] & 0xffff0000u)),
+                    pack_bf16x2(p[2] - __uint_as_float(h[1] << 16), p[3] - __uint_as_float(h[1] & 0xffff0000u)),
+                    pack_bf16x2(q[0] - __uint_as_float(h[2] << 16), q[1] - __uint_as_float(h[2] & 0xffff0000u)),
+                    pack_bf16x2(q[2] - __uint_as_float(h[3] << 16), q[3] - __uint_as_float(h[3] & 0xffff0000u))};
+  hi = __builtin_bit_cast(v8bf, h);
+  lo = __builtin_bit_cast(v8bf, l);
 }
 
-// u = x A^T for 32 rows per workgroup: the 4 waves split K in quarters, each runs 2 row tiles x RT rank
-// tiles of v_mfma_f32_16x16x32_bf16 (x hi and x lo), and the partial sums meet in LDS where wave 0..3
-// are added in that fixed order (deterministic).  Fragments come straight from global memory in MFMA
-// layout: lane l holds row l%16 (of x, or of A) and 8 contiguous k at 8*(l/16) of each 32-wide step.
-template <int RT>
-__global__ __launch_bounds__(256) void lora_down_kernel(const uint16_t* __restrict__ x, int64_t M, int K,
-                                                        int64_t ldx, const uint16_t* __restrict__ hi,
-                                                        const uint16_t* __restrict__ lo,
-                                                        float* __restrict__ u) {
-  constexpr int UNR = RT <= 2 ? 4 : (RT <= 4 ? 2 : 1);   // 32-wide k steps whose loads fly together
-  __shared__ float part[4][2][RT][4][64];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int64_t m0 = (int64_t)blockIdx.x * 32;
-  const int kq = K / 4;                 // this wave's quarter of K (a multiple of 32)
-  const int kbeg = wave * kq;
-  const int kofs = 8 * (lane >> 4);
-  const uint16_t* xp[2];
+// u (or one K-slice's partial of it) for 16*TT rows: workgroup (blockIdx.x, blockIdx.y) covers rows
+// 16*TT*blockIdx.x .. and the K-slice blockIdx.y * kslice .. + kslice; its 4 waves take a quarter of the
+// slice each and run TT row tiles x RT rank tiles of 16x16 MFMAs (x hi and x lo).  Fragments come straight
+// from global memory in MFMA layout (lane l: row l%16 of x or of A, 8 contiguous k at 8*(l/16) of each
+// 32-wide step), double-buffered so one batch of loads is in flight while the previous one is multiplied.
+// The wave partials meet in LDS and are added in the fixed order wave 0 + 1 + 2 + 3 (deterministic).
+// out: u (M x 16RT) when gridDim.y == 1, else the partial slices [gridDim.y][M][16RT].
+template <int RT, int TT>
+__global__ __launch_bounds__(256) void lora_down_kernel(const uint16_t* __restrict__ x, int64_t M, int64_t ldx,
+                                                        const float* __restrict__ a, int64_t K, int kslice,
+                                                        float* __restrict__ out) {
+  constexpr int UNR = RT <= 2 ? 2 : 1;   // 32-wide k steps per load batch
+  constexpr int R = 16 * RT;
+  __shared__ float part[3][TT][RT][4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t m0 = (int64_t)blockIdx.x * 16 * TT;
+  const int nst = kslice / 128;          // this wave's 32-wide steps
+  const int64_t kb = (int64_t)blockIdx.y * kslice + (int64_t)wave * (kslice / 4) + 8 * (lane >> 4);
+  const uint16_t* xp[TT];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < TT; ++t) {
     int64_t mr = m0 + 16 * t + (lane & 15);
     mr = mr < M ? mr : M - 1;
-    xp[t] = x + mr * ldx + kofs;
+    xp[t] = x + mr * ldx + kb;
   }
-  const int64_t arow = (int64_t)(lane & 15) * K + kofs;
+  const float* ap = a + (int64_t)(lane & 15) * K + kb;
+  // Every workgroup reads all of A; starting each at its own step of the slice spreads those reads over
+  // the L2 channels instead of having every CU request the same lines at the same time.
+  const int rot = (int)(((int64_t)blockIdx.x * 7 + blockIdx.y) % nst);
 
-  v4f acc[2][RT];
+  v4f acc[TT][RT];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int t = 0; t < TT; ++t)
 #pragma unroll
     for (int j = 0; j < RT; ++j) acc[t][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  for (int k0 = kbeg; k0 < kbeg + kq; k0 += 32 * UNR) {
-    v4i fx[UNR][2], fh[UNR][RT], fl[UNR][RT];
+  auto load = [&](v4i (&fx)[UNR][TT], v4f (&fa)[UNR][RT][2], int s0) {
 #pragma unroll
     for (int q = 0; q < UNR; ++q) {
-      const int k = k0 + 32 * q;
-      const bool ok = k < kbeg + kq;
+      int s = s0 + q < nst ? s0 + q : nst - 1;   // past the end: a harmless re-load
+      s += rot;
+      s -= s >= nst ? nst : 0;
 #pragma unroll
-      for (int t = 0; t < 2; ++t) fx[q][t] = ok ? *reinterpret_cast<const v4i*>(xp[t] + k) : v4i{0, 0, 0, 0};
+      for (int t = 0; t < TT; ++t) fx[q][t] = *reinterpret_cast<const v4i*>(xp[t] + 32 * s);
 #pragma unroll
       for (int j = 0; j < RT; ++j) {
-        const int64_t ao = (int64_t)16 * j * K + arow + (ok ? k : kbeg);
-        fh[q][j] = *reinterpret_cast<const v4i*>(hi + ao);
-        fl[q][j] = *reinterpret_cast<const v4i*>(lo + ao);
+        fa[q][j][0] = *reinterpret_cast<const v4f*>(ap + 16 * j * K + 32 * s);
+        fa[q][j][1] = *reinterpret_cast<const v4f*>(ap + 16 * j * K + 32 * s + 4);
       }
     }
+  };
+  auto compute = [&](const v4i (&fx)[UNR][TT], const v4f (&fa)[UNR][RT][2], int s0) {
 #pragma unroll
-    for (int q = 0; q < UNR; ++q)
+    for (int q = 0; q < UNR; ++q) {
+      if (s0 + q >= nst) break;
+      v8bf hi[RT], lo[RT];
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int j = 0; j < RT; ++j) split8(fa[q][j][0], fa[q][j][1], hi[j], lo[j]);
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        const v8bf xa = __builtin_bit_cast(v8bf, fx[q][t]);
 #pragma unroll
         for (int j = 0; j < RT; ++j) {
-          const v8bf xa = __builtin_bit_cast(v8bf, fx[q][t]);
-          acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, __builtin_bit_cast(v8bf, fh[q][j]), acc[t][j], 0, 0, 0);
-          acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, __builtin_bit_cast(v8bf, fl[q][j]), acc[t][j], 0, 0, 0);
+          acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, hi[j], acc[t][j], 0, 0, 0);
+          acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, lo[j], acc[t][j], 0, 0, 0);
         }
+      }
+    }
+  };
+  v4i fx0[UNR][TT], fx1[UNR][TT];
+  v4f fa0[UNR][RT][2], fa1[UNR][RT][2];
+  load(fx0, fa0, 0);
+  for (int s = 0; s < nst; s += 2 * UNR) {
+    load(fx1, fa1, s + UNR);
+    compute(fx0, fa0, s);
+    load(fx0, fa0, s + 2 * UNR);
+    compute(fx1, fa1, s + UNR);
   }
+
+  if (wave > 0) {
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+      for (int j = 0; j < RT; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part[wave - 1][t][j][i][lane] = acc[t][j][i];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float* o = out + (int64_t)blockIdx.y * M * R;
+  // C layout (16x16): lane l owns column (rank) l%16 and rows 4*(l/16) + i.
+#pragma unroll
+  for (int t = 0; t < TT; ++t)
 #pragma unroll
     for (int j = 0; j < RT; ++j)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) part[wave][t][j][i][lane] = acc[t][j][i];
-  __syncthreads();
-  // C layout (16x16): lane l owns column l%16 and rows 4*(l/16) + i.  Thread = (t, j, lane) slot.
-  for (int slot = threadIdx.x; slot < 2 * RT * 64; slot += 256) {
-    const int ln = slot & 63, j = (slot >> 6) % RT, t = (slot >> 6) / RT;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float v = ((part[0][t][j][i][ln] + part[1][t][j][i][ln]) + part[2][t][j][i][ln]) + part[3][t][j][i][ln];
-      const int64_t m = m0 + 16 * t + 4 * (ln >> 4) + i;
-      if (m < M) u[m * (16 * RT) + 16 * j + (ln & 15)] = v;
+      for (int i = 0; i < 4; ++i) {
+        const float v = ((acc[t][j][i] + part[0][t][j][i][lane]) + part[1][t][j][i][lane]) + part[2][t][j][i][lane];
+        const int64_t m = m0 + 16 * t + 4 * (lane >> 4) + i;
+        if (m < M) o[m * R + 16 * j + (lane & 15)] = v;
+      }
+}
+
+// u = sum of the K-slice partials in slice order (deterministic); n4 = M*r/4 float4 elements.
+__global__ __launch_bounds__(256) void lora_reduce_kernel(const v4f* __restrict__ part, int ks, int64_t n4,
+                                                          v4f* __restrict__ u) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  v4f s = part[i];
+  for (int p = 1; p < ks; ++p) s += part[p * n4 + i];
+  u[i] = s;
+}
+
+// Launch plan: TT row tiles per workgroup (fewer for tiny M), and K cut into ks slices (K % (128 ks) == 0,
+// slices of at least 512) until the grid covers the CUs; ks > 1 needs ks*M*r floats of workspace.
+struct LoraPlan {
+  int tt, ks;
+  int64_t row_blocks;
+};
+
+LoraPlan lora_plan(int64_t M, int64_t K, int64_t r) {
+  LoraPlan p{};
+  p.tt = r / 16 <= 4 ? 4 : 2;
+  while (p.tt > 1 && 16 * (p.tt / 2) >= M) p.tt /= 2;
+  p.row_blocks = (M + 16 * p.tt - 1) / (16 * p.tt);
+  const int cus = k2q_cu_count();
+  p.ks = 1;
+  if (p.row_blocks < cus)
+    for (int d = 2; d <= 16; ++d) {
+      if (K % (128 * d) || K / d < 512) continue;
+      p.ks = d;
+      if (p.row_blocks * d >= cus) break;
     }
-  }
+  return p;
+}
+
+template <int RT>
+void launch_lora_down(int tt, dim3 grid, hipStream_t st, const uint16_t* x, int64_t M, int64_t ldx, const float* a,
+                      int64_t K, int kslice, float* out) {
+  if (tt == 4)
+    hipLaunchKernelGGL((lora_down_kernel<RT, (RT <= 4 ? 4 : 2)>), grid, dim3(256), 0, st, x, M, ldx, a, K, kslice, out);
+  else if (tt == 2)
+    hipLaunchKernelGGL((lora_down_kernel<RT, 2>), grid, dim3(256), 0, st, x, M, ldx, a, K, kslice, out);
+  else
+    hipLaunchKernelGGL((lora_down_kernel<RT, 1>), grid, dim3(256), 0, st, x, M, ldx, a, K, kslice, out);
 }
 
 // wt[k][n] = bf16(W_hat[n][k]) for a 64 x 64 tile; W_hat = s_w[n] q[n][k] (int8) or
@@ -170,28 +238,38 @@ __global__ __launch_bounds__(256) void transpose_f32_kernel(const float* __restr
 
 }  // namespace
 
+extern "C" int64_t k2q_lora_down_ws_bytes(int64_t M, int64_t K, int64_t r) {
+  if (M < 1 || K < 128 || K % 128 || r < 16 || r > 128 || r % 16) return 0;
+  const LoraPlan p = lora_plan(M, K, r);
+  return p.ks > 1 ? (int64_t)p.ks * M * r * 4 : 0;
+}
+
 extern "C" int k2q_lora_down(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const float* lora_a,
-                             int64_t r, uint16_t* ws, float* u, void* stream) {
-  if (!x || !lora_a || !ws || !u || M < 1 || K < 128 || K % 128 || ldx < K || ldx % 8) return K2Q_EINVAL;
+                             int64_t r, void* ws, int64_t ws_bytes, float* u, void* stream) {
+  if (!x || !lora_a || !u || M < 1 || K < 128 || K % 128 || ldx < K || ldx % 8) return K2Q_EINVAL;
   if (r < 16 || r > 128 || r % 16) return K2Q_EINVAL;
-  if (!k2q_aligned(x, 16) || !k2q_aligned(ws, 16) || !k2q_aligned(u, 16)) return K2Q_EINVAL;
+  if (!k2q_aligned(x, 16) || !k2q_aligned(lora_a, 16) || !k2q_aligned(u, 16) || (ws && !k2q_aligned(ws, 16)))
+    return K2Q_EINVAL;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int64_t n = r * K;
-  uint16_t* hi = ws;
-  uint16_t* lo = ws + n;
-  hipLaunchKernelGGL(split_bf16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, lora_a, n, hi,
-                     lo);
-  const dim3 grid((unsigned)((M + 31) / 32));
+  LoraPlan p = lora_plan(M, K, r);
+  if (p.ks > 1 && (!ws || ws_bytes < (int64_t)p.ks * M * r * 4)) p.ks = 1;   // no room: one slice
+  if (p.row_blocks > 0x7fffffff) return K2Q_EUNSUPPORTED;
+  const dim3 grid((unsigned)p.row_blocks, (unsigned)p.ks);
+  float* out = p.ks > 1 ? static_cast<float*>(ws) : u;
+  const int kslice = (int)(K / p.ks);
   switch (r / 16) {
-#define K2Q_LD_CASE(RT)                                                                                     \
-  case RT:                                                                                                  \
-    hipLaunchKernelGGL(lora_down_kernel<RT>, grid, dim3(256), 0, st, x, M, (int)K, ldx, hi, lo, u);        \
-    break;
+#define K2Q_LD_CASE(RT) \
+  case RT: launch_lora_down<RT>(p.tt, grid, st, x, M, ldx, lora_a, K, kslice, out); break;
     K2Q_LD_CASE(1) K2Q_LD_CASE(2) K2Q_LD_CASE(3) K2Q_LD_CASE(4)
     K2Q_LD_CASE(5) K2Q_LD_CASE(6) K2Q_LD_CASE(7) K2Q_LD_CASE(8)
 #undef K2Q_LD_CASE
     default:
       return K2Q_EINVAL;
+  }
+  if (p.ks > 1) {
+    const int64_t n4 = M * r / 4;
+    hipLaunchKernelGGL(lora_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st,
+                       static_cast<const v4f*>(ws), p.ks, n4, reinterpret_cast<v4f*>(u));
   }
   return k2q_launch_status();
 }

@@ -189,6 +189,57 @@ def test_forward_w4a8(k2, dev, M, K, N, r, bias):
     assert rel_frob(y.float().cpu().numpy(), ref["y64"]) < 4e-3
 
 
+@pytest.mark.parametrize("M,K,r", [(2, 3072, 16), (1024, 12288, 16), (4608, 12288, 64), (100, 640, 48),
+                                   (33, 1024, 128), (17, 2048, 80), (16896, 3072, 32)])
+def test_lora_down_launch_plans(k2, dev, M, K, r):
+    """Every launch plan of the down-projection (row tiles per workgroup, K slices summed in slice order)
+    against the f64 product; the unsliced fallback (no workspace) too; repeated calls are bit-identical."""
+    x = make_x(M, K, seed=M + r)
+    A = torch.randn(r, K, generator=torch.Generator().manual_seed(r)) * 0.01
+    xd, Ad = x.to(dev), A.to(dev)
+    u = k2._lib.lora_down(xd, Ad)
+    ref = orc.lora_down(x.float().numpy(), A.numpy())
+    assert rel_frob(u.cpu().numpy(), ref) < 1e-5
+    assert torch.equal(u, k2._lib.lora_down(xd, Ad))
+    u1 = torch.empty_like(u)
+    lib = k2._lib.load()
+    assert lib.k2q_lora_down(xd.data_ptr(), M, K, K, Ad.data_ptr(), r, None, 0, u1.data_ptr(),
+                             torch.cuda.current_stream(dev).cuda_stream) == 0
+    assert rel_frob(u1.cpu().numpy(), ref) < 1e-5
+
+
+# Skinny M (1 <= M <= 8: the adaLN modulation linears run at M = batch) takes the GEMV path.
+@pytest.mark.parametrize("Ms,K,N,bias", [(1, 128, 4, False), (2, 3072, 1000, True), (5, 640, 260, False),
+                                         (8, 12288, 256, True), (3, 16384, 36, False)])
+def test_skinny_m_matches_mfma_rows_bit_exact(k2, dev, Ms, K, N, bias):
+    """Without LoRA the GEMV's bf16 output equals the MFMA path's rows bit for bit (same int32 sums,
+    same epilogue arithmetic); with LoRA the two differ by at most one bf16 ulp (summation order of L)."""
+    x = make_x(300, K, seed=Ms + K)
+    w = make_w(N, K, seed=N)
+    g = torch.Generator().manual_seed(9)
+    b = (torch.randn(N, generator=g) * 0.02).to(dev) if bias else None
+    A = (torch.randn(16, K, generator=g) * 0.01).to(dev)
+    B = (torch.randn(N, 16, generator=g) * 0.01).to(dev)
+    qx, sx, _ = k2._lib.rotquant(x.to(dev))
+    qw, sw = k2._lib.quant_weight_i8(w.to(dev))
+    y_big = k2._lib.gemm_w8a8(qx, sx, qw, sw, b, None, None, 1.0)
+    y_small = k2._lib.gemm_w8a8(qx[:Ms], sx[:Ms], qw, sw, b, None, None, 1.0)
+    assert torch.equal(y_small.view(torch.int16), y_big[:Ms].view(torch.int16))
+    u = k2._lib.lora_down(x.to(dev), A)
+    y_big = k2._lib.gemm_w8a8(qx, sx, qw, sw, b, u, B, 0.5)
+    y_small = k2._lib.gemm_w8a8(qx[:Ms], sx[:Ms], qw, sw, b, u[:Ms], B, 0.5)
+    assert ulp_dist_bf16(bits16(y_small), bits16(y_big[:Ms])).max() <= 1
+
+
+@pytest.mark.parametrize("M,K,N,r,bias", [(2, 3072, 18432, 16, False), (1, 256, 128, 128, True),
+                                          (7, 1024, 520, 64, True)])
+def test_forward_w8a8_skinny_m(k2, dev, M, K, N, r, bias):
+    """(2, 3072, 18432): the adaLN modulation linear of a double-stream block at CFG batch 2."""
+    y, u, ref = _forward_case(k2, dev, M, K, N, r, False, bias, seed=M + N)
+    assert rel_frob(y.float().cpu().numpy(), ref["y64"]) < 4e-3
+    assert rel_frob(u.cpu().numpy(), ref["u"]) < 1e-5
+
+
 # ------------------------------------------------------------------------------------------- kernel (4)
 @pytest.mark.parametrize("M,K,N,r,w4", [(256, 256, 256, 0, False), (200, 384, 320, 16, False),
                                         (512, 1024, 512, 64, False), (256, 512, 256, 32, True)])

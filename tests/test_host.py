@@ -17,13 +17,13 @@ ROOT = Path(__file__).resolve().parents[1]
 
 def header_symbols():
     text = (ROOT / "include" / "k2q.h").read_text()
-    return sorted(set(re.findall(r"^(?:const char\*|int)\s+(k2q_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^(?:const char\*|int|int64_t)\s+(k2q_\w+)\(", text, re.M)))
 
 
 def test_library_exports_every_declared_symbol(k2):
     lib = k2._lib.load()
     syms = header_symbols()
-    assert len(syms) >= 11
+    assert len(syms) >= 12
     for name in syms:
         assert hasattr(lib, name), name
     assert sorted(k2._lib.EXPORTS) == syms
@@ -50,7 +50,9 @@ def test_status_codes_for_bad_arguments_without_gpu(k2):
     assert lib.k2q_gemm_w8a8(p, p, p, p, None, p, p, 8, 1.0, 4, 4, 128, p, None) == -1   # rank 8
     assert lib.k2q_gemm_w8a8(p, p, p, p, None, None, None, 0, 0.0, 4, 6, 128, p, None) == -1  # N % 4
     assert lib.k2q_gemm_dx(p, p, 4, 96, 128, None, None, 0, p, None) == -1    # N % 64
-    assert lib.k2q_lora_down(p, 4, 128, 128, p, 200, p, p, None) == -1       # rank > 128
+    assert lib.k2q_lora_down(p, 4, 128, 128, p, 200, p, 0, p, None) == -1    # rank > 128
+    assert lib.k2q_lora_down(p, 4, 100, 100, p, 16, None, 0, p, None) == -1  # K % 128
+    assert lib.k2q_lora_down_ws_bytes(4, 128, 200) == 0                      # no plan for a bad rank
 
 
 def test_wrappers_validate_before_launch(k2):
