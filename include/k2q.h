@@ -58,13 +58,26 @@ int64_t k2q_lora_down_ws_bytes(int64_t M, int64_t K, int64_t r);
 int k2q_lora_down(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const float* lora_a, int64_t r,
                   void* ws, int64_t ws_bytes, float* u, void* stream);
 
+/* LoRA gradients through the frozen base (the autograd of lora.py:47-48):
+ *   g = scale * dy @ lora_b (M x r), dA = g^T x (r x K), dB = scale * dy^T u (N x r),
+ * all f32 from bf16 dy (M x N) / x (M x K) and f32 u (M x r) / lora_b (N x r).  dA / dB nullable (x / u
+ * then unused).  N % 128 == 0, K % 128 == 0.  ws: k2q_lora_grads_ws_bytes(M, N, K, r) bytes, 256-aligned. */
+int64_t k2q_lora_grads_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t r);
+int k2q_lora_grads(const uint16_t* dy, const uint16_t* x, const float* u, const float* lora_b, int64_t r,
+                   float scale, int64_t M, int64_t N, int64_t K, float* g, float* dA, float* dB, void* ws,
+                   int64_t ws_bytes, void* stream);
+
 /* (2)+(3) W8A8 GEMM with the fused epilogue, replacing F.linear(x, W_deq, b) of quantize.py:49-51 and
  * the LoRA add of lora.py:47-48:
  *   y = bf16(2^-7 s_x[m] s_w[n] acc[m,n] + bias[n] + lora_scale * sum_j u[m,j] lora_b[n,j]).
- * bias, u, lora_b nullable (r ignored when u is null). */
+ * bias, u, lora_b nullable (r ignored when u is null).  M <= 8 runs a GEMV.  When the 256 x 256 tiles
+ * leave the last round of the GPU partly empty, the remainder tiles are cut along K into pieces whose
+ * int32 sums meet in ws (k2q_gemm_w8a8_ws_bytes(M, N, K) bytes, 0 = not used); the result is identical.
+ * ws == NULL or too small: full-K tiles only. */
+int64_t k2q_gemm_w8a8_ws_bytes(int64_t M, int64_t N, int64_t K);
 int k2q_gemm_w8a8(const int8_t* qx, const float* sx, const int8_t* qw, const float* sw, const float* bias,
                   const float* u, const float* lora_b, int64_t r, float lora_scale,
-                  int64_t M, int64_t N, int64_t K, uint16_t* y, void* stream);
+                  int64_t M, int64_t N, int64_t K, uint16_t* y, void* ws, int64_t ws_bytes, void* stream);
 
 /* W4A8 variant: per-group int32 partials scaled by the bf16 group scales. */
 int k2q_gemm_w4a8(const int8_t* qx, const float* sx, const uint8_t* qw4, const uint16_t* sw4,
@@ -74,7 +87,7 @@ int k2q_gemm_w4a8(const int8_t* qx, const float* sx, const uint8_t* qw4, const u
 /* Debug entries: raw int32 accumulators acc[m,n] = sum_k qx[m,k] qw[n,k] (W8), and for W4 the f32
  * value sum_g sw4[n,g] * acc_g[m,n] without s_x, 2^-7, bias or LoRA. */
 int k2q_gemm_w8a8_acc(const int8_t* qx, const int8_t* qw, int64_t M, int64_t N, int64_t K,
-                      int32_t* acc, void* stream);
+                      int32_t* acc, void* ws, int64_t ws_bytes, void* stream);   /* ws as k2q_gemm_w8a8 */
 int k2q_gemm_w4a8_f32(const int8_t* qx, const uint8_t* qw4, const uint16_t* sw4,
                       int64_t M, int64_t N, int64_t K, float* out, void* stream);
 
@@ -82,12 +95,15 @@ int k2q_gemm_w4a8_f32(const int8_t* qx, const uint8_t* qw4, const uint16_t* sw4,
  *   dx = bf16(2^-7 (dy W_hat) R + g A),   W_hat[n,k] = s_w[n] q[n,k] (or s_w4[n,k/64] q4[n,k]).
  * k2q_dx_prep writes wt = bf16(W_hat)^T (K x N) and at = A^T (K x r, f32) into caller workspaces;
  * k2q_gemm_dx then runs the bf16 MFMA GEMM with the inverse rotation and the LoRA term fused.
- * g = lora_scale * dy @ lora_b (M x r f32) is supplied by the caller; g/at nullable. */
+ * g = lora_scale * dy @ lora_b (M x r f32) is supplied by the caller; g/at nullable.  ws: as for
+ * k2q_gemm_w8a8 (f32 pieces, added in a fixed order), k2q_gemm_dx_ws_bytes(M, N, K) bytes. */
 int k2q_dx_prep(const int8_t* qw, const float* sw, const uint8_t* qw4, const uint16_t* sw4,
                 int64_t N, int64_t K, const float* lora_a, int64_t r,
                 uint16_t* wt, float* at, void* stream);
+int64_t k2q_gemm_dx_ws_bytes(int64_t M, int64_t N, int64_t K);
 int k2q_gemm_dx(const uint16_t* dy, const uint16_t* wt, int64_t M, int64_t N, int64_t K,
-                const float* g, const float* at, int64_t r, uint16_t* dx, void* stream);
+                const float* g, const float* at, int64_t r, uint16_t* dx, void* ws, int64_t ws_bytes,
+                void* stream);
 
 #ifdef __cplusplus
 }

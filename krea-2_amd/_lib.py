@@ -37,12 +37,16 @@ _SIGNATURES = {
     "k2q_quant_weight_i4": ([_p, _int, _i64, _i64, _p, _p, _p], _int),
     "k2q_lora_down_ws_bytes": ([_i64, _i64, _i64], _i64),
     "k2q_lora_down": ([_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _p], _int),
-    "k2q_gemm_w8a8": ([_p, _p, _p, _p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p], _int),
+    "k2q_lora_grads_ws_bytes": ([_i64, _i64, _i64, _i64], _i64),
+    "k2q_lora_grads": ([_p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p], _int),
+    "k2q_gemm_w8a8_ws_bytes": ([_i64, _i64, _i64], _i64),
+    "k2q_gemm_w8a8": ([_p, _p, _p, _p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p, _i64, _p], _int),
     "k2q_gemm_w4a8": ([_p, _p, _p, _p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p], _int),
-    "k2q_gemm_w8a8_acc": ([_p, _p, _i64, _i64, _i64, _p, _p], _int),
+    "k2q_gemm_w8a8_acc": ([_p, _p, _i64, _i64, _i64, _p, _p, _i64, _p], _int),
     "k2q_gemm_w4a8_f32": ([_p, _p, _p, _i64, _i64, _i64, _p, _p], _int),
     "k2q_dx_prep": ([_p, _p, _p, _p, _i64, _i64, _p, _i64, _p, _p, _p], _int),
-    "k2q_gemm_dx": ([_p, _p, _i64, _i64, _i64, _p, _p, _i64, _p, _p], _int),
+    "k2q_gemm_dx_ws_bytes": ([_i64, _i64, _i64], _i64),
+    "k2q_gemm_dx": ([_p, _p, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _p], _int),
 }
 EXPORTS = tuple(_SIGNATURES)
 
@@ -110,6 +114,13 @@ def _need(t: torch.Tensor, name: str, dtype, ndim: int | None = None, dev: torch
         raise ValueError(f"{name} is on {t.device}, expected {dev}")
     if t.data_ptr() % 16:
         raise ValueError(f"{name} must be 16-byte aligned")
+
+
+def _workspace(nbytes: int, dev: torch.device):
+    """Scratch device memory for a kernel's split pieces (from PyTorch's caching allocator), or none."""
+    if nbytes <= 0:
+        return None, 0
+    return torch.empty((nbytes,), dtype=torch.uint8, device=dev), nbytes
 
 
 def _check_k(K: int) -> None:
@@ -191,6 +202,43 @@ def lora_down(x: torch.Tensor, A: torch.Tensor) -> torch.Tensor:
     return u
 
 
+def lora_grads(dy, x, u, lora_b, lora_scale: float):
+    """LoRA gradients (the autograd of ``lora.py:47-48``): ``g = s dy B`` (M,r), ``dA = g^T x`` (r,K) when
+    ``x`` is given, ``dB = s dy^T u`` (N,r) when ``u`` is given; all f32.  ``dy`` (M,N) and ``x`` (M,K) bf16,
+    ``u`` (M,r) and ``lora_b`` (N,r) f32.  Returns ``(g, dA | None, dB | None)``."""
+    _need(dy, "dy", torch.bfloat16, 2)
+    dev = dy.device
+    M, N = dy.shape
+    _need(lora_b, "lora_B", torch.float32, 2, dev)
+    r = lora_b.shape[1]
+    if lora_b.shape[0] != N:
+        raise ValueError(f"lora_B has {lora_b.shape[0]} rows, dy has {N} columns")
+    _check_rank(r)
+    if N % HADAMARD_BLOCK:
+        raise ValueError(f"out_features={N} must be a multiple of {HADAMARD_BLOCK} for the LoRA gradients")
+    K = HADAMARD_BLOCK
+    if x is not None:
+        _need(x, "x", torch.bfloat16, 2, dev)
+        if x.shape[0] != M:
+            raise ValueError("x rows != dy rows")
+        K = x.shape[1]
+        _check_k(K)
+    if u is not None:
+        _need(u, "u", torch.float32, 2, dev)
+        if u.shape != (M, r):
+            raise ValueError(f"u must be {(M, r)}, got {tuple(u.shape)}")
+    _device_check(dev)
+    lib = load()
+    nws = lib.k2q_lora_grads_ws_bytes(M, N, K, r)
+    ws = torch.empty((nws,), dtype=torch.uint8, device=dev)
+    g = torch.empty((M, r), dtype=torch.float32, device=dev)
+    dA = torch.empty((r, K), dtype=torch.float32, device=dev) if x is not None else None
+    dB = torch.empty((N, r), dtype=torch.float32, device=dev) if u is not None else None
+    _check(lib.k2q_lora_grads(_ptr(dy), _ptr(x), _ptr(u), _ptr(lora_b), r, float(lora_scale), M, N, K, _ptr(g),
+                              _ptr(dA), _ptr(dB), _ptr(ws), nws, _stream(dev)), "k2q_lora_grads")
+    return g, dA, dB
+
+
 # ----------------------------------------------------------------------------------------------------------
 # (2)+(3) GEMMs with fused epilogue
 # ----------------------------------------------------------------------------------------------------------
@@ -220,8 +268,10 @@ def _gemm_common(qx, sx, N, bias, u, lora_b):
     return dev, M, K, r
 
 
-def gemm_w8a8(qx, sx, qw, sw, bias=None, u=None, lora_b=None, lora_scale: float = 1.0) -> torch.Tensor:
-    """``y = bf16(2^-7 s_x s_w acc + bias + lora_scale u lora_B^T)`` (M,N)."""
+def gemm_w8a8(qx, sx, qw, sw, bias=None, u=None, lora_b=None, lora_scale: float = 1.0, *,
+              split: bool = True) -> torch.Tensor:
+    """``y = bf16(2^-7 s_x s_w acc + bias + lora_scale u lora_B^T)`` (M,N).  ``split=False`` runs every tile
+    over the full K (the result is the same; the split schedule only fills the GPU's last round)."""
     _need(qw, "q_w", torch.int8, 2)
     N = qw.shape[0]
     dev, M, K, r = _gemm_common(qx, sx, N, bias, u, lora_b)
@@ -233,8 +283,10 @@ def gemm_w8a8(qx, sx, qw, sw, bias=None, u=None, lora_b=None, lora_scale: float 
     _check_k(K)
     _device_check(dev)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-    _check(load().k2q_gemm_w8a8(_ptr(qx), _ptr(sx), _ptr(qw), _ptr(sw), _ptr(bias), _ptr(u), _ptr(lora_b), r,
-                                float(lora_scale), M, N, K, _ptr(y), _stream(dev)), "k2q_gemm_w8a8")
+    lib = load()
+    ws, nws = _workspace(lib.k2q_gemm_w8a8_ws_bytes(M, N, K) if split else 0, dev)
+    _check(lib.k2q_gemm_w8a8(_ptr(qx), _ptr(sx), _ptr(qw), _ptr(sw), _ptr(bias), _ptr(u), _ptr(lora_b), r,
+                             float(lora_scale), M, N, K, _ptr(y), _ptr(ws), nws, _stream(dev)), "k2q_gemm_w8a8")
     return y
 
 
@@ -256,7 +308,7 @@ def gemm_w4a8(qx, sx, q4, s4, bias=None, u=None, lora_b=None, lora_scale: float 
     return y
 
 
-def gemm_w8a8_acc(qx, qw) -> torch.Tensor:
+def gemm_w8a8_acc(qx, qw, *, split: bool = True) -> torch.Tensor:
     """Debug: raw int32 accumulators ``qx @ qw^T`` (M,N)."""
     _need(qx, "q_x", torch.int8, 2)
     dev = qx.device
@@ -268,7 +320,10 @@ def gemm_w8a8_acc(qx, qw) -> torch.Tensor:
     _check_k(K)
     _device_check(dev)
     acc = torch.empty((M, N), dtype=torch.int32, device=dev)
-    _check(load().k2q_gemm_w8a8_acc(_ptr(qx), _ptr(qw), M, N, K, _ptr(acc), _stream(dev)), "k2q_gemm_w8a8_acc")
+    lib = load()
+    ws, nws = _workspace(lib.k2q_gemm_w8a8_ws_bytes(M, N, K) if split else 0, dev)
+    _check(lib.k2q_gemm_w8a8_acc(_ptr(qx), _ptr(qw), M, N, K, _ptr(acc), _ptr(ws), nws, _stream(dev)),
+           "k2q_gemm_w8a8_acc")
     return acc
 
 
@@ -293,7 +348,7 @@ def gemm_w4a8_f32(qx, q4, s4) -> torch.Tensor:
 # ----------------------------------------------------------------------------------------------------------
 # (4) input gradient
 # ----------------------------------------------------------------------------------------------------------
-def gemm_dx(dy, qw, sw, *, w4: bool = False, g=None, lora_a=None) -> torch.Tensor:
+def gemm_dx(dy, qw, sw, *, w4: bool = False, g=None, lora_a=None, split: bool = True) -> torch.Tensor:
     """``dx = bf16(2^-7 (dy W_hat) R + g lora_A)`` (M,K); ``dy`` (M,N) bf16, ``g`` (M,r) f32 already
     scaled (``lora_scale * dy @ lora_B``), ``lora_a`` (r,K) f32."""
     _need(dy, "dy", torch.bfloat16, 2)
@@ -333,5 +388,7 @@ def gemm_dx(dy, qw, sw, *, w4: bool = False, g=None, lora_a=None) -> torch.Tenso
                            _ptr(sw) if w4 else None, N, K, _ptr(lora_a) if r else None, r, _ptr(wt), _ptr(at), st),
            "k2q_dx_prep")
     dx = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
-    _check(lib.k2q_gemm_dx(_ptr(dy), _ptr(wt), M, N, K, _ptr(g), _ptr(at), r, _ptr(dx), st), "k2q_gemm_dx")
+    ws, nws = _workspace(lib.k2q_gemm_dx_ws_bytes(M, N, K) if split else 0, dev)
+    _check(lib.k2q_gemm_dx(_ptr(dy), _ptr(wt), M, N, K, _ptr(g), _ptr(at), r, _ptr(dx), _ptr(ws), nws, st),
+           "k2q_gemm_dx")
     return dx

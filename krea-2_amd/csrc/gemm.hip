@@ -43,16 +43,37 @@ struct GemmArgs {
   const float* lora_ra;  // per-A-row LoRA factor rows (lora_b or A^T), rows_a x r f32
   int r;
   float lora_scale;
+  // Split schedule for the last, partly filled round of tiles: tiles 0 .. dp_tiles-1 run over the full
+  // reduction; each of the sk_rem remainder tiles dp_tiles + i is cut into sk_s pieces (piece q covers
+  // reduction slice q / sk_rem) whose accumulators go to part, and a fixup launch adds them.
+  int64_t dp_tiles;
+  int sk_rem, sk_s;
+  int32_t* part;
 };
 
 __device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
-__device__ __forceinline__ void tile_coords(int64_t tiles_a, int64_t tiles_b, int64_t& ta, int64_t& tb) {
-  const int nwg = gridDim.x;
-  const int bid = blockIdx.x;
+// Workgroup ids are dealt round-robin over the 8 XCDs; renumber them so that consecutive ids share an XCD.
+__device__ __forceinline__ int xcd_remap(int bid, int nwg) {
   const int xcd = bid & 7, idx = bid >> 3;
   const int per = (nwg + 7) >> 3, rem = nwg & 7;
-  const int lid = (rem == 0 || xcd < rem) ? xcd * per + idx : rem * per + (xcd - rem) * (per - 1) + idx;
+  return (rem == 0 || xcd < rem) ? xcd * per + idx : rem * per + (xcd - rem) * (per - 1) + idx;
+}
+
+// Linear tile id -> (A tile, B tile), 8 B-tiles per group so tiles running together share operand strips.
+__device__ __forceinline__ void group_coords(int64_t lid, int64_t tiles_a, int64_t tiles_b, int64_t& ta, int64_t& tb) {
+  constexpr int GB = 8;
+  const int64_t in_group = (int64_t)GB * tiles_a;
+  const int64_t g = lid / in_group;
+  const int64_t first_b = g * GB;
+  const int64_t gsize = (tiles_b - first_b) < GB ? (tiles_b - first_b) : GB;
+  const int64_t r = lid % in_group;
+  tb = first_b + r % gsize;
+  ta = r / gsize;
+}
+
+__device__ __forceinline__ void tile_coords(int64_t tiles_a, int64_t tiles_b, int64_t& ta, int64_t& tb) {
+  const int lid = xcd_remap(blockIdx.x, gridDim.x);
   constexpr int GB = 8;
   const int64_t in_group = (int64_t)GB * tiles_a;
   const int64_t g = lid / in_group;
@@ -334,15 +355,34 @@ constexpr int GT = 64 * GW;             // threads per workgroup
 constexpr int WB = 2;                   // 32-wide B blocks per wave
 constexpr int DMA_PER_WAVE = STAGE_TILE / 1024 / GW;   // DMA instructions per wave, operand and stage
 
-template <int EPI>
+enum { MODE_TILE = 0, MODE_PIECE = 1, MODE_FIXUP = 2 };
+
+// MODE_TILE: one full-K tile per workgroup (tiles 0 .. gridDim.x-1) and the epilogue.  MODE_PIECE: one
+// piece of a remainder tile, accumulators parked in part.  MODE_FIXUP: the pieces of remainder tile
+// dp_tiles + blockIdx.x added in slice order, then the epilogue.  Separate kernels, so the register
+// allocation of the tile kernel is not shared with the other paths.
+template <int EPI, int MODE>
 __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_nt_kernel(GemmArgs p) {
   constexpr bool BF16 = (EPI == EPI_DX);
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // [NSTAGE][A tile | B tile]
 
   const int64_t tiles_a = (p.rows_a + BT - 1) / BT;
   const int64_t tiles_b = (p.rows_b + BT - 1) / BT;
+  int nk = (int)(p.kbytes / SBK);
+  int kbeg = 0;
+  int64_t lid;
+  if constexpr (MODE == MODE_FIXUP) {
+    lid = p.dp_tiles + blockIdx.x;
+  } else if constexpr (MODE == MODE_PIECE) {
+    const int sl = (int)blockIdx.x / p.sk_rem;
+    lid = p.dp_tiles + (int)blockIdx.x % p.sk_rem;
+    kbeg = sl * nk / p.sk_s;
+    nk = (sl + 1) * nk / p.sk_s - kbeg;
+  } else {
+    lid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+  }
   int64_t ta, tb;
-  tile_coords(tiles_a, tiles_b, ta, tb);
+  group_coords(lid, tiles_a, tiles_b, ta, tb);
   const int64_t A0 = ta * BT, B0 = tb * BT;
 
   const int lane = threadIdx.x & 63;
@@ -368,7 +408,6 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     pre_bi = p.bias ? p.bias[ra] : 0.f;
   }
 
-  const int nk = (int)(p.kbytes / SBK);
   uint32_t offa[DMA_PER_WAVE], offb[DMA_PER_WAVE];
 #pragma unroll
   for (int i = 0; i < DMA_PER_WAVE; ++i) {
@@ -380,8 +419,8 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     offa[i] = (uint32_t)(ra * p.lda_b) + ch;
     offb[i] = (uint32_t)(rb * p.ldb_b) + ch;
   }
-  const uint8_t* gA = p.a + A0 * p.lda_b;
-  const uint8_t* gB = p.b + B0 * p.ldb_b;
+  const uint8_t* gA = p.a + A0 * p.lda_b + (int64_t)kbeg * SBK;
+  const uint8_t* gB = p.b + B0 * p.ldb_b + (int64_t)kbeg * SBK;
   uint8_t* ldsw = smem + 1024 * DMA_PER_WAVE * wave;   // this wave's DMA rows inside a tile
 
   // DMA of reduction stage `src` into ring slot `slot`.
@@ -419,38 +458,78 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
   // stage the DMA re-loads stage nk-1 into the freed slot (never one still in use) and the extra
   // fragment reads are discarded, which keeps the count of outstanding DMA groups fixed at the wait.
   constexpr int G = 2 * DMA_PER_WAVE;   // DMA instructions per wave per stage
-  v4i f0a[4], f0b[WB], f1a[4], f1b[WB];
+  // Accumulator storage of a piece in part: 16-byte unit ((ia * WB + ib) * 4 + q) of thread t at byte
+  // 8 KB * unit + 16 t, so each wave instruction moves 1 KB of consecutive bytes.  The per-unit base is
+  // workgroup-uniform (scalar registers) and the thread offset a 32-bit vector register.
+  constexpr int64_t PIECE_BYTES = (int64_t)BT * BT * 4;
+  const uint32_t toff = 16u * threadIdx.x;
+  if constexpr (MODE == MODE_FIXUP) {
+    for (int sl = 0; sl < p.sk_s; ++sl) {
+      const uint8_t* pc = reinterpret_cast<const uint8_t*>(p.part) + ((int64_t)sl * p.sk_rem + blockIdx.x) * PIECE_BYTES;
 #pragma unroll
-  for (int st = 0; st < NSTAGE - 1; ++st) issue(st < nk ? st : nk - 1, st);
-  wait_vmcnt<G * (NSTAGE - 2)>();
-  lds_barrier();
-  read_frags(0, 0, f0a, f0b);
-  for (int kt = 0; kt < nk; ++kt) {
-    read_frags(kt, 1, f1a, f1b);
-    mfmas(f0a, f0b);
+      for (int ia = 0; ia < 4; ++ia)
 #pragma unroll
-    for (int i = 0; i < 4 + WB; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+        for (int ib = 0; ib < WB; ++ib) {
+          const uint8_t* u = pc + (int64_t)(ia * WB + ib) * 4 * GT * 16;
+          const v4i q0 = *reinterpret_cast<const v4i*>(u + toff);
+          const v4i q1 = *reinterpret_cast<const v4i*>(u + GT * 16 + toff);
+          const v4i q2 = *reinterpret_cast<const v4i*>(u + 2 * GT * 16 + toff);
+          const v4i q3 = *reinterpret_cast<const v4i*>(u + 3 * GT * 16 + toff);
+          const v16i v = __builtin_shufflevector(__builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7),
+                                                 __builtin_shufflevector(q2, q3, 0, 1, 2, 3, 4, 5, 6, 7), 0, 1, 2,
+                                                 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
+          if constexpr (BF16)
+            acc[ia][ib] = __builtin_bit_cast(v16i, __builtin_bit_cast(v16f, acc[ia][ib]) + __builtin_bit_cast(v16f, v));
+          else
+            acc[ia][ib] += v;
+        }
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4 * WB - (4 + WB), 0);
-    wait_vmcnt<G * (NSTAGE - 3)>();
+  } else {
+    v4i f0a[4], f0b[WB], f1a[4], f1b[WB];
+#pragma unroll
+    for (int st = 0; st < NSTAGE - 1; ++st) issue(st < nk ? st : nk - 1, st);
+    wait_vmcnt<G * (NSTAGE - 2)>();
     lds_barrier();
-    issue(kt + NSTAGE - 1 < nk ? kt + NSTAGE - 1 : nk - 1, (kt + NSTAGE - 1) % NSTAGE);
-    read_frags(kt + 1, 0, f0a, f0b);
-    mfmas(f1a, f1b);
+    read_frags(0, 0, f0a, f0b);
+    for (int kt = 0; kt < nk; ++kt) {
+      read_frags(kt, 1, f1a, f1b);
+      mfmas(f0a, f0b);
 #pragma unroll
-    for (int i = 0; i < G; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM (LDS-DMA)
-    }
+      for (int i = 0; i < 4 + WB; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4 * WB - (4 + WB), 0);
+      wait_vmcnt<G * (NSTAGE - 3)>();
+      lds_barrier();
+      issue(kt + NSTAGE - 1 < nk ? kt + NSTAGE - 1 : nk - 1, (kt + NSTAGE - 1) % NSTAGE);
+      read_frags(kt + 1, 0, f0a, f0b);
+      mfmas(f1a, f1b);
 #pragma unroll
-    for (int i = 0; i < 4 + WB; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      for (int i = 0; i < G; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM (LDS-DMA)
+      }
+#pragma unroll
+      for (int i = 0; i < 4 + WB; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4 * WB - G, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4 * WB - G, 0);
+    wait_vmcnt<0>();   // no LDS-DMA may still be in flight when the workgroup's LDS is released
   }
-  wait_vmcnt<0>();   // no LDS-DMA may still be in flight when the workgroup's LDS is released
+  if constexpr (MODE == MODE_PIECE) {   // park the accumulators for the fixup launch
+    uint8_t* dst = reinterpret_cast<uint8_t*>(p.part) + (int64_t)blockIdx.x * PIECE_BYTES;
+#pragma unroll
+    for (int ia = 0; ia < 4; ++ia)
+#pragma unroll
+      for (int ib = 0; ib < WB; ++ib)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<v4i*>(dst + (int64_t)((ia * WB + ib) * 4 + q) * GT * 16 + toff) =
+              v4i{acc[ia][ib][4 * q], acc[ia][ib][4 * q + 1], acc[ia][ib][4 * q + 2], acc[ia][ib][4 * q + 3]};
+    return;
+  }
 
   const int64_t a0 = A0 + 128 * wa;   // first A-row of this wave
   const int64_t b0 = B0 + 64 * wb;    // first B-row of this wave
@@ -793,15 +872,68 @@ int launch_w4(const W4Args& p, hipStream_t st) {
   return k2q_launch_status();
 }
 
+// Split plan for the tiles of the last, partly filled round, in units of one reduction stage of one tile
+// (measured on MI355X): a full-K tile costs nk + 8 (epilogue); cutting the rem remainder tiles into s
+// pieces (one round of pieces when rem * s <= CUs) costs nk / s per piece plus ~12 (ramp and piece
+// store), and the fixup launch ~20 + 3 per piece read back.  The s with the lowest cost is taken if it
+// saves at least 10 %.
+struct SplitPlan {
+  int64_t dp_tiles;
+  int rem, s;
+};
+
+SplitPlan split_plan(int64_t tiles, int nk, int cus) {
+  SplitPlan q{tiles, 0, 1};
+  const int64_t full = tiles / cus, rem = tiles - full * cus;
+  if (rem == 0) return q;
+  const double tile = nk + 8.0;
+  const double t_full = (double)(full + 1) * tile;
+  double best = 0.9 * t_full;
+  for (int s = 2; s <= 8 && rem * s <= cus && nk / s >= 8; ++s) {
+    const double t = (double)full * tile + (double)nk / s + 12.0 + 20.0 + 3.0 * s;
+    if (t < best) {
+      best = t;
+      q.s = s;
+    }
+  }
+  if (q.s > 1) {
+    q.dp_tiles = full * cus;
+    q.rem = (int)rem;
+  }
+  return q;
+}
+
+int64_t split_ws_bytes(int64_t rows_a, int64_t rows_b, int64_t kbytes) {
+  const int64_t tiles = ((rows_a + BT - 1) / BT) * ((rows_b + BT - 1) / BT);
+  const SplitPlan q = split_plan(tiles, (int)(kbytes / SBK), k2q_cu_count());
+  return q.s > 1 ? (int64_t)q.rem * q.s * BT * BT * 4 : 0;
+}
+
 template <int EPI>
-int launch_gemm(const GemmArgs& p, hipStream_t st) {
+int launch_gemm(GemmArgs p, void* ws, int64_t ws_bytes, hipStream_t st) {
   constexpr int lds = GEMM_LDS_BYTES;
-  if (hipFuncSetAttribute((const void*)gemm_nt_kernel<EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
+  if (hipFuncSetAttribute((const void*)gemm_nt_kernel<EPI, MODE_TILE>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          lds) != hipSuccess ||
+      hipFuncSetAttribute((const void*)gemm_nt_kernel<EPI, MODE_PIECE>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          lds) != hipSuccess ||
+      hipFuncSetAttribute((const void*)gemm_nt_kernel<EPI, MODE_FIXUP>, hipFuncAttributeMaxDynamicSharedMemorySize,
                           lds) != hipSuccess)
     return K2Q_ELAUNCH;
   const int64_t tiles = ((p.rows_a + BT - 1) / BT) * ((p.rows_b + BT - 1) / BT);
   if (tiles > 0x7fffffff) return K2Q_EUNSUPPORTED;
-  hipLaunchKernelGGL(gemm_nt_kernel<EPI>, dim3((unsigned)tiles), dim3(GT), lds, st, p);
+  SplitPlan q = split_plan(tiles, (int)(p.kbytes / SBK), k2q_cu_count());
+  if (q.s > 1 && (!ws || ws_bytes < (int64_t)q.rem * q.s * BT * BT * 4 || !k2q_aligned(ws, 16)))
+    q = SplitPlan{tiles, 0, 1};   // no room for the pieces: full-K tiles only
+  p.dp_tiles = q.dp_tiles;
+  p.sk_rem = q.rem;
+  p.sk_s = q.s;
+  p.part = static_cast<int32_t*>(ws);
+  // Pieces first: they fill the GPU for a short round, then the full tiles, then the fixup.
+  if (q.s > 1)
+    hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_PIECE>), dim3((unsigned)(q.rem * q.s)), dim3(GT), lds, st, p);
+  if (q.dp_tiles > 0)
+    hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_TILE>), dim3((unsigned)q.dp_tiles), dim3(GT), lds, st, p);
+  if (q.s > 1) hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_FIXUP>), dim3((unsigned)q.rem), dim3(GT), lds, st, p);
   return k2q_launch_status();
 }
 
@@ -820,10 +952,20 @@ int check_lora(const float* u, const float* lb, int64_t r) {
 
 }  // namespace
 
+extern "C" int64_t k2q_gemm_w8a8_ws_bytes(int64_t M, int64_t N, int64_t K) {
+  if (check_common(M, N, K) || M <= K2Q_GEMV_MAX_M) return 0;
+  return split_ws_bytes(N, M, K);
+}
+
+extern "C" int64_t k2q_gemm_dx_ws_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || K < K2Q_HADAMARD || K % K2Q_HADAMARD || N < 64 || N % 64) return 0;
+  return split_ws_bytes(K, M, 2 * N);
+}
+
 extern "C" int k2q_gemm_w8a8(const int8_t* qx, const float* sx, const int8_t* qw, const float* sw,
                              const float* bias, const float* u, const float* lora_b, int64_t r,
                              float lora_scale, int64_t M, int64_t N, int64_t K, uint16_t* y,
-                             void* stream) {
+                             void* ws, int64_t ws_bytes, void* stream) {
   int rc = check_common(M, N, K);
   if (rc) return rc;
   if (!k2q_aligned(y, 16)) return K2Q_EINVAL;
@@ -842,11 +984,11 @@ extern "C" int k2q_gemm_w8a8(const int8_t* qx, const float* sx, const int8_t* qw
   p.out = y; p.ldo = N;
   p.sx = sx; p.sw = sw; p.bias = bias;
   p.lora_rb = u; p.lora_ra = lora_b; p.r = u ? (int)r : 0; p.lora_scale = lora_scale;
-  return launch_gemm<EPI_W8>(p, static_cast<hipStream_t>(stream));
+  return launch_gemm<EPI_W8>(p, ws, ws_bytes, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int k2q_gemm_w8a8_acc(const int8_t* qx, const int8_t* qw, int64_t M, int64_t N, int64_t K,
-                                 int32_t* acc, void* stream) {
+                                 int32_t* acc, void* ws, int64_t ws_bytes, void* stream) {
   int rc = check_common(M, N, K);
   if (rc) return rc;
   if (!qx || !qw || !acc || !k2q_aligned(qx, 16) || !k2q_aligned(qw, 16) || !k2q_aligned(acc, 16))
@@ -856,11 +998,12 @@ extern "C" int k2q_gemm_w8a8_acc(const int8_t* qx, const int8_t* qw, int64_t M, 
   p.b = reinterpret_cast<const uint8_t*>(qx);
   p.rows_a = N; p.rows_b = M; p.kbytes = K; p.lda_b = K; p.ldb_b = K;
   p.out = acc; p.ldo = N;
-  return launch_gemm<EPI_ACC>(p, static_cast<hipStream_t>(stream));
+  return launch_gemm<EPI_ACC>(p, ws, ws_bytes, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int k2q_gemm_dx(const uint16_t* dy, const uint16_t* wt, int64_t M, int64_t N, int64_t K,
-                           const float* g, const float* at, int64_t r, uint16_t* dx, void* stream) {
+                           const float* g, const float* at, int64_t r, uint16_t* dx, void* ws, int64_t ws_bytes,
+                           void* stream) {
   if (M < 1 || K < K2Q_HADAMARD || K % K2Q_HADAMARD || N < 64 || N % 64) return K2Q_EINVAL;
   if (!dy || !wt || !dx || !k2q_aligned(dy, 16) || !k2q_aligned(wt, 16) || !k2q_aligned(dx, 16))
     return K2Q_EINVAL;
@@ -872,7 +1015,7 @@ extern "C" int k2q_gemm_dx(const uint16_t* dy, const uint16_t* wt, int64_t M, in
   p.rows_a = K; p.rows_b = M; p.kbytes = 2 * N; p.lda_b = 2 * N; p.ldb_b = 2 * N;
   p.out = dx; p.ldo = K;
   p.lora_rb = g; p.lora_ra = at; p.r = g ? (int)r : 0; p.lora_scale = 1.f;
-  return launch_gemm<EPI_DX>(p, static_cast<hipStream_t>(stream));
+  return launch_gemm<EPI_DX>(p, ws, ws_bytes, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int k2q_gemm_w4a8(const int8_t* qx, const float* sx, const uint8_t* qw4, const uint16_t* sw4,

@@ -8,9 +8,10 @@ Mirrors ``lora.py`` of the reference: ``LoRALinear`` (``lora.py:27-48``) with th
 metadata (``:154-222``).
 
 The one behavioural addition: when ``base`` is a :class:`~.quantize.ConvRotLinear` and the rank fits the fused
-kernels (a multiple of 16, at most 128), ``forward`` runs base + LoRA as one fused HIP pass (the LoRA
-down-projection on bf16 MFMA, the up-projection inside the GEMM epilogue) instead of three extra GEMMs and
-three elementwise kernels.  ``scale_mul == 0`` still returns exactly ``base(x)`` (``lora.py:45-46``).
+kernels (a multiple of 16, at most 128; ``out_features`` a multiple of 128), ``forward`` runs base + LoRA as
+one fused HIP pass (the LoRA down-projection on bf16 MFMA, the up-projection inside the GEMM epilogue) instead
+of three extra GEMMs and three elementwise kernels, and the backward computes the LoRA gradients with the
+library's own kernels.  ``scale_mul == 0`` still returns exactly ``base(x)`` (``lora.py:45-46``).
 """
 from __future__ import annotations
 
@@ -45,6 +46,7 @@ class LoRALinear(nn.Module):
 
     def _fusable(self) -> bool:
         return (isinstance(self.base, ConvRotLinear) and self.rank % 16 == 0 and self.rank <= 128
+                and self.base.out_features % 128 == 0
                 and self.lora_A.dtype == torch.float32 and self.lora_B.dtype == torch.float32)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:

@@ -49,12 +49,8 @@ class _ConvRotLinearFn(torch.autograd.Function):
             dy = dy.to(torch.bfloat16)
         g = dA = dB = None
         if A is not None:
-            dyf = dy.float()
-            g = (ctx.lora_scale * (dyf @ B)).contiguous()
-            if ctx.needs_input_grad[1]:
-                dA = g.t() @ x2.float()
-            if ctx.needs_input_grad[2]:
-                dB = ctx.lora_scale * (dyf.t() @ u)
+            g, dA, dB = _lib.lora_grads(dy, x2 if ctx.needs_input_grad[1] else None,
+                                        u if ctx.needs_input_grad[2] else None, B, ctx.lora_scale)
         dx = None
         if ctx.needs_input_grad[0]:
             dx = _lib.gemm_dx(dy, qweight, wscale, w4=ctx.w4, g=g, lora_a=A if g is not None else None)

@@ -208,6 +208,26 @@ def test_lora_down_launch_plans(k2, dev, M, K, r):
     assert rel_frob(u1.cpu().numpy(), ref) < 1e-5
 
 
+@pytest.mark.parametrize("M,N,K,r", [(192, 256, 512, 16), (100, 128, 384, 48), (1, 384, 128, 128),
+                                     (777, 640, 1280, 80), (4608, 3072, 12288, 64)])
+def test_lora_grads(k2, dev, M, N, K, r):
+    """g = s dY B, dA = g^T x, dB = s dY^T u (the autograd of lora.py:47-48) against float64; the last case
+    is BASELINE.json cfg3 at full size."""
+    gen = torch.Generator().manual_seed(M + N + r)
+    dy = (torch.randn(M, N, generator=gen) * 1e-3).to(torch.bfloat16)
+    x = make_x(M, K, seed=r)
+    u = torch.randn(M, r, generator=gen)
+    B = torch.randn(N, r, generator=gen) * 0.01
+    s = 0.75
+    g, dA, dB = k2._lib.lora_grads(dy.to(dev), x.to(dev), u.to(dev), B.to(dev), s)
+    g64 = s * (dy.double() @ B.double())
+    assert rel_frob(g.cpu().numpy(), g64.numpy()) < 2e-5
+    assert rel_frob(dA.cpu().numpy(), (g64.t() @ x.double()).numpy()) < 2e-5
+    assert rel_frob(dB.cpu().numpy(), (s * (dy.double().t() @ u.double())).numpy()) < 2e-5
+    g2, dA2, dB2 = k2._lib.lora_grads(dy.to(dev), None, None, B.to(dev), s)
+    assert dA2 is None and dB2 is None and torch.equal(g2, g)      # deterministic; optional outputs
+
+
 # Skinny M (1 <= M <= 8: the adaLN modulation linears run at M = batch) takes the GEMV path.
 @pytest.mark.parametrize("Ms,K,N,bias", [(1, 128, 4, False), (2, 3072, 1000, True), (5, 640, 260, False),
                                          (8, 12288, 256, True), (3, 16384, 36, False)])
@@ -261,6 +281,55 @@ def test_input_gradient(k2, dev, M, K, N, r, w4):
     ref = orc.backward(dy.float().numpy(), x_dummy, qo, so, w4=w4, lora_A=None if A is None else A.numpy(),
                        lora_B=None if B is None else B.numpy(), lora_scale=1.0)
     assert rel_frob(dx.float().cpu().numpy(), ref["dx64"]) < REL_FROB_TOL
+
+
+# ------------------------------------------------------------------------------------------- split schedule
+@pytest.mark.parametrize("M,N,K", [(512, 768, 4096), (1024, 3072, 12288), (8192, 3072, 12288)])
+def test_gemm_split_schedule_bit_exact(k2, dev, M, N, K):
+    """Shapes whose last round of 256 x 256 tiles leaves the GPU partly empty (cfg4's text-stream and
+    image-stream down projections are the last two): the remainder tiles are cut along K into pieces whose
+    int32 sums a fixup launch adds.  Accumulators equal the exact product, and the bf16 outputs (bias,
+    LoRA) equal those of the full-K schedule bit for bit."""
+    assert k2._lib.load().k2q_gemm_w8a8_ws_bytes(M, N, K) > 0      # the split schedule is taken
+    rng = np.random.default_rng(M + N + K)
+    qx_h = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    qw_h = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    qx, qw = torch.from_numpy(qx_h).to(dev), torch.from_numpy(qw_h).to(dev)
+    acc = k2._lib.gemm_w8a8_acc(qx, qw)
+    assert torch.equal(acc, k2._lib.gemm_w8a8_acc(qx, qw, split=False))
+    rows = np.arange(M) if M <= 1024 else np.array([0, 1, 255, 256, M // 2, M - 257, M - 1])
+    assert np.array_equal(acc.cpu().numpy()[rows], orc.gemm_acc_fast(qx_h[rows], qw_h))
+    g = torch.Generator().manual_seed(1)
+    sx = (torch.rand(M, generator=g) * 0.01 + 1e-3).to(dev)
+    sw = (torch.rand(N, generator=g) * 0.01 + 1e-3).to(dev)
+    bias = (torch.randn(N, generator=g) * 0.02).to(dev)
+    u = torch.randn(M, 16, generator=g).to(dev)
+    B = (torch.randn(N, 16, generator=g) * 0.01).to(dev)
+    y = k2._lib.gemm_w8a8(qx, sx, qw, sw, bias, u, B, 0.5)
+    y0 = k2._lib.gemm_w8a8(qx, sx, qw, sw, bias, u, B, 0.5, split=False)
+    assert torch.equal(y.view(torch.int16), y0.view(torch.int16))
+
+
+def test_input_gradient_split_schedule(k2, dev):
+    """dX with the remainder tiles cut along N (f32 pieces added in slice order): against the oracle, and
+    within f32 summation-order noise of the full-N schedule; repeated calls are bit-identical."""
+    M, K, N, r = 512, 768, 4096, 32
+    assert k2._lib.load().k2q_gemm_dx_ws_bytes(M, N, K) > 0
+    w = make_w(N, K, seed=7)
+    g = torch.Generator().manual_seed(8)
+    dy = (torch.randn(M, N, generator=g) * 1e-3).to(torch.bfloat16)
+    A = torch.randn(r, K, generator=g) * 0.01
+    B = torch.randn(N, r, generator=g) * 0.01
+    qw, sw = k2._lib.quant_weight_i8(w.to(dev))
+    qo, so = orc.quant_weight_i8(w.float().numpy())
+    gd = (dy.float() @ B).contiguous().to(dev)
+    dx = k2._lib.gemm_dx(dy.to(dev), qw, sw, g=gd, lora_a=A.to(dev))
+    dx0 = k2._lib.gemm_dx(dy.to(dev), qw, sw, g=gd, lora_a=A.to(dev), split=False)
+    ref = orc.backward(dy.float().numpy(), np.zeros((M, K)), qo, so, lora_A=A.numpy(), lora_B=B.numpy(),
+                       lora_scale=1.0)
+    assert rel_frob(dx.float().cpu().numpy(), ref["dx64"]) < 4e-3
+    assert rel_frob(dx.float().cpu().numpy(), dx0.float().cpu().numpy()) < 1e-3
+    assert torch.equal(dx, k2._lib.gemm_dx(dy.to(dev), qw, sw, g=gd, lora_a=A.to(dev)))
 
 
 # ------------------------------------------------------------------------------------------- module

@@ -47,9 +47,9 @@ def test_status_codes_for_bad_arguments_without_gpu(k2):
     assert lib.k2q_rotquant(None, 0, 4, 128, 128, p, p, None, None) == -1     # null
     assert lib.k2q_rotquant(p + 2, 0, 4, 128, 128, p, p, None, None) == -1    # misaligned
     assert lib.k2q_rotquant(p, 0, 4, 32768, 32768, p, p, None, None) == -4    # K too large
-    assert lib.k2q_gemm_w8a8(p, p, p, p, None, p, p, 8, 1.0, 4, 4, 128, p, None) == -1   # rank 8
-    assert lib.k2q_gemm_w8a8(p, p, p, p, None, None, None, 0, 0.0, 4, 6, 128, p, None) == -1  # N % 4
-    assert lib.k2q_gemm_dx(p, p, 4, 96, 128, None, None, 0, p, None) == -1    # N % 64
+    assert lib.k2q_gemm_w8a8(p, p, p, p, None, p, p, 8, 1.0, 4, 4, 128, p, None, 0, None) == -1   # rank 8
+    assert lib.k2q_gemm_w8a8(p, p, p, p, None, None, None, 0, 0.0, 4, 6, 128, p, None, 0, None) == -1  # N % 4
+    assert lib.k2q_gemm_dx(p, p, 4, 96, 128, None, None, 0, p, None, 0, None) == -1    # N % 64
     assert lib.k2q_lora_down(p, 4, 128, 128, p, 200, p, 0, p, None) == -1    # rank > 128
     assert lib.k2q_lora_down(p, 4, 100, 100, p, 16, None, 0, p, None) == -1  # K % 128
     assert lib.k2q_lora_down_ws_bytes(4, 128, 200) == 0                      # no plan for a bad rank
