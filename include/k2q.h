@@ -105,6 +105,24 @@ int k2q_gemm_dx(const uint16_t* dy, const uint16_t* wt, int64_t M, int64_t N, in
                 const float* g, const float* at, int64_t r, uint16_t* dx, void* ws, int64_t ws_bytes,
                 void* stream);
 
+/* fp8-e4m3 weight-only base, the reference's Fp8Linear (quantize.py:23-51).
+ * k2q_quant_weight_fp8 replaces Fp8Linear.__init__ (quantize.py:34-37): s = max(amax_k |w[n,k]|, 1e-8) / 448,
+ * q[n,k] = e4m3(clamp(w / s, +-448)) (round to nearest even), s written as bf16 bits.
+ * k2q_dequant_fp8 replaces `weight_fp8.to(bf16) * scale.to(bf16)` (quantize.py:49): out = bf16(q * s), N x K,
+ * or its transpose (K x N, for the input gradient) when transpose != 0.  K % 64 == 0.
+ * k2q_gemm_bf16 replaces F.linear(x, w, b) (quantize.py:51) plus the LoRA add (lora.py:47-48):
+ * y = bf16(x w^T + bias) + LoRA as in k2q_gemm_w8a8; bf16 MFMA with f32 accumulation.
+ * k2q_gemm_dx_lin: dx = bf16(dy w) + g A (w given transposed, K x N), the autograd of the same. */
+int k2q_quant_weight_fp8(const void* w, int w_dtype, int64_t N, int64_t K, uint8_t* q, uint16_t* s, void* stream);
+int k2q_dequant_fp8(const uint8_t* q, const uint16_t* s, int64_t N, int64_t K, int transpose, uint16_t* out,
+                    void* stream);
+int64_t k2q_gemm_bf16_ws_bytes(int64_t M, int64_t N, int64_t K);
+int k2q_gemm_bf16(const uint16_t* x, const uint16_t* w, const float* bias, const float* u, const float* lora_b,
+                  int64_t r, float lora_scale, int64_t M, int64_t N, int64_t K, uint16_t* y, void* ws,
+                  int64_t ws_bytes, void* stream);
+int k2q_gemm_dx_lin(const uint16_t* dy, const uint16_t* wt, int64_t M, int64_t N, int64_t K, const float* g,
+                    const float* at, int64_t r, uint16_t* dx, void* ws, int64_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

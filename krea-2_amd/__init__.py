@@ -1,7 +1,8 @@
 """krea-2_amd — MI355X (gfx950) ConvRot QuantLinear + LoRA for the Krea 2 DiT.
 
 Drop-in for the reference's quantized-base / LoRA module API (``quantize.py``, ``lora.py``):
-:class:`ConvRotLinear` replaces ``Fp8Linear``, :func:`quantize_dit_convrot` replaces ``quantize_dit_fp8``, and
+:class:`ConvRotLinear` replaces ``Fp8Linear``, :func:`quantize_dit_convrot` replaces ``quantize_dit_fp8``,
+:class:`Fp8Linear` / :func:`quantize_dit_fp8` are the reference's fp8 weight-only base on the same kernels, and
 :mod:`.lora` mirrors the adapter API.  The arithmetic runs in hand-written gfx950 HIP kernels behind the C ABI
 of ``include/k2q.h`` (``libk2q.so``, built by ``build.py``), reached through :mod:`._lib`.
 
@@ -11,8 +12,8 @@ registers it as ``krea2_amd``.
 from . import _lib
 from .lora import (DEFAULT_TARGETS, LoRALinear, inject_lora, load_lora, load_lora_weights, lora_disabled,
                    lora_parameters, lora_scaled, save_lora)
-from .quantize import MODES, ConvRotLinear, quantize_dit_convrot
+from .quantize import MODES, ConvRotLinear, Fp8Linear, quantize_dit_convrot, quantize_dit_fp8
 
-__all__ = ["ConvRotLinear", "quantize_dit_convrot", "MODES", "LoRALinear", "inject_lora", "lora_scaled",
+__all__ = ["ConvRotLinear", "quantize_dit_convrot", "MODES", "Fp8Linear", "quantize_dit_fp8", "LoRALinear", "inject_lora", "lora_scaled",
            "lora_disabled", "lora_parameters", "save_lora", "load_lora_weights", "load_lora", "DEFAULT_TARGETS",
            "_lib"]

@@ -44,6 +44,11 @@ _SIGNATURES = {
     "k2q_gemm_w4a8": ([_p, _p, _p, _p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p], _int),
     "k2q_gemm_w8a8_acc": ([_p, _p, _i64, _i64, _i64, _p, _p, _i64, _p], _int),
     "k2q_gemm_w4a8_f32": ([_p, _p, _p, _i64, _i64, _i64, _p, _p], _int),
+    "k2q_quant_weight_fp8": ([_p, _int, _i64, _i64, _p, _p, _p], _int),
+    "k2q_dequant_fp8": ([_p, _p, _i64, _i64, _int, _p, _p], _int),
+    "k2q_gemm_bf16_ws_bytes": ([_i64, _i64, _i64], _i64),
+    "k2q_gemm_bf16": ([_p, _p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p, _i64, _p], _int),
+    "k2q_gemm_dx_lin": ([_p, _p, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _p], _int),
     "k2q_dx_prep": ([_p, _p, _p, _p, _i64, _i64, _p, _i64, _p, _p, _p], _int),
     "k2q_gemm_dx_ws_bytes": ([_i64, _i64, _i64], _i64),
     "k2q_gemm_dx": ([_p, _p, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _p], _int),
@@ -391,4 +396,103 @@ def gemm_dx(dy, qw, sw, *, w4: bool = False, g=None, lora_a=None, split: bool = 
     ws, nws = _workspace(lib.k2q_gemm_dx_ws_bytes(M, N, K) if split else 0, dev)
     _check(lib.k2q_gemm_dx(_ptr(dy), _ptr(wt), M, N, K, _ptr(g), _ptr(at), r, _ptr(dx), _ptr(ws), nws, st),
            "k2q_gemm_dx")
+    return dx
+
+
+# ----------------------------------------------------------------------------------------------------------
+# fp8-e4m3 weight-only base (the reference's Fp8Linear, quantize.py:23-51)
+# ----------------------------------------------------------------------------------------------------------
+def quant_weight_fp8(w: torch.Tensor):
+    """``Fp8Linear.__init__`` (``quantize.py:34-37``) on the GPU: ``(q float8_e4m3fn (N,K), scale bf16 (N,1))``."""
+    if w.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"w must be bf16 or f32, got {w.dtype}")
+    _need(w, "w", w.dtype, 2)
+    N, K = w.shape
+    _device_check(w.device)
+    q = torch.empty((N, K), dtype=torch.uint8, device=w.device)
+    s = torch.empty((N, 1), dtype=torch.bfloat16, device=w.device)
+    dt = DTYPE_BF16 if w.dtype == torch.bfloat16 else DTYPE_F32
+    _check(load().k2q_quant_weight_fp8(_ptr(w), dt, N, K, _ptr(q), _ptr(s), _stream(w.device)), "k2q_quant_weight_fp8")
+    return q.view(torch.float8_e4m3fn), s
+
+
+def _fp8_operands(q, s):
+    if q.dtype != torch.float8_e4m3fn:
+        raise ValueError(f"fp8 weight must be float8_e4m3fn, got {q.dtype}")
+    _need(q, "weight_fp8", q.dtype, 2)
+    N, K = q.shape
+    if s.dtype != torch.bfloat16 or s.numel() != N or not s.is_contiguous() or s.device != q.device:
+        raise ValueError("scale must be a contiguous bf16 tensor with one value per output row")
+    if K % 64:
+        raise ValueError(f"in_features={K} must be a multiple of 64 for the fp8 base")
+    return N, K
+
+
+def dequant_fp8(q, s, transpose: bool = False) -> torch.Tensor:
+    """``bf16(q * s)`` per element (``quantize.py:49``): (N,K), or (K,N) with ``transpose``."""
+    N, K = _fp8_operands(q, s)
+    if transpose and N % 8:
+        raise ValueError("the transposed dequantization needs out_features % 8 == 0")
+    _device_check(q.device)
+    out = torch.empty((K, N) if transpose else (N, K), dtype=torch.bfloat16, device=q.device)
+    _check(load().k2q_dequant_fp8(_ptr(q), _ptr(s), N, K, int(transpose), _ptr(out), _stream(q.device)),
+           "k2q_dequant_fp8")
+    return out
+
+
+def gemm_bf16(x, w, bias=None, u=None, lora_b=None, lora_scale: float = 1.0, *, split: bool = True) -> torch.Tensor:
+    """``y = bf16(x w^T + bias) + LoRA`` (``quantize.py:51`` + ``lora.py:47-48``); x (M,K), w (N,K) bf16."""
+    _need(x, "x", torch.bfloat16, 2)
+    dev = x.device
+    _need(w, "w", torch.bfloat16, 2, dev)
+    M, K = x.shape
+    N = w.shape[0]
+    if w.shape[1] != K or K % 64 or N % 4:
+        raise ValueError(f"shapes x{tuple(x.shape)} w{tuple(w.shape)}: need matching K % 64 == 0 and N % 4 == 0")
+    r = 0
+    if bias is not None:
+        _need(bias, "bias", torch.float32, 1, dev)
+        if bias.shape[0] != N:
+            raise ValueError("bias length != out_features")
+    if u is not None:
+        _need(u, "u", torch.float32, 2, dev)
+        _need(lora_b, "lora_B", torch.float32, 2, dev)
+        r = u.shape[1]
+        if u.shape[0] != M or lora_b.shape != (N, r):
+            raise ValueError("LoRA shapes do not match")
+        _check_rank(r)
+    _device_check(dev)
+    lib = load()
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    ws, nws = _workspace(lib.k2q_gemm_bf16_ws_bytes(M, N, K) if split else 0, dev)
+    _check(lib.k2q_gemm_bf16(_ptr(x), _ptr(w), _ptr(bias), _ptr(u), _ptr(lora_b), r, float(lora_scale), M, N, K,
+                             _ptr(y), _ptr(ws), nws, _stream(dev)), "k2q_gemm_bf16")
+    return y
+
+
+def gemm_dx_fp8(dy, q, s, *, g=None, lora_a=None, split: bool = True) -> torch.Tensor:
+    """``dx = bf16(dy W_deq) + g lora_A`` for the fp8 base (``W_deq = bf16(q s)``)."""
+    _need(dy, "dy", torch.bfloat16, 2)
+    dev = dy.device
+    N, K = _fp8_operands(q, s)
+    M = dy.shape[0]
+    if dy.shape[1] != N or N % 64:
+        raise ValueError(f"dy has {dy.shape[1]} columns; need out_features = {N} and a multiple of 64")
+    r = 0
+    if g is not None:
+        _need(g, "g", torch.float32, 2, dev)
+        _need(lora_a, "lora_A", torch.float32, 2, dev)
+        r = g.shape[1]
+        if g.shape[0] != M or lora_a.shape != (r, K):
+            raise ValueError("LoRA gradient shapes mismatch")
+        _check_rank(r)
+    _device_check(dev)
+    lib = load()
+    st = _stream(dev)
+    wt = dequant_fp8(q, s, transpose=True)
+    at = lora_a.t().contiguous() if r else None   # (K, r): the LoRA factor rows the epilogue reads per k
+    dx = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+    ws, nws = _workspace(lib.k2q_gemm_dx_ws_bytes(M, N, K) if split else 0, dev)
+    _check(lib.k2q_gemm_dx_lin(_ptr(dy), _ptr(wt), M, N, K, _ptr(g), _ptr(at), r, _ptr(dx), _ptr(ws), nws, st),
+           "k2q_gemm_dx_lin")
     return dx

@@ -20,11 +20,13 @@
 //   EPI_ACC  raw int32 acc (debug entry for bit-exact checks).
 //   EPI_DX   inverse rotation: FWHT over each 128-block of k (a wave's 128 A-rows are one block),
 //            times 2^-7, plus the LoRA term g[m,:] . at[k,:], stored bf16.
+//   EPI_LIN  bf16 x bf16 linear (the fp8 weight-only base, quantize.py:48-51): y = bf16(acc + bias[n]) + LoRA.
+//   EPI_DXLIN its input gradient: dx = bf16(acc) + LoRA, no rotation.
 #include "k2q_common.h"
 
 namespace {
 
-enum { EPI_W8 = 0, EPI_ACC = 1, EPI_DX = 2 };
+enum { EPI_W8 = 0, EPI_ACC = 1, EPI_DX = 2, EPI_LIN = 3, EPI_DXLIN = 4 };
 
 constexpr int BT = 256;     // tile rows (A) and columns (B)
 constexpr int BKB = 128;    // reduction bytes per stage
@@ -363,7 +365,8 @@ enum { MODE_TILE = 0, MODE_PIECE = 1, MODE_FIXUP = 2 };
 // allocation of the tile kernel is not shared with the other paths.
 template <int EPI, int MODE>
 __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_nt_kernel(GemmArgs p) {
-  constexpr bool BF16 = (EPI == EPI_DX);
+  constexpr bool BF16 = (EPI == EPI_DX || EPI == EPI_LIN || EPI == EPI_DXLIN);
+  constexpr bool SCALED = (EPI == EPI_W8 || EPI == EPI_LIN);   // per-row scale / bias epilogue
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // [NSTAGE][A tile | B tile]
 
   const int64_t tiles_a = (p.rows_a + BT - 1) / BT;
@@ -399,12 +402,17 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
   // Epilogue operands of this tile, fetched now so their latency hides under the main loop:
   // thread t < 256 holds s_x of B-row B0+t (times 2^-7), s_w and bias of A-row A0+t.
   float pre_sx = 0.f, pre_sw = 0.f, pre_bi = 0.f;
-  if constexpr (EPI == EPI_W8) {
+  if constexpr (SCALED) {
     const int t = threadIdx.x & (BT - 1);
     const int64_t rb = B0 + t < p.rows_b ? B0 + t : p.rows_b - 1;
     const int64_t ra = A0 + t < p.rows_a ? A0 + t : p.rows_a - 1;
-    pre_sx = p.sx[rb] * 0.0078125f;  // 2^-7: the two unnormalised rotations
-    pre_sw = p.sw[ra];
+    if constexpr (EPI == EPI_W8) {
+      pre_sx = p.sx[rb] * 0.0078125f;  // 2^-7: the two unnormalised rotations
+      pre_sw = p.sw[ra];
+    } else {
+      pre_sx = 1.f;                    // fma(acc, 1, bias) = acc + bias, rounded once
+      pre_sw = 1.f;
+    }
     pre_bi = p.bias ? p.bias[ra] : 0.f;
   }
 
@@ -562,7 +570,7 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     float* s_sx = reinterpret_cast<float*>(smem + SCALE_OFF);
     float* s_sw = s_sx + BT;
     float* s_bi = s_sw + BT;
-    if constexpr (EPI == EPI_W8) {
+    if constexpr (SCALED) {
       if (threadIdx.x < BT) {
         s_sx[threadIdx.x] = pre_sx;
         s_sw[threadIdx.x] = pre_sw;
@@ -572,7 +580,7 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     const bool lora = p.lora_rb != nullptr && p.r > 0;
     lds_barrier();
     uint8_t* ctile = smem;
-    if constexpr (EPI == EPI_W8) {
+    if constexpr (SCALED) {
 #pragma unroll
       for (int ia = 0; ia < 4; ++ia) {
         v4f sw[4], bi[4];
@@ -585,12 +593,16 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
 #pragma unroll
         for (int ib = 0; ib < WB; ++ib) {
           const float sxm = s_sx[64 * wb + 32 * ib + c32];
+          v16f a;   // whole-vector conversions (element-wise bit casts of vector lanes have miscompiled here)
+          if constexpr (BF16)
+            a = __builtin_bit_cast(v16f, acc[ia][ib]);
+          else
+            a = __builtin_convertvector(acc[ia][ib], v16f);
           v16f f;
 #pragma unroll
           for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-              f[4 * j + i] = __builtin_fmaf((float)acc[ia][ib][4 * j + i], sxm * sw[j][i], bi[j][i]);
+            for (int i = 0; i < 4; ++i) f[4 * j + i] = __builtin_fmaf(a[4 * j + i], sxm * sw[j][i], bi[j][i]);
           ctile_put(ctile, 64 * wb + 32 * ib, 128 * wa + 32 * ia, lane, f);
         }
       }
@@ -600,7 +612,7 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
         v16f f[4];
 #pragma unroll
         for (int ia = 0; ia < 4; ++ia) f[ia] = __builtin_bit_cast(v16f, acc[ia][ib]);
-        fwht128_rows(f, h);
+        if constexpr (EPI == EPI_DX) fwht128_rows(f, h);
 #pragma unroll
         for (int ia = 0; ia < 4; ++ia) ctile_put(ctile, 64 * wb + 32 * ib, 128 * wa + 32 * ia, lane, f[ia]);
       }
@@ -1016,6 +1028,46 @@ extern "C" int k2q_gemm_dx(const uint16_t* dy, const uint16_t* wt, int64_t M, in
   p.out = dx; p.ldo = K;
   p.lora_rb = g; p.lora_ra = at; p.r = g ? (int)r : 0; p.lora_scale = 1.f;
   return launch_gemm<EPI_DX>(p, ws, ws_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t k2q_gemm_bf16_ws_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M < 1 || N < 1 || N % 4 || K < 64 || K % 64) return 0;
+  return split_ws_bytes(N, M, 2 * K);
+}
+
+extern "C" int k2q_gemm_bf16(const uint16_t* x, const uint16_t* w, const float* bias, const float* u,
+                             const float* lora_b, int64_t r, float lora_scale, int64_t M, int64_t N, int64_t K,
+                             uint16_t* y, void* ws, int64_t ws_bytes, void* stream) {
+  if (M < 1 || N < 1 || N % 4 || K < 64 || K % 64) return K2Q_EINVAL;
+  if (!x || !w || !y || !k2q_aligned(x, 16) || !k2q_aligned(w, 16) || !k2q_aligned(y, 16)) return K2Q_EINVAL;
+  if (bias && !k2q_aligned(bias, 16)) return K2Q_EINVAL;
+  int rc = check_lora(u, lora_b, r);
+  if (rc) return rc;
+  GemmArgs p{};
+  p.a = reinterpret_cast<const uint8_t*>(w);
+  p.b = reinterpret_cast<const uint8_t*>(x);
+  p.rows_a = N; p.rows_b = M; p.kbytes = 2 * K; p.lda_b = 2 * K; p.ldb_b = 2 * K;
+  p.out = y; p.ldo = N;
+  p.bias = bias;
+  p.lora_rb = u; p.lora_ra = lora_b; p.r = u ? (int)r : 0; p.lora_scale = lora_scale;
+  return launch_gemm<EPI_LIN>(p, ws, ws_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int k2q_gemm_dx_lin(const uint16_t* dy, const uint16_t* wt, int64_t M, int64_t N, int64_t K,
+                               const float* g, const float* at, int64_t r, uint16_t* dx, void* ws, int64_t ws_bytes,
+                               void* stream) {
+  if (M < 1 || K < 64 || K % 64 || N < 64 || N % 64) return K2Q_EINVAL;
+  if (!dy || !wt || !dx || !k2q_aligned(dy, 16) || !k2q_aligned(wt, 16) || !k2q_aligned(dx, 16))
+    return K2Q_EINVAL;
+  int rc = check_lora(g, at, r);
+  if (rc) return rc;
+  GemmArgs p{};
+  p.a = reinterpret_cast<const uint8_t*>(wt);
+  p.b = reinterpret_cast<const uint8_t*>(dy);
+  p.rows_a = K; p.rows_b = M; p.kbytes = 2 * N; p.lda_b = 2 * N; p.ldb_b = 2 * N;
+  p.out = dx; p.ldo = K;
+  p.lora_rb = g; p.lora_ra = at; p.r = g ? (int)r : 0; p.lora_scale = 1.f;
+  return launch_gemm<EPI_DXLIN>(p, ws, ws_bytes, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int k2q_gemm_w4a8(const int8_t* qx, const float* sx, const uint8_t* qw4, const uint16_t* sw4,

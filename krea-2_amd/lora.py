@@ -7,7 +7,8 @@ Mirrors ``lora.py`` of the reference: ``LoRALinear`` (``lora.py:27-48``) with th
 (``:119-123``); ``save_lora`` / ``load_lora_weights`` / ``load_lora`` with the same safetensors keys and
 metadata (``:154-222``).
 
-The one behavioural addition: when ``base`` is a :class:`~.quantize.ConvRotLinear` and the rank fits the fused
+The one behavioural addition: when ``base`` is a :class:`~.quantize.ConvRotLinear` or
+:class:`~.quantize.Fp8Linear` and the rank fits the fused
 kernels (a multiple of 16, at most 128; ``out_features`` a multiple of 128), ``forward`` runs base + LoRA as
 one fused HIP pass (the LoRA down-projection on bf16 MFMA, the up-projection inside the GEMM epilogue) instead
 of three extra GEMMs and three elementwise kernels, and the backward computes the LoRA gradients with the
@@ -22,7 +23,7 @@ import os
 import torch
 import torch.nn as nn
 
-from .quantize import ConvRotLinear
+from .quantize import ConvRotLinear, Fp8Linear
 
 DEFAULT_TARGETS = ("attn.wq", "attn.wk", "attn.wv", "attn.wo", "attn.gate",
                    "mlp.gate", "mlp.up", "mlp.down")
@@ -45,8 +46,8 @@ class LoRALinear(nn.Module):
         nn.init.kaiming_uniform_(self.lora_A, a=math.sqrt(5))
 
     def _fusable(self) -> bool:
-        return (isinstance(self.base, ConvRotLinear) and self.rank % 16 == 0 and self.rank <= 128
-                and self.base.out_features % 128 == 0
+        return (isinstance(self.base, (ConvRotLinear, Fp8Linear)) and self.rank % 16 == 0 and self.rank <= 128
+                and self.base.in_features % 128 == 0 and self.base.out_features % 128 == 0
                 and self.lora_A.dtype == torch.float32 and self.lora_B.dtype == torch.float32)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:

@@ -180,3 +180,109 @@ def quantize_dit_convrot(dit, mode: str = "w8a8") -> int:
     for mod, name, child in targets:
         setattr(mod, name, ConvRotLinear(child, mode))
     return len(targets)
+
+
+# ----------------------------------------------------------------------------------------------------------
+# fp8-e4m3 weight-only base: the reference's own quantized Linear (quantize.py:23-51), on the same kernels
+# ----------------------------------------------------------------------------------------------------------
+class _Fp8LinearFn(torch.autograd.Function):
+    """Forward ``quantize.py:48-51`` (dequantize to bf16, bf16 GEMM with f32 accumulation, bias) with the LoRA
+    term of ``lora.py:47-48`` fused; backward ``dX = dY W_deq + g A``, ``dA = g^T x``, ``dB = s dY^T u``."""
+
+    @staticmethod
+    def forward(ctx, x2, lora_A, lora_B, q, scale, bias, lora_scale):
+        w = _lib.dequant_fp8(q, scale)            # the reference's per-forward bf16 temporary
+        u = _lib.lora_down(x2, lora_A) if lora_A is not None else None
+        y = _lib.gemm_bf16(x2, w, bias, u, lora_B, lora_scale)
+        ctx.lora_scale = lora_scale
+        ctx.save_for_backward(x2 if lora_A is not None else None, u, lora_A, lora_B, q, scale)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, u, A, B, q, scale = ctx.saved_tensors
+        dy = dy.contiguous()
+        if dy.dtype != torch.bfloat16:
+            dy = dy.to(torch.bfloat16)
+        g = dA = dB = None
+        if A is not None:
+            g, dA, dB = _lib.lora_grads(dy, x2 if ctx.needs_input_grad[1] else None,
+                                        u if ctx.needs_input_grad[2] else None, B, ctx.lora_scale)
+        dx = None
+        if ctx.needs_input_grad[0]:
+            dx = _lib.gemm_dx_fp8(dy, q, scale, g=g, lora_a=A if g is not None else None)
+        return dx, dA, dB, None, None, None, None
+
+
+class Fp8Linear(nn.Module):
+    """Frozen ``nn.Linear`` with the weight in fp8 (e4m3) and a per-output-row bf16 scale: the reference's
+    ``Fp8Linear`` (``quantize.py:23-51``) with the same attributes (``weight_fp8``, ``scale``, ``bias``,
+    ``in_features``, ``out_features``, the ``weight`` probe) and the same numerics, run by gfx950 kernels:
+    quantization ``q = e4m3(clamp(W / s, +-448))`` with ``s = max(amax, 1e-8)/448``; forward
+    ``F.linear(x, bf16(q) * bf16(s), bias.bf16)`` on bf16 MFMA with f32 accumulation."""
+
+    is_quant_linear = True
+
+    def __init__(self, lin: nn.Linear):
+        super().__init__()
+        w = lin.weight.data
+        N, K = w.shape
+        if K % 64 or N % 4:
+            raise ValueError(f"Fp8Linear needs in_features % 64 == 0 and out_features % 4 == 0, got {K}, {N}")
+        home = w.device
+        if home.type != "cuda":
+            if not torch.cuda.is_available():
+                raise RuntimeError("Fp8Linear quantizes on the GPU (libk2q, gfx950); no GPU is available")
+            w = w.to("cuda")
+        w = w.contiguous()
+        if w.dtype not in (torch.bfloat16, torch.float32):
+            w = w.float()
+        q, s = _lib.quant_weight_fp8(w)
+        self.weight_fp8 = nn.Parameter(q.to(home), requires_grad=False)
+        self.scale = nn.Parameter(s.to(home), requires_grad=False)
+        self.bias = (nn.Parameter(lin.bias.data.clone(), requires_grad=False)
+                     if lin.bias is not None else None)
+        self.in_features, self.out_features = K, N
+
+    @property
+    def weight(self) -> torch.Tensor:  # device probe for LoRALinear (quantize.py:44-46)
+        return self.weight_fp8
+
+    def extra_repr(self) -> str:
+        return f"in_features={self.in_features}, out_features={self.out_features}, fp8=e4m3, " \
+               f"bias={self.bias is not None}"
+
+    def forward_lora(self, x: torch.Tensor, lora_A: torch.Tensor | None, lora_B: torch.Tensor | None,
+                     lora_scale: float) -> torch.Tensor:
+        if x.shape[-1] != self.in_features:
+            raise ValueError(f"x has {x.shape[-1]} features, layer expects {self.in_features}")
+        if x.dtype != torch.bfloat16:
+            raise NotImplementedError(f"Fp8Linear runs bf16 activations (the DiT dtype); got {x.dtype}")
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, self.in_features)
+        if not x2.is_contiguous() or x2.data_ptr() % 16:
+            x2 = x2.contiguous()
+        if x2.shape[0] == 0:
+            return x.new_empty(*lead, self.out_features)
+        # the reference adds the bias in x.dtype (quantize.py:50): round it to bf16 first
+        b = self.bias.to(torch.bfloat16).float().contiguous() if self.bias is not None else None
+        scale = self.scale.to(torch.bfloat16).contiguous()
+        y = _Fp8LinearFn.apply(x2, lora_A, lora_B, self.weight_fp8, scale, b, float(lora_scale))
+        return y.reshape(*lead, self.out_features)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.forward_lora(x, None, None, 0.0)
+
+
+def quantize_dit_fp8(dit) -> int:
+    """Replace the transformer blocks' ``nn.Linear`` with :class:`Fp8Linear` in place: the walk and return
+    value of the reference's ``quantize_dit_fp8`` (``quantize.py:54-68``).  Call BEFORE ``inject_lora``."""
+    targets = []
+    for block in dit.blocks:
+        for mod in block.modules():
+            for name, child in mod.named_children():
+                if isinstance(child, nn.Linear):
+                    targets.append((mod, name, child))
+    for mod, name, child in targets:
+        setattr(mod, name, Fp8Linear(child))
+    return len(targets)

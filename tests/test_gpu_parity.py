@@ -494,3 +494,121 @@ def test_full_size_cfg3_input_gradient_sampled(k2, dev):
     ref = orc.backward(dy.float().numpy()[rows], np.zeros((16, K)), qw.cpu().numpy(), sw.cpu().numpy(),
                        lora_A=A.numpy(), lora_B=B.numpy(), lora_scale=1.0)
     assert rel_frob(dx.float().cpu().numpy()[rows], ref["dx64"]) < REL_FROB_TOL
+
+
+# ------------------------------------------------------------------------------------------- fp8 base (f3)
+def _fp8_special_rows(K):
+    """Rows whose amax is 448 (scale 1): RNE ties in the normal range (17 -> 16, 1.0625 -> 1, 1.1875 -> 1.25,
+    248 -> 256 with the carry into the exponent), subnormal ties (2.5 * 2^-9 -> 2 * 2^-9, 7.5 * 2^-9 -> the
+    smallest normal), -0, and a zero row (scale floor 1e-8/448)."""
+    v = torch.zeros(3, K)
+    ties = [448.0, 17.0, 1.0625, 1.1875, 248.0, 2.5 * 2 ** -9, 7.5 * 2 ** -9, -0.0, -17.0, 0.5 * 2 ** -9, 300.0]
+    v[0, : len(ties)] = torch.tensor(ties)
+    v[1] = torch.linspace(-448, 448, K)
+    return v                                               # row 2 stays zero
+
+
+@pytest.mark.parametrize("N,K,dtype", [(64, 256, torch.bfloat16), (33, 3072, torch.float32), (8, 12288, torch.bfloat16)])
+def test_fp8_weight_quant_bit_exact(k2, dev, N, K, dtype):
+    """Fp8Linear.__init__ (quantize.py:34-37) on the GPU: e4m3 codes and bf16 scale bits equal torch's CPU
+    computation (the oracle calls the same cast the reference does)."""
+    w = torch.randn(N, K, generator=torch.Generator().manual_seed(N + K)) * 0.02
+    w[:3] = _fp8_special_rows(K)
+    w = w.to(dtype)
+    q, s = k2._lib.quant_weight_fp8(w.to(dev))
+    q0, s0 = orc.fp8_weight_quant(w.float().numpy())
+    assert torch.equal(q.cpu().view(torch.uint8), q0.view(torch.uint8))
+    assert torch.equal(s.cpu().view(torch.int16), s0.view(torch.int16))
+    assert q.cpu().view(torch.uint8)[0, :11].tolist() == [0x7E, 0x58, 0x38, 0x3A, 0x78, 0x02, 0x08, 0x80, 0xD8, 0x00, 0x79]
+
+
+def test_fp8_dequant_exact(k2, dev):
+    """bf16(q * s) per element, as `weight_fp8.to(bf16) * scale.to(bf16)` (quantize.py:49), and transposed."""
+    w = torch.randn(96, 640, generator=torch.Generator().manual_seed(5)) * 0.02
+    w[:3] = _fp8_special_rows(640)
+    q, s = k2._lib.quant_weight_fp8(w.to(dev))
+    ref = q.cpu().to(torch.bfloat16) * s.cpu().to(torch.bfloat16)
+    assert torch.equal(k2._lib.dequant_fp8(q, s).cpu().view(torch.int16), ref.view(torch.int16))
+    assert torch.equal(k2._lib.dequant_fp8(q, s, transpose=True).cpu().view(torch.int16), ref.t().contiguous().view(torch.int16))
+
+
+@pytest.mark.parametrize("M,K,N,bias", [(256, 256, 256, False), (300, 640, 260, True), (1000, 3072, 1024, True)])
+def test_fp8_linear_matches_reference(k2, dev, M, K, N, bias):
+    """The Fp8Linear module against the reference's forward restated on the CPU (dequantize, bf16 F.linear):
+    the same bf16 weights and bias, so only the f32 summation order differs."""
+    lin = torch.nn.Linear(K, N, bias=bias, dtype=torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(make_w(N, K, seed=K))
+        if bias:
+            lin.bias.copy_(torch.randn(N, generator=torch.Generator().manual_seed(2)) * 0.02)
+    base = k2.Fp8Linear(lin.to(dev))
+    x = make_x(M, K, seed=M)
+    with torch.no_grad():
+        y = base(x.to(dev)).float().cpu()
+    q0, s0 = orc.fp8_weight_quant(lin.weight.detach().float().cpu().numpy())
+    ref = orc.fp8_linear(x, q0, s0, None if not bias else lin.bias.detach().cpu()).float()
+    assert rel_frob(y.numpy(), ref.numpy()) < 1e-3
+
+
+def test_fp8_lora_forward_backward(k2, dev):
+    """LoRALinear over the fp8 base (fused path): forward against lora.py:47-48 on the reference forward, and
+    dX, dA, dB against float64 autograd of the same dequantized weights."""
+    M, K, N, r = 192, 512, 384, 32
+    lin = torch.nn.Linear(K, N, bias=True, dtype=torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(make_w(N, K, seed=3))
+        lin.bias.copy_(torch.randn(N, generator=torch.Generator().manual_seed(4)) * 0.02)
+    base = k2.Fp8Linear(lin.to(dev))
+    lora = k2.LoRALinear(base, r, float(r))
+    g = torch.Generator().manual_seed(6)
+    with torch.no_grad():
+        lora.lora_A.copy_(torch.randn(r, K, generator=g) * 0.01)
+        lora.lora_B.copy_(torch.randn(N, r, generator=g) * 0.01)
+    assert lora._fusable()
+    x = make_x(M, K, seed=7)
+    dy = (torch.randn(M, N, generator=g) * 1e-3).to(torch.bfloat16)
+    xd = x.to(dev).requires_grad_(True)
+    y = lora(xd)
+    y.backward(dy.to(dev))
+    q0, s0 = orc.fp8_weight_quant(lin.weight.detach().float().cpu().numpy())
+    A, B = lora.lora_A.detach().cpu(), lora.lora_B.detach().cpu()
+    base_ref = orc.fp8_linear(x, q0, s0, lin.bias.detach().cpu())
+    ref = base_ref + (((x.float() @ A.t()) @ B.t()).to(torch.bfloat16))   # lora.py:47-48, scale 1
+    assert rel_frob(y.detach().float().cpu().numpy(), ref.float().numpy()) < 4e-3
+    wd = (q0.to(torch.bfloat16) * s0.to(torch.bfloat16)).double()
+    x64 = x.double().requires_grad_(True)
+    A64, B64 = A.double().requires_grad_(True), B.double().requires_grad_(True)
+    y64 = x64 @ wd.t() + (x64 @ A64.t()) @ B64.t()
+    y64.backward(dy.double())
+    assert rel_frob(xd.grad.float().cpu().numpy(), x64.grad.numpy()) < REL_FROB_TOL
+    assert rel_frob(lora.lora_A.grad.cpu().numpy(), A64.grad.numpy()) < 1e-3
+    assert rel_frob(lora.lora_B.grad.cpu().numpy(), B64.grad.numpy()) < 1e-3
+
+
+def test_quantize_dit_fp8_walker(k2, dev):
+    """quantize_dit_fp8 (quantize.py:54-68): same walk and count; the blocks then run on the fp8 kernels."""
+    import torch.nn as nn
+
+    class Blk(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.attn = nn.Module()
+            self.attn.wq = nn.Linear(256, 256, bias=False, dtype=torch.bfloat16)
+            self.mlp = nn.Module()
+            self.mlp.up = nn.Linear(256, 512, bias=False, dtype=torch.bfloat16)
+
+    class Dit(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.first = nn.Linear(8, 256, dtype=torch.bfloat16)
+            self.blocks = nn.ModuleList([Blk(), Blk(), Blk()])
+
+    dit = Dit().to(dev)
+    w_up = dit.blocks[0].mlp.up.weight.detach().float().cpu().numpy()
+    assert k2.quantize_dit_fp8(dit) == 6
+    assert isinstance(dit.blocks[0].mlp.up, k2.Fp8Linear) and isinstance(dit.first, nn.Linear)
+    x = make_x(32, 256, seed=1)
+    with torch.no_grad():
+        y = dit.blocks[0].mlp.up(x.to(dev)).float().cpu()
+    q0, s0 = orc.fp8_weight_quant(w_up)
+    assert rel_frob(y.numpy(), orc.fp8_linear(x, q0, s0).float().numpy()) < 1e-3
