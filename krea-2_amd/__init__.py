@@ -12,8 +12,10 @@ registers it as ``krea2_amd``.
 from . import _lib
 from .lora import (DEFAULT_TARGETS, LoRALinear, inject_lora, load_lora, load_lora_weights, lora_disabled,
                    lora_parameters, lora_scaled, save_lora)
+from .checkpoint import load_quantized_base, save_quantized_base
 from .quantize import MODES, ConvRotLinear, Fp8Linear, quantize_dit_convrot, quantize_dit_fp8
 
-__all__ = ["ConvRotLinear", "quantize_dit_convrot", "MODES", "Fp8Linear", "quantize_dit_fp8", "LoRALinear", "inject_lora", "lora_scaled",
+__all__ = ["ConvRotLinear", "quantize_dit_convrot", "MODES", "Fp8Linear", "quantize_dit_fp8", "save_quantized_base",
+           "load_quantized_base", "LoRALinear", "inject_lora", "lora_scaled",
            "lora_disabled", "lora_parameters", "save_lora", "load_lora_weights", "load_lora", "DEFAULT_TARGETS",
            "_lib"]

@@ -244,6 +244,22 @@ class Fp8Linear(nn.Module):
                      if lin.bias is not None else None)
         self.in_features, self.out_features = K, N
 
+    @classmethod
+    def from_quantized(cls, weight_fp8: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None) -> "Fp8Linear":
+        """Wrap already-quantized tensors (e.g. loaded from disk): float8_e4m3fn codes (N,K) and bf16 scales."""
+        if weight_fp8.dtype != torch.float8_e4m3fn or weight_fp8.dim() != 2:
+            raise ValueError("weight_fp8 must be a 2-D float8_e4m3fn tensor")
+        N, K = weight_fp8.shape
+        if scale.dtype != torch.bfloat16 or scale.numel() != N:
+            raise ValueError("scale must hold one bf16 value per output row")
+        m = cls.__new__(cls)
+        nn.Module.__init__(m)
+        m.weight_fp8 = nn.Parameter(weight_fp8, requires_grad=False)
+        m.scale = nn.Parameter(scale.reshape(N, 1), requires_grad=False)
+        m.bias = nn.Parameter(bias, requires_grad=False) if bias is not None else None
+        m.in_features, m.out_features = K, N
+        return m
+
     @property
     def weight(self) -> torch.Tensor:  # device probe for LoRALinear (quantize.py:44-46)
         return self.weight_fp8

@@ -612,3 +612,32 @@ def test_quantize_dit_fp8_walker(k2, dev):
         y = dit.blocks[0].mlp.up(x.to(dev)).float().cpu()
     q0, s0 = orc.fp8_weight_quant(w_up)
     assert rel_frob(y.numpy(), orc.fp8_linear(x, q0, s0).float().numpy()) < 1e-3
+
+
+# ------------------------------------------------------------------------------------------- on-disk base (f4)
+@pytest.mark.parametrize("mode", ["w8a8", "w4a8", "fp8"])
+def test_quantized_base_file_reproduces_outputs(k2, dev, mode, tmp_path):
+    """Quantize on the GPU, save, load into a fresh model (no re-quantization): bit-identical outputs."""
+    import torch.nn as nn
+
+    def make():
+        torch.manual_seed(0)
+        blk = nn.Module()
+        blk.mlp = nn.Module()
+        blk.mlp.up = nn.Linear(256, 512, bias=True, dtype=torch.bfloat16)
+        dit = nn.Module()
+        dit.blocks = nn.ModuleList([blk])
+        return dit.to(dev)
+
+    src = make()
+    if mode == "fp8":
+        k2.quantize_dit_fp8(src)
+    else:
+        k2.quantize_dit_convrot(src, mode)
+    f = str(tmp_path / "q.safetensors")
+    assert k2.save_quantized_base(src, f) == 1
+    dst = make()
+    assert k2.load_quantized_base(dst, f, device=dev) == 1
+    x = make_x(64, 256, seed=2).to(dev)
+    with torch.no_grad():
+        assert torch.equal(src.blocks[0].mlp.up(x).view(torch.int16), dst.blocks[0].mlp.up(x).view(torch.int16))

@@ -193,3 +193,103 @@ def test_walker_requires_gpu_and_says_so(k2):
         pytest.skip("GPU present")
     with pytest.raises(RuntimeError, match="GPU"):
         k2.quantize_dit_convrot(_Dit(), "w8a8")
+
+
+# ------------------------------------------------------------------------------------------- on-disk base
+def _tiny_dit():
+    class Blk(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.attn = nn.Module()
+            self.attn.wq = nn.Linear(256, 128, bias=True, dtype=torch.bfloat16)
+            self.mlp = nn.Module()
+            self.mlp.up = nn.Linear(128, 256, bias=False, dtype=torch.bfloat16)
+
+    class Dit(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.first = nn.Linear(8, 128, dtype=torch.bfloat16)
+            self.blocks = nn.ModuleList([Blk(), Blk()])
+    return Dit()
+
+
+def _fill_quantized(k2, dit, seed=0):
+    """Replace the block Linears with quantized modules built from random stored tensors (no GPU needed)."""
+    g = torch.Generator().manual_seed(seed)
+    kinds = ["w8a8", "w4a8", "fp8", "w8a8"]
+    i = 0
+    for bi, blk in enumerate(dit.blocks):
+        for parent, name in ((blk.attn, "wq"), (blk.mlp, "up")):
+            lin = getattr(parent, name)
+            N, K = lin.out_features, lin.in_features
+            bias = torch.randn(N, generator=g) if lin.bias is not None else None
+            kind = kinds[i % len(kinds)]
+            i += 1
+            if kind == "w8a8":
+                m = k2.ConvRotLinear.from_quantized(torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8),
+                                                    torch.rand(N, generator=g).view(torch.int32), bias, "w8a8")
+            elif kind == "w4a8":
+                m = k2.ConvRotLinear.from_quantized(torch.randint(0, 256, (N, K // 2), generator=g, dtype=torch.uint8),
+                                                    torch.rand(K // 64, N, generator=g).to(torch.bfloat16).view(torch.int16),
+                                                    bias, "w4a8")
+            else:
+                q = torch.randint(0, 256, (N, K), generator=g, dtype=torch.uint8)
+                q[q == 0x7F] = 0
+                q[q == 0xFF] = 0
+                m = k2.Fp8Linear.from_quantized(q.view(torch.float8_e4m3fn),
+                                                torch.rand(N, 1, generator=g).to(torch.bfloat16), bias)
+            setattr(parent, name, m)
+
+
+def _state(dit):
+    return {k: v.view(torch.uint8) if v.dtype == torch.float8_e4m3fn else v for k, v in dit.state_dict().items()}
+
+
+def test_quantized_base_save_load_roundtrip(k2, tmp_path):
+    """Every mode (w8a8, w4a8 packed int4 with group-major scales, fp8) round-trips bit for bit, whether
+    saved before or after inject_lora (the LoRA wrapper's `.base` is not part of the key)."""
+    src = _tiny_dit()
+    _fill_quantized(k2, src)
+    f1 = str(tmp_path / "base.safetensors")
+    assert k2.save_quantized_base(src, f1) == 4
+    k2.inject_lora(src, 16, include_txtfusion=False, include_txtmlp=False)
+    f2 = str(tmp_path / "base_after_lora.safetensors")
+    assert k2.save_quantized_base(src, f2) == 4
+    from safetensors import safe_open
+    with safe_open(f1, framework="pt") as a, safe_open(f2, framework="pt") as b:
+        assert sorted(a.keys()) == sorted(b.keys())
+        assert "blocks.0.attn.wq.qweight" in a.keys() and "blocks.1.attn.wq.weight_fp8" in a.keys()
+        assert a.metadata()["format"] == "krea2-quantized-base" and a.metadata()["modes"] == "fp8,w4a8,w8a8"
+    dst = _tiny_dit()
+    assert k2.load_quantized_base(dst, f1) == 4
+    assert isinstance(dst.first, nn.Linear) and isinstance(dst.blocks[0].mlp.up, k2.ConvRotLinear)
+    ref = _tiny_dit()
+    _fill_quantized(k2, ref)
+    s_ref, s_dst = _state(ref), _state(dst)
+    assert s_ref.keys() == s_dst.keys()
+    for k in s_ref:
+        if k.startswith("blocks"):
+            assert torch.equal(s_ref[k], s_dst[k]), k
+    assert dst.blocks[0].mlp.up.mode == "w4a8" and dst.blocks[0].attn.wq.mode == "w8a8"
+
+
+def test_quantized_base_load_rejects_mismatches(k2, tmp_path):
+    src = _tiny_dit()
+    _fill_quantized(k2, src)
+    f = str(tmp_path / "base.safetensors")
+    k2.save_quantized_base(src, f)
+    wrong = _tiny_dit()
+    wrong.blocks[1].mlp.up = nn.Linear(128, 384, bias=False, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        k2.load_quantized_base(wrong, f)
+    extra = _tiny_dit()
+    extra.blocks.append(extra.blocks[0].__class__())
+    with pytest.raises(KeyError):
+        k2.load_quantized_base(extra, f)
+    from safetensors.torch import save_file
+    g = str(tmp_path / "other.safetensors")
+    save_file({"x": torch.zeros(1)}, g, metadata={"format": "krea2-lora"})
+    with pytest.raises(ValueError):
+        k2.load_quantized_base(_tiny_dit(), g)
+    with pytest.raises(ValueError):
+        k2.save_quantized_base(_tiny_dit(), str(tmp_path / "none.safetensors"))
