@@ -123,6 +123,91 @@ __global__ __launch_bounds__(256) void lora_down_kernel(const uint16_t* __restri
       }
 }
 
+// A-stationary down-projection: workgroup (blockIdx.x, blockIdx.y) = rows [rows_per_wg * blockIdx.x, +rows_per_wg)
+// x K-slice blockIdx.y of LD_NW * 32 * NS columns; wave w keeps the split fragments of its 32*NS columns of A in
+// registers for the whole row range (A is read once per workgroup) and walks the 16-row tiles, the next tile's
+// x fragments in flight while the current one is multiplied.  Per tile the 8 wave partials meet in LDS and
+// are added in wave order (deterministic); out gets u (one slice) or the slice partial [slice][M][16RT].
+constexpr int LD_NW = 8;   // waves per workgroup
+template <int RT>
+struct LdShape {
+  static constexpr int NS = RT <= 4 ? 4 : 2;   // 32-wide k steps per wave
+  static constexpr int SPAN = LD_NW * 32 * NS; // k columns per workgroup
+};
+
+template <int RT>
+__global__ __launch_bounds__(64 * LD_NW) void lora_down_as_kernel(const uint16_t* __restrict__ x, int64_t M,
+                                                                  int64_t ldx, const float* __restrict__ a, int64_t K,
+                                                                  int64_t rows_per_wg, float* __restrict__ out) {
+  constexpr int NS = LdShape<RT>::NS;
+  constexpr int R = 16 * RT;
+  __shared__ float red[2][LD_NW][RT][4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t k0 = (int64_t)blockIdx.y * LdShape<RT>::SPAN + (int64_t)w * 32 * NS;
+  const bool kok = k0 < K;                        // waves past K (a short last slice) contribute 0
+  const int64_t kb = (kok ? k0 : 0) + 8 * (lane >> 4);
+  const int64_t m_beg = (int64_t)blockIdx.x * rows_per_wg;
+  const int64_t m_end = M < m_beg + rows_per_wg ? M : m_beg + rows_per_wg;
+  const int ntiles = (int)((m_end - m_beg + 15) / 16);
+
+  v8bf ah[RT][NS], al[RT][NS];
+#pragma unroll
+  for (int jt = 0; jt < RT; ++jt)
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const float* pa = a + (int64_t)(16 * jt + (lane & 15)) * K + kb + 32 * s;
+      split8(*reinterpret_cast<const v4f*>(pa), *reinterpret_cast<const v4f*>(pa + 4), ah[jt][s], al[jt][s]);
+    }
+
+  auto load_x = [&](v4i (&f)[NS], int t) {
+    int64_t m = m_beg + 16 * (int64_t)t + (lane & 15);
+    m = m < m_end ? m : m_end - 1;
+    const uint16_t* px = x + m * ldx + kb;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) f[s] = *reinterpret_cast<const v4i*>(px + 32 * s);
+  };
+  auto tile = [&](const v4i (&f)[NS], int t) {
+    if (t >= ntiles) return;
+    v4f acc[RT];
+#pragma unroll
+    for (int jt = 0; jt < RT; ++jt) acc[jt] = v4f{0.f, 0.f, 0.f, 0.f};
+    if (kok) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const v8bf xa = __builtin_bit_cast(v8bf, f[s]);
+#pragma unroll
+        for (int jt = 0; jt < RT; ++jt) {
+          acc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, ah[jt][s], acc[jt], 0, 0, 0);
+          acc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, al[jt][s], acc[jt], 0, 0, 0);
+        }
+      }
+    }
+    const int buf = t & 1;
+#pragma unroll
+    for (int jt = 0; jt < RT; ++jt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[buf][w][jt][i][lane] = acc[jt][i];
+    __syncthreads();
+    // C layout (16x16): lane l owns column (rank) l%16 and rows 4*(l/16) + i of rank tile jt.
+    for (int idx = threadIdx.x; idx < 256 * RT; idx += 64 * LD_NW) {
+      const int ln = idx & 63, i = (idx >> 6) & 3, jt = idx >> 8;
+      float v = red[buf][0][jt][i][ln];
+#pragma unroll
+      for (int ww = 1; ww < LD_NW; ++ww) v += red[buf][ww][jt][i][ln];
+      const int64_t m = m_beg + 16 * (int64_t)t + 4 * (ln >> 4) + i;
+      if (m < m_end) out[(int64_t)blockIdx.y * M * R + m * R + 16 * jt + (ln & 15)] = v;
+    }
+  };
+  v4i x0[NS], x1[NS];
+  load_x(x0, 0);
+  for (int t = 0; t < ntiles; t += 2) {
+    load_x(x1, t + 1);
+    tile(x0, t);
+    load_x(x0, t + 2);
+    tile(x1, t + 1);
+  }
+}
+
 // u = sum of the K-slice partials in slice order (deterministic); n4 = M*r/4 float4 elements.
 __global__ __launch_bounds__(256) void lora_reduce_kernel(const v4f* __restrict__ part, int ks, int64_t n4,
                                                           v4f* __restrict__ u) {
@@ -238,10 +323,36 @@ __global__ __launch_bounds__(256) void transpose_f32_kernel(const float* __restr
 
 }  // namespace
 
+// A-stationary plan: K cut into workgroup spans (slices), rows split so that slices x row groups ~ CUs.
+struct AsPlan {
+  int64_t slices, groups, rows;
+};
+
+AsPlan as_plan(int64_t M, int64_t K, int64_t r) {
+  AsPlan p{};
+  const int64_t span = r / 16 <= 4 ? LdShape<1>::SPAN : LdShape<8>::SPAN;
+  p.slices = (K + span - 1) / span;
+  const int64_t cus = k2q_cu_count();
+  int64_t g = cus / p.slices;
+  g = g < 1 ? 1 : g;
+  const int64_t tiles = (M + 15) / 16;
+  g = g > tiles ? tiles : g;
+  p.rows = (tiles + g - 1) / g * 16;
+  p.groups = (M + p.rows - 1) / p.rows;
+  return p;
+}
+
+template <int RT>
+void launch_as(const AsPlan& p, hipStream_t st, const uint16_t* x, int64_t M, int64_t ldx, const float* a, int64_t K,
+               float* out) {
+  hipLaunchKernelGGL(lora_down_as_kernel<RT>, dim3((unsigned)p.groups, (unsigned)p.slices), dim3(64 * LD_NW), 0, st,
+                     x, M, ldx, a, K, p.rows, out);
+}
+
 extern "C" int64_t k2q_lora_down_ws_bytes(int64_t M, int64_t K, int64_t r) {
   if (M < 1 || K < 128 || K % 128 || r < 16 || r > 128 || r % 16) return 0;
-  const LoraPlan p = lora_plan(M, K, r);
-  return p.ks > 1 ? (int64_t)p.ks * M * r * 4 : 0;
+  const AsPlan p = as_plan(M, K, r);
+  return p.slices > 1 ? p.slices * M * r * 4 : 0;
 }
 
 extern "C" int k2q_lora_down(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const float* lora_a,
@@ -251,8 +362,29 @@ extern "C" int k2q_lora_down(const uint16_t* x, int64_t M, int64_t K, int64_t ld
   if (!k2q_aligned(x, 16) || !k2q_aligned(lora_a, 16) || !k2q_aligned(u, 16) || (ws && !k2q_aligned(ws, 16)))
     return K2Q_EINVAL;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const AsPlan q = as_plan(M, K, r);
+  if (q.slices == 1 || (ws && ws_bytes >= q.slices * M * r * 4)) {
+    if (q.groups > 0x7fffffff || q.slices > 0xffff) return K2Q_EUNSUPPORTED;
+    float* out = q.slices > 1 ? static_cast<float*>(ws) : u;
+    switch (r / 16) {
+#define K2Q_AS_CASE(RT) \
+  case RT: launch_as<RT>(q, st, x, M, ldx, lora_a, K, out); break;
+      K2Q_AS_CASE(1) K2Q_AS_CASE(2) K2Q_AS_CASE(3) K2Q_AS_CASE(4)
+      K2Q_AS_CASE(5) K2Q_AS_CASE(6) K2Q_AS_CASE(7) K2Q_AS_CASE(8)
+#undef K2Q_AS_CASE
+      default:
+        return K2Q_EINVAL;
+    }
+    if (q.slices > 1) {
+      const int64_t n4 = M * r / 4;
+      hipLaunchKernelGGL(lora_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st,
+                         static_cast<const v4f*>(ws), (int)q.slices, n4, reinterpret_cast<v4f*>(u));
+    }
+    return k2q_launch_status();
+  }
+  // No room for the slice partials: the row-tiled kernel over the whole of K in one launch.
   LoraPlan p = lora_plan(M, K, r);
-  if (p.ks > 1 && (!ws || ws_bytes < (int64_t)p.ks * M * r * 4)) p.ks = 1;   // no room: one slice
+  p.ks = 1;
   if (p.row_blocks > 0x7fffffff) return K2Q_EUNSUPPORTED;
   const dim3 grid((unsigned)p.row_blocks, (unsigned)p.ks);
   float* out = p.ks > 1 ? static_cast<float*>(ws) : u;
