@@ -9,9 +9,9 @@
 // g is the LoRA down-projection kernel applied to dY with the rank-major factor scale * B^T.  dA and dB
 // reduce over the M tokens: "wgrad" = P^T Q with a small f32 factor P (M x R) and a large bf16 Q (M x C,
 // row-major).  The MFMA needs 8 consecutive m per lane for each column of Q, so Q tiles pass through LDS:
-// stored row-major as loaded (coalesced 512-byte row segments) and gathered column-wise by 16-bit LDS
-// reads.  P goes through a transposing split first (R x M rows of hi and lo).  Each workgroup owns 256
-// columns and one slice of M; the slices' partials are added in slice order by a second kernel
+// copied row-major by LDS-DMA (512-byte row segments) and gathered column-wise by 16-bit LDS reads.  P goes
+// through a transposing split first (R x M rows of hi and lo) and reaches LDS the same way.  Each workgroup
+// owns 256 columns and one slice of M; the slices' partials are added in slice order by a second kernel
 // (deterministic).
 #include "k2q_common.h"
 
@@ -48,58 +48,88 @@ __global__ __launch_bounds__(256) void transpose_kernel(const float* __restrict_
 }
 
 constexpr int WG_KB = 256;              // Q columns per workgroup (64 per wave)
-constexpr int WG_MS = 32;               // m rows per step
-constexpr int QROW = 2 * WG_KB + 8;     // LDS row stride (bytes): the 4 lane groups' 8-row bands sit 16 banks apart
+constexpr int WG_MS = 32;               // m rows per stage
+constexpr int WG_NST = 4;               // LDS ring depth (stages in flight: WG_NST - 1)
+constexpr int WG_QBYTES = WG_MS * 2 * WG_KB;   // 16 KB of Q per stage: 32 rows of 512 B
+constexpr int WG_QG = WG_QBYTES / 1024 / 4;    // Q DMA instructions per wave per stage
+
+// Per stage, P^T arrives as 2 RT blocks of 16 rows x 32 m (1 KB: hi blocks 0 .. RT-1, lo blocks RT ..), one DMA
+// instruction each, dealt PI per wave (padding instructions re-load block 0 into spare blocks).
+template <int RT>
+struct WgShape {
+  static constexpr int PI = (2 * RT + 3) / 4;              // P DMA instructions per wave per stage
+  static constexpr int G = WG_QG + PI;                     // all DMA instructions per wave per stage
+  static constexpr int STAGE = WG_QBYTES + 4 * PI * 1024;  // bytes per ring slot
+};
+
+// Q: the 16-byte chunk c of row r sits at chunk c ^ wg_swz(r), so the four lane groups of a fragment
+// gather (rows 8g + i) hit four different 64-byte bank windows.  P: chunk c of block row jr sits at
+// c ^ ((jr >> 2) & 3), so the 16 rows of a fragment read cover all 64 banks.
+__device__ __forceinline__ int wg_swz(int r) { return ((r >> 3) & 3) << 2; }
+
+template <int N>
+__device__ __forceinline__ void wg_wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 // out (+ slice offset) = scale * P^T Q over the rows [mchunk*blockIdx.y, +mchunk) of M.
-//   pth/ptl: R x Mp bf16 (P^T hi and lo, zero past M); q: M x C bf16, row stride ldq.
+//   pth/ptl: R x Mp bf16 (P^T hi and lo, zero past M, Mp a multiple of 32); q: M x C bf16, row stride ldq.
 //   trans == 0: out[j][c] (R x C); trans == 1: out[c][j] (C x R).  With gridDim.y > 1 the partial of slice
 //   blockIdx.y goes to out + blockIdx.y * R * C in the [j][c] layout, unscaled (wgrad_reduce finishes it).
+// Both operands arrive by LDS-DMA (global_load_lds_dwordx4) through a WG_NST-slot ring, one s_waitcnt and
+// one s_barrier per stage (no __syncthreads: its fence would drain the prefetches).  Q rows past M are read
+// clamped (finite values) and meet the zero padding of P^T, so they add nothing.
 template <int RT>
 __global__ __launch_bounds__(256) void wgrad_kernel(const uint16_t* __restrict__ pth, const uint16_t* __restrict__ ptl,
                                                     int64_t M, int64_t Mp, const uint16_t* __restrict__ q, int64_t C,
                                                     int64_t ldq, int64_t mchunk, float scale, int trans,
                                                     float* __restrict__ out) {
+  using S = WgShape<RT>;
   constexpr int R = 16 * RT;
-  __shared__ __attribute__((aligned(16))) uint8_t qs[2][WG_MS * QROW];
+  __shared__ __attribute__((aligned(16))) uint8_t ring[WG_NST * S::STAGE];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int64_t kb = (int64_t)blockIdx.x * WG_KB;
   const int64_t mb = (int64_t)blockIdx.y * mchunk;
   const int64_t me = M < mb + mchunk ? M : mb + mchunk;
   const int nsteps = (int)((me - mb + WG_MS - 1) / WG_MS);
 
-  // Q tile: thread t holds rows (t/32) + 8i of the step, columns 8(t%32) .. +8 of the workgroup's 256.
-  const int qc = 8 * (t & 31);
-  const bool col_ok = kb + qc < C;
-  const int64_t qcol = col_ok ? kb + qc : C - 8;
-  v4i qr[4];
-  auto load_q = [&](int s) {
+  // Q sources: wave w's instruction i fills stage rows 2(WG_QG w + i) + lane/32, LDS chunk lane%32, which
+  // holds the row's logical chunk (lane%32) ^ wg_swz(row).  Columns past C read the last valid chunk.
+  uint32_t qrow[WG_QG];
+  int64_t qcol[WG_QG];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t m = mb + WG_MS * s + (t >> 5) + 8 * i;
-      const v4i v = *reinterpret_cast<const v4i*>(q + (m < me ? m : me - 1) * ldq + qcol);
-      qr[i] = (m < me && col_ok) ? v : v4i{0, 0, 0, 0};   // rows of other slices / past M contribute 0
-    }
-  };
-  auto store_q = [&](int buf) {
+  for (int i = 0; i < WG_QG; ++i) {
+    const int row = 2 * (WG_QG * w + i) + (lane >> 5);
+    qrow[i] = (uint32_t)row;
+    const int64_t c = kb + 8 * ((lane & 31) ^ wg_swz(row));
+    qcol[i] = c + 8 <= C ? c : C - 8;
+  }
+  // P sources: instruction PI w + i loads block b = PI w + i (block 0 again when b >= 2 RT): lane L -> block
+  // row L/4, LDS chunk L%4, holding logical chunk (L%4) ^ ((row >> 2) & 3) of that row's 32 m.
+  const uint16_t* prow[S::PI];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint8_t* d = qs[buf] + ((t >> 5) + 8 * i) * QROW + 2 * qc;
-      *reinterpret_cast<v2u*>(d) = v2u{(uint32_t)qr[i][0], (uint32_t)qr[i][1]};
-      *reinterpret_cast<v2u*>(d + 8) = v2u{(uint32_t)qr[i][2], (uint32_t)qr[i][3]};
-    }
-  };
-  // P^T fragments: lane l holds row 16 jt + l%16 and m = step base + 8 (l/16) .. +8.
-  v4i ph[RT], pl[RT];
-  auto load_p = [&](int s) {
-    int64_t m = mb + WG_MS * s + 8 * (lane >> 4);
-    m = m < Mp - 8 ? m : Mp - 8;
+  for (int i = 0; i < S::PI; ++i) {
+    const int b = S::PI * w + i < 2 * RT ? S::PI * w + i : 0;
+    const int jr = lane >> 2;
+    const uint16_t* base = b < RT ? pth : ptl;
+    prow[i] = base + (int64_t)(16 * (b % RT) + jr) * Mp + 8 * ((lane & 3) ^ ((jr >> 2) & 3));
+  }
+  auto issue = [&](int st, int slot) {
+    uint8_t* dst = ring + slot * S::STAGE;
 #pragma unroll
-    for (int jt = 0; jt < RT; ++jt) {
-      const int64_t o = (int64_t)(16 * jt + (lane & 15)) * Mp + m;
-      ph[jt] = *reinterpret_cast<const v4i*>(pth + o);
-      pl[jt] = *reinterpret_cast<const v4i*>(ptl + o);
+    for (int i = 0; i < WG_QG; ++i) {
+      int64_t m = mb + (int64_t)WG_MS * st + qrow[i];
+      m = m < M ? m : M - 1;
+      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(q + m * ldq + qcol[i]),
+                                       (__attribute__((address_space(3))) void*)(dst + 1024 * (WG_QG * w + i)), 16,
+                                       0, 0);
     }
+    const int64_t m0 = mb + (int64_t)WG_MS * st;   // < Mp: stages never pass the 32-padded end of P^T
+#pragma unroll
+    for (int i = 0; i < S::PI; ++i)
+      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(prow[i] + m0),
+                                       (__attribute__((address_space(3))) void*)(dst + WG_QBYTES + 1024 * (S::PI * w + i)),
+                                       16, 0, 0);
   };
 
   v4f acc[RT][4];
@@ -108,40 +138,43 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const uint16_t* __restrict__
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) acc[jt][kt] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  load_q(0);
-  store_q(0);
-  load_p(0);
-  __syncthreads();
+  // Past the last stage the DMA re-loads stage nsteps-1 into the freed slot (never one in use), which keeps
+  // the count of outstanding instructions at the wait fixed.
+#pragma unroll
+  for (int st = 0; st < WG_NST - 1; ++st) issue(st < nsteps ? st : nsteps - 1, st);
+  const int jr = lane & 15, g = lane >> 4;
   for (int s = 0; s < nsteps; ++s) {
-    const int buf = s & 1;
-    v4i ch[RT], cl[RT];
+    wg_wait_vmcnt<(WG_NST - 2) * S::G>();
+    asm volatile("s_barrier" ::: "memory");   // stage s landed for every wave; stage s-1's slot is free
+    const int nx = s + WG_NST - 1;
+    issue(nx < nsteps ? nx : nsteps - 1, nx % WG_NST);
+    const uint8_t* stg = ring + (s % WG_NST) * S::STAGE;
+    v8bf ph[RT], pl[RT];
 #pragma unroll
     for (int jt = 0; jt < RT; ++jt) {
-      ch[jt] = ph[jt];
-      cl[jt] = pl[jt];
+      const int off = jr * 64 + 16 * (g ^ ((jr >> 2) & 3));
+      ph[jt] = *reinterpret_cast<const v8bf*>(stg + WG_QBYTES + 1024 * jt + off);
+      pl[jt] = *reinterpret_cast<const v8bf*>(stg + WG_QBYTES + 1024 * (RT + jt) + off);
     }
-    if (s + 1 < nsteps) {
-      load_q(s + 1);
-      load_p(s + 1);
-    }
-    const uint8_t* base = qs[buf] + 8 * (lane >> 4) * QROW;
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
       const int c = 64 * w + 16 * kt + (lane & 15);
       uint32_t e[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) e[i] = *reinterpret_cast<const uint16_t*>(base + i * QROW + 2 * c);
+      for (int i = 0; i < 8; ++i) {
+        const int r = 8 * g + i;
+        e[i] = *reinterpret_cast<const uint16_t*>(stg + r * (2 * WG_KB) + 16 * ((c >> 3) ^ wg_swz(r)) + 2 * (c & 7));
+      }
       const v8bf qf = __builtin_bit_cast(v8bf, v4u{e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16),
                                                    e[6] | (e[7] << 16)});
 #pragma unroll
       for (int jt = 0; jt < RT; ++jt) {
-        acc[jt][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, ch[jt]), qf, acc[jt][kt], 0, 0, 0);
-        acc[jt][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, cl[jt]), qf, acc[jt][kt], 0, 0, 0);
+        acc[jt][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph[jt], qf, acc[jt][kt], 0, 0, 0);
+        acc[jt][kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl[jt], qf, acc[jt][kt], 0, 0, 0);
       }
     }
-    if (s + 1 < nsteps) store_q(buf ^ 1);   // the other buffer: every wave left it at the last barrier
-    __syncthreads();
   }
+  wg_wait_vmcnt<0>();   // no LDS-DMA in flight when the workgroup ends
 
   // C layout (16x16): lane l holds rows j = 4 (l/16) + i and column c = l%16 of tile (jt, kt).
   const bool partial = gridDim.y > 1;
@@ -205,7 +238,7 @@ struct GradLayout {
 
 GradLayout grad_layout(int64_t M, int64_t N, int64_t K, int64_t r) {
   GradLayout L{};
-  L.mp = (M + 7) / 8 * 8;
+  L.mp = (M + 31) / 32 * 32;
   L.pa = wgrad_plan(M, K);
   L.pb = wgrad_plan(M, N);
   int64_t off = 0;
