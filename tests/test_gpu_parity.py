@@ -641,3 +641,39 @@ def test_quantized_base_file_reproduces_outputs(k2, dev, mode, tmp_path):
     x = make_x(64, 256, seed=2).to(dev)
     with torch.no_grad():
         assert torch.equal(src.blocks[0].mlp.up(x).view(torch.int16), dst.blocks[0].mlp.up(x).view(torch.int16))
+
+
+# ------------------------------------------------------------------------------------------- shared input (f1)
+def test_shared_input_quantized_once(k2, dev):
+    """wq/wk/wv/gate of one attention read the same tensor (mmdit.py:199): it is rotated and quantized once,
+    and every output equals the one computed with its own quantization; an in-place write to the input or a
+    different tensor forces a fresh quantization."""
+    import importlib
+    cache = importlib.import_module("krea2_amd.quantize").shared_input_quant
+    layers = [_layers(k2, dev, K=512, N=384, r=16, seed=s)[2] for s in range(4)]
+    x = make_x(96, 512, seed=21).to(dev)
+    with torch.no_grad():
+        m0 = cache.misses
+        ys = [l(x) for l in layers]
+        assert cache.misses == m0 + 1
+        cache.enabled = False
+        try:
+            ref = [l(x) for l in layers]
+        finally:
+            cache.enabled = True
+        for a, b in zip(ys, ref):
+            assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+        m1 = cache.misses
+        x.mul_(2)                                   # in-place write: version bump
+        y2 = layers[0](x)
+        assert cache.misses == m1 + 1
+        cache.enabled = False
+        try:
+            assert torch.equal(y2.view(torch.int16), layers[0](x).view(torch.int16))
+        finally:
+            cache.enabled = True
+        m2 = cache.misses
+        layers[1](x)                                # same tensor, unchanged since: reused
+        assert cache.misses == m2
+        layers[1](x.clone())                        # another tensor with equal values: quantized afresh
+        assert cache.misses == m2 + 1
