@@ -221,7 +221,7 @@ def run_cfg4(k2, steps, dev):
 
 def profile_pass(k2, dev):
     """Fixed launches for rocprofv3 counter passes: cfg2 rotate/quant, LoRA down, GEMM, 3 times each, then a
-    plain 256 MiB device copy (torch's copy kernel) 3 times, the calibration point for FETCH/WRITE_SIZE."""
+    plain 256 MiB device copy (Tensor.copy_) 3 times, the calibration point for FETCH/WRITE_SIZE."""
     L = k2._lib
     c = CONFIGS[2]
     x, W, b, A, B = synth(c["M"], c["K"], c["N"], c["r"], c["bias"])
