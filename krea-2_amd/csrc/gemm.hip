@@ -274,11 +274,15 @@ __device__ __forceinline__ v4i frag64(const uint8_t* s, int row, int chunk) {
 
 // Epilogue LDS use (after the main loop has drained the ring): the bf16 output tile, 256 rows of CROW
 // bytes (256 values + 16 B of padding, which spreads a lane group's 8-byte writes over all banks), then
-// 3 x 256 floats of scales at SCALE_OFF.
+// 3 x 256 floats of scales at SCALE_OFF, then the LoRA factor rows of one 16-rank chunk as bf16 (A-side
+// rows, then B-side rows, LROW bytes each: 48, so the 16 rows read by a lane group start 12 words apart and
+// cover all 64 banks).
 constexpr int CROW = 2 * BT + 16;
 constexpr int SCALE_OFF = BT * CROW;
-constexpr int GEMM_LDS_BYTES =
-    NSTAGE * STAGE_BYTES > SCALE_OFF + 3 * BT * 4 ? NSTAGE * STAGE_BYTES : SCALE_OFF + 3 * BT * 4;
+constexpr int LROW = 48;
+constexpr int LORA_OFF = SCALE_OFF + 3 * BT * 4;
+constexpr int EPI_BYTES = LORA_OFF + 2 * BT * LROW;
+constexpr int GEMM_LDS_BYTES = NSTAGE * STAGE_BYTES > EPI_BYTES ? NSTAGE * STAGE_BYTES : EPI_BYTES;
 static_assert(GEMM_LDS_BYTES <= 160 * 1024, "gfx950 LDS is 160 KB per workgroup");
 
 // One 32 x 32 block of f32 (MFMA C layout) into the LDS tile as bf16: lane l owns tile row mrow0 + l%32
@@ -299,40 +303,6 @@ __device__ __forceinline__ void ctile_add(uint8_t* ct, int mrow0, int ncol0, int
     *reinterpret_cast<v2u*>(row + 16 * j) =
         v2u{pack_bf16x2(bf16_bits_to_f32(o[0] & 0xffffu) + f[4 * j], bf16_bits_to_f32(o[0] >> 16) + f[4 * j + 1]),
             pack_bf16x2(bf16_bits_to_f32(o[1] & 0xffffu) + f[4 * j + 2], bf16_bits_to_f32(o[1] >> 16) + f[4 * j + 3])};
-  }
-}
-
-// The wave's LoRA fragments for ranks c0 .. c0+31 (f32, converted later): la[i][kq] = lora_ra row
-// a0 + 32i + l%32, ranks c0 + 16kq + 8(l/32) .. +7; lb likewise from lora_rb rows b0 + 32i + l%32.
-template <int NB, typename Args>
-__device__ __forceinline__ void load_lora_frags(const Args& p, int64_t a0, int64_t b0, int c0, int lane,
-                                                v4f (&la)[4][2][2], v4f (&lb)[NB][2][2]) {
-  const int h = lane >> 5, c = lane & 31;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    int64_t ra = a0 + 32 * i + c;
-    ra = ra < p.rows_a ? ra : p.rows_a - 1;
-#pragma unroll
-    for (int kq = 0; kq < 2; ++kq) {
-      const int k = c0 + 16 * kq + 8 * h;
-      if (c0 + 16 * kq < p.r) {
-        la[i][kq][0] = *reinterpret_cast<const v4f*>(p.lora_ra + ra * p.r + k);
-        la[i][kq][1] = *reinterpret_cast<const v4f*>(p.lora_ra + ra * p.r + k + 4);
-      }
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < NB; ++i) {
-    int64_t rb = b0 + 32 * i + c;
-    rb = rb < p.rows_b ? rb : p.rows_b - 1;
-#pragma unroll
-    for (int kq = 0; kq < 2; ++kq) {
-      const int k = c0 + 16 * kq + 8 * h;
-      if (c0 + 16 * kq < p.r) {
-        lb[i][kq][0] = *reinterpret_cast<const v4f*>(p.lora_rb + rb * p.r + k);
-        lb[i][kq][1] = *reinterpret_cast<const v4f*>(p.lora_rb + rb * p.r + k + 4);
-      }
-    }
   }
 }
 
@@ -618,28 +588,41 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
       }
     }
     if (lora) {
+      // Per 16-rank chunk the workgroup stages the tile's 256 A-side and 256 B-side factor rows in LDS as
+      // bf16 (B side times lora_scale), each f32 read once: thread t converts 8 ranks of row t/2.
       v16f L[4][WB];
 #pragma unroll
       for (int ia = 0; ia < 4; ++ia)
 #pragma unroll
         for (int ib = 0; ib < WB; ++ib) L[ia][ib] = v16f{0.f};
-      for (int c0 = 0; c0 < p.r; c0 += 32) {
-        v4f la[4][2][2], lb[WB][2][2];
-        load_lora_frags<WB>(p, a0, b0, c0, lane, la, lb);
+      uint8_t* sla = smem + LORA_OFF;
+      uint8_t* slb = sla + BT * LROW;
+      const int srow = threadIdx.x >> 1, shalf = threadIdx.x & 1;
+      int64_t ra = A0 + srow, rb = B0 + srow;
+      ra = ra < p.rows_a ? ra : p.rows_a - 1;
+      rb = rb < p.rows_b ? rb : p.rows_b - 1;
+      const float* pra = p.lora_ra + ra * p.r + 8 * shalf;
+      const float* prb = p.lora_rb + rb * p.r + 8 * shalf;
+      for (int c0 = 0; c0 < p.r; c0 += 16) {
+        *reinterpret_cast<v8bf*>(sla + srow * LROW + 16 * shalf) =
+            f32x8_to_bf16v(*reinterpret_cast<const v4f*>(pra + c0), *reinterpret_cast<const v4f*>(pra + c0 + 4), 1.f);
+        *reinterpret_cast<v8bf*>(slb + srow * LROW + 16 * shalf) =
+            f32x8_to_bf16v(*reinterpret_cast<const v4f*>(prb + c0), *reinterpret_cast<const v4f*>(prb + c0 + 4),
+                           p.lora_scale);
+        lds_barrier();
+        v8bf fa[4], fb[WB];
 #pragma unroll
-        for (int kq = 0; kq < 2; ++kq) {
-          if (c0 + 16 * kq >= p.r) break;
-          v8bf fa[4], fb[WB];
+        for (int i = 0; i < 4; ++i)
+          fa[i] = *reinterpret_cast<const v8bf*>(sla + (128 * wa + 32 * i + c32) * LROW + 16 * h);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) fa[i] = f32x8_to_bf16v(la[i][kq][0], la[i][kq][1], 1.f);
+        for (int i = 0; i < WB; ++i)
+          fb[i] = *reinterpret_cast<const v8bf*>(slb + (64 * wb + 32 * i + c32) * LROW + 16 * h);
 #pragma unroll
-          for (int i = 0; i < WB; ++i) fb[i] = f32x8_to_bf16v(lb[i][kq][0], lb[i][kq][1], p.lora_scale);
+        for (int ia = 0; ia < 4; ++ia)
 #pragma unroll
-          for (int ia = 0; ia < 4; ++ia)
-#pragma unroll
-            for (int ib = 0; ib < WB; ++ib)
-              L[ia][ib] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ia], fb[ib], L[ia][ib], 0, 0, 0);
-        }
+          for (int ib = 0; ib < WB; ++ib)
+            L[ia][ib] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ia], fb[ib], L[ia][ib], 0, 0, 0);
+        lds_barrier();   // every wave has its fragments before the next chunk overwrites them
       }
 #pragma unroll
       for (int ia = 0; ia < 4; ++ia)
