@@ -5,10 +5,12 @@ A step is one QuantLinear+LoRA forward over one batch of synthetic input residen
 The default workload is BASELINE.json configs[2] (M=16384+512, K=3072, N=12288, r=32), the configuration the
 north_star's targets are stated on.  ``value`` is the forward's throughput in TOPS (2*M*N*K per step time).
 Rank 0 prints one JSON line; ``roofline`` covers the dominant kernel (the GEMM, int8-MFMA bound) with its
-average duration measured by HIP events on the stream the kernels run on; ``cpu_baseline`` times the CPU
-oracle (a port of the same arithmetic) on a bounded sample of rows.
+average duration measured by HIP events around it inside the timed steps, on the stream the kernels run
+on; ``cpu_baseline`` times the CPU oracle (a port of the same arithmetic) on a bounded sample of rows.
+Before the W warmup steps, ``--settle`` seconds of untimed steps let the GPU clocks leave their ramp-up
+state (``extra.settle_s`` reports it).
 
-    python bench.py [--steps K] [--warmup W] [--config 2] [--all] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--settle S] [--config 2] [--all] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -63,6 +65,20 @@ def synth(M, K, N, r, bias, seed=0):
     return x, W, b, A, B
 
 
+def settle(fn, seconds):
+    """Runs ``fn`` untimed for ``seconds`` of wall time.  The MI355X's clock governor takes about a second
+    of sustained load to leave its ramp-up state (measured: ~1.5 GHz for the first ~1-1.5 s of a GEMM loop,
+    then ~1.9 GHz at the 1.4 kW board limit), so a timed region that starts on a cold GPU measures the ramp,
+    not the kernels."""
+    if seconds <= 0:
+        return
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(4):
+            fn()
+        torch.cuda.synchronize()
+
+
 def time_loop(fn, iters, warm=3):
     for _ in range(warm):
         fn()
@@ -114,7 +130,7 @@ def cpu_baseline(cfg, x, W, b, A, B, budget_s=12.0, rows=2048):
                       f"({t * 1e3:.0f} ms each) on {cpu_model()}"}
 
 
-def run_config(k2, cfg, steps, warmup, dev):
+def run_config(k2, cfg, steps, warmup, dev, settle_s=0.0):
     L = k2._lib
     M, K, N, r = cfg["M"], cfg["K"], cfg["N"], cfg["r"]
     x, W, b, A, B = synth(M, K, N, r, cfg["bias"])
@@ -128,28 +144,55 @@ def run_config(k2, cfg, steps, warmup, dev):
         gemm = L.gemm_w8a8
     torch.cuda.synchronize()
 
-    def step():
+    def step(ev=None):
+        if ev is not None:
+            ev[0].record()
         qx, sx, _ = L.rotquant(xd)
+        if ev is not None:
+            ev[1].record()
         u = L.lora_down(xd, Ad)
-        return gemm(qx, sx, qw, sw, bd, u, Bd, 1.0)
+        if ev is not None:
+            ev[2].record()
+        y = gemm(qx, sx, qw, sw, bd, u, Bd, 1.0)
+        if ev is not None:
+            ev[3].record()
+        return y
 
+    settle(step, settle_s)
     for _ in range(warmup):
         step()
+    # Timed region: K steps between two events; inside each step, events on the same stream (torch's
+    # current stream, where the kernels run) bracket rotate/quant, the LoRA down-projection and the GEMM,
+    # so the per-kernel averages come from the timed steps themselves.
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    ms_step = time_loop(step, steps, warm=0)
+    s_ev.record()
+    for i in range(steps):
+        step(evs[i])
+    e_ev.record()
+    torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    ms_step = s_ev.elapsed_time(e_ev) / steps
+    ms_rot = sum(ev[0].elapsed_time(ev[1]) for ev in evs) / steps
+    ms_lora = sum(ev[1].elapsed_time(ev[2]) for ev in evs) / steps
+    ms_gemm = sum(ev[2].elapsed_time(ev[3]) for ev in evs) / steps
+    # Rotate/quant as a stream: back to back over 4 distinct inputs (4 x 2MK bytes, beyond the 256 MB
+    # last-level cache for cfg2), so every call reads its input from HBM.  (Inside the step, the interval
+    # before rotate/quant also absorbs the write-back of the previous GEMM's output.)
+    xs = [xd] + [xd.roll(i, 0).contiguous() for i in range(1, 4)]
 
-    # per-kernel averages (events on torch's current stream, which is the stream the kernels run on)
-    qx, sx, _ = L.rotquant(xd)
-    u = L.lora_down(xd, Ad)
-    iters = max(steps, 10)
-    ms_rot = time_loop(lambda: L.rotquant(xd), iters)
-    ms_lora = time_loop(lambda: L.lora_down(xd, Ad), iters)
-    ms_gemm = time_loop(lambda: gemm(qx, sx, qw, sw, bd, u, Bd, 1.0), iters)
+    def rot4():
+        for xi in xs:
+            L.rotquant(xi)
+
+    ms_rot_stream = time_loop(rot4, max(steps // 2, 5)) / len(xs)
+    del xs
     ops = 2.0 * M * N * K
     rot_bytes = 2 * M * K + M * K + 4 * M
-    return dict(ms_step=ms_step, wall=wall, ms_rot=ms_rot, ms_lora=ms_lora, ms_gemm=ms_gemm, ops=ops,
+    return dict(ms_step=ms_step, wall=wall, ms_rot=ms_rot, ms_rot_stream=ms_rot_stream, ms_lora=ms_lora,
+                ms_gemm=ms_gemm, ops=ops,
                 rot_bytes=rot_bytes, tops=ops / (ms_step * 1e-3) / 1e12, x=x, W=W, b=b, A=A, B=B)
 
 
@@ -167,7 +210,7 @@ def make_layer(k2, K, N, r, dev, seed=0, bias=False):
     return layer
 
 
-def run_cfg3(k2, steps, dev):
+def run_cfg3(k2, steps, dev, settle_s=0.0):
     """Forward + backward (dX through the frozen base with the inverse rotation, dA, dB) of one layer."""
     c = CFG3
     layer = make_layer(k2, c["K"], c["N"], c["r"], dev, seed=3)
@@ -181,6 +224,7 @@ def run_cfg3(k2, steps, dev):
         layer.lora_B.grad = None
         layer(x).backward(dy)
 
+    settle(step, settle_s)
     ms = time_loop(step, steps)
     with torch.no_grad():
         ms_fwd = time_loop(lambda: layer(x), steps)
@@ -190,7 +234,7 @@ def run_cfg3(k2, steps, dev):
             "dx_tflops": round(ops_fwd / ((ms - ms_fwd) * 1e-3) / 1e12, 1)}
 
 
-def run_cfg4(k2, steps, dev):
+def run_cfg4(k2, steps, dev, settle_s=0.0):
     """Summed forward time of one double-stream block's quantized linears (image + text stream, plus the
     per-stream adaLN modulation at M=2), each a LoRALinear (r=16) over a W8A8 ConvRot base."""
     total_ops = 0.0
@@ -212,6 +256,7 @@ def run_cfg4(k2, steps, dev):
             layer(xs[(M, K)])
 
     with torch.no_grad():
+        settle(block, settle_s)
         ms = time_loop(block, steps)
         per = {}
         for name, layer, M, K, N in layers:
@@ -255,6 +300,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--settle", type=float, default=2.0,
+                    help="seconds of untimed steps before the warmup steps, so the clocks leave their ramp-up "
+                         "state (0 disables)")
     ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
     ap.add_argument("--all", action="store_true", help="also report configs 0 and 1 (stderr)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -276,22 +324,24 @@ def main():
         profile_pass(k2, dev)
         return
     cfg = CONFIGS[a.config]
-    res = run_config(k2, cfg, a.steps, a.warmup, dev)
+    res = run_config(k2, cfg, a.steps, a.warmup, dev, a.settle)
 
     gemm_tops = res["ops"] / (res["ms_gemm"] * 1e-3) / 1e12
-    rot_gbs = res["rot_bytes"] / (res["ms_rot"] * 1e-3) / 1e9
+    rot_gbs = res["rot_bytes"] / (res["ms_rot_stream"] * 1e-3) / 1e9
     extra = {
         "fwd_tops": round(res["tops"], 1),
         "fwd_pct_int8_peak": round(100 * res["tops"] / INT8_PEAK_TOPS, 2),
         "gemm_ms": round(res["ms_gemm"], 4), "gemm_tops": round(gemm_tops, 1),
         "gemm_pct_int8_peak": round(100 * gemm_tops / INT8_PEAK_TOPS, 2),
-        "rotquant_ms": round(res["ms_rot"], 4), "rotquant_GBps": round(rot_gbs, 1),
+        "rotquant_ms": round(res["ms_rot_stream"], 4), "rotquant_GBps": round(rot_gbs, 1),
+        "rotquant_ms_in_step": round(res["ms_rot"], 4),
         "rotquant_pct_hbm": round(100 * rot_gbs / HBM_PEAK_GBS, 2),
         "lora_down_ms": round(res["ms_lora"], 4),
         "lora_ops": 2.0 * cfg["M"] * cfg["r"] * (cfg["K"] + cfg["N"]),
     }
-    extra["cfg3"] = run_cfg3(k2, max(5, a.steps // 2), dev)
-    extra["cfg4"] = run_cfg4(k2, max(5, a.steps // 2), dev)
+    extra["settle_s"] = a.settle
+    extra["cfg3"] = run_cfg3(k2, max(5, a.steps // 2), dev, a.settle / 2)
+    extra["cfg4"] = run_cfg4(k2, max(5, a.steps // 2), dev, a.settle / 2)
     cpu = None
     if not a.no_cpu:
         cpu = cpu_baseline(cfg, res["x"], res["W"], res["b"], res["A"], res["B"])
@@ -323,10 +373,10 @@ def main():
         for c in (0, 1):
             if c == a.config:
                 continue
-            r2 = run_config(k2, CONFIGS[c], a.steps, a.warmup, dev)
+            r2 = run_config(k2, CONFIGS[c], a.steps, a.warmup, dev, a.settle / 2)
             print(json.dumps({"config": CONFIGS[c]["name"], "ms_step": round(r2["ms_step"], 4),
                               "tops": round(r2["tops"], 1), "gemm_ms": round(r2["ms_gemm"], 4),
-                              "rotquant_ms": round(r2["ms_rot"], 4)}), file=sys.stderr, flush=True)
+                              "rotquant_ms": round(r2["ms_rot_stream"], 4)}), file=sys.stderr, flush=True)
 
 
 if __name__ == "__main__":

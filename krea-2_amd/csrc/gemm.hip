@@ -20,8 +20,9 @@
 //   EPI_ACC  raw int32 acc (debug entry for bit-exact checks).
 //   EPI_DX   inverse rotation: FWHT over each 128-block of k (a wave's 128 A-rows are one block),
 //            times 2^-7, plus the LoRA term g[m,:] . at[k,:], stored bf16.
-//   EPI_LIN  bf16 x bf16 linear (the fp8 weight-only base, quantize.py:48-51): y = bf16(acc + bias[n]) + LoRA.
-//   EPI_DXLIN its input gradient: dx = bf16(acc) + LoRA, no rotation.
+//   EPI_LIN  bf16 x bf16 linear (the fp8 weight-only base, quantize.py:48-51): y = bf16(acc + bias[n] + LoRA).
+//   EPI_DXLIN its input gradient: dx = bf16(acc + LoRA), no rotation.
+// Every bf16 output is rounded once, after the LoRA term is added in f32.
 #include "k2q_common.h"
 
 namespace {
@@ -294,18 +295,6 @@ __device__ __forceinline__ void ctile_put(uint8_t* ct, int mrow0, int ncol0, int
     *reinterpret_cast<v2u*>(row + 16 * j) = v2u{pack_bf16x2(f[4 * j], f[4 * j + 1]), pack_bf16x2(f[4 * j + 2], f[4 * j + 3])};
 }
 
-// Adds f onto the same positions (each lane touches only the values it wrote itself).
-__device__ __forceinline__ void ctile_add(uint8_t* ct, int mrow0, int ncol0, int lane, const v16f& f) {
-  uint8_t* row = ct + (mrow0 + (lane & 31)) * CROW + 2 * (ncol0 + 4 * (lane >> 5));
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const v2u o = *reinterpret_cast<const v2u*>(row + 16 * j);
-    *reinterpret_cast<v2u*>(row + 16 * j) =
-        v2u{pack_bf16x2(bf16_bits_to_f32(o[0] & 0xffffu) + f[4 * j], bf16_bits_to_f32(o[0] >> 16) + f[4 * j + 1]),
-            pack_bf16x2(bf16_bits_to_f32(o[1] & 0xffffu) + f[4 * j + 2], bf16_bits_to_f32(o[1] >> 16) + f[4 * j + 3])};
-  }
-}
-
 __device__ __forceinline__ v8bf f32x8_to_bf16v(v4f a, v4f b, float s) {
   const v4u w = v4u{pack_bf16x2(a[0] * s, a[1] * s), pack_bf16x2(a[2] * s, a[3] * s), pack_bf16x2(b[0] * s, b[1] * s),
                     pack_bf16x2(b[2] * s, b[3] * s)};
@@ -531,11 +520,32 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
       }
     return;
   } else {
-    // Epilogue in three passes over an LDS copy of the output tile (256 rows of CROW bytes, bf16):
-    //   A  dequantize (W8: f32 = 2^-7 s_x s_w acc + bias; DX: inverse FWHT, 2^-7) -> bf16 -> LDS
-    //   B  LoRA: fresh f32 accumulators (the integer ones are dead by now) over bf16 MFMAs, added onto
-    //      the staged values and re-rounded (the reference also adds a bf16 delta to a bf16 base)
-    //   C  coalesced 16-byte stores, 512 contiguous bytes per output row segment.
+    // Epilogue:
+    //   A  dequantize in registers, in place of the accumulators (W8/LIN: f32 = s acc + bias; DX: inverse
+    //      FWHT, 2^-7)
+    //   B  LoRA: bf16 MFMAs accumulate the adapter term straight onto those f32 values (the factor rows
+    //      staged in LDS per 16-rank chunk); base + adapter is rounded to bf16 once
+    //   C  the bf16 tile goes to LDS (256 rows of CROW bytes), then out with coalesced 16-byte stores,
+    //      512 contiguous bytes per output row segment.
+    // This thread's share of the LoRA factor rows for the staging below (A-side row A0 + t/2, B-side row
+    // B0 + t/2, ranks 8 (t&1) .. +8 of each 16-rank chunk): the first chunk is fetched now, so its latency
+    // hides under pass A, and each later chunk while the previous one is multiplied.
+    const bool lora = p.lora_rb != nullptr && p.r > 0;
+    const int srow = threadIdx.x >> 1, shalf = threadIdx.x & 1;
+    const float* pra = nullptr;
+    const float* prb = nullptr;
+    v4f lfa[2], lfb[2];
+    if (lora) {
+      int64_t ra = A0 + srow, rb = B0 + srow;
+      ra = ra < p.rows_a ? ra : p.rows_a - 1;
+      rb = rb < p.rows_b ? rb : p.rows_b - 1;
+      pra = p.lora_ra + ra * p.r + 8 * shalf;
+      prb = p.lora_rb + rb * p.r + 8 * shalf;
+      lfa[0] = *reinterpret_cast<const v4f*>(pra);
+      lfa[1] = *reinterpret_cast<const v4f*>(pra + 4);
+      lfb[0] = *reinterpret_cast<const v4f*>(prb);
+      lfb[1] = *reinterpret_cast<const v4f*>(prb + 4);
+    }
     lds_barrier();   // every wave is done with the LDS ring
     float* s_sx = reinterpret_cast<float*>(smem + SCALE_OFF);
     float* s_sw = s_sx + BT;
@@ -547,7 +557,6 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
         s_bi[threadIdx.x] = pre_bi;
       }
     }
-    const bool lora = p.lora_rb != nullptr && p.r > 0;
     lds_barrier();
     uint8_t* ctile = smem;
     if constexpr (SCALED) {
@@ -573,7 +582,7 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
           for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int i = 0; i < 4; ++i) f[4 * j + i] = __builtin_fmaf(a[4 * j + i], sxm * sw[j][i], bi[j][i]);
-          ctile_put(ctile, 64 * wb + 32 * ib, 128 * wa + 32 * ia, lane, f);
+          acc[ia][ib] = __builtin_bit_cast(v16i, f);   // in place: the f32 tile reuses the accumulators
         }
       }
     } else {  // EPI_DX: one 32-column slice (ib) at a time; the FWHT needs all 4 row slices of it.
@@ -584,31 +593,28 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
         for (int ia = 0; ia < 4; ++ia) f[ia] = __builtin_bit_cast(v16f, acc[ia][ib]);
         if constexpr (EPI == EPI_DX) fwht128_rows(f, h);
 #pragma unroll
-        for (int ia = 0; ia < 4; ++ia) ctile_put(ctile, 64 * wb + 32 * ib, 128 * wa + 32 * ia, lane, f[ia]);
+        for (int ia = 0; ia < 4; ++ia) acc[ia][ib] = __builtin_bit_cast(v16i, f[ia]);
       }
     }
+    // Pin the dequantized tile in registers here: otherwise the compiler sinks pass A's arithmetic past the
+    // LoRA branch (to the stores) and keeps its scale operands live across it, which spills.
+#pragma unroll
+    for (int ia = 0; ia < 4; ++ia)
+#pragma unroll
+      for (int ib = 0; ib < WB; ++ib) asm volatile("" : "+v"(acc[ia][ib]));
     if (lora) {
       // Per 16-rank chunk the workgroup stages the tile's 256 A-side and 256 B-side factor rows in LDS as
       // bf16 (B side times lora_scale), each f32 read once: thread t converts 8 ranks of row t/2.
-      v16f L[4][WB];
-#pragma unroll
-      for (int ia = 0; ia < 4; ++ia)
-#pragma unroll
-        for (int ib = 0; ib < WB; ++ib) L[ia][ib] = v16f{0.f};
       uint8_t* sla = smem + LORA_OFF;
       uint8_t* slb = sla + BT * LROW;
-      const int srow = threadIdx.x >> 1, shalf = threadIdx.x & 1;
-      int64_t ra = A0 + srow, rb = B0 + srow;
-      ra = ra < p.rows_a ? ra : p.rows_a - 1;
-      rb = rb < p.rows_b ? rb : p.rows_b - 1;
-      const float* pra = p.lora_ra + ra * p.r + 8 * shalf;
-      const float* prb = p.lora_rb + rb * p.r + 8 * shalf;
       for (int c0 = 0; c0 < p.r; c0 += 16) {
-        *reinterpret_cast<v8bf*>(sla + srow * LROW + 16 * shalf) =
-            f32x8_to_bf16v(*reinterpret_cast<const v4f*>(pra + c0), *reinterpret_cast<const v4f*>(pra + c0 + 4), 1.f);
-        *reinterpret_cast<v8bf*>(slb + srow * LROW + 16 * shalf) =
-            f32x8_to_bf16v(*reinterpret_cast<const v4f*>(prb + c0), *reinterpret_cast<const v4f*>(prb + c0 + 4),
-                           p.lora_scale);
+        *reinterpret_cast<v8bf*>(sla + srow * LROW + 16 * shalf) = f32x8_to_bf16v(lfa[0], lfa[1], 1.f);
+        *reinterpret_cast<v8bf*>(slb + srow * LROW + 16 * shalf) = f32x8_to_bf16v(lfb[0], lfb[1], p.lora_scale);
+        const int cn = c0 + 16 < p.r ? c0 + 16 : c0;   // next chunk (the last re-reads its own)
+        lfa[0] = *reinterpret_cast<const v4f*>(pra + cn);
+        lfa[1] = *reinterpret_cast<const v4f*>(pra + cn + 4);
+        lfb[0] = *reinterpret_cast<const v4f*>(prb + cn);
+        lfb[1] = *reinterpret_cast<const v4f*>(prb + cn + 4);
         lds_barrier();
         v8bf fa[4], fb[WB];
 #pragma unroll
@@ -621,14 +627,16 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
         for (int ia = 0; ia < 4; ++ia)
 #pragma unroll
           for (int ib = 0; ib < WB; ++ib)
-            L[ia][ib] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ia], fb[ib], L[ia][ib], 0, 0, 0);
+            acc[ia][ib] = __builtin_bit_cast(
+                v16i, __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ia], fb[ib], __builtin_bit_cast(v16f, acc[ia][ib]), 0, 0, 0));
         lds_barrier();   // every wave has its fragments before the next chunk overwrites them
       }
-#pragma unroll
-      for (int ia = 0; ia < 4; ++ia)
-#pragma unroll
-        for (int ib = 0; ib < WB; ++ib) ctile_add(ctile, 64 * wb + 32 * ib, 128 * wa + 32 * ia, lane, L[ia][ib]);
     }
+#pragma unroll
+    for (int ia = 0; ia < 4; ++ia)
+#pragma unroll
+      for (int ib = 0; ib < WB; ++ib)
+        ctile_put(ctile, 64 * wb + 32 * ib, 128 * wa + 32 * ia, lane, __builtin_bit_cast(v16f, acc[ia][ib]));
     lds_barrier();
     // Pass C: wave w stores tile rows 32w .. 32w+31, two rows (2 x 512 B) per instruction.
     uint16_t* out = static_cast<uint16_t*>(p.out);

@@ -6,10 +6,10 @@
 // v_dot4_i32_i8 (exact int32, the same sums as the MFMA path), and reduces across the wave with
 // shuffles (integer adds: exact, order-free).
 //
-// The epilogue is the MFMA kernel's, term for term: f = fma(float(acc), (s_x 2^-7) s_w, bias) rounded
-// to bf16; with LoRA, L = sum_j bf16(B[n,j]) bf16(s u[m,j]) in f32 is added to that bf16 value and the sum
-// rounded again.  Without LoRA both paths give identical bits; with LoRA only L's summation order
-// differs (the MFMA's internal order vs sequential here).
+// The epilogue is the MFMA kernel's, term for term: f = fma(float(acc), (s_x 2^-7) s_w, bias); with LoRA,
+// L = sum_j bf16(B[n,j]) bf16(s u[m,j]) in f32 is added to f; the result is rounded to bf16 once.  Without
+// LoRA both paths give identical bits; with LoRA only L's summation order differs (the MFMA's internal
+// order vs sequential here).
 #include "k2q_common.h"
 
 namespace {
@@ -96,7 +96,6 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_w8_kernel(GemvArgs p) {
   const float sxm = p.sx[m] * 0.0078125f;   // 2^-7: the two unnormalised rotations
   const float bi = p.bias ? p.bias[n] : 0.f;
   float f = __builtin_fmaf((float)a, sxm * p.sw[n], bi);
-  uint32_t out = f32_to_bf16_bits(f);
   if (p.u) {
     const float* ub = p.u + (int64_t)m * p.r;
     const float* bb = p.lora_b + n * p.r;
@@ -109,9 +108,9 @@ __global__ __launch_bounds__(64 * GV_WAVES) void gemv_w8_kernel(GemvArgs p) {
         l = __builtin_fmaf(bf16_bits_to_f32(f32_to_bf16_bits(bv[e])),
                            bf16_bits_to_f32(f32_to_bf16_bits(uv[e] * p.lora_scale)), l);
     }
-    out = f32_to_bf16_bits(bf16_bits_to_f32(out) + l);
+    f += l;
   }
-  p.y[(int64_t)m * p.N + n] = (uint16_t)out;
+  p.y[(int64_t)m * p.N + n] = (uint16_t)f32_to_bf16_bits(f);
 }
 
 template <int MT>
