@@ -244,23 +244,23 @@ def run_cfg4(k2, steps, dev, settle_s=0.0):
             layers.append((f"{sname}.{lname}", make_layer(k2, K, N, 16, dev, seed=K + N + M), M, K, N))
         K, N, Ma = CFG4_ADALN
         layers.append((f"{sname}.adaln", make_layer(k2, K, N, 16, dev, seed=7 + M), Ma, K, N))
+    # One input tensor per linear: in the block each linear reads a different activation, so nothing here
+    # may reuse another linear's quantized input.
     xs = {}
-    for name, layer, M, K, N in layers:
-        key = (M, K)
-        if key not in xs:
-            xs[key] = torch.randn(M, K, generator=torch.Generator().manual_seed(M + K)).to(torch.bfloat16).to(dev)
+    for i, (name, layer, M, K, N) in enumerate(layers):
+        xs[name] = torch.randn(M, K, generator=torch.Generator().manual_seed(M + K + i)).to(torch.bfloat16).to(dev)
         total_ops += 2.0 * M * N * K
 
     def block():
         for name, layer, M, K, N in layers:
-            layer(xs[(M, K)])
+            layer(xs[name])
 
     with torch.no_grad():
         settle(block, settle_s)
         ms = time_loop(block, steps)
         per = {}
         for name, layer, M, K, N in layers:
-            per[name] = round(time_loop(lambda: layer(xs[(M, K)]), max(3, steps // 2)), 4)
+            per[name] = round(time_loop(lambda: layer(xs[name]), max(3, steps // 2)), 4)
     return {"block_linears_ms": round(ms, 4), "tops": round(total_ops / (ms * 1e-3) / 1e12, 1), "per_linear_ms": per}
 
 
@@ -282,6 +282,73 @@ def profile_pass(k2, dev):
         dst.copy_(src)
     torch.cuda.synchronize()
     print("profile pass done", flush=True)
+
+
+def _smi_sample():
+    """(socket power W, GFX clock MHz) from amd-smi, run as a child process; None fields if unavailable."""
+    import re
+    import subprocess
+    try:
+        out = subprocess.run(["amd-smi", "metric", "-p", "-c", "-g", "0"], capture_output=True, text=True,
+                             timeout=5).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None, None
+    p = re.search(r"SOCKET_POWER:\s*(\d+)", out)
+    c = re.search(r"\bCLK:\s*(\d+)\s*MHz", out)
+    return (int(p.group(1)) if p else None), (int(c.group(1)) if c else None)
+
+
+def power_pass(k2, dev, seconds=4.0):
+    """The cfg2 GEMM (this build's kernel, no LoRA) next to hipBLASLt's int8 GEMM (torch._int_mm, int32 out,
+    no epilogue) and torch's bf16 GEMM at the same shape, each run back to back for ``seconds`` while
+    amd-smi samples board power and GFX clock from a child process.  Prints one JSON line."""
+    import threading
+    L = k2._lib
+    c = CONFIGS[2]
+    M, K, N = c["M"], c["K"], c["N"]
+    g = torch.Generator(device=dev).manual_seed(0)
+    qx = torch.randint(-127, 128, (M, K), device=dev, dtype=torch.int8, generator=g)
+    qw = torch.randint(-127, 128, (N, K), device=dev, dtype=torch.int8, generator=g)
+    sx = torch.rand(M, device=dev) + 0.5
+    sw = torch.rand(N, device=dev) * 0.01
+    xb = torch.randn(M, K, device=dev, dtype=torch.bfloat16, generator=g)
+    wb = torch.randn(N, K, device=dev, dtype=torch.bfloat16, generator=g)
+    qwt = qw.t()
+    ops = 2.0 * M * N * K
+    res = {}
+    for name, fn in (("k2q gemm_w8a8 (bf16 out, dequant epilogue)", lambda: L.gemm_w8a8(qx, sx, qw, sw, None)),
+                     ("torch._int_mm / hipBLASLt (int32 out)", lambda: torch._int_mm(qx, qwt)),
+                     ("torch.mm bf16", lambda: torch.mm(xb, wb.t()))):
+        samples, stop = [], threading.Event()
+
+        def sampler():
+            while not stop.is_set():
+                samples.append(_smi_sample())
+                stop.wait(0.25)
+
+        settle(fn, 1.0)
+        th = threading.Thread(target=sampler)
+        th.start()
+        s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n, t_end = 0, time.perf_counter() + seconds
+        s_ev.record()
+        while time.perf_counter() < t_end:
+            for _ in range(10):
+                fn()
+            n += 10
+            torch.cuda.synchronize()
+        e_ev.record()
+        torch.cuda.synchronize()
+        stop.set()
+        th.join()
+        ms = s_ev.elapsed_time(e_ev) / n
+        pw = [p for p, _ in samples[2:] if p]      # the first samples lag the load
+        ck = [ck for _, ck in samples[2:] if ck]
+        res[name] = {"ms": round(ms, 4), "TOPS": round(ops / ms / 1e9, 1),
+                     "power_W_median": sorted(pw)[len(pw) // 2] if pw else None,
+                     "gfx_clock_MHz_median": sorted(ck)[len(ck) // 2] if ck else None, "samples": len(pw)}
+    print(json.dumps({"power_pass": f"cfg2 GEMM shape M={M} K={K} N={N}, {seconds} s each", "results": res}),
+          flush=True)
 
 
 def measured_traffic(kernel_key: str):
@@ -307,6 +374,8 @@ def main():
     ap.add_argument("--all", action="store_true", help="also report configs 0 and 1 (stderr)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--profile-pass", action="store_true", help="fixed launches for rocprofv3 counter runs")
+    ap.add_argument("--power", action="store_true",
+                    help="GEMM vs hipBLASLt int8 vs bf16 at the cfg2 shape with board power / clock samples")
     a = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus > 1 or world > 1:
@@ -322,6 +391,9 @@ def main():
     dev = torch.device("cuda:0")
     if a.profile_pass:
         profile_pass(k2, dev)
+        return
+    if a.power:
+        power_pass(k2, dev)
         return
     cfg = CONFIGS[a.config]
     res = run_config(k2, cfg, a.steps, a.warmup, dev, a.settle)
