@@ -210,6 +210,15 @@ def make_layer(k2, K, N, r, dev, seed=0, bias=False):
     return layer
 
 
+def _no_input_reuse(k2):
+    """Switches off the reuse of the last input's int8 codes (``quantize.shared_input_quant``) while a leg
+    times the same input tensor over and over: in training every step brings a new activation, so each
+    timed call must rotate and quantize its input.  Returns the previous setting."""
+    prev = k2.quantize.shared_input_quant.enabled
+    k2.quantize.shared_input_quant.enabled = False
+    return prev
+
+
 def run_cfg3(k2, steps, dev, settle_s=0.0):
     """Forward + backward (dX through the frozen base with the inverse rotation, dA, dB) of one layer."""
     c = CFG3
@@ -224,10 +233,14 @@ def run_cfg3(k2, steps, dev, settle_s=0.0):
         layer.lora_B.grad = None
         layer(x).backward(dy)
 
-    settle(step, settle_s)
-    ms = time_loop(step, steps)
-    with torch.no_grad():
-        ms_fwd = time_loop(lambda: layer(x), steps)
+    prev = _no_input_reuse(k2)
+    try:
+        settle(step, settle_s)
+        ms = time_loop(step, steps)
+        with torch.no_grad():
+            ms_fwd = time_loop(lambda: layer(x), steps)
+    finally:
+        k2.quantize.shared_input_quant.enabled = prev
     ops_fwd = 2.0 * c["M"] * c["N"] * c["K"]
     return {"step_ms": round(ms, 4), "fwd_ms": round(ms_fwd, 4), "bwd_ms": round(ms - ms_fwd, 4),
             "fwd_tops": round(ops_fwd / (ms_fwd * 1e-3) / 1e12, 1),
@@ -255,12 +268,16 @@ def run_cfg4(k2, steps, dev, settle_s=0.0):
         for name, layer, M, K, N in layers:
             layer(xs[name])
 
-    with torch.no_grad():
-        settle(block, settle_s)
-        ms = time_loop(block, steps)
-        per = {}
-        for name, layer, M, K, N in layers:
-            per[name] = round(time_loop(lambda: layer(xs[name]), max(3, steps // 2)), 4)
+    prev = _no_input_reuse(k2)
+    try:
+        with torch.no_grad():
+            settle(block, settle_s)
+            ms = time_loop(block, steps)
+            per = {}
+            for name, layer, M, K, N in layers:
+                per[name] = round(time_loop(lambda: layer(xs[name]), max(3, steps // 2)), 4)
+    finally:
+        k2.quantize.shared_input_quant.enabled = prev
     return {"block_linears_ms": round(ms, 4), "tops": round(total_ops / (ms * 1e-3) / 1e12, 1), "per_linear_ms": per}
 
 
