@@ -6,13 +6,13 @@
 // so one skeleton serves both: operand "A" supplies the rows of the MFMA output (n, or k for dX),
 // operand "B" its columns (m); out[b_row][a_row] is row-major over (m, n|k).
 //
-// Tiling: 256 x 256 output tile per 256-thread workgroup (4 waves, 2 x 2, 128 x 128 per wave as 4 x 4
-// MFMA 32x32 blocks), 128 bytes of reduction per stage (128 int8 or 64 bf16), LDS double-buffered
-// (2 x 2 x 32 KB).  LDS rows are 128 B; the 16-byte chunk c of row r lives at chunk c ^ f(r) with
-// f(r) = (r & 7) ^ ((r >> 3) & 1), which keeps both the 16-byte stores of the global->LDS copy and the
-// 16-byte MFMA fragment reads free of bank conflicts.  Workgroup ids are remapped so that consecutive
-// tiles land on the same XCD (ids are dealt round-robin over the 8 XCDs), then grouped 8 B-tiles at a
-// time so concurrently running tiles share operand strips in that XCD's L2.
+// Tiling: 256 x 256 output tile per 512-thread workgroup (8 waves, 2 per SIMD; wave w owns 128 A-rows x
+// 64 B-rows as 4 x 2 MFMA 32x32 blocks), 128 bytes of reduction per stage (128 int8 or 64 bf16), LDS
+// double-buffered (2 x 64 KB) and filled by LDS-DMA.  LDS rows are 128 B; the 16-byte chunk c of row r
+// lives at chunk c ^ f(r) with f(r) = (r & 7) ^ ((r >> 3) & 1), which keeps the 16-byte MFMA fragment
+// reads free of bank conflicts.  Workgroup ids are remapped so that consecutive tiles land on the same
+// XCD (ids are dealt round-robin over the 8 XCDs), then grouped 8 B-tiles at a time so concurrently
+// running tiles share operand strips in that XCD's L2.
 //
 // Epilogues (in registers, MFMA C layout: lane l owns output column l%32 and rows 8j+4(l/32)+i):
 //   EPI_W8   y = bf16(2^-7 s_x[m] s_w[n] acc + bias[n] + LoRA), LoRA = one bf16 MFMA per 16 of rank
@@ -224,55 +224,21 @@ __device__ __forceinline__ void fwht128_rows(v16f (&f)[4], int h) {
 
 // ---------------------------------------------------------------------------------------------------------
 // Main-loop data movement: global -> LDS by the gfx950 LDS-DMA path (global_load_lds_dwordx4), no VGPR
-// staging.  The reduction axis is cut in 64-byte stages that rotate through a 5-slot LDS ring.  A stage
-// holds 256 A-rows and 256 B-rows of 64 B (16 KB each); the 16-byte chunk c of LDS row r sits at
-// c ^ swz64(r), conflict-free for the fragment reads.  One DMA wave instruction fills 16 consecutive LDS
-// rows (1 KB: lane l -> row l/4, physical chunk l%4), so each lane fetches the logical chunk
-// (l%4) ^ swz64(row) of its row.  Stages are fetched in pairs, the instruction for rows R of stage s
-// directly followed by the one for the same rows of stage s+1, so the two 64-byte halves of each
-// 128-byte line are requested together.  Measured on MI355X with random data, same box: the cfg2 GEMM
-// 0.628 -> 0.611 ms and the cfg3 input-gradient GEMM 0.342 -> 0.333 ms; in a copy-only loop the pairs
-// cut the time for the same bytes by ~25%, and under the board power limit the fewer cache requests
-// show up as a higher clock.  A stage is consumed after every wave's `s_waitcnt vmcnt` for it plus one
-// s_barrier (raw, without __syncthreads' full memory fence, which would drain the prefetches).
-constexpr int SBK = 64;                   // reduction bytes per stage
-constexpr int NSTAGE = 5;                 // LDS ring depth
-constexpr int STAGE_TILE = BT * SBK;      // 16 KB per operand per stage
-constexpr int STAGE_BYTES = 2 * STAGE_TILE;
-
-__device__ __forceinline__ int swz64(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
-
-struct DmaOffsets {
-  uint32_t o[4];
-};
-
-// Per-lane source offsets (bytes from the tile's first row) of the 4 DMA instructions a wave issues per
-// operand and stage: LDS rows 64*wave + 16*i + lane/4; rows past the matrix end are clamped (never stored).
-__device__ __forceinline__ DmaOffsets dma_offsets(int64_t row0, int64_t nrows, int64_t ld) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  DmaOffsets d;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int lrow = 64 * wave + 16 * i + (lane >> 2);
-    int64_t rr = lrow;
-    rr = row0 + rr < nrows ? rr : nrows - 1 - row0;
-    d.o[i] = (uint32_t)(rr * ld) + 16u * (uint32_t)((lane & 3) ^ swz64(lrow));
-  }
-  return d;
-}
+// staging.  A stage is 128 bytes of the reduction axis for the tile's 256 A-rows and 256 B-rows (32 KB
+// each, the frag()/swz() layout above); two stages alternate in LDS.  One DMA wave instruction fills 8
+// consecutive LDS rows (1 KB: lane l -> row l/8, physical chunk l%8) and each lane fetches the logical
+// chunk (l%8) ^ swz(row) of its row, so every instruction reads 8 whole 128-byte lines.  Measured on
+// MI355X (same box, random data) against 64-byte stages fetched as paired half lines through a 5-slot
+// ring: cfg2 GEMM 643.6 -> 626.6 us, cfg3 input-gradient GEMM 331.5 -> 323.1 us; in a copy-only loop with
+// the same waits and barriers, half lines, paired half lines and whole lines move 24, 31 and 35 B/clk/CU.
+// A stage is consumed after every wave's `s_waitcnt vmcnt` for it plus one s_barrier (raw, without
+// __syncthreads' full memory fence, which would drain the prefetches).
+constexpr int SBK = 64;                   // unit of reduction lengths in the split plan (half a stage)
+constexpr int WBK = 128;                  // reduction bytes per stage
+constexpr int WSTAGE = 2 * BT * WBK;      // one stage of both operands: 64 KB
 
 #define K2Q_GPTR(p) ((__attribute__((address_space(1))) void*)(p))
 #define K2Q_LPTR(p) ((__attribute__((address_space(3))) void*)(p))
-
-__device__ __forceinline__ void dma_tile(const uint8_t* src, const DmaOffsets& d, uint8_t* lds_wave) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    __builtin_amdgcn_global_load_lds(K2Q_GPTR(src + d.o[i]), K2Q_LPTR(lds_wave + 1024 * i), 16, 0, 0);
-}
-
-__device__ __forceinline__ v4i frag64(const uint8_t* s, int row, int chunk) {
-  return *reinterpret_cast<const v4i*>(s + row * SBK + 16 * (chunk ^ swz64(row)));
-}
 
 // Epilogue LDS use (after the main loop has drained the ring): the bf16 output tile, 256 rows of CROW
 // bytes (256 values + 16 B of padding, which spreads a lane group's 8-byte writes over all banks), then
@@ -284,7 +250,7 @@ constexpr int SCALE_OFF = BT * CROW;
 constexpr int LROW = 48;
 constexpr int LORA_OFF = SCALE_OFF + 3 * BT * 4;
 constexpr int EPI_BYTES = LORA_OFF + 2 * BT * LROW;
-constexpr int GEMM_LDS_BYTES = NSTAGE * STAGE_BYTES > EPI_BYTES ? NSTAGE * STAGE_BYTES : EPI_BYTES;
+constexpr int GEMM_LDS_BYTES = 2 * WSTAGE > EPI_BYTES ? 2 * WSTAGE : EPI_BYTES;
 static_assert(GEMM_LDS_BYTES <= 160 * 1024, "gfx950 LDS is 160 KB per workgroup");
 
 // One 32 x 32 block of f32 (MFMA C layout) into the LDS tile as bf16: lane l owns tile row mrow0 + l%32
@@ -312,45 +278,65 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "me
 // Eight waves (two per SIMD) on a 256 x 256 tile: wave w covers A-rows 128*(w&1) .. +128 and B-rows
 // 64*(w>>1) .. +64 (4 x 2 MFMA blocks, 128 accumulator registers), so both waves of a SIMD issue LDS-DMA
 // and MFMAs and each can run while the other waits.
-constexpr int GW = 8;                   // waves per workgroup
+#ifndef K2Q_GW
+#define K2Q_GW 8
+#endif
+constexpr int GW = K2Q_GW;              // waves per workgroup (8: two per SIMD; 4: one per SIMD)
 constexpr int GT = 64 * GW;             // threads per workgroup
-constexpr int WB = 2;                   // 32-wide B blocks per wave
-constexpr int DMA_PER_WAVE = STAGE_TILE / 1024 / GW;   // DMA instructions per wave, operand and stage
+constexpr int WB = 16 / GW;             // 32-wide B blocks per wave
+constexpr int WBR = 32 * WB;            // B-rows per wave
+constexpr int WDMA = BT / 8 / GW;       // DMA instructions per wave, operand and stage (8 rows each)
 
 enum { MODE_TILE = 0, MODE_PIECE = 1, MODE_FIXUP = 2 };
 
-// MODE_TILE: one full-K tile per workgroup (tiles 0 .. gridDim.x-1) and the epilogue.  MODE_PIECE: one
-// piece of a remainder tile, accumulators parked in part.  MODE_FIXUP: the pieces of remainder tile
-// dp_tiles + blockIdx.x added in slice order, then the epilogue.  Separate kernels, so the register
-// allocation of the tile kernel is not shared with the other paths.
+// MODE_TILE: full-K tiles 0 .. dp_tiles-1 with their epilogues; workgroup b takes tiles r * gridDim.x + b'
+// (b' its XCD-remapped id) for rounds r = 0, 1, ... while they exist, so the launch can use fewer
+// workgroups than CUs and give each the same number of tiles.  MODE_PIECE: one piece of a remainder tile,
+// accumulators parked in part.  MODE_FIXUP: the pieces of remainder tile dp_tiles + blockIdx.x added in
+// slice order, then the epilogue.  Separate kernels, so the register allocation of the tile kernel is not
+// shared with the other paths.
 template <int EPI, int MODE>
-__global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_nt_kernel(GemmArgs p) {
+__device__ __forceinline__ void gemm_tile(const GemmArgs& p, int64_t lid, int kbeg, int nk);
+
+template <int EPI, int MODE>
+__global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(GW / 4, GW / 4))) void gemm_nt_kernel(GemmArgs p) {
+  const int64_t nk_full = p.kbytes / SBK;
+  if constexpr (MODE == MODE_FIXUP) {
+    gemm_tile<EPI, MODE>(p, p.dp_tiles + blockIdx.x, 0, (int)nk_full);
+  } else if constexpr (MODE == MODE_PIECE) {   // pieces cover whole stage pairs
+    const int sl = (int)blockIdx.x / p.sk_rem;
+    const int np = (int)(nk_full / 2);
+    const int kbeg = 2 * (sl * np / p.sk_s);
+    gemm_tile<EPI, MODE>(p, p.dp_tiles + (int)blockIdx.x % p.sk_rem, kbeg, 2 * ((sl + 1) * np / p.sk_s) - kbeg);
+  } else {
+    const int64_t me = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    for (int64_t base = 0; base + me < p.dp_tiles; base += gridDim.x) {
+      if (base > 0) lds_barrier();   // every wave is done with the previous tile's LDS
+      gemm_tile<EPI, MODE>(p, base + me, 0, (int)nk_full);
+    }
+  }
+}
+
+// One output tile (linear id lid) over reduction stages kbeg .. kbeg+nk-1, then its epilogue (MODE_TILE,
+// MODE_FIXUP) or its parked accumulators (MODE_PIECE).
+template <int EPI, int MODE>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& p, int64_t lid, int kbeg, int nk) {
   constexpr bool BF16 = (EPI == EPI_DX || EPI == EPI_LIN || EPI == EPI_DXLIN);
   constexpr bool SCALED = (EPI == EPI_W8 || EPI == EPI_LIN);   // per-row scale / bias epilogue
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // [NSTAGE][A tile | B tile]
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // [2][A stage | B stage], then epilogue
+  // The thread index through an empty asm: values derived from it are then computed per tile, not hoisted
+  // out of the tile loop of MODE_TILE (where they would stay live through the main loop and spill).
+  int tid = (int)threadIdx.x;
+  asm volatile("" : "+v"(tid));
 
   const int64_t tiles_a = (p.rows_a + BT - 1) / BT;
   const int64_t tiles_b = (p.rows_b + BT - 1) / BT;
-  int nk = (int)(p.kbytes / SBK);
-  int kbeg = 0;
-  int64_t lid;
-  if constexpr (MODE == MODE_FIXUP) {
-    lid = p.dp_tiles + blockIdx.x;
-  } else if constexpr (MODE == MODE_PIECE) {   // pieces cover whole stage pairs
-    const int sl = (int)blockIdx.x / p.sk_rem;
-    lid = p.dp_tiles + (int)blockIdx.x % p.sk_rem;
-    const int np = nk / 2;
-    kbeg = 2 * (sl * np / p.sk_s);
-    nk = 2 * ((sl + 1) * np / p.sk_s) - kbeg;
-  } else {
-    lid = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-  }
   int64_t ta, tb;
   group_coords(lid, tiles_a, tiles_b, ta, tb);
   const int64_t A0 = ta * BT, B0 = tb * BT;
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int wa = wave & 1, wb = wave >> 1;
   const int h = lane >> 5, c32 = lane & 31;
 
@@ -364,7 +350,7 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
   // thread t < 256 holds s_x of B-row B0+t (times 2^-7), s_w and bias of A-row A0+t.
   float pre_sx = 0.f, pre_sw = 0.f, pre_bi = 0.f;
   if constexpr (SCALED) {
-    const int t = threadIdx.x & (BT - 1);
+    const int t = tid & (BT - 1);
     const int64_t rb = B0 + t < p.rows_b ? B0 + t : p.rows_b - 1;
     const int64_t ra = A0 + t < p.rows_a ? A0 + t : p.rows_a - 1;
     if constexpr (EPI == EPI_W8) {
@@ -377,47 +363,42 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     pre_bi = p.bias ? p.bias[ra] : 0.f;
   }
 
-  uint32_t offa[DMA_PER_WAVE], offb[DMA_PER_WAVE];
+  // Per-lane source offsets (bytes from the tile's first row) of the DMA instructions: LDS rows
+  // 8 (WDMA wave + i) + lane/8; rows past the matrix end are clamped onto its last row (never stored).
+  uint32_t offa[WDMA], offb[WDMA];
 #pragma unroll
-  for (int i = 0; i < DMA_PER_WAVE; ++i) {
-    const int lrow = 16 * (DMA_PER_WAVE * wave + i) + (lane >> 2);
+  for (int i = 0; i < WDMA; ++i) {
+    const int lrow = 8 * (WDMA * wave + i) + (lane >> 3);
     int64_t ra = lrow, rb = lrow;
     ra = A0 + ra < p.rows_a ? ra : p.rows_a - 1 - A0;
     rb = B0 + rb < p.rows_b ? rb : p.rows_b - 1 - B0;
-    const uint32_t ch = 16u * (uint32_t)((lane & 3) ^ swz64(lrow));
+    const uint32_t ch = 16u * (uint32_t)((lane & 7) ^ swz(lrow));
     offa[i] = (uint32_t)(ra * p.lda_b) + ch;
     offb[i] = (uint32_t)(rb * p.ldb_b) + ch;
   }
   const uint8_t* gA = p.a + A0 * p.lda_b + (int64_t)kbeg * SBK;
   const uint8_t* gB = p.b + B0 * p.ldb_b + (int64_t)kbeg * SBK;
-  uint8_t* ldsw = smem + 1024 * DMA_PER_WAVE * wave;   // this wave's DMA rows inside a tile
+  uint8_t* ldsw = smem + 1024 * WDMA * wave;   // this wave's DMA rows inside a stage
 
-  // DMA of reduction stages s0 and s1 = s0 + 1 (or a clamped repeat past the end) into ring slots slot0 and
-  // slot1, the two instructions for the same rows back to back.  The last instruction of stage s0 is
-  // followed by exactly one of stage s1.
-  auto issue_pair = [&](int s0, int slot0, int s1, int slot1) {
-    uint8_t* buf0 = ldsw + slot0 * STAGE_BYTES;
-    uint8_t* buf1 = ldsw + slot1 * STAGE_BYTES;
+  // DMA of stage st (128 reduction bytes) into LDS slot `slot`.
+  auto issue = [&](int st, int slot) {
+    uint8_t* buf = ldsw + slot * WSTAGE;
 #pragma unroll
-    for (int i = 0; i < DMA_PER_WAVE; ++i) {
-      __builtin_amdgcn_global_load_lds(K2Q_GPTR(gA + (int64_t)s0 * SBK + offa[i]), K2Q_LPTR(buf0 + 1024 * i), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(K2Q_GPTR(gA + (int64_t)s1 * SBK + offa[i]), K2Q_LPTR(buf1 + 1024 * i), 16, 0, 0);
-    }
+    for (int i = 0; i < WDMA; ++i)
+      __builtin_amdgcn_global_load_lds(K2Q_GPTR(gA + (int64_t)st * WBK + offa[i]), K2Q_LPTR(buf + 1024 * i), 16, 0, 0);
 #pragma unroll
-    for (int i = 0; i < DMA_PER_WAVE; ++i) {
-      __builtin_amdgcn_global_load_lds(K2Q_GPTR(gB + (int64_t)s0 * SBK + offb[i]),
-                                       K2Q_LPTR(buf0 + STAGE_TILE + 1024 * i), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(K2Q_GPTR(gB + (int64_t)s1 * SBK + offb[i]),
-                                       K2Q_LPTR(buf1 + STAGE_TILE + 1024 * i), 16, 0, 0);
-    }
+    for (int i = 0; i < WDMA; ++i)
+      __builtin_amdgcn_global_load_lds(K2Q_GPTR(gB + (int64_t)st * WBK + offb[i]), K2Q_LPTR(buf + BT * WBK + 1024 * i),
+                                       16, 0, 0);
   };
-  auto read_frags = [&](int st, int kk, v4i (&fa)[4], v4i (&fb)[WB]) {
-    const uint8_t* tA = smem + (st % NSTAGE) * STAGE_BYTES;
-    const uint8_t* tB = tA + STAGE_TILE;
+  // Fragments of substep kk (32 reduction bytes) of the stage in LDS slot `slot`.
+  auto read_frags = [&](int slot, int kk, v4i (&fa)[4], v4i (&fb)[WB]) {
+    const uint8_t* tA = smem + slot * WSTAGE;
+    const uint8_t* tB = tA + BT * WBK;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fa[i] = frag64(tA, 128 * wa + 32 * i + c32, 2 * kk + h);
+    for (int i = 0; i < 4; ++i) fa[i] = frag(tA, 128 * wa + 32 * i + c32, 2 * kk + h);
 #pragma unroll
-    for (int i = 0; i < WB; ++i) fb[i] = frag64(tB, 64 * wb + 32 * i + c32, 2 * kk + h);
+    for (int i = 0; i < WB; ++i) fb[i] = frag(tB, WBR * wb + 32 * i + c32, 2 * kk + h);
   };
   auto mfmas = [&](const v4i (&fa)[4], const v4i (&fb)[WB]) {
 #pragma unroll
@@ -426,25 +407,22 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
       for (int ib = 0; ib < WB; ++ib) mma<BF16>(fa[ia], fb[ib], acc[ia][ib]);
   };
 
-  // Software pipeline, two stages (kt even, kt+1) per iteration, each stage in two halves:
-  //   stage kt, first half    : read stage kt substep-1 fragments | 8 MFMAs on substep 0
-  //   mid-stage kt            : wait for stage kt+1's DMA, s_barrier
-  //   stage kt, second half   : read stage kt+1 substep-0 fragments | 8 MFMAs on substep 1
-  //   stage kt+1, first half  : read stage kt+1 substep-1 fragments | 8 MFMAs on its substep 0
-  //   mid-stage kt+1          : wait for stage kt+2's DMA, s_barrier (the slots of kt-1 and kt are free)
-  //   stage kt+1, second half : DMA the pair kt+4, kt+5 into those slots, read stage kt+2 substep-0
-  //                             fragments | 8 MFMAs on substep 1
-  // so fragments are always in registers before their MFMAs, and each pair is in flight for two stages
-  // before its first wait.  The body has no branches: past the last stage the DMA re-loads stage nk-1
-  // into the freed slots (never one still in use) and the extra fragment reads are discarded, which keeps
-  // the count of outstanding DMA instructions fixed at the waits.  nk is even (every reduction length is
-  // a multiple of 128 bytes).
-  constexpr int G = 2 * DMA_PER_WAVE;   // DMA instructions per wave per stage
+  // Software pipeline, per stage s (slot s & 1) in four substeps of 32 bytes:
+  //   substeps 0-2 : read the next substep's fragments | 8 MFMAs
+  //   end of stage : wait for stage s+1's DMA and for this wave's own fragment reads, s_barrier (every
+  //                  wave is done with slot s & 1), DMA stage s+2 into it
+  //   substep 3    : read stage s+1 substep-0 fragments | 8 MFMAs, the DMA instructions interleaved
+  // so fragments are always in registers before their MFMAs and each stage's DMA is in flight for one
+  // stage before its wait.  The body has no branches: past the last stage the DMA re-loads the last stage
+  // into the freed slot (never one still in use) and the extra fragment reads are discarded, which keeps
+  // the count of outstanding DMA instructions fixed at the waits.  nk counts 64-byte halves and is even
+  // (every reduction length is a multiple of 128 bytes).
+  constexpr int G = 2 * WDMA;   // DMA instructions per wave per stage
   // Accumulator storage of a piece in part: 16-byte unit ((ia * WB + ib) * 4 + q) of thread t at byte
   // 8 KB * unit + 16 t, so each wave instruction moves 1 KB of consecutive bytes.  The per-unit base is
   // workgroup-uniform (scalar registers) and the thread offset a 32-bit vector register.
   constexpr int64_t PIECE_BYTES = (int64_t)BT * BT * 4;
-  const uint32_t toff = 16u * threadIdx.x;
+  const uint32_t toff = 16u * tid;
   if constexpr (MODE == MODE_FIXUP) {
     for (int sl = 0; sl < p.sk_s; ++sl) {
       const uint8_t* pc = reinterpret_cast<const uint8_t*>(p.part) + ((int64_t)sl * p.sk_rem + blockIdx.x) * PIECE_BYTES;
@@ -468,9 +446,9 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     }
   } else {
     v4i f0a[4], f0b[WB], f1a[4], f1b[WB];
-    auto clampk = [&](int s) { return s < nk ? s : nk - 1; };
-    // MFMAs of one half-stage interleaved with the next fragment reads.
-    auto half = [&](const v4i (&fa)[4], const v4i (&fb)[WB]) {
+    const int ns = nk / 2;   // stages
+    // MFMAs of one substep interleaved with the next substep's fragment reads.
+    auto sub = [&](const v4i (&fa)[4], const v4i (&fb)[WB]) {
       mfmas(fa, fb);
 #pragma unroll
       for (int i = 0; i < 4 + WB; ++i) {
@@ -479,38 +457,33 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
       }
       __builtin_amdgcn_sched_group_barrier(0x008, 4 * WB - (4 + WB), 0);
     };
-    issue_pair(0, 0, clampk(1), 1);
-    issue_pair(clampk(2), 2, clampk(3), 3);
-    wait_vmcnt<2 * G + 1>();   // stage 0 (one instruction of stage 1 and the second pair may be in flight)
+    issue(0, 0);
+    issue(ns > 1 ? 1 : 0, 1);
+    wait_vmcnt<G>();           // stage 0 (stage 1 may be in flight)
     lds_barrier();
     read_frags(0, 0, f0a, f0b);
-    int slot = 0;              // ring slot of stage kt
-    for (int kt = 0; kt < nk; kt += 2) {
-      read_frags(kt, 1, f1a, f1b);
-      half(f0a, f0b);
-      wait_vmcnt<2 * G>();     // stage kt+1 (the pair kt+2, kt+3 may be in flight)
+    for (int st = 0; st < ns; ++st) {
+      const int sl = st & 1;
+      read_frags(sl, 1, f1a, f1b);
+      sub(f0a, f0b);
+      read_frags(sl, 2, f0a, f0b);
+      sub(f1a, f1b);
+      read_frags(sl, 3, f1a, f1b);
+      sub(f0a, f0b);
+      wait_vmcnt<0>();                                      // stage st+1
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this wave's reads of slot sl have landed
       lds_barrier();
-      read_frags(kt + 1, 0, f0a, f0b);
-      half(f1a, f1b);
-      read_frags(kt + 1, 1, f1a, f1b);
-      half(f0a, f0b);
-      wait_vmcnt<1>();         // stage kt+2 (one instruction of kt+3 may be in flight)
-      lds_barrier();
-      const int s4 = slot == 0 ? NSTAGE - 1 : slot - 1;   // slot of kt-1 = slot of kt+4
-      issue_pair(clampk(kt + 4), s4, clampk(kt + 5), slot);
-      slot = slot + 2 >= NSTAGE ? slot + 2 - NSTAGE : slot + 2;
-      read_frags(kt + 2, 0, f0a, f0b);
+      issue(st + 2 < ns ? st + 2 : ns - 1, sl);
+      read_frags(sl ^ 1, 0, f0a, f0b);
       mfmas(f1a, f1b);
 #pragma unroll
-      for (int i = 0; i < 2 * G; ++i) {
+      for (int i = 0; i < G; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
         __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM (LDS-DMA)
       }
 #pragma unroll
-      for (int i = 0; i < 4 + WB; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-      }
-      if constexpr (4 * WB > 2 * G) __builtin_amdgcn_sched_group_barrier(0x008, 4 * WB - 2 * G, 0);
+      for (int i = 0; i < 4 + WB; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      if constexpr (4 * WB > G) __builtin_amdgcn_sched_group_barrier(0x008, 4 * WB - G, 0);
     }
     wait_vmcnt<0>();   // no LDS-DMA may still be in flight when the workgroup's LDS is released
   }
@@ -528,7 +501,7 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
   }
 
   const int64_t a0 = A0 + 128 * wa;   // first A-row of this wave
-  const int64_t b0 = B0 + 64 * wb;    // first B-row of this wave
+  const int64_t b0 = B0 + WBR * wb;   // first B-row of this wave
 
   if constexpr (EPI == EPI_ACC) {
     int32_t* out = static_cast<int32_t*>(p.out);
@@ -560,7 +533,7 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     // B0 + t/2, ranks 8 (t&1) .. +8 of each 16-rank chunk): the first chunk is fetched now, so its latency
     // hides under pass A, and each later chunk while the previous one is multiplied.
     const bool lora = p.lora_rb != nullptr && p.r > 0;
-    const int srow = threadIdx.x >> 1, shalf = threadIdx.x & 1;
+    const int srow = tid >> 1, shalf = tid & 1;
     const float* pra = nullptr;
     const float* prb = nullptr;
     v4f lfa[2], lfb[2];
@@ -580,10 +553,10 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     float* s_sw = s_sx + BT;
     float* s_bi = s_sw + BT;
     if constexpr (SCALED) {
-      if (threadIdx.x < BT) {
-        s_sx[threadIdx.x] = pre_sx;
-        s_sw[threadIdx.x] = pre_sw;
-        s_bi[threadIdx.x] = pre_bi;
+      if (tid < BT) {
+        s_sx[tid] = pre_sx;
+        s_sw[tid] = pre_sw;
+        s_bi[tid] = pre_bi;
       }
     }
     lds_barrier();
@@ -600,7 +573,7 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
         }
 #pragma unroll
         for (int ib = 0; ib < WB; ++ib) {
-          const float sxm = s_sx[64 * wb + 32 * ib + c32];
+          const float sxm = s_sx[WBR * wb + 32 * ib + c32];
           v16f a;   // whole-vector conversions (element-wise bit casts of vector lanes have miscompiled here)
           if constexpr (BF16)
             a = __builtin_bit_cast(v16f, acc[ia][ib]);
@@ -651,7 +624,7 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
           fa[i] = *reinterpret_cast<const v8bf*>(sla + (128 * wa + 32 * i + c32) * LROW + 16 * h);
 #pragma unroll
         for (int i = 0; i < WB; ++i)
-          fb[i] = *reinterpret_cast<const v8bf*>(slb + (64 * wb + 32 * i + c32) * LROW + 16 * h);
+          fb[i] = *reinterpret_cast<const v8bf*>(slb + (WBR * wb + 32 * i + c32) * LROW + 16 * h);
 #pragma unroll
         for (int ia = 0; ia < 4; ++ia)
 #pragma unroll
@@ -665,7 +638,7 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) v
     for (int ia = 0; ia < 4; ++ia)
 #pragma unroll
       for (int ib = 0; ib < WB; ++ib)
-        ctile_put(ctile, 64 * wb + 32 * ib, 128 * wa + 32 * ia, lane, __builtin_bit_cast(v16f, acc[ia][ib]));
+        ctile_put(ctile, WBR * wb + 32 * ib, 128 * wa + 32 * ia, lane, __builtin_bit_cast(v16f, acc[ia][ib]));
     lds_barrier();
     // Pass C: wave w stores tile rows 32w .. 32w+31, two rows (2 x 512 B) per instruction.
     uint16_t* out = static_cast<uint16_t*>(p.out);
@@ -963,8 +936,15 @@ int launch_gemm(GemmArgs p, void* ws, int64_t ws_bytes, hipStream_t st) {
   // Pieces first: they fill the GPU for a short round, then the full tiles, then the fixup.
   if (q.s > 1)
     hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_PIECE>), dim3((unsigned)(q.rem * q.s)), dim3(GT), lds, st, p);
-  if (q.dp_tiles > 0)
-    hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_TILE>), dim3((unsigned)q.dp_tiles), dim3(GT), lds, st, p);
+  if (q.dp_tiles > 0) {
+    // Balanced grid: as many rounds as the tiles need on this GPU's CUs, and just enough workgroups for
+    // that many rounds, each taking the same number of tiles (3168 tiles on 256 CUs: 244 workgroups of
+    // 13), instead of a last round that leaves most CUs idle.
+    const int cus = k2q_cu_count();
+    const int64_t rounds = (q.dp_tiles + cus - 1) / cus;
+    const int64_t nwg = (q.dp_tiles + rounds - 1) / rounds;
+    hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_TILE>), dim3((unsigned)nwg), dim3(GT), lds, st, p);
+  }
   if (q.s > 1) hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_FIXUP>), dim3((unsigned)q.rem), dim3(GT), lds, st, p);
   return k2q_launch_status();
 }
