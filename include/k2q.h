@@ -93,16 +93,15 @@ int k2q_gemm_w4a8_f32(const int8_t* qx, const uint8_t* qw4, const uint16_t* sw4,
 
 /* (4) Input gradient through the frozen base (autograd of quantize.py:51 + lora.py:47-48):
  *   dx = bf16(2^-7 (dy W_hat) R + g A),   W_hat[n,k] = s_w[n] q[n,k] (or s_w4[n,k/64] q4[n,k]).
- * k2q_dx_prep writes wt = bf16(W_hat)^T (K x N) and at = A^T (K x r, f32) into caller workspaces;
- * k2q_gemm_dx then runs the bf16 MFMA GEMM with the inverse rotation and the LoRA term fused.
- * g = lora_scale * dy @ lora_b (M x r f32) is supplied by the caller; g/at nullable.  ws: as for
- * k2q_gemm_w8a8 (f32 pieces, added in a fixed order), k2q_gemm_dx_ws_bytes(M, N, K) bytes. */
+ * k2q_dx_prep writes wt = bf16(W_hat)^T (K x N) into a caller workspace; k2q_gemm_dx then runs the
+ * bf16 MFMA GEMM with the inverse rotation and the LoRA term fused.  g = lora_scale * dy @ lora_b
+ * (M x r f32) is supplied by the caller, lora_a is the module's A (r x K f32, lora.py:39); both nullable.
+ * ws: as for k2q_gemm_w8a8 (f32 pieces, added in a fixed order), k2q_gemm_dx_ws_bytes(M, N, K) bytes. */
 int k2q_dx_prep(const int8_t* qw, const float* sw, const uint8_t* qw4, const uint16_t* sw4,
-                int64_t N, int64_t K, const float* lora_a, int64_t r,
-                uint16_t* wt, float* at, void* stream);
+                int64_t N, int64_t K, uint16_t* wt, void* stream);
 int64_t k2q_gemm_dx_ws_bytes(int64_t M, int64_t N, int64_t K);
 int k2q_gemm_dx(const uint16_t* dy, const uint16_t* wt, int64_t M, int64_t N, int64_t K,
-                const float* g, const float* at, int64_t r, uint16_t* dx, void* ws, int64_t ws_bytes,
+                const float* g, const float* lora_a, int64_t r, uint16_t* dx, void* ws, int64_t ws_bytes,
                 void* stream);
 
 /* fp8-e4m3 weight-only base, the reference's Fp8Linear (quantize.py:23-51).
@@ -111,8 +110,9 @@ int k2q_gemm_dx(const uint16_t* dy, const uint16_t* wt, int64_t M, int64_t N, in
  * k2q_dequant_fp8 replaces `weight_fp8.to(bf16) * scale.to(bf16)` (quantize.py:49): out = bf16(q * s), N x K,
  * or its transpose (K x N, for the input gradient) when transpose != 0.  K % 64 == 0.
  * k2q_gemm_bf16 replaces F.linear(x, w, b) (quantize.py:51) plus the LoRA add (lora.py:47-48):
- * y = bf16(x w^T + bias) + LoRA as in k2q_gemm_w8a8; bf16 MFMA with f32 accumulation.
- * k2q_gemm_dx_lin: dx = bf16(dy w) + g A (w given transposed, K x N), the autograd of the same. */
+ * y = bf16(x w^T + bias + LoRA), LoRA as in k2q_gemm_w8a8; bf16 MFMA with f32 accumulation.
+ * k2q_gemm_dx_lin: dx = bf16(dy w + g A) (w given transposed, K x N; lora_a = A, r x K), the autograd of
+ * the same. */
 int k2q_quant_weight_fp8(const void* w, int w_dtype, int64_t N, int64_t K, uint8_t* q, uint16_t* s, void* stream);
 int k2q_dequant_fp8(const uint8_t* q, const uint16_t* s, int64_t N, int64_t K, int transpose, uint16_t* out,
                     void* stream);
@@ -121,7 +121,7 @@ int k2q_gemm_bf16(const uint16_t* x, const uint16_t* w, const float* bias, const
                   int64_t r, float lora_scale, int64_t M, int64_t N, int64_t K, uint16_t* y, void* ws,
                   int64_t ws_bytes, void* stream);
 int k2q_gemm_dx_lin(const uint16_t* dy, const uint16_t* wt, int64_t M, int64_t N, int64_t K, const float* g,
-                    const float* at, int64_t r, uint16_t* dx, void* ws, int64_t ws_bytes, void* stream);
+                    const float* lora_a, int64_t r, uint16_t* dx, void* ws, int64_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -49,7 +49,7 @@ _SIGNATURES = {
     "k2q_gemm_bf16_ws_bytes": ([_i64, _i64, _i64], _i64),
     "k2q_gemm_bf16": ([_p, _p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p, _i64, _p], _int),
     "k2q_gemm_dx_lin": ([_p, _p, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _p], _int),
-    "k2q_dx_prep": ([_p, _p, _p, _p, _i64, _i64, _p, _i64, _p, _p, _p], _int),
+    "k2q_dx_prep": ([_p, _p, _p, _p, _i64, _i64, _p, _p], _int),
     "k2q_gemm_dx_ws_bytes": ([_i64, _i64, _i64], _i64),
     "k2q_gemm_dx": ([_p, _p, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _p], _int),
 }
@@ -387,15 +387,13 @@ def gemm_dx(dy, qw, sw, *, w4: bool = False, g=None, lora_a=None, split: bool = 
     _device_check(dev)
     st = _stream(dev)
     wt = torch.empty((K, N), dtype=torch.bfloat16, device=dev)
-    at = torch.empty((K, r), dtype=torch.float32, device=dev) if r else None
     lib = load()
     _check(lib.k2q_dx_prep(None if w4 else _ptr(qw), None if w4 else _ptr(sw), _ptr(qw) if w4 else None,
-                           _ptr(sw) if w4 else None, N, K, _ptr(lora_a) if r else None, r, _ptr(wt), _ptr(at), st),
-           "k2q_dx_prep")
+                           _ptr(sw) if w4 else None, N, K, _ptr(wt), st), "k2q_dx_prep")
     dx = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
     ws, nws = _workspace(lib.k2q_gemm_dx_ws_bytes(M, N, K) if split else 0, dev)
-    _check(lib.k2q_gemm_dx(_ptr(dy), _ptr(wt), M, N, K, _ptr(g), _ptr(at), r, _ptr(dx), _ptr(ws), nws, st),
-           "k2q_gemm_dx")
+    _check(lib.k2q_gemm_dx(_ptr(dy), _ptr(wt), M, N, K, _ptr(g), _ptr(lora_a) if r else None, r, _ptr(dx),
+                           _ptr(ws), nws, st), "k2q_gemm_dx")
     return dx
 
 
@@ -471,7 +469,7 @@ def gemm_bf16(x, w, bias=None, u=None, lora_b=None, lora_scale: float = 1.0, *, 
 
 
 def gemm_dx_fp8(dy, q, s, *, g=None, lora_a=None, split: bool = True) -> torch.Tensor:
-    """``dx = bf16(dy W_deq) + g lora_A`` for the fp8 base (``W_deq = bf16(q s)``)."""
+    """``dx = bf16(dy W_deq + g lora_A)`` for the fp8 base (``W_deq = bf16(q s)``)."""
     _need(dy, "dy", torch.bfloat16, 2)
     dev = dy.device
     N, K = _fp8_operands(q, s)
@@ -490,9 +488,8 @@ def gemm_dx_fp8(dy, q, s, *, g=None, lora_a=None, split: bool = True) -> torch.T
     lib = load()
     st = _stream(dev)
     wt = dequant_fp8(q, s, transpose=True)
-    at = lora_a.t().contiguous() if r else None   # (K, r): the LoRA factor rows the epilogue reads per k
     dx = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
     ws, nws = _workspace(lib.k2q_gemm_dx_ws_bytes(M, N, K) if split else 0, dev)
-    _check(lib.k2q_gemm_dx_lin(_ptr(dy), _ptr(wt), M, N, K, _ptr(g), _ptr(at), r, _ptr(dx), _ptr(ws), nws, st),
-           "k2q_gemm_dx_lin")
+    _check(lib.k2q_gemm_dx_lin(_ptr(dy), _ptr(wt), M, N, K, _ptr(g), _ptr(lora_a) if r else None, r, _ptr(dx),
+                               _ptr(ws), nws, st), "k2q_gemm_dx_lin")
     return dx

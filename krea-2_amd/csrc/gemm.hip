@@ -19,7 +19,7 @@
 //            accumulating lora_scale*u[m,:] . lora_b[n,:] onto the dequantized f32 value.
 //   EPI_ACC  raw int32 acc (debug entry for bit-exact checks).
 //   EPI_DX   inverse rotation: FWHT over each 128-block of k (a wave's 128 A-rows are one block),
-//            times 2^-7, plus the LoRA term g[m,:] . at[k,:], stored bf16.
+//            times 2^-7, plus the LoRA term g[m,:] . A[:,k], stored bf16.
 //   EPI_LIN  bf16 x bf16 linear (the fp8 weight-only base, quantize.py:48-51): y = bf16(acc + bias[n] + LoRA).
 //   EPI_DXLIN its input gradient: dx = bf16(acc + LoRA), no rotation.
 // Every bf16 output is rounded once, after the LoRA term is added in f32.
@@ -43,7 +43,8 @@ struct GemmArgs {
   const float* sw;    // EPI_W8: per-A-row scale
   const float* bias;  // EPI_W8: per-A-row bias (nullable)
   const float* lora_rb;  // per-B-row LoRA factor rows (u or g), rows_b x r f32 (nullable)
-  const float* lora_ra;  // per-A-row LoRA factor rows (lora_b or A^T), rows_a x r f32
+  const float* lora_ra;  // per-A-row LoRA factors: lora_b (rows_a x r f32) for the forward epilogues, the
+                         // LoRA A itself (r x rows_a f32, so column a holds row a's factors) for EPI_DX/DXLIN
   int r;
   float lora_scale;
   // Split schedule for the last, partly filled round of tiles: tiles 0 .. dp_tiles-1 run over the full
@@ -531,20 +532,32 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int64_t lid, int kb
     //      512 contiguous bytes per output row segment.
     // This thread's share of the LoRA factor rows for the staging below (A-side row A0 + t/2, B-side row
     // B0 + t/2, ranks 8 (t&1) .. +8 of each 16-rank chunk): the first chunk is fetched now, so its latency
-    // hides under pass A, and each later chunk while the previous one is multiplied.
+    // hides under pass A, and each later chunk while the previous one is multiplied.  The input-gradient
+    // epilogues read their A-side factors straight from LoRA A (r x rows_a): 8 loads of 4 bytes, rank by
+    // rank, consecutive threads on consecutive columns.
+    constexpr bool RA_T = (EPI == EPI_DX || EPI == EPI_DXLIN);
     const bool lora = p.lora_rb != nullptr && p.r > 0;
     const int srow = tid >> 1, shalf = tid & 1;
     const float* pra = nullptr;
     const float* prb = nullptr;
     v4f lfa[2], lfb[2];
+    auto load_ra = [&](int c0) {
+      if constexpr (RA_T) {
+        const float* q = pra + (int64_t)c0 * p.rows_a;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) lfa[j >> 2][j & 3] = q[(int64_t)j * p.rows_a];
+      } else {
+        lfa[0] = *reinterpret_cast<const v4f*>(pra + c0);
+        lfa[1] = *reinterpret_cast<const v4f*>(pra + c0 + 4);
+      }
+    };
     if (lora) {
       int64_t ra = A0 + srow, rb = B0 + srow;
       ra = ra < p.rows_a ? ra : p.rows_a - 1;
       rb = rb < p.rows_b ? rb : p.rows_b - 1;
-      pra = p.lora_ra + ra * p.r + 8 * shalf;
+      pra = RA_T ? p.lora_ra + (int64_t)(8 * shalf) * p.rows_a + ra : p.lora_ra + ra * p.r + 8 * shalf;
       prb = p.lora_rb + rb * p.r + 8 * shalf;
-      lfa[0] = *reinterpret_cast<const v4f*>(pra);
-      lfa[1] = *reinterpret_cast<const v4f*>(pra + 4);
+      load_ra(0);
       lfb[0] = *reinterpret_cast<const v4f*>(prb);
       lfb[1] = *reinterpret_cast<const v4f*>(prb + 4);
     }
@@ -613,8 +626,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int64_t lid, int kb
         *reinterpret_cast<v8bf*>(sla + srow * LROW + 16 * shalf) = f32x8_to_bf16v(lfa[0], lfa[1], 1.f);
         *reinterpret_cast<v8bf*>(slb + srow * LROW + 16 * shalf) = f32x8_to_bf16v(lfb[0], lfb[1], p.lora_scale);
         const int cn = c0 + 16 < p.r ? c0 + 16 : c0;   // next chunk (the last re-reads its own)
-        lfa[0] = *reinterpret_cast<const v4f*>(pra + cn);
-        lfa[1] = *reinterpret_cast<const v4f*>(pra + cn + 4);
+        load_ra(cn);
         lfb[0] = *reinterpret_cast<const v4f*>(prb + cn);
         lfb[1] = *reinterpret_cast<const v4f*>(prb + cn + 4);
         lds_barrier();
@@ -1014,19 +1026,19 @@ extern "C" int k2q_gemm_w8a8_acc(const int8_t* qx, const int8_t* qw, int64_t M, 
 }
 
 extern "C" int k2q_gemm_dx(const uint16_t* dy, const uint16_t* wt, int64_t M, int64_t N, int64_t K,
-                           const float* g, const float* at, int64_t r, uint16_t* dx, void* ws, int64_t ws_bytes,
+                           const float* g, const float* lora_a, int64_t r, uint16_t* dx, void* ws, int64_t ws_bytes,
                            void* stream) {
   if (M < 1 || K < K2Q_HADAMARD || K % K2Q_HADAMARD || N < 64 || N % 64) return K2Q_EINVAL;
   if (!dy || !wt || !dx || !k2q_aligned(dy, 16) || !k2q_aligned(wt, 16) || !k2q_aligned(dx, 16))
     return K2Q_EINVAL;
-  int rc = check_lora(g, at, r);
+  int rc = check_lora(g, lora_a, r);
   if (rc) return rc;
   GemmArgs p{};
   p.a = reinterpret_cast<const uint8_t*>(wt);
   p.b = reinterpret_cast<const uint8_t*>(dy);
   p.rows_a = K; p.rows_b = M; p.kbytes = 2 * N; p.lda_b = 2 * N; p.ldb_b = 2 * N;
   p.out = dx; p.ldo = K;
-  p.lora_rb = g; p.lora_ra = at; p.r = g ? (int)r : 0; p.lora_scale = 1.f;
+  p.lora_rb = g; p.lora_ra = lora_a; p.r = g ? (int)r : 0; p.lora_scale = 1.f;
   return launch_gemm<EPI_DX>(p, ws, ws_bytes, static_cast<hipStream_t>(stream));
 }
 
@@ -1054,19 +1066,19 @@ extern "C" int k2q_gemm_bf16(const uint16_t* x, const uint16_t* w, const float* 
 }
 
 extern "C" int k2q_gemm_dx_lin(const uint16_t* dy, const uint16_t* wt, int64_t M, int64_t N, int64_t K,
-                               const float* g, const float* at, int64_t r, uint16_t* dx, void* ws, int64_t ws_bytes,
+                               const float* g, const float* lora_a, int64_t r, uint16_t* dx, void* ws, int64_t ws_bytes,
                                void* stream) {
   if (M < 1 || K < 64 || K % 64 || N < 64 || N % 64) return K2Q_EINVAL;
   if (!dy || !wt || !dx || !k2q_aligned(dy, 16) || !k2q_aligned(wt, 16) || !k2q_aligned(dx, 16))
     return K2Q_EINVAL;
-  int rc = check_lora(g, at, r);
+  int rc = check_lora(g, lora_a, r);
   if (rc) return rc;
   GemmArgs p{};
   p.a = reinterpret_cast<const uint8_t*>(wt);
   p.b = reinterpret_cast<const uint8_t*>(dy);
   p.rows_a = K; p.rows_b = M; p.kbytes = 2 * N; p.lda_b = 2 * N; p.ldb_b = 2 * N;
   p.out = dx; p.ldo = K;
-  p.lora_rb = g; p.lora_ra = at; p.r = g ? (int)r : 0; p.lora_scale = 1.f;
+  p.lora_rb = g; p.lora_ra = lora_a; p.r = g ? (int)r : 0; p.lora_scale = 1.f;
   return launch_gemm<EPI_DXLIN>(p, ws, ws_bytes, static_cast<hipStream_t>(stream));
 }
 

@@ -313,14 +313,6 @@ __global__ __launch_bounds__(256) void dequant_t_kernel(const int8_t* __restrict
   }
 }
 
-__global__ __launch_bounds__(256) void transpose_f32_kernel(const float* __restrict__ a, int64_t R,
-                                                            int64_t C, float* __restrict__ at) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // index into at (C x R)
-  if (i >= R * C) return;
-  const int64_t c = i / R, r = i % R;
-  at[i] = a[r * C + c];
-}
-
 }  // namespace
 
 // A-stationary plan: K cut into workgroup spans (slices), rows split so that slices x row groups ~ CUs.
@@ -407,23 +399,16 @@ extern "C" int k2q_lora_down(const uint16_t* x, int64_t M, int64_t K, int64_t ld
 }
 
 extern "C" int k2q_dx_prep(const int8_t* qw, const float* sw, const uint8_t* qw4, const uint16_t* sw4,
-                           int64_t N, int64_t K, const float* lora_a, int64_t r, uint16_t* wt, float* at,
-                           void* stream) {
+                           int64_t N, int64_t K, uint16_t* wt, void* stream) {
   const bool w4 = qw4 != nullptr;
   if (N < 1 || K < 128 || K % 128 || !wt) return K2Q_EINVAL;
   if (w4 ? (!sw4 || !k2q_aligned(qw4, 16)) : (!qw || !sw || !k2q_aligned(qw, 16))) return K2Q_EINVAL;
   if (!k2q_aligned(wt, 16) || N % 8) return K2Q_EINVAL;
-  if (lora_a && (!at || r < 1)) return K2Q_EINVAL;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)((N + 63) / 64), (unsigned)(K / 64));
   if (w4)
     hipLaunchKernelGGL(dequant_t_kernel<true>, grid, dim3(256), 0, st, nullptr, nullptr, qw4, sw4, N, K, wt);
   else
     hipLaunchKernelGGL(dequant_t_kernel<false>, grid, dim3(256), 0, st, qw, sw, nullptr, nullptr, N, K, wt);
-  if (lora_a) {
-    const int64_t n = r * K;
-    hipLaunchKernelGGL(transpose_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, lora_a, r,
-                       K, at);
-  }
   return k2q_launch_status();
 }
