@@ -36,6 +36,11 @@ int k2q_launch_gemv_w8a8(const int8_t* qx, const float* sx, const int8_t* qw, co
                          const float* u, const float* lora_b, int r, float lora_scale, int64_t M, int64_t N,
                          int64_t K, uint16_t* y, hipStream_t st);
 
+// LoRA down-projection u = x (scale F)^T (lora.hip); F is r x K row-major (a_kstride = 1) or given as its
+// K x r transpose (a_kstride = r).  k2q_lora_down is the a_kstride = 1, scale = 1 case.
+int lora_down_impl(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const float* a, int64_t a_kstride,
+                   float a_scale, int64_t r, void* ws, int64_t ws_bytes, float* u, hipStream_t st);
+
 // Status helpers for the C ABI.
 static inline int k2q_launch_status() {
   hipError_t e = hipGetLastError();

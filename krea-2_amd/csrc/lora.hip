@@ -138,6 +138,7 @@ struct LdShape {
 template <int RT>
 __global__ __launch_bounds__(64 * LD_NW) void lora_down_as_kernel(const uint16_t* __restrict__ x, int64_t M,
                                                                   int64_t ldx, const float* __restrict__ a, int64_t K,
+                                                                  int64_t a_kstride, float a_scale,
                                                                   int64_t rows_per_wg, float* __restrict__ out) {
   constexpr int NS = LdShape<RT>::NS;
   constexpr int R = 16 * RT;
@@ -155,8 +156,21 @@ __global__ __launch_bounds__(64 * LD_NW) void lora_down_as_kernel(const uint16_t
   for (int jt = 0; jt < RT; ++jt)
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      const float* pa = a + (int64_t)(16 * jt + (lane & 15)) * K + kb + 32 * s;
-      split8(*reinterpret_cast<const v4f*>(pa), *reinterpret_cast<const v4f*>(pa + 4), ah[jt][s], al[jt][s]);
+      const int64_t rank = 16 * jt + (lane & 15), k = kb + 32 * s;
+      v4f f0, f1;
+      if (a_kstride == 1) {   // factor rows (r x K), as nn.Linear stores A
+        const float* pa = a + rank * K + k;
+        f0 = *reinterpret_cast<const v4f*>(pa);
+        f1 = *reinterpret_cast<const v4f*>(pa + 4);
+      } else {                // factor columns (K x r, e.g. lora_B for g = s dY B), scaled
+        const float* pa = a + k * a_kstride + rank;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          f0[e] = pa[e * a_kstride] * a_scale;
+          f1[e] = pa[(e + 4) * a_kstride] * a_scale;
+        }
+      }
+      split8(f0, f1, ah[jt][s], al[jt][s]);
     }
 
   auto load_x = [&](v4i (&f)[NS], int t) {
@@ -336,9 +350,9 @@ AsPlan as_plan(int64_t M, int64_t K, int64_t r) {
 
 template <int RT>
 void launch_as(const AsPlan& p, hipStream_t st, const uint16_t* x, int64_t M, int64_t ldx, const float* a, int64_t K,
-               float* out) {
+               int64_t a_kstride, float a_scale, float* out) {
   hipLaunchKernelGGL(lora_down_as_kernel<RT>, dim3((unsigned)p.groups, (unsigned)p.slices), dim3(64 * LD_NW), 0, st,
-                     x, M, ldx, a, K, p.rows, out);
+                     x, M, ldx, a, K, a_kstride, a_scale, p.rows, out);
 }
 
 extern "C" int64_t k2q_lora_down_ws_bytes(int64_t M, int64_t K, int64_t r) {
@@ -349,18 +363,23 @@ extern "C" int64_t k2q_lora_down_ws_bytes(int64_t M, int64_t K, int64_t r) {
 
 extern "C" int k2q_lora_down(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const float* lora_a,
                              int64_t r, void* ws, int64_t ws_bytes, float* u, void* stream) {
+  return lora_down_impl(x, M, K, ldx, lora_a, 1, 1.f, r, ws, ws_bytes, u, static_cast<hipStream_t>(stream));
+}
+
+// The transposed-factor form needs the A-stationary path (one K slice, or a workspace for the slices).
+int lora_down_impl(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const float* lora_a, int64_t a_kstride,
+                   float a_scale, int64_t r, void* ws, int64_t ws_bytes, float* u, hipStream_t st) {
   if (!x || !lora_a || !u || M < 1 || K < 128 || K % 128 || ldx < K || ldx % 8) return K2Q_EINVAL;
   if (r < 16 || r > 128 || r % 16) return K2Q_EINVAL;
   if (!k2q_aligned(x, 16) || !k2q_aligned(lora_a, 16) || !k2q_aligned(u, 16) || (ws && !k2q_aligned(ws, 16)))
     return K2Q_EINVAL;
-  hipStream_t st = static_cast<hipStream_t>(stream);
   const AsPlan q = as_plan(M, K, r);
   if (q.slices == 1 || (ws && ws_bytes >= q.slices * M * r * 4)) {
     if (q.groups > 0x7fffffff || q.slices > 0xffff) return K2Q_EUNSUPPORTED;
     float* out = q.slices > 1 ? static_cast<float*>(ws) : u;
     switch (r / 16) {
 #define K2Q_AS_CASE(RT) \
-  case RT: launch_as<RT>(q, st, x, M, ldx, lora_a, K, out); break;
+  case RT: launch_as<RT>(q, st, x, M, ldx, lora_a, K, a_kstride, a_scale, out); break;
       K2Q_AS_CASE(1) K2Q_AS_CASE(2) K2Q_AS_CASE(3) K2Q_AS_CASE(4)
       K2Q_AS_CASE(5) K2Q_AS_CASE(6) K2Q_AS_CASE(7) K2Q_AS_CASE(8)
 #undef K2Q_AS_CASE
@@ -375,6 +394,7 @@ extern "C" int k2q_lora_down(const uint16_t* x, int64_t M, int64_t K, int64_t ld
     return k2q_launch_status();
   }
   // No room for the slice partials: the row-tiled kernel over the whole of K in one launch.
+  if (a_kstride != 1) return K2Q_EINVAL;
   LoraPlan p = lora_plan(M, K, r);
   p.ks = 1;
   if (p.row_blocks > 0x7fffffff) return K2Q_EUNSUPPORTED;

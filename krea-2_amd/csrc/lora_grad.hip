@@ -231,7 +231,7 @@ WgradPlan wgrad_plan(int64_t M, int64_t C) {
 int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
 
 struct GradLayout {
-  int64_t bt, ld, pt, part_a, part_b, total;   // byte offsets into the workspace
+  int64_t ld, pt, part_a, part_b, total;   // byte offsets into the workspace
   int64_t mp;
   WgradPlan pa, pb;
 };
@@ -242,7 +242,6 @@ GradLayout grad_layout(int64_t M, int64_t N, int64_t K, int64_t r) {
   L.pa = wgrad_plan(M, K);
   L.pb = wgrad_plan(M, N);
   int64_t off = 0;
-  L.bt = off;     off += align256(r * N * 4);
   L.ld = off;     off += align256(k2q_lora_down_ws_bytes(M, N, r));
   L.pt = off;     off += 4 * align256(r * L.mp * 2);
   L.part_a = off; off += L.pa.slices > 1 ? align256(L.pa.slices * r * K * 4) : 0;
@@ -303,18 +302,14 @@ extern "C" int k2q_lora_grads(const uint16_t* dy, const uint16_t* x, const float
   if (L.pa.kblocks > 0xffff || L.pa.slices > 0xffff || L.pb.slices > 0xffff) return K2Q_EUNSUPPORTED;
   hipStream_t st = static_cast<hipStream_t>(stream);
   uint8_t* w = static_cast<uint8_t*>(ws);
-  float* bt = reinterpret_cast<float*>(w + L.bt);
   const int64_t pt_bytes = align256(r * L.mp * 2);
   uint16_t* pt[4];
   for (int i = 0; i < 4; ++i) pt[i] = reinterpret_cast<uint16_t*>(w + L.pt + i * pt_bytes);
 
-  // g = dY (scale B^T)^T: the down-projection kernel with dY as the activation and scale * B^T as the factor.
-  {
-    const dim3 grid((unsigned)((N + 31) / 32), (unsigned)((r + 31) / 32));
-    hipLaunchKernelGGL(transpose_kernel<false>, grid, dim3(256), 0, st, lora_b, N, r, N, scale, bt, nullptr, nullptr);
-  }
+  // g = dY (scale B^T)^T: the down-projection kernel with dY as the activation and scale * B^T as the factor,
+  // read from B (N x r) directly.
   const int64_t ld_bytes = k2q_lora_down_ws_bytes(M, N, r);
-  int rc = k2q_lora_down(dy, M, N, N, bt, r, ld_bytes ? w + L.ld : nullptr, ld_bytes, g, stream);
+  int rc = lora_down_impl(dy, M, N, N, lora_b, r, scale, r, ld_bytes ? w + L.ld : nullptr, ld_bytes, g, st);
   if (rc) return rc;
   const int rt = (int)(r / 16);
   if (dA) {
