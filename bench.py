@@ -282,8 +282,9 @@ def run_cfg4(k2, steps, dev, settle_s=0.0):
 
 
 def profile_pass(k2, dev):
-    """Fixed launches for rocprofv3 counter passes: cfg2 rotate/quant, LoRA down, GEMM, 3 times each, then a
-    plain 256 MiB device copy (Tensor.copy_) 3 times, the calibration point for FETCH/WRITE_SIZE."""
+    """Fixed launches for rocprofv3 counter passes: cfg2 rotate/quant, LoRA down, GEMM, 3 times each; the cfg3
+    input-gradient GEMM (with its LoRA term) 3 times; then a plain 256 MiB device copy (Tensor.copy_) 3 times,
+    the calibration point for FETCH/WRITE_SIZE."""
     L = k2._lib
     c = CONFIGS[2]
     x, W, b, A, B = synth(c["M"], c["K"], c["N"], c["r"], c["bias"])
@@ -293,6 +294,14 @@ def profile_pass(k2, dev):
         qx, sx, _ = L.rotquant(xd)
         u = L.lora_down(xd, Ad)
         L.gemm_w8a8(qx, sx, qw, sw, None, u, Bd, 1.0)
+    c3 = CFG3
+    g3 = torch.Generator().manual_seed(3)
+    qw3, sw3 = L.quant_weight_i8((torch.randn(c3["N"], c3["K"], generator=g3) * 0.02).to(torch.bfloat16).to(dev))
+    dy = (torch.randn(c3["M"], c3["N"], generator=g3) * 1e-3).to(torch.bfloat16).to(dev)
+    A3 = (torch.randn(c3["r"], c3["K"], generator=g3) * 0.01).to(dev)
+    g = (torch.randn(c3["M"], c3["r"], generator=g3) * 1e-3).to(dev)
+    for _ in range(3):
+        L.gemm_dx(dy, qw3, sw3, g=g, lora_a=A3)
     src = torch.ones(1 << 28, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     for _ in range(3):
