@@ -130,6 +130,57 @@ def cpu_baseline(cfg, x, W, b, A, B, budget_s=12.0, rows=2048):
                       f"({t * 1e3:.0f} ms each) on {cpu_model()}"}
 
 
+def cpu_reference_path(cfg, x, W, b, A, B, budget_s=6.0, rows=2048):
+    """The reference's own quantized linear + adapter on the CPU, restated (oracle.convrot.fp8_linear is
+    Fp8Linear.forward, quantize.py:48-51: bf16 dequant then F.linear; the adapter is lora.py:47-48 in fp32):
+    the same bounded sample as the ConvRot CPU baseline, for comparison.  Returns TOPS (2*rows*N*K/time)."""
+    import numpy as np
+    from oracle import convrot as orc
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    K, N = cfg["K"], cfg["N"]
+    wq, sc = orc.fp8_weight_quant(W.float().numpy())
+    xs = x[:rows].contiguous()
+    bb = None if b is None else b.to(torch.bfloat16)
+
+    def run():
+        out = orc.fp8_linear(xs, wq, sc, bb)
+        delta = (xs.float() @ A.t()) @ B.t()
+        return out + delta.to(out.dtype)
+
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while not times or (time.perf_counter() < t_end and len(times) < 30):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    return {"value": round(2.0 * rows * N * K / t / 1e12, 4), "unit": "TOPS", "cores": torch.get_num_threads(),
+            "kind": "port", "path": "Fp8Linear + LoRALinear forward (bf16 F.linear, fp32 adapter)",
+            "sample": f"{rows} of {cfg['M']} rows, median of {len(times)} runs ({t * 1e3:.0f} ms each)"}
+
+
+def mfma_probe(k2, dev, seconds=1.0):
+    """Sustained int8 MFMA rate of this board in this run (register-only v_mfma_i32_32x32x32_i8 loop, two
+    waves per SIMD on every CU, pseudo-random operands): the same-run ceiling the GEMM is compared with."""
+    L = k2._lib
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    iters = 2000
+    settle(lambda: L.mfma_probe_i8(iters, cus, dev), 0.5)
+    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ops, n, t_end = 0, 0, time.perf_counter() + seconds
+    s_ev.record()
+    while time.perf_counter() < t_end:
+        for _ in range(4):
+            ops += L.mfma_probe_i8(iters, cus, dev)
+        n += 4
+        torch.cuda.synchronize()
+    e_ev.record()
+    torch.cuda.synchronize()
+    ms = s_ev.elapsed_time(e_ev)
+    return ops / (ms * 1e-3) / 1e12
+
+
 def run_config(k2, cfg, steps, warmup, dev, settle_s=0.0):
     L = k2._lib
     M, K, N, r = cfg["M"], cfg["K"], cfg["N"], cfg["r"]
@@ -438,11 +489,15 @@ def main():
         "lora_ops": 2.0 * cfg["M"] * cfg["r"] * (cfg["K"] + cfg["N"]),
     }
     extra["settle_s"] = a.settle
+    probe = mfma_probe(k2, dev)
+    extra["mfma_probe_int8_tops"] = round(probe, 1)
+    extra["gemm_pct_of_mfma_probe"] = round(100 * gemm_tops / probe, 2)
     extra["cfg3"] = run_cfg3(k2, max(5, a.steps // 2), dev, a.settle / 2)
     extra["cfg4"] = run_cfg4(k2, max(5, a.steps // 2), dev, a.settle / 2)
     cpu = None
     if not a.no_cpu:
         cpu = cpu_baseline(cfg, res["x"], res["W"], res["b"], res["A"], res["B"])
+        extra["cpu_reference_fp8_path"] = cpu_reference_path(cfg, res["x"], res["W"], res["b"], res["A"], res["B"])
     line = {
         "metric": METRIC,
         "value": round(res["tops"], 2),

@@ -123,6 +123,12 @@ int k2q_gemm_bf16(const uint16_t* x, const uint16_t* w, const float* bias, const
 int k2q_gemm_dx_lin(const uint16_t* dy, const uint16_t* wt, int64_t M, int64_t N, int64_t K, const float* g,
                     const float* lora_a, int64_t r, uint16_t* dx, void* ws, int64_t ws_bytes, void* stream);
 
+/* Same-run MFMA ceiling (no counterpart in the reference; a measurement aid for bench.py): a loop of
+ * iters x 64 v_mfma_i32_32x32x32_i8 per wave, 8 waves per workgroup, register operands only.
+ * k2q_mfma_probe_i8_ops gives the int8 operations one launch performs; out holds workgroups*512 int32. */
+int64_t k2q_mfma_probe_i8_ops(int64_t iters, int64_t workgroups);
+int k2q_mfma_probe_i8(int64_t iters, int64_t workgroups, int32_t* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -49,6 +49,8 @@ _SIGNATURES = {
     "k2q_gemm_bf16_ws_bytes": ([_i64, _i64, _i64], _i64),
     "k2q_gemm_bf16": ([_p, _p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p, _i64, _p], _int),
     "k2q_gemm_dx_lin": ([_p, _p, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _p], _int),
+    "k2q_mfma_probe_i8_ops": ([_i64, _i64], _i64),
+    "k2q_mfma_probe_i8": ([_i64, _i64, _p, _p], _int),
     "k2q_dx_prep": ([_p, _p, _p, _p, _i64, _i64, _p, _p], _int),
     "k2q_gemm_dx_ws_bytes": ([_i64, _i64, _i64], _i64),
     "k2q_gemm_dx": ([_p, _p, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _p], _int),
@@ -493,3 +495,23 @@ def gemm_dx_fp8(dy, q, s, *, g=None, lora_a=None, split: bool = True) -> torch.T
     _check(lib.k2q_gemm_dx_lin(_ptr(dy), _ptr(wt), M, N, K, _ptr(g), _ptr(lora_a) if r else None, r, _ptr(dx),
                                _ptr(ws), nws, st), "k2q_gemm_dx_lin")
     return dx
+
+
+# ----------------------------------------------------------------------------------------------------------
+# Measurement aid
+# ----------------------------------------------------------------------------------------------------------
+def mfma_probe_i8(iters: int, workgroups: int, dev=None) -> int:
+    """Launches the register-only int8 MFMA loop on the current stream; returns the int8 operations it
+    performs (time it with events around the call)."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if dev is None else dev
+    _device_check(dev)
+    lib = load()
+    out = _probe_out.get(dev)
+    if out is None or out.numel() < workgroups * 512:
+        out = torch.empty(workgroups * 512, dtype=torch.int32, device=dev)
+        _probe_out[dev] = out
+    _check(lib.k2q_mfma_probe_i8(iters, workgroups, _ptr(out), _stream(dev)), "k2q_mfma_probe_i8")
+    return lib.k2q_mfma_probe_i8_ops(iters, workgroups)
+
+
+_probe_out: dict = {}
