@@ -496,6 +496,51 @@ def test_full_size_cfg3_input_gradient_sampled(k2, dev):
     assert rel_frob(dx.float().cpu().numpy()[rows], ref["dx64"]) < REL_FROB_TOL
 
 
+def test_full_size_cfg2_every_tile(k2, dev):
+    """Every one of cfg2's 3168 tiles (the balanced persistent grid: 244 workgroups of 13 tiles): the int32
+    accumulators equal hipBLASLt's exact int8 GEMM (torch._int_mm) element for element, and the W8 epilogue
+    (2^-7 s_x s_w acc + bias + LoRA, one bf16 rounding) is within one bf16 rounding of the same formula
+    evaluated in float32 by torch on the exact accumulators."""
+    M, K, N, r = 16896, 3072, 12288, 32
+    g = torch.Generator(device=dev).manual_seed(5)
+    qx = torch.randint(-127, 128, (M, K), device=dev, dtype=torch.int8, generator=g)
+    qw = torch.randint(-127, 128, (N, K), device=dev, dtype=torch.int8, generator=g)
+    acc = k2._lib.gemm_w8a8_acc(qx, qw)
+    ref = torch._int_mm(qx, qw.t())
+    assert torch.equal(acc, ref)
+    del ref
+    sx = torch.rand(M, device=dev, generator=g) * 0.01 + 1e-3
+    sw = torch.rand(N, device=dev, generator=g) * 0.01 + 1e-3
+    bias = torch.randn(N, device=dev, generator=g) * 0.02
+    u = torch.randn(M, r, device=dev, generator=g)
+    B = torch.randn(N, r, device=dev, generator=g) * 0.01
+    y = k2._lib.gemm_w8a8(qx, sx, qw, sw, bias, u, B, 1.0).float()
+    lora = u.bfloat16().float() @ B.bfloat16().float().t()
+    yr = acc.float() * ((sx * 0.0078125)[:, None] * sw[None, :]) + bias[None, :] + lora
+    err = (y - yr).abs()
+    tol = yr.abs() * 2 ** -8 + 1e-6                        # one bf16 rounding (2^-9 relative) plus the
+    assert bool((err <= tol).all()), float((err - tol).max())   # f32 ordering differences
+
+
+def test_full_size_cfg3_input_gradient_every_tile(k2, dev):
+    """Every tile of cfg3's input gradient (864 tiles on 216 workgroups) against torch in float32: the dense
+    product dY W_hat, then the inverse rotation as a block-diagonal Hadamard matmul, times 2^-7, plus g A."""
+    M, K, N, r = 4608, 12288, 3072, 64
+    w = make_w(N, K, seed=6)
+    g = torch.Generator(device=dev).manual_seed(7)
+    dy = (torch.randn(M, N, device=dev, generator=g) * 1e-3).to(torch.bfloat16)
+    A = torch.randn(r, K, device=dev, generator=g) * 0.01
+    gd = torch.randn(M, r, device=dev, generator=g) * 1e-3
+    qw, sw = k2._lib.quant_weight_i8(w.to(dev))
+    dx = k2._lib.gemm_dx(dy, qw, sw, g=gd, lora_a=A).float()
+    w_hat = (qw.float() * sw[:, None]).bfloat16().float()           # bf16(s_w q_w), N x K
+    t = dy.float() @ w_hat                                          # M x K, f32
+    H = torch.from_numpy(__import__("scipy.linalg").linalg.hadamard(128).astype(np.float32)).to(dev)
+    t = (t.view(M, K // 128, 128) @ H).view(M, K) * 0.0078125
+    ref = t + gd.bfloat16().float() @ A.bfloat16().float()
+    assert rel_frob(dx.cpu().numpy(), ref.cpu().numpy()) < 3e-3   # bf16 output rounding: ~1.1e-3 RMS
+
+
 # ------------------------------------------------------------------------------------------- fp8 base (f3)
 def _fp8_special_rows(K):
     """Rows whose amax is 448 (scale 1): RNE ties in the normal range (17 -> 16, 1.0625 -> 1, 1.1875 -> 1.25,
