@@ -678,19 +678,28 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int64_t lid, int kb
 
 // ---------------------------------------------------------------------------------------------------------
 // W4A8: A operand = packed int4 weights (rows n, K/2 bytes per row), bf16 group scales sw4[g][n].
-// Tile 128 (n) x 128 (m), 4 waves 2 x 2 of 64 x 64.  A row in LDS is 64 B = 8 units of 8 B, unit u of
-// row r stored at u ^ ((r >> 2) & 7) (conflict-free 8-byte fragment reads).  A lane's 8 packed bytes hold
-// the 16 codes of one 16-wide K chunk; `w << 4 & 0xF0F0F0F0` and `w & 0xF0F0F0F0` give them as int8
+// Tile 128 (n) x 128 (m) per 256-thread workgroup, two workgroups per CU so that one wave's per-group
+// scaling runs while another's MFMAs do.  Wave w owns the 32 n-rows 32w..32w+31 and all 128 m, so every
+// packed weight byte is unpacked by exactly one wave.  The MFMA takes the x codes as its first operand, so
+// a lane's 16 results share one n (the lane's column) and need one group scale.  A stage is 128 of K,
+// double-buffered in LDS and filled by LDS-DMA from buffer resources (per-lane offsets fixed, the stage
+// offset scalar): the packed A rows (64 B each, 16-byte chunk c of row r at c ^ ((r >> 2) & 3)), the int8
+// B rows (the frag()/swz() layout) and the stage's two groups of 128 scales.  A lane's 8 packed bytes
+// hold the 16 codes of one 16-wide K chunk; `w << 4 & 0xF0F0F0F0` and `w & 0xF0F0F0F0` give them as int8
 // values 16*q in K order, so one v_mfma_i32_32x32x32_i8 per 32 of K sees 16x the true products (exact,
-// |16 acc_g| <= 16*64*127*7 < 2^20).  Each 64-wide group is accumulated in int32, converted once and
+// |16 acc_g| <= 16*64*127*8 < 2^20).  Each 64-wide group is accumulated in int32, converted once and
 // scaled: accf += float(acc_g) * s[g][n]; the 1/16 is folded into the final scale.  The per-group
 // convert + FMA (2 VALU ops per output per group) bounds this kernel, not the MFMAs.
 constexpr int W4_BA = 128;                // n rows per tile
 constexpr int W4_BB = 128;                // m rows per tile
-constexpr int W4_IA = 2, W4_IB = 2;       // 32x32 blocks per wave along n and m
-constexpr int W4_TILE_A = W4_BA * 64;     // bytes per stage (128 K codes per row, packed)
-constexpr int W4_TILE_B = W4_BB * BKB;
-constexpr int W4_SCALES = 2 * W4_BA * 2;  // 2 groups x 128 n x bf16
+constexpr int W4_IB = 4;                  // 32-row m blocks per wave (one 32-row n block)
+constexpr int W4_SA = W4_BA * 64;         // packed A bytes per stage (128 K codes per row)
+constexpr int W4_SB = W4_BB * WBK;        // B bytes per stage
+constexpr int W4_SS = 2 * W4_BA * 2;      // 2 groups x 128 n x bf16
+constexpr int W4_STAGE = W4_SA + W4_SB + W4_SS;
+constexpr int W4_G = 7;                   // DMA instructions per wave and stage: 2 A, 4 B, 1 scales
+constexpr int W4_CROW = 2 * W4_BA + 16;   // epilogue bf16 tile row (padded: rows m and m + 4 on other banks)
+static_assert(W4_BB * W4_CROW <= 2 * W4_STAGE, "epilogue tile fits the stage buffers");
 
 struct W4Args {
   const uint8_t* a;      // N x K/2 packed
@@ -706,14 +715,23 @@ struct W4Args {
   float lora_scale;
 };
 
-__device__ __forceinline__ int swz4(int row) { return (row >> 2) & 7; }
+__device__ __forceinline__ int swz4(int row) { return (row >> 2) & 3; }
+
+// Raw byte buffer over [base, base + bytes) for the workgroup-uniform base and extent.  The pieces go
+// through readfirstlane so the descriptor is built in SGPRs (a descriptor the compiler cannot prove
+// uniform is used through a per-lane loop).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t k2q_rsrc(const void* base, int64_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  const int n = __builtin_amdgcn_readfirstlane((int)bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0, n,
+                                          0x00020000);
+}
 
 template <int EPI>
-__global__ __launch_bounds__(256, 1) void gemm_w4_kernel(W4Args p) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  uint8_t* sA = smem;                                  // [2][W4_TILE_A]
-  uint8_t* sB = smem + 2 * W4_TILE_A;                  // [2][W4_TILE_B]
-  uint16_t* sS = reinterpret_cast<uint16_t*>(smem + 2 * W4_TILE_A + 2 * W4_TILE_B);  // [2][2][128]
+__global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) void gemm_w4_kernel(W4Args p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];   // [2][A | B | scales]
 
   const int64_t tiles_a = (p.N + W4_BA - 1) / W4_BA;
   const int64_t tiles_b = (p.M + W4_BB - 1) / W4_BB;
@@ -722,156 +740,164 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(W4Args p) {
   const int64_t A0 = ta * W4_BA, B0 = tb * W4_BB;
 
   const int t = threadIdx.x;
-  const int lane = t & 63, wave = t >> 6;
-  const int wa = wave & 1, wb = wave >> 1;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int h = lane >> 5, c32 = lane & 31;
   const int64_t kb = p.K / 2;   // packed bytes per A row
+  const int64_t na = (p.N - A0) < W4_BA ? (p.N - A0) : W4_BA;
+  const int64_t nb = (p.M - B0) < W4_BB ? (p.M - B0) : W4_BB;
 
-  v16f accf[W4_IA][W4_IB];
+  v16f accf[W4_IB];
 #pragma unroll
-  for (int i = 0; i < W4_IA; ++i)
-#pragma unroll
-    for (int j = 0; j < W4_IB; ++j) accf[i][j] = v16f{0.f};
+  for (int j = 0; j < W4_IB; ++j) accf[j] = v16f{0.f};
 
-  uint32_t offa4[2];
+  // DMA sources, as offsets into buffer resources that start at the tile's first row (rows past the
+  // matrix end clamped onto its last row; never stored).  A: wave w fills rows 32w + 16i + l/4, physical
+  // chunk l%4; B: rows 32w + 8i + l/8, physical chunk l%8; scales: wave w copies group w/2, columns
+  // 64 (w&1) + 2l, 2l+1 with lanes 0-31.
+  const __amdgpu_buffer_rsrc_t ra = k2q_rsrc(p.a + A0 * kb, na * kb);
+  const __amdgpu_buffer_rsrc_t rb = k2q_rsrc(reinterpret_cast<const uint8_t*>(p.b) + B0 * p.K, nb * p.K);
+  const __amdgpu_buffer_rsrc_t rs = k2q_rsrc(p.s4, (p.K / 64) * p.N * 2);
+  int offa[2], offb[4];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    int64_t rr = (t >> 2) + 64 * i;
-    rr = A0 + rr < p.N ? rr : p.N - 1 - A0;
-    offa4[i] = (uint32_t)(rr * kb) + 16u * (uint32_t)(t & 3);
+    const int lrow = 32 * wave + 16 * i + (lane >> 2);
+    const int rr = lrow < na ? lrow : (int)na - 1;
+    offa[i] = (int)(rr * kb) + 16 * ((lane & 3) ^ swz4(lrow));
   }
-  const TileOffsets<4> offb = tile_offsets<4>(B0, p.M, p.K);
-  const uint8_t* gA = p.a + A0 * kb;
-  const uint8_t* gB = reinterpret_cast<const uint8_t*>(p.b) + B0 * p.K;
-  int64_t ns = A0 + 4 * (t & 31);
-  ns = ns < p.N ? ns : p.N - 4;
-  const uint16_t* gS = p.s4 + (int64_t)((t >> 5) & 1) * p.N + ns;   // read by t < 64 only
-  v4i ra[2], rb[4];
-  v2u rs = v2u{0u, 0u};
-  auto load_stage = [&](int kt) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) ra[i] = *reinterpret_cast<const v4i*>(gA + kt * 64 + offa4[i]);
-    g2r<4>(gB + kt * BKB, offb, rb);
-    if (t < 64) rs = *reinterpret_cast<const v2u*>(gS + (int64_t)kt * 2 * p.N);
-  };
-  auto store_stage = [&](int buf) {
-    uint8_t* tA = sA + buf * W4_TILE_A;
+  for (int i = 0; i < 4; ++i) {
+    const int lrow = 32 * wave + 8 * i + (lane >> 3);
+    const int rr = lrow < nb ? lrow : (int)nb - 1;
+    offb[i] = (int)(rr * p.K) + 16 * ((lane & 7) ^ swz(lrow));
+  }
+  int64_t ncol = A0 + 64 * (wave & 1) + 2 * (lane & 31);
+  ncol = ncol < p.N ? ncol : p.N - 2;
+  const int offs = (int)(((int64_t)(wave >> 1) * p.N + ncol) * 2);
+  auto issue = [&](int st, int slot) {
+    uint8_t* base = smem + slot * W4_STAGE;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int row = (t >> 2) + 64 * i;
-      const int u0 = 2 * (t & 3);
-      *reinterpret_cast<v2u*>(tA + row * 64 + 8 * (u0 ^ swz4(row))) = v2u{(uint32_t)ra[i][0], (uint32_t)ra[i][1]};
-      *reinterpret_cast<v2u*>(tA + row * 64 + 8 * ((u0 + 1) ^ swz4(row))) =
-          v2u{(uint32_t)ra[i][2], (uint32_t)ra[i][3]};
-    }
-    r2s<4>(sB + buf * W4_TILE_B, rb);
-    if (t < 64) *reinterpret_cast<v2u*>(sS + buf * 2 * W4_BA + (t >> 5) * W4_BA + 4 * (t & 31)) = rs;
+    for (int i = 0; i < 2; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, K2Q_LPTR(base + 1024 * (2 * wave + i)), 16, offa[i], st * 64, 0,
+                                               0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, K2Q_LPTR(base + W4_SA + 1024 * (4 * wave + i)), 16, offb[i],
+                                               st * WBK, 0, 0);
+    if (lane < 32)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, K2Q_LPTR(base + W4_SA + W4_SB + 256 * (wave >> 1) + 128 * (wave & 1)), 4, offs,
+          (int)(st * 4 * p.N), 0, 0);
   };
 
-  auto compute = [&](int buf) {
-    const uint8_t* tA = sA + buf * W4_TILE_A;
-    const uint8_t* tB = sB + buf * W4_TILE_B;
-    const uint16_t* tS = sS + buf * 2 * W4_BA;
+  auto compute = [&](int slot) {
+    const uint8_t* tA = smem + slot * W4_STAGE;
+    const uint8_t* tB = tA + W4_SA;
+    const uint16_t* tS = reinterpret_cast<const uint16_t*>(tB + W4_SB);
+    const int arow = 32 * wave + c32;
 #pragma unroll
     for (int grp = 0; grp < 2; ++grp) {
-      v16i acc[W4_IA][W4_IB];
+      v16i acc[W4_IB];
 #pragma unroll
-      for (int i = 0; i < W4_IA; ++i)
-#pragma unroll
-        for (int j = 0; j < W4_IB; ++j) acc[i][j] = v16i{0};
+      for (int j = 0; j < W4_IB; ++j) acc[j] = v16i{0};
 #pragma unroll
       for (int k2 = 0; k2 < 2; ++k2) {
         const int kk = 2 * grp + k2;
-        v4i fa[W4_IA], fb[W4_IB];
+        const v2u w = *reinterpret_cast<const v2u*>(tA + arow * 64 + 16 * (kk ^ swz4(arow)) + 8 * h);
+        const v4i fa = v4i{(int)((w[0] << 4) & 0xF0F0F0F0u), (int)((w[1] << 4) & 0xF0F0F0F0u),
+                           (int)(w[0] & 0xF0F0F0F0u), (int)(w[1] & 0xF0F0F0F0u)};
+        v4i fb[W4_IB];
 #pragma unroll
-        for (int i = 0; i < W4_IA; ++i) {
-          const int row = 32 * W4_IA * wa + 32 * i + c32;
-          const v2u w = *reinterpret_cast<const v2u*>(tA + row * 64 + 8 * ((2 * kk + h) ^ swz4(row)));
-          fa[i] = v4i{(int)((w[0] << 4) & 0xF0F0F0F0u), (int)((w[1] << 4) & 0xF0F0F0F0u),
-                      (int)(w[0] & 0xF0F0F0F0u), (int)(w[1] & 0xF0F0F0F0u)};
-        }
+        for (int i = 0; i < W4_IB; ++i) fb[i] = frag(tB, 32 * i + c32, 2 * kk + h);
 #pragma unroll
-        for (int i = 0; i < W4_IB; ++i) fb[i] = frag(tB, 32 * W4_IB * wb + 32 * i + c32, 2 * kk + h);
-#pragma unroll
-        for (int ia = 0; ia < W4_IA; ++ia)
-#pragma unroll
-          for (int ib = 0; ib < W4_IB; ++ib)
-            acc[ia][ib] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[ia], fb[ib], acc[ia][ib], 0, 0, 0);
+        for (int ib = 0; ib < W4_IB; ++ib)   // rows m (x codes), columns n (weights): lane c32 is one n
+          acc[ib] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[ib], fa, acc[ib], 0, 0, 0);
       }
+      const float sv = bf16_bits_to_f32(tS[grp * W4_BA + arow]);
 #pragma unroll
-      for (int ia = 0; ia < W4_IA; ++ia)
+      for (int ib = 0; ib < W4_IB; ++ib)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const v2u sp =
-              *reinterpret_cast<const v2u*>(tS + grp * W4_BA + 32 * W4_IA * wa + 32 * ia + 8 * j + 4 * h);
-          const float sv[4] = {bf16_bits_to_f32(sp[0] & 0xffffu), bf16_bits_to_f32(sp[0] >> 16),
-                               bf16_bits_to_f32(sp[1] & 0xffffu), bf16_bits_to_f32(sp[1] >> 16)};
-#pragma unroll
-          for (int ib = 0; ib < W4_IB; ++ib)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              accf[ia][ib][4 * j + i] = __builtin_fmaf((float)acc[ia][ib][4 * j + i], sv[i],
-                                                       accf[ia][ib][4 * j + i]);
-        }
+        for (int e = 0; e < 16; ++e) accf[ib][e] = __builtin_fmaf((float)acc[ib][e], sv, accf[ib][e]);
+      // One group's int32 accumulators live at a time: the scaled sums pass through here before the next
+      // group's fragment reads (the memory clobber keeps those below), so its MFMAs cannot be hoisted
+      // above this group's conversion.
+      asm volatile("" : "+v"(accf[0]), "+v"(accf[1]), "+v"(accf[2]), "+v"(accf[3])::"memory");
     }
   };
 
-  const int nk = (int)(p.K / BKB);
-  load_stage(0);
-  store_stage(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk - 1; ++kt) {
-    const int buf = kt & 1;
-    load_stage(kt + 1);
-    compute(buf);
-    store_stage(buf ^ 1);
-    __syncthreads();
+  // Double-buffered: stage s+2 is fetched into stage s's slot once every wave is done with it.  Unrolled
+  // by two so that the slot, and with it every LDS address, is a compile-time offset.
+  const int ns = (int)(p.K / 128);
+  auto step = [&](int st, int slot) {
+    compute(slot);
+    wait_vmcnt<0>();                                       // stage st+1
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this wave's reads of the slot have landed
+    lds_barrier();
+    if (st + 2 < ns) issue(st + 2, slot);
+  };
+  issue(0, 0);
+  issue(ns > 1 ? 1 : 0, 1);
+  wait_vmcnt<W4_G>();
+  lds_barrier();
+  for (int st = 0; st < ns; st += 2) {
+    step(st, 0);
+    if (st + 1 < ns) step(st + 1, 1);
   }
-  compute((nk - 1) & 1);
+  wait_vmcnt<0>();   // no LDS-DMA may still be in flight when the workgroup's LDS is released
 
-  const int64_t a0 = A0 + 32 * W4_IA * wa, b0 = B0 + 32 * W4_IB * wb;
+  // accf[ib][e]: n = a0 + c32, m = B0 + 32 ib + 8 (e / 4) + 4 h + e % 4.
+  const int64_t a0 = A0 + 32 * wave;
   if constexpr (EPI == EPI_ACC) {
     float* out = static_cast<float*>(p.out);
+    const int64_t n = a0 + c32;
+    if (n < p.N) {
 #pragma unroll
-    for (int ia = 0; ia < W4_IA; ++ia)
+      for (int ib = 0; ib < W4_IB; ++ib)
 #pragma unroll
-      for (int ib = 0; ib < W4_IB; ++ib) {
-        const int64_t m = b0 + 32 * ib + c32;
-        if (m >= p.M) continue;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int64_t n = a0 + 32 * ia + 8 * j + 4 * h;
-          if (n >= p.N) continue;
-          const v4f v = v4f{accf[ia][ib][4 * j] * 0.0625f, accf[ia][ib][4 * j + 1] * 0.0625f,
-                            accf[ia][ib][4 * j + 2] * 0.0625f, accf[ia][ib][4 * j + 3] * 0.0625f};
-          *reinterpret_cast<v4f*>(out + m * p.N + n) = v;
+        for (int e = 0; e < 16; ++e) {
+          const int64_t m = B0 + 32 * ib + 8 * (e >> 2) + 4 * h + (e & 3);
+          if (m < p.M) out[m * p.N + n] = accf[ib][e] * 0.0625f;
         }
-      }
+    }
   } else {
-    uint16_t* out = static_cast<uint16_t*>(p.out);
+    // Scales, bias and LoRA in registers, then the bf16 tile goes through LDS (row m: 128 n, W4_CROW
+    // bytes) for row-contiguous stores.
+    uint16_t* ctile = reinterpret_cast<uint16_t*>(smem);
+    lds_barrier();   // every wave is past its last fragment read
+    int64_t n = a0 + c32;
+    n = n < p.N ? n : p.N - 1;
+    const float bi = p.bias ? p.bias[n] : 0.f;
 #pragma unroll
     for (int ib = 0; ib < W4_IB; ++ib) {
-      int64_t m = b0 + 32 * ib + c32;
-      m = m < p.M ? m : p.M - 1;
-      const float sxm = p.sx[m] * (0.0078125f * 0.0625f);  // 2^-7 rotations, 1/16 nibble placement
+      v16f f;
 #pragma unroll
-      for (int ia = 0; ia < W4_IA; ++ia) {
-        v16f f;
+      for (int e = 0; e < 16; ++e) {
+        int64_t m = B0 + 32 * ib + 8 * (e >> 2) + 4 * h + (e & 3);
+        m = m < p.M ? m : p.M - 1;
+        f[e] = accf[ib][e] * (p.sx[m] * (0.0078125f * 0.0625f)) + bi;   // 2^-7 rotations, 1/16 nibbles
+      }
+      if (p.lora_rb && p.r > 0)   // f[m][n] += u[m, :] . (scale lora_b[n, :])
+        f = lora_block(p.lora_rb, p.lora_ra, p.r, p.lora_scale, p.M, p.N, B0 + 32 * ib, a0, lane, f);
+      const int col = 32 * wave + c32;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          int64_t n = a0 + 32 * ia + 8 * j + 4 * h;
-          n = n < p.N ? n : p.N - 4;
-          const float4 bi =
-              p.bias ? *reinterpret_cast<const float4*>(p.bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
-          f[4 * j + 0] = accf[ia][ib][4 * j + 0] * sxm + bi.x;
-          f[4 * j + 1] = accf[ia][ib][4 * j + 1] * sxm + bi.y;
-          f[4 * j + 2] = accf[ia][ib][4 * j + 2] * sxm + bi.z;
-          f[4 * j + 3] = accf[ia][ib][4 * j + 3] * sxm + bi.w;
-        }
-        if (p.lora_rb && p.r > 0)
-          f = lora_block(p.lora_ra, p.lora_rb, p.r, p.lora_scale, p.N, p.M, a0 + 32 * ia, b0 + 32 * ib, lane,
-                         f);
-        store_block(out, p.N, p.N, p.M, a0 + 32 * ia, b0 + 32 * ib, lane, f);
+      for (int e = 0; e < 16; e += 2) {
+        const uint32_t v = pack_bf16x2(f[e], f[e + 1]);
+        const int row = 32 * ib + 8 * (e >> 2) + 4 * h + (e & 3);
+        ctile[(row * W4_CROW) / 2 + col] = (uint16_t)(v & 0xffffu);
+        ctile[((row + 1) * W4_CROW) / 2 + col] = (uint16_t)(v >> 16);
+      }
+    }
+    lds_barrier();
+    uint16_t* out = static_cast<uint16_t*>(p.out);
+    const int cq = t & 31;                   // 4 n per thread
+    const int64_t n4 = A0 + 4 * cq;
+    if (n4 < p.N) {
+#pragma unroll 4
+      for (int row = t >> 5; row < W4_BB; row += 8) {
+        const int64_t m = B0 + row;
+        if (m < p.M)
+          *reinterpret_cast<v2u*>(out + m * p.N + n4) =
+              *reinterpret_cast<const v2u*>(reinterpret_cast<const uint8_t*>(ctile) + row * W4_CROW + 8 * cq);
       }
     }
   }
@@ -879,7 +905,9 @@ __global__ __launch_bounds__(256, 1) void gemm_w4_kernel(W4Args p) {
 
 template <int EPI>
 int launch_w4(const W4Args& p, hipStream_t st) {
-  constexpr int lds = 2 * W4_TILE_A + 2 * W4_TILE_B + 2 * W4_SCALES;
+  constexpr int lds = 2 * W4_STAGE;
+  // Buffer-resource extents are 32-bit: a tile's rows of either operand and the whole scale array.
+  if (p.K * W4_BB >= (int64_t(1) << 31) || (p.K / 64) * p.N * 2 >= (int64_t(1) << 31)) return K2Q_EUNSUPPORTED;
   if (hipFuncSetAttribute((const void*)gemm_w4_kernel<EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
                           lds) != hipSuccess)
     return K2Q_ELAUNCH;
