@@ -76,14 +76,15 @@ __device__ __forceinline__ void group_coords(int64_t lid, int64_t tiles_a, int64
   ta = r / gsize;
 }
 
-__device__ __forceinline__ void tile_coords(int64_t tiles_a, int64_t tiles_b, int64_t& ta, int64_t& tb) {
-  const int lid = xcd_remap(blockIdx.x, gridDim.x);
-  constexpr int GB = 8;
-  const int64_t in_group = (int64_t)GB * tiles_a;
-  const int64_t g = lid / in_group;
-  const int64_t first_b = g * GB;
-  const int64_t gsize = (tiles_b - first_b) < GB ? (tiles_b - first_b) : GB;
-  const int64_t r = lid % in_group;
+// The same in 32-bit arithmetic, for the W4 kernel's one tile per workgroup (tile counts < 2^31).
+__device__ __forceinline__ void tile_coords(uint32_t tiles_a, uint32_t tiles_b, uint32_t& ta, uint32_t& tb) {
+  const uint32_t lid = (uint32_t)xcd_remap(blockIdx.x, gridDim.x);
+  constexpr uint32_t GB = 8;
+  const uint32_t in_group = GB * tiles_a;
+  const uint32_t g = lid / in_group;
+  const uint32_t first_b = g * GB;
+  const uint32_t gsize = (tiles_b - first_b) < GB ? (tiles_b - first_b) : GB;
+  const uint32_t r = lid - g * in_group;
   tb = first_b + r % gsize;
   ta = r / gsize;
 }
@@ -699,7 +700,7 @@ constexpr int W4_SS = 2 * W4_BA * 2;      // 2 groups x 128 n x bf16
 constexpr int W4_STAGE = W4_SA + W4_SB + W4_SS;
 constexpr int W4_G = 7;                   // DMA instructions per wave and stage: 2 A, 4 B, 1 scales
 constexpr int W4_CROW = 2 * W4_BA + 16;   // epilogue bf16 tile row (padded: rows m and m + 4 on other banks)
-static_assert(W4_BB * W4_CROW <= 2 * W4_STAGE, "epilogue tile fits the stage buffers");
+static_assert(W4_BB * W4_CROW + 4 * W4_BB <= 2 * W4_STAGE, "epilogue tile and s_x fit the stage buffers");
 
 struct W4Args {
   const uint8_t* a;      // N x K/2 packed
@@ -733,11 +734,11 @@ template <int EPI>
 __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) void gemm_w4_kernel(W4Args p) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];   // [2][A | B | scales]
 
-  const int64_t tiles_a = (p.N + W4_BA - 1) / W4_BA;
-  const int64_t tiles_b = (p.M + W4_BB - 1) / W4_BB;
-  int64_t ta, tb;
+  const uint32_t tiles_a = (uint32_t)((p.N + W4_BA - 1) / W4_BA);
+  const uint32_t tiles_b = (uint32_t)((p.M + W4_BB - 1) / W4_BB);
+  uint32_t ta, tb;
   tile_coords(tiles_a, tiles_b, ta, tb);
-  const int64_t A0 = ta * W4_BA, B0 = tb * W4_BB;
+  const int64_t A0 = (int64_t)ta * W4_BA, B0 = (int64_t)tb * W4_BB;
 
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -860,21 +861,24 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
         }
     }
   } else {
-    // Scales, bias and LoRA in registers, then the bf16 tile goes through LDS (row m: 128 n, W4_CROW
-    // bytes) for row-contiguous stores.
+    // s_x (times 2^-7 for the rotations and 1/16 for the nibble placement) staged in LDS for the tile's
+    // 128 rows; scales, bias and LoRA applied in registers; then the bf16 tile goes through LDS (row m:
+    // 128 n, W4_CROW bytes) for row-contiguous stores.
     uint16_t* ctile = reinterpret_cast<uint16_t*>(smem);
+    float* sxs = reinterpret_cast<float*>(smem + W4_BB * W4_CROW);
     lds_barrier();   // every wave is past its last fragment read
-    int64_t n = a0 + c32;
-    n = n < p.N ? n : p.N - 1;
+    if (t < W4_BB) sxs[t] = p.sx[B0 + t < p.M ? B0 + t : p.M - 1] * (0.0078125f * 0.0625f);
+    lds_barrier();
+    const int64_t n = a0 + c32 < p.N ? a0 + c32 : p.N - 1;
     const float bi = p.bias ? p.bias[n] : 0.f;
 #pragma unroll
     for (int ib = 0; ib < W4_IB; ++ib) {
       v16f f;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        int64_t m = B0 + 32 * ib + 8 * (e >> 2) + 4 * h + (e & 3);
-        m = m < p.M ? m : p.M - 1;
-        f[e] = accf[ib][e] * (p.sx[m] * (0.0078125f * 0.0625f)) + bi;   // 2^-7 rotations, 1/16 nibbles
+      for (int j = 0; j < 4; ++j) {
+        const v4f sc = *reinterpret_cast<const v4f*>(sxs + 32 * ib + 8 * j + 4 * h);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) f[4 * j + i] = __builtin_fmaf(accf[ib][4 * j + i], sc[i], bi);
       }
       if (p.lora_rb && p.r > 0)   // f[m][n] += u[m, :] . (scale lora_b[n, :])
         f = lora_block(p.lora_rb, p.lora_ra, p.r, p.lora_scale, p.M, p.N, B0 + 32 * ib, a0, lane, f);
@@ -888,16 +892,17 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
       }
     }
     lds_barrier();
-    uint16_t* out = static_cast<uint16_t*>(p.out);
-    const int cq = t & 31;                   // 4 n per thread
+    const int cq = t & 31;                   // 4 n per thread, 8 rows per pass
     const int64_t n4 = A0 + 4 * cq;
+    const int rows = (int)nb;
     if (n4 < p.N) {
+      uint16_t* o = static_cast<uint16_t*>(p.out) + (B0 + (t >> 5)) * p.N + n4;
+      const uint8_t* c = reinterpret_cast<const uint8_t*>(ctile) + (t >> 5) * W4_CROW + 8 * cq;
 #pragma unroll 4
-      for (int row = t >> 5; row < W4_BB; row += 8) {
-        const int64_t m = B0 + row;
-        if (m < p.M)
-          *reinterpret_cast<v2u*>(out + m * p.N + n4) =
-              *reinterpret_cast<const v2u*>(reinterpret_cast<const uint8_t*>(ctile) + row * W4_CROW + 8 * cq);
+      for (int row = t >> 5; row < rows; row += 8) {
+        *reinterpret_cast<v2u*>(o) = *reinterpret_cast<const v2u*>(c);
+        o += 8 * p.N;
+        c += 8 * W4_CROW;
       }
     }
   }
