@@ -233,8 +233,8 @@ __device__ __forceinline__ void fwht128_rows(v16f (&f)[4], int h) {
 // MI355X (same box, random data) against 64-byte stages fetched as paired half lines through a 5-slot
 // ring: cfg2 GEMM 643.6 -> 626.6 us, cfg3 input-gradient GEMM 331.5 -> 323.1 us; in a copy-only loop with
 // the same waits and barriers, half lines, paired half lines and whole lines move 24, 31 and 35 B/clk/CU.
-// A stage is consumed after every wave's `s_waitcnt vmcnt` for it plus one s_barrier (raw, without
-// __syncthreads' full memory fence, which would drain the prefetches).
+// A stage is consumed after every wave's `s_waitcnt vmcnt` for it plus one lds_barrier() (the wave's LDS
+// operations, then s_barrier; not __syncthreads, whose full memory fence would drain the prefetches).
 constexpr int SBK = 64;                   // unit of reduction lengths in the split plan (half a stage)
 constexpr int WBK = 128;                  // reduction bytes per stage
 constexpr int WSTAGE = 2 * BT * WBK;      // one stage of both operands: 64 KB
@@ -275,7 +275,10 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
+// Workgroup barrier for LDS hand-offs: the wave's own LDS operations complete first (s_barrier alone does
+// not wait for them, and a ds_write still queued when another wave passes the barrier is not yet visible
+// to it); outstanding global loads, the LDS-DMA prefetches among them, are not waited for.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Eight waves (two per SIMD) on a 256 x 256 tile: wave w covers A-rows 128*(w&1) .. +128 and B-rows
 // 64*(w>>1) .. +64 (4 x 2 MFMA blocks, 128 accumulator registers), so both waves of a SIMD issue LDS-DMA
@@ -830,6 +833,14 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
   // by two so that the slot, and with it every LDS address, is a compile-time offset.
   const int ns = (int)(p.K / 128);
   auto step = [&](int st, int slot) {
+    // Priority by work left (3 in the first quarter of the stages .. 0 in the last): under oldest-first
+    // issue the three workgroups sharing a CU otherwise drift apart, and the last one finishes alone with
+    // no other wave to fill its MFMA/VALU gaps.
+    const int lvl = (4 * (ns - st) - 1) / ns;   // 3 .. 0
+    if (lvl == 3) __builtin_amdgcn_s_setprio(3);
+    else if (lvl == 2) __builtin_amdgcn_s_setprio(2);
+    else if (lvl == 1) __builtin_amdgcn_s_setprio(1);
+    else __builtin_amdgcn_s_setprio(0);
     compute(slot);
     wait_vmcnt<0>();                                       // stage st+1
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this wave's reads of the slot have landed

@@ -522,6 +522,47 @@ def test_full_size_cfg2_every_tile(k2, dev):
     assert bool((err <= tol).all()), float((err - tol).max())   # f32 ordering differences
 
 
+@pytest.mark.parametrize("M,N", [(4096, 3072), (16896, 12288)])
+def test_full_size_w4_every_tile(k2, dev, M, N):
+    """W4A8 at full size, every tile (cfg1's shape and the cfg2 shape with int4 weights; codes -8..7, so
+    the unpacking of -8 is covered too).  Group partials come from torch._int_mm per 64-wide group (exact
+    int32).  Unit scales: the f32 result is the exact integer sum.  Random bf16 scales: within the f32
+    accumulation bound of the float64 sum.  The forward epilogue (2^-7 s_x sum_g s acc_g + bias + LoRA,
+    one bf16 rounding) within one bf16 rounding of the same formula in float64."""
+    K, r = 3072, 32
+    g = torch.Generator(device=dev).manual_seed(11)
+    qx = torch.randint(-127, 128, (M, K), device=dev, dtype=torch.int8, generator=g)
+    q = torch.randint(-8, 8, (N, K), device=dev, dtype=torch.int8, generator=g)
+    q4 = torch.from_numpy(orc.pack_i4(q.cpu().numpy())).to(dev)
+    G = K // 64
+    s4 = (torch.rand(G, N, device=dev, generator=g) * 0.02 + 1e-3).bfloat16()
+    exact = torch.zeros(M, N, dtype=torch.float64, device=dev)
+    ref = torch.zeros(M, N, dtype=torch.float64, device=dev)
+    mag = torch.zeros(M, N, dtype=torch.float64, device=dev)
+    for i in range(G):
+        pg = torch._int_mm(qx[:, 64 * i:64 * i + 64].contiguous(), q[:, 64 * i:64 * i + 64].t().contiguous()).double()
+        exact += pg
+        pg *= s4[i].double()[None, :]
+        ref += pg
+        mag += pg.abs()
+    out = k2._lib.gemm_w4a8_f32(qx, q4, torch.ones(G, N, dtype=torch.bfloat16, device=dev))
+    assert torch.equal(out.double(), exact)
+    del exact
+    out = k2._lib.gemm_w4a8_f32(qx, q4, s4).double()
+    assert bool(((out - ref).abs() <= mag * (G * 2.0 ** -24) + 1e-6).all())
+    del out
+    sx = torch.rand(M, device=dev, generator=g) * 0.01 + 1e-3
+    bias = torch.randn(N, device=dev, generator=g) * 0.02
+    u = torch.randn(M, r, device=dev, generator=g)
+    B = torch.randn(N, r, device=dev, generator=g) * 0.01
+    y = k2._lib.gemm_w4a8(qx, sx, q4, s4, bias, u, B, 1.0).double()
+    lora = (u.bfloat16().double() @ B.bfloat16().double().t())
+    yr = ref * (sx.double() * 0.0078125)[:, None] + bias.double()[None, :] + lora
+    err = (y - yr).abs()
+    tol = yr.abs() * 2 ** -8 + mag * (sx.double() * 0.0078125)[:, None] * (G * 2.0 ** -24) + 1e-6
+    assert bool((err <= tol).all()), float((err - tol).max())
+
+
 def test_full_size_cfg3_input_gradient_every_tile(k2, dev):
     """Every tile of cfg3's input gradient (864 tiles on 216 workgroups) against torch in float32: the dense
     product dY W_hat, then the inverse rotation as a block-diagonal Hadamard matmul, times 2^-7, plus g A."""
