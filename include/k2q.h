@@ -93,10 +93,16 @@ int k2q_gemm_w4a8_f32(const int8_t* qx, const uint8_t* qw4, const uint16_t* sw4,
 
 /* (4) Input gradient through the frozen base (autograd of quantize.py:51 + lora.py:47-48):
  *   dx = bf16(2^-7 (dy W_hat) R + g A),   W_hat[n,k] = s_w[n] q[n,k] (or s_w4[n,k/64] q4[n,k]).
- * k2q_dx_prep writes wt = bf16(W_hat)^T (K x N) into a caller workspace; k2q_gemm_dx then runs the
- * bf16 MFMA GEMM with the inverse rotation and the LoRA term fused.  g = lora_scale * dy @ lora_b
- * (M x r f32) is supplied by the caller, lora_a is the module's A (r x K f32, lora.py:39); both nullable.
- * ws: as for k2q_gemm_w8a8 (f32 pieces, added in a fixed order), k2q_gemm_dx_ws_bytes(M, N, K) bytes. */
+ * Two equivalent routes (same bar, different rounding points):
+ * - k2q_dx_prep_eff writes wt = bf16(2^-7 W_hat R)^T (K x N), the effective weight of the straight-through
+ *   forward with the rotation folded in, and k2q_gemm_dx_lin(dy, wt, ...) is then the whole gradient
+ *   (the route the module's backward takes);
+ * - k2q_dx_prep writes wt = bf16(W_hat)^T and k2q_gemm_dx applies the inverse rotation in its epilogue.
+ * g = lora_scale * dy @ lora_b (M x r f32) is supplied by the caller, lora_a is the module's A (r x K
+ * f32, lora.py:39); both nullable.  ws: as for k2q_gemm_w8a8 (f32 pieces, added in a fixed order),
+ * k2q_gemm_dx_ws_bytes(M, N, K) bytes, for either GEMM. */
+int k2q_dx_prep_eff(const int8_t* qw, const float* sw, const uint8_t* qw4, const uint16_t* sw4,
+                    int64_t N, int64_t K, uint16_t* wt, void* stream);
 int k2q_dx_prep(const int8_t* qw, const float* sw, const uint8_t* qw4, const uint16_t* sw4,
                 int64_t N, int64_t K, uint16_t* wt, void* stream);
 int64_t k2q_gemm_dx_ws_bytes(int64_t M, int64_t N, int64_t K);

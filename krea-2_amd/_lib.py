@@ -52,6 +52,7 @@ _SIGNATURES = {
     "k2q_mfma_probe_i8_ops": ([_i64, _i64], _i64),
     "k2q_mfma_probe_i8": ([_i64, _i64, _p, _p], _int),
     "k2q_dx_prep": ([_p, _p, _p, _p, _i64, _i64, _p, _p], _int),
+    "k2q_dx_prep_eff": ([_p, _p, _p, _p, _i64, _i64, _p, _p], _int),
     "k2q_gemm_dx_ws_bytes": ([_i64, _i64, _i64], _i64),
     "k2q_gemm_dx": ([_p, _p, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _p], _int),
 }
@@ -355,9 +356,12 @@ def gemm_w4a8_f32(qx, q4, s4) -> torch.Tensor:
 # ----------------------------------------------------------------------------------------------------------
 # (4) input gradient
 # ----------------------------------------------------------------------------------------------------------
-def gemm_dx(dy, qw, sw, *, w4: bool = False, g=None, lora_a=None, split: bool = True) -> torch.Tensor:
+def gemm_dx(dy, qw, sw, *, w4: bool = False, g=None, lora_a=None, split: bool = True,
+            fold_rotation: bool = True) -> torch.Tensor:
     """``dx = bf16(2^-7 (dy W_hat) R + g lora_A)`` (M,K); ``dy`` (M,N) bf16, ``g`` (M,r) f32 already
-    scaled (``lora_scale * dy @ lora_B``), ``lora_a`` (r,K) f32."""
+    scaled (``lora_scale * dy @ lora_B``), ``lora_a`` (r,K) f32.  ``fold_rotation`` (default) builds the
+    effective weight ``bf16(2^-7 W_hat R)^T`` and runs the plain GEMM; otherwise ``bf16(W_hat)^T`` and the
+    GEMM with the inverse rotation in its epilogue."""
     _need(dy, "dy", torch.bfloat16, 2)
     dev = dy.device
     M, N = dy.shape
@@ -390,12 +394,14 @@ def gemm_dx(dy, qw, sw, *, w4: bool = False, g=None, lora_a=None, split: bool = 
     st = _stream(dev)
     wt = torch.empty((K, N), dtype=torch.bfloat16, device=dev)
     lib = load()
-    _check(lib.k2q_dx_prep(None if w4 else _ptr(qw), None if w4 else _ptr(sw), _ptr(qw) if w4 else None,
-                           _ptr(sw) if w4 else None, N, K, _ptr(wt), st), "k2q_dx_prep")
+    prep = lib.k2q_dx_prep_eff if fold_rotation else lib.k2q_dx_prep
+    _check(prep(None if w4 else _ptr(qw), None if w4 else _ptr(sw), _ptr(qw) if w4 else None,
+                _ptr(sw) if w4 else None, N, K, _ptr(wt), st), "k2q_dx_prep")
     dx = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
     ws, nws = _workspace(lib.k2q_gemm_dx_ws_bytes(M, N, K) if split else 0, dev)
-    _check(lib.k2q_gemm_dx(_ptr(dy), _ptr(wt), M, N, K, _ptr(g), _ptr(lora_a) if r else None, r, _ptr(dx),
-                           _ptr(ws), nws, st), "k2q_gemm_dx")
+    gemm = lib.k2q_gemm_dx_lin if fold_rotation else lib.k2q_gemm_dx
+    _check(gemm(_ptr(dy), _ptr(wt), M, N, K, _ptr(g), _ptr(lora_a) if r else None, r, _ptr(dx),
+                _ptr(ws), nws, st), "k2q_gemm_dx")
     return dx
 
 

@@ -327,6 +327,78 @@ __global__ __launch_bounds__(256) void dequant_t_kernel(const int8_t* __restrict
   }
 }
 
+// wt[k][n] = bf16(2^-7 (W_hat R)[n][k]) for a 64 (n) x 128 (k) tile: the effective weight of the
+// straight-through forward (x -> 2^-7 s_x (x R) W_hat^T, R the unnormalised block Hadamard), transposed, so
+// the input gradient is the plain product dy wt^T.  Thread t holds 32 k of row n = t/4 (k = 32 (t%4) +
+// 0..31 of the 128-wide Hadamard block); the butterflies on k bits 0-4 run in registers, bits 5 and 6
+// between the four threads of a quad (DPP).  Then an LDS transpose, as in dequant_t_kernel.
+template <bool W4>
+__global__ __launch_bounds__(256) void rot_dequant_t_kernel(const int8_t* __restrict__ qw,
+                                                            const float* __restrict__ sw,
+                                                            const uint8_t* __restrict__ qw4,
+                                                            const uint16_t* __restrict__ sw4, int64_t N,
+                                                            int64_t K, uint16_t* __restrict__ wt) {
+  __shared__ uint16_t tile[128][64 + 2];
+  const int t = threadIdx.x;
+  const int64_t n0 = (int64_t)blockIdx.x * 64, k0 = (int64_t)blockIdx.y * 128;
+  {
+    const int nl = t >> 2, kq = t & 3;
+    const int64_t n = n0 + nl < N ? n0 + nl : N - 1;   // rows past N computed on row N-1, never written
+    float v[32];
+    if (W4) {
+      const uint4 p = *reinterpret_cast<const uint4*>(qw4 + n * (K / 2) + (k0 + 32 * kq) / 2);
+      const float s = bf16_bits_to_f32(sw4[((k0 + 32 * kq) / 64) * N + n]);
+      const uint32_t w[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+      for (int c = 0; c < 2; ++c)        // two 16-wide chunks: byte j holds codes j and j + 8
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t byte = (w[2 * c + (j >> 2)] >> (8 * (j & 3))) & 0xffu;
+          v[16 * c + j] = (float)((int)((byte & 0xfu) ^ 8u) - 8) * s;
+          v[16 * c + j + 8] = (float)((int)((byte >> 4) ^ 8u) - 8) * s;
+        }
+    } else {
+      const uint4 p0 = *reinterpret_cast<const uint4*>(qw + n * K + k0 + 32 * kq);
+      const uint4 p1 = *reinterpret_cast<const uint4*>(qw + n * K + k0 + 32 * kq + 16);
+      const float s = sw[n];
+      const uint32_t w[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+      for (int j = 0; j < 32; ++j) v[j] = (float)(int8_t)((w[j >> 2] >> (8 * (j & 3))) & 0xffu) * s;
+    }
+#pragma unroll
+    for (int st = 1; st < 32; st <<= 1)
+#pragma unroll
+      for (int j = 0; j < 32; ++j)
+        if (!(j & st)) {
+          const float a = v[j], b = v[j + st];
+          v[j] = a + b;
+          v[j + st] = a - b;
+        }
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {   // k bit 5: partner t ^ 1 (quad_perm 1,0,3,2)
+      const float o = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[j]), 0xB1, 0xF, 0xF, false));
+      v[j] = (kq & 1) ? o - v[j] : v[j] + o;
+    }
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {   // k bit 6: partner t ^ 2 (quad_perm 2,3,0,1)
+      const float o = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[j]), 0x4E, 0xF, 0xF, false));
+      v[j] = (kq & 2) ? o - v[j] : v[j] + o;
+    }
+#pragma unroll
+    for (int j = 0; j < 32; ++j) tile[32 * kq + j][nl] = (uint16_t)f32_to_bf16_bits(v[j] * 0.0078125f);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    const int kl = 32 * pass + (t >> 3), nl = 8 * (t & 7);
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = (uint32_t)tile[kl][nl + 2 * j] | ((uint32_t)tile[kl][nl + 2 * j + 1] << 16);
+    uint16_t* dst = wt + (k0 + kl) * N + n0 + nl;
+    if (n0 + nl + 8 <= N) *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 }  // namespace
 
 // A-stationary plan: K cut into workgroup spans (slices), rows split so that slices x row groups ~ CUs.
@@ -415,6 +487,21 @@ int lora_down_impl(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const f
     hipLaunchKernelGGL(lora_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st,
                        static_cast<const v4f*>(ws), p.ks, n4, reinterpret_cast<v4f*>(u));
   }
+  return k2q_launch_status();
+}
+
+extern "C" int k2q_dx_prep_eff(const int8_t* qw, const float* sw, const uint8_t* qw4, const uint16_t* sw4,
+                               int64_t N, int64_t K, uint16_t* wt, void* stream) {
+  const bool w4 = qw4 != nullptr;
+  if (N < 1 || K < 128 || K % 128 || !wt) return K2Q_EINVAL;
+  if (w4 ? (!sw4 || !k2q_aligned(qw4, 16)) : (!qw || !sw || !k2q_aligned(qw, 16))) return K2Q_EINVAL;
+  if (!k2q_aligned(wt, 16) || N % 8) return K2Q_EINVAL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)((N + 63) / 64), (unsigned)(K / 128));
+  if (w4)
+    hipLaunchKernelGGL(rot_dequant_t_kernel<true>, grid, dim3(256), 0, st, nullptr, nullptr, qw4, sw4, N, K, wt);
+  else
+    hipLaunchKernelGGL(rot_dequant_t_kernel<false>, grid, dim3(256), 0, st, qw, sw, nullptr, nullptr, N, K, wt);
   return k2q_launch_status();
 }
 

@@ -261,9 +261,10 @@ def test_forward_w8a8_skinny_m(k2, dev, M, K, N, r, bias):
 
 
 # ------------------------------------------------------------------------------------------- kernel (4)
+@pytest.mark.parametrize("fold", [True, False])
 @pytest.mark.parametrize("M,K,N,r,w4", [(256, 256, 256, 0, False), (200, 384, 320, 16, False),
                                         (512, 1024, 512, 64, False), (256, 512, 256, 32, True)])
-def test_input_gradient(k2, dev, M, K, N, r, w4):
+def test_input_gradient(k2, dev, M, K, N, r, w4, fold):
     w = make_w(N, K, seed=M + K)
     g = torch.Generator().manual_seed(5)
     dy = (torch.randn(M, N, generator=g) * 1e-3).to(torch.bfloat16)
@@ -276,11 +277,38 @@ def test_input_gradient(k2, dev, M, K, N, r, w4):
         qw, sw = k2._lib.quant_weight_i8(w.to(dev))
         qo, so = orc.quant_weight_i8(w.float().numpy())
     gd = (dy.float() @ B).contiguous() if r else None
-    dx = k2._lib.gemm_dx(dy.to(dev), qw, sw, w4=w4, g=gd.to(dev) if r else None, lora_a=A.to(dev) if r else None)
+    dx = k2._lib.gemm_dx(dy.to(dev), qw, sw, w4=w4, g=gd.to(dev) if r else None, lora_a=A.to(dev) if r else None,
+                         fold_rotation=fold)
     x_dummy = np.zeros((M, K))
     ref = orc.backward(dy.float().numpy(), x_dummy, qo, so, w4=w4, lora_A=None if A is None else A.numpy(),
                        lora_B=None if B is None else B.numpy(), lora_scale=1.0)
     assert rel_frob(dx.float().cpu().numpy(), ref["dx64"]) < REL_FROB_TOL
+
+
+@pytest.mark.parametrize("N,K,w4", [(64, 128, False), (200, 384, False), (3072, 12288, False), (96, 512, True)])
+def test_effective_weight_prep(k2, dev, N, K, w4):
+    """k2q_dx_prep_eff: wt = bf16(2^-7 W_hat R)^T against the dense block-Hadamard product in float32 (one
+    bf16 rounding apart at most: the butterfly and the matmul add in different orders)."""
+    w = make_w(N, K, seed=N + K + 1)
+    if w4:
+        qw, sw = k2._lib.quant_weight_i4(w.to(dev))
+        q = torch.from_numpy(orc.unpack_i4(qw.cpu().numpy())).to(dev).float()
+        what = q * sw.float().t().repeat_interleave(64, dim=1)
+    else:
+        qw, sw = k2._lib.quant_weight_i8(w.to(dev))
+        what = qw.float() * sw[:, None]
+    lib = k2._lib.load()
+    wt = torch.empty(K, N, dtype=torch.bfloat16, device=dev)
+    P = k2._lib._ptr
+    rc = lib.k2q_dx_prep_eff(None if w4 else P(qw), None if w4 else P(sw), P(qw) if w4 else None,
+                             P(sw) if w4 else None, N, K, P(wt), k2._lib._stream(dev))
+    assert rc == 0
+    torch.cuda.synchronize()
+    H = torch.from_numpy(__import__("scipy.linalg").linalg.hadamard(128).astype(np.float32)).to(dev)
+    ref = ((what.view(N, K // 128, 128) @ H).view(N, K) * 0.0078125).t()
+    err = (wt.float() - ref).abs()
+    tol = ref.abs() * 2 ** -8 + float(ref.abs().max()) * 2 ** -20   # plus f32 order noise near zero
+    assert bool((err <= tol).all()), float((err - tol).max())
 
 
 # ------------------------------------------------------------------------------------------- split schedule
@@ -563,7 +591,8 @@ def test_full_size_w4_every_tile(k2, dev, M, N):
     assert bool((err <= tol).all()), float((err - tol).max())
 
 
-def test_full_size_cfg3_input_gradient_every_tile(k2, dev):
+@pytest.mark.parametrize("fold", [True, False])
+def test_full_size_cfg3_input_gradient_every_tile(k2, dev, fold):
     """Every tile of cfg3's input gradient (864 tiles on 216 workgroups) against torch in float32: the dense
     product dY W_hat, then the inverse rotation as a block-diagonal Hadamard matmul, times 2^-7, plus g A."""
     M, K, N, r = 4608, 12288, 3072, 64
@@ -573,7 +602,7 @@ def test_full_size_cfg3_input_gradient_every_tile(k2, dev):
     A = torch.randn(r, K, device=dev, generator=g) * 0.01
     gd = torch.randn(M, r, device=dev, generator=g) * 1e-3
     qw, sw = k2._lib.quant_weight_i8(w.to(dev))
-    dx = k2._lib.gemm_dx(dy, qw, sw, g=gd, lora_a=A).float()
+    dx = k2._lib.gemm_dx(dy, qw, sw, g=gd, lora_a=A, fold_rotation=fold).float()
     w_hat = (qw.float() * sw[:, None]).bfloat16().float()           # bf16(s_w q_w), N x K
     t = dy.float() @ w_hat                                          # M x K, f32
     H = torch.from_numpy(__import__("scipy.linalg").linalg.hadamard(128).astype(np.float32)).to(dev)
