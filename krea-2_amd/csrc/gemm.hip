@@ -682,8 +682,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int64_t lid, int kb
 
 // ---------------------------------------------------------------------------------------------------------
 // W4A8: A operand = packed int4 weights (rows n, K/2 bytes per row), bf16 group scales sw4[g][n].
-// Tile 128 (n) x 128 (m) per 256-thread workgroup, two workgroups per CU so that one wave's per-group
-// scaling runs while another's MFMAs do.  Wave w owns the 32 n-rows 32w..32w+31 and all 128 m, so every
+// Tile 128 (n) x 128 (m) per 256-thread workgroup, three workgroups per CU (166 VGPRs) so that one wave's
+// per-group scaling runs while another's MFMAs do (wave priority follows the work left, see step()).
+// Wave w owns the 32 n-rows 32w..32w+31 and all 128 m, so every
 // packed weight byte is unpacked by exactly one wave.  The MFMA takes the x codes as its first operand, so
 // a lane's 16 results share one n (the lane's column) and need one group scale.  A stage is 128 of K,
 // double-buffered in LDS and filled by LDS-DMA from buffer resources (per-lane offsets fixed, the stage
