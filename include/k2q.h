@@ -51,6 +51,26 @@ int k2q_rotquant(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
 int k2q_quant_weight_i4(const void* w, int w_dtype, int64_t N, int64_t K,
                         uint8_t* qw4, uint16_t* sw4, void* stream);
 
+/* Producer-fused rotate/quant: the op that makes a quantized linear's input, computed in the same pass
+ * that rotates and quantizes it.  Each writes h (M x K bf16, row stride K: the tensor the linear receives,
+ * which its LoRA down-projection and backward read) and the codes / scales of k2q_rotquant(h), bit-identical
+ * to a separate call on h.
+ * k2q_swiglu_rotquant replaces `F.silu(self.gate(x)) * self.up(x)` of SwiGLU.forward (mmdit.py:177-178):
+ *   h = bf16(bf16(silu(g)) * u), g / u the bf16 gate / up outputs (row strides ldg / ldu).
+ * k2q_rmsmod_rotquant replaces `(1 + scale) * self.prenorm(x) + shift` of SingleStreamBlock.forward
+ * (mmdit.py:314-317) with RMSNorm.forward (mmdit.py:156-161):
+ *   n = bf16((x * rsqrt(mean_k x^2 + eps)) * (norm_scale + 1)),  h = bf16(bf16(bf16(1 + p) * n) + b),
+ *   p / b = bf16 mod_scale / mod_shift at entry (row / rows_per_batch) * ld_mod (ld_mod 0: one entry).
+ * k2q_swiglu_bwd is the autograd of the SwiGLU product (n bf16 elements, n % 8 == 0):
+ *   du = bf16(dh * bf16(silu(g))),  dg = bf16((bf16(dh * u) * sig) * (1 + g (1 - sig))),  sig = sigmoid(g). */
+int k2q_swiglu_rotquant(const uint16_t* gate, int64_t ldg, const uint16_t* up, int64_t ldu, int64_t M, int64_t K,
+                        uint16_t* h, int8_t* q, float* s, void* stream);
+int k2q_rmsmod_rotquant(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, const float* norm_scale, float eps,
+                        const uint16_t* mod_scale, const uint16_t* mod_shift, int64_t ld_mod,
+                        int64_t rows_per_batch, uint16_t* h, int8_t* q, float* s, void* stream);
+int k2q_swiglu_bwd(const uint16_t* dh, const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* dgate,
+                   uint16_t* dup, void* stream);
+
 /* LoRA down-projection u = x.f32 @ A^T (lora.py:47, first product).  When the rows alone do not fill the
  * GPU, K is cut into slices whose partials meet in ws (k2q_lora_down_ws_bytes(M, K, r) bytes; 0 means none
  * is used) and are added in slice order; with ws == NULL or ws_bytes too small it runs unsliced. */

@@ -35,6 +35,9 @@ _SIGNATURES = {
     "k2q_check_device": ([], _int),
     "k2q_rotquant": ([_p, _int, _i64, _i64, _i64, _p, _p, _p, _p], _int),
     "k2q_quant_weight_i4": ([_p, _int, _i64, _i64, _p, _p, _p], _int),
+    "k2q_swiglu_rotquant": ([_p, _i64, _p, _i64, _i64, _i64, _p, _p, _p, _p], _int),
+    "k2q_rmsmod_rotquant": ([_p, _i64, _i64, _i64, _p, _f32, _p, _p, _i64, _i64, _p, _p, _p, _p], _int),
+    "k2q_swiglu_bwd": ([_p, _p, _p, _i64, _p, _p, _p], _int),
     "k2q_lora_down_ws_bytes": ([_i64, _i64, _i64], _i64),
     "k2q_lora_down": ([_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _p], _int),
     "k2q_lora_grads_ws_bytes": ([_i64, _i64, _i64, _i64], _i64),
@@ -164,6 +167,93 @@ def rotquant(x: torch.Tensor, want_xrot: bool = False):
     _check(load().k2q_rotquant(_ptr(x), dt, M, K, K, _ptr(q), _ptr(s), _ptr(xr), _stream(x.device)),
            "k2q_rotquant")
     return q, s, xr
+
+
+def _need_rows(t: torch.Tensor, name: str, dev: torch.device | None = None) -> None:
+    """A 2-D bf16 tensor whose rows are contiguous and 16-byte aligned (the row stride may exceed K)."""
+    if not isinstance(t, torch.Tensor) or t.dtype != torch.bfloat16 or t.dim() != 2:
+        raise ValueError(f"{name} must be a 2-D bf16 tensor")
+    if t.stride(1) != 1 or t.stride(0) < t.shape[1] or t.stride(0) % 8 or t.data_ptr() % 16:
+        raise ValueError(f"{name} needs contiguous 16-byte aligned rows (strides {t.stride()})")
+    if dev is not None and t.device != dev:
+        raise ValueError(f"{name} is on {t.device}, expected {dev}")
+
+
+def swiglu_rotquant(g: torch.Tensor, u: torch.Tensor):
+    """``h = bf16(bf16(silu(g)) * u)`` with the codes of ``rotquant(h)`` from the same pass.
+    ``g``, ``u`` (M,K) bf16 with contiguous rows.  Returns ``(h bf16 (M,K), q int8 (M,K), s f32 (M,))``."""
+    _need_rows(g, "gate")
+    _need_rows(u, "up", g.device)
+    if g.shape != u.shape:
+        raise ValueError(f"gate {tuple(g.shape)} and up {tuple(u.shape)} differ in shape")
+    M, K = g.shape
+    _check_k(K)
+    if M < 1:
+        raise ValueError("no rows")
+    _device_check(g.device)
+    h = torch.empty((M, K), dtype=torch.bfloat16, device=g.device)
+    q = torch.empty((M, K), dtype=torch.int8, device=g.device)
+    s = torch.empty((M,), dtype=torch.float32, device=g.device)
+    _check(load().k2q_swiglu_rotquant(_ptr(g), g.stride(0), _ptr(u), u.stride(0), M, K, _ptr(h), _ptr(q), _ptr(s),
+                                      _stream(g.device)), "k2q_swiglu_rotquant")
+    return h, q, s
+
+
+def rmsmod_rotquant(x: torch.Tensor, norm_scale: torch.Tensor, eps: float, mod_scale: torch.Tensor,
+                    mod_shift: torch.Tensor, rows_per_batch: int):
+    """Modulated RMSNorm ``h = bf16(bf16(bf16(1 + p) * n) + b)``, ``n = bf16(rms_norm(x) * (norm_scale + 1))``,
+    with the codes of ``rotquant(h)`` from the same pass.  ``x`` (M,K) bf16 rows; ``norm_scale`` (K,) f32;
+    ``mod_scale`` / ``mod_shift`` (B,K) bf16 with contiguous rows and one common row stride, row ``m`` using
+    entry ``m // rows_per_batch`` (B == 1: every row uses entry 0).  Returns ``(h, q, s)``."""
+    _need_rows(x, "x")
+    dev = x.device
+    M, K = x.shape
+    _check_k(K)
+    if M < 1:
+        raise ValueError("no rows")
+    _need(norm_scale, "norm_scale", torch.float32, 1, dev)
+    if norm_scale.shape[0] != K:
+        raise ValueError(f"norm_scale has {norm_scale.shape[0]} entries, x has {K} features")
+    for t, nm in ((mod_scale, "mod_scale"), (mod_shift, "mod_shift")):
+        if not isinstance(t, torch.Tensor) or t.dtype != torch.bfloat16 or t.dim() != 2 or t.shape[1] != K:
+            raise ValueError(f"{nm} must be a (B, {K}) bf16 tensor")
+        if t.stride(1) != 1 or t.data_ptr() % 16 or t.device != dev:
+            raise ValueError(f"{nm} needs contiguous 16-byte aligned rows on {dev}")
+    if mod_scale.shape != mod_shift.shape:
+        raise ValueError("mod_scale and mod_shift differ in shape")
+    B = mod_scale.shape[0]
+    ldm = 0 if B == 1 else mod_scale.stride(0)
+    if B > 1 and (mod_shift.stride(0) != ldm or ldm % 8):
+        raise ValueError("mod_scale and mod_shift need one common row stride, a multiple of 8")
+    rows_per_batch = int(rows_per_batch)
+    if rows_per_batch < 1 or (B > 1 and rows_per_batch * B != M):
+        raise ValueError(f"rows_per_batch={rows_per_batch} does not split {M} rows into {B} entries")
+    _device_check(dev)
+    h = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+    q = torch.empty((M, K), dtype=torch.int8, device=dev)
+    s = torch.empty((M,), dtype=torch.float32, device=dev)
+    _check(load().k2q_rmsmod_rotquant(_ptr(x), x.stride(0), M, K, _ptr(norm_scale), float(eps), _ptr(mod_scale),
+                                      _ptr(mod_shift), ldm, rows_per_batch if B > 1 else M, _ptr(h), _ptr(q),
+                                      _ptr(s), _stream(dev)), "k2q_rmsmod_rotquant")
+    return h, q, s
+
+
+def swiglu_bwd(dh: torch.Tensor, g: torch.Tensor, u: torch.Tensor):
+    """Autograd of ``bf16(bf16(silu(g)) * u)``: ``(dg, du)``, bf16, shapes of ``g``; all contiguous."""
+    _need(dh, "dh", torch.bfloat16)
+    _need(g, "gate", torch.bfloat16, dev=dh.device)
+    _need(u, "up", torch.bfloat16, dev=dh.device)
+    if not (dh.shape == g.shape == u.shape):
+        raise ValueError("dh, gate and up differ in shape")
+    n = dh.numel()
+    if n < 1 or n % 8:
+        raise ValueError(f"element count {n} must be a positive multiple of 8")
+    _device_check(dh.device)
+    dg = torch.empty_like(g)
+    du = torch.empty_like(u)
+    _check(load().k2q_swiglu_bwd(_ptr(dh), _ptr(g), _ptr(u), n, _ptr(dg), _ptr(du), _stream(dh.device)),
+           "k2q_swiglu_bwd")
+    return dg, du
 
 
 def quant_weight_i8(w: torch.Tensor):

@@ -15,7 +15,7 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 INCLUDE = HERE.parent / "include"
 LIB = HERE / "libk2q.so"
-SOURCES = ("api.hip", "rotquant.hip", "gemm.hip", "gemv.hip", "lora.hip", "lora_grad.hip", "fp8.hip", "probe.hip")
+SOURCES = ("api.hip", "rotquant.hip", "producers.hip", "gemm.hip", "gemv.hip", "lora.hip", "lora_grad.hip", "fp8.hip", "probe.hip")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

@@ -9,14 +9,8 @@
 //     correctly rounded float32 division; q = rint(v*inv) (round half to even), |q| <= 127.
 //   * int4 groups: absmax of each 64-wide group, s = bf16_rne(absmax/7), q = clamp(rint(v/s), -7, 7).
 //
-// Layout in registers: a team of T = 64*WPR lanes owns one row.  Each lane holds 16 contiguous elements
-// per chunk (two 16-byte loads for bf16).  Inside a 16-lane DPP row, lane bit 2 selects one of two
-// Hadamard blocks and lane bits 0, 1, 3 are block bits 4, 5, 6, so the four in-lane stages are strides
-// 1..8 and the three cross-lane stages are single DPP ops: quad_perm xor1, quad_perm xor2, row_ror:8.
-// Cross-lane stages are one exact FMA per element: v <- partner * c + v with c = -1 on the lane holding
-// the upper element, which leaves that lane holding the negated result.  The sign each lane ends with is
-// (-1)^(lane bit0 + bit1 + bit3); it is folded into the quantizer's multiplier (sign flips are exact).
-#include "k2q_common.h"
+// The register layout and the butterfly are in rotation.h.
+#include "rotation.h"
 
 namespace {
 
@@ -24,47 +18,7 @@ constexpr int kMaxNCH = 4;  // chunks of 16 elements per lane (K <= 1024 * WPR *
 
 enum { MODE_ROW_I8 = 0, MODE_GROUP_I4 = 1 };
 
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-
-template <typename Tin>
-__device__ __forceinline__ void load16(const Tin* p, bool ok, float (&v)[16]);
-
-template <>
-__device__ __forceinline__ void load16<__bf16>(const __bf16* p, bool ok, float (&v)[16]) {
-  uint4 a = make_uint4(0, 0, 0, 0), b = make_uint4(0, 0, 0, 0);
-  if (ok) {
-    a = *reinterpret_cast<const uint4*>(p);
-    b = *reinterpret_cast<const uint4*>(p + 8);
-  }
-  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    v[2 * j] = __uint_as_float(w[j] << 16);
-    v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
-  }
-}
-
-template <>
-__device__ __forceinline__ void load16<float>(const float* p, bool ok, float (&v)[16]) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (ok) a = reinterpret_cast<const float4*>(p)[j];
-    v[4 * j] = a.x;
-    v[4 * j + 1] = a.y;
-    v[4 * j + 2] = a.z;
-    v[4 * j + 3] = a.w;
-  }
-}
-
-__device__ __forceinline__ float wave_max(float m) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-  return m;
-}
+using namespace k2q_rot;
 
 template <typename Tin, int WPR, int MODE, int kNCH>
 __global__ __launch_bounds__(256) void rotquant_kernel(const Tin* __restrict__ x, int64_t M, int K,
@@ -83,9 +37,7 @@ __global__ __launch_bounds__(256) void rotquant_kernel(const Tin* __restrict__ x
   const int64_t row = (int64_t)blockIdx.x * ROWS + wave / WPR;
   const int t = (wave % WPR) * 64 + lane;
   const int l = t & 15;
-  const int blk = 2 * (t >> 4) + ((l >> 2) & 1);
-  const int pos = 16 * ((l & 1) | (((l >> 1) & 1) << 1) | (((l >> 3) & 1) << 2));
-  const int off = blk * K2Q_HADAMARD + pos;
+  const int off = lane_offset(t);
   const bool row_ok = row < M;
   constexpr int nch = kNCH;
 
@@ -106,31 +58,7 @@ __global__ __launch_bounds__(256) void rotquant_kernel(const Tin* __restrict__ x
   float amax = 0.f;
 #pragma unroll
   for (int c = 0; c < kNCH; ++c) {
-#pragma unroll
-    for (int st = 1; st < 16; st <<= 1) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        if (i & st) continue;
-        const float a = v[c][i], b = v[c][i + st];
-        v[c][i] = a + b;
-        v[c][i + st] = a - b;
-      }
-    }
-    // One v_fmac_f32_dpp per element and stage: v += partner(v) * c.  The 16 registers are visited
-    // round-robin, so a DPP read never follows the VALU write of its own source closer than 15
-    // instructions; the s_nop before each stage covers the in-lane stage's last writes.
-    asm volatile("s_nop 1" ::: "memory");
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-      asm volatile("v_fmac_f32_dpp %0, %0, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf" : "+v"(v[c][i]) : "v"(c1));
-    asm volatile("s_nop 1" ::: "memory");
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-      asm volatile("v_fmac_f32_dpp %0, %0, %1 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf" : "+v"(v[c][i]) : "v"(c2));
-    asm volatile("s_nop 1" ::: "memory");
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-      asm volatile("v_fmac_f32_dpp %0, %0, %1 row_ror:8 row_mask:0xf bank_mask:0xf" : "+v"(v[c][i]) : "v"(c8));
+    rotate16(v[c], c1, c2, c8);
     if (MODE == MODE_ROW_I8) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[c][i]));
@@ -157,25 +85,12 @@ __global__ __launch_bounds__(256) void rotquant_kernel(const Tin* __restrict__ x
     for (int c = 0; c < kNCH; ++c) {
       const int col = c * CW + off;
       if (c >= nch || col >= K) continue;
-      uint32_t w[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        uint32_t p = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int qi = (int)__builtin_rintf(v[c][4 * j + e] * mul);
-          p |= ((uint32_t)qi & 0xffu) << (8 * e);
-        }
-        w[j] = p;
-      }
-      *reinterpret_cast<uint4*>(qr + col) = make_uint4(w[0], w[1], w[2], w[3]);
+      store_codes16(qr + col, v[c], mul);
       if (xrot) {
-        uint32_t h[8];
+        float xo[16];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) h[j] = pack_bf16x2(v[c][2 * j] * rs, v[c][2 * j + 1] * rs);
-        uint16_t* xo = xrot + row * (int64_t)K + col;
-        reinterpret_cast<uint4*>(xo)[0] = make_uint4(h[0], h[1], h[2], h[3]);
-        reinterpret_cast<uint4*>(xo)[1] = make_uint4(h[4], h[5], h[6], h[7]);
+        for (int i = 0; i < 16; ++i) xo[i] = v[c][i] * rs;
+        store16_bf16(xrot + row * (int64_t)K + col, xo);
       }
     }
   } else {

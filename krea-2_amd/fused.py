@@ -1,0 +1,168 @@
+"""Producer fusion: the ops that make the quantized linears' inputs, fused with their rotate/quant.
+
+In a Krea 2 block every ConvRot linear receives one of three tensors (reference ``mmdit.py:310-319``):
+the modulated RMSNorm output ``(1 + scale) * norm(x) + shift`` (read by ``wq/wk/wv/gate`` and by
+``mlp.gate/up``), the attention output (read by ``wo``) and the SwiGLU product ``silu(gate) * up`` (read by
+``mlp.down``).  The two producers here compute that tensor AND its int8 codes in one gfx950 pass
+(``k2q_rmsmod_rotquant`` / ``k2q_swiglu_rotquant``), then hand the codes to the shared-input cache, so the
+layers that read the tensor run no rotate/quant of their own.  Outputs are the reference's eager bf16
+results (same rounding points), and the codes equal a separate rotate/quant of them bit for bit.
+
+:func:`fuse_producers` patches a DiT's blocks in place (call it after ``quantize_dit_convrot`` and
+``inject_lora``); :func:`modulated_rmsnorm` and :func:`swiglu` are the two operations for model code that
+calls them directly.
+"""
+from __future__ import annotations
+
+import types
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _lib
+from .quantize import ConvRotLinear, shared_input_quant
+
+
+def _rows(t: torch.Tensor, K: int) -> torch.Tensor:
+    t2 = t.reshape(-1, K)
+    if t2.stride(1) != 1 or t2.stride(0) % 8 or t2.data_ptr() % 16:
+        t2 = t2.contiguous()
+    return t2
+
+
+class _SwiGLUQuantFn(torch.autograd.Function):
+    """Forward ``h = bf16(bf16(silu(g)) * u)`` (``mmdit.py:178``) with the codes of ``h``; backward
+    ``k2q_swiglu_bwd`` (the autograd of the two eager bf16 ops)."""
+
+    @staticmethod
+    def forward(ctx, g2, u2):
+        h, q, s = _lib.swiglu_rotquant(g2, u2)
+        ctx.save_for_backward(g2, u2)
+        ctx.mark_non_differentiable(q, s)
+        return h, q, s
+
+    @staticmethod
+    def backward(ctx, dh, _dq, _ds):
+        g2, u2 = ctx.saved_tensors
+        dh = dh.contiguous()
+        if dh.dtype != torch.bfloat16:
+            dh = dh.to(torch.bfloat16)
+        g2, u2 = g2.contiguous(), u2.contiguous()
+        dg, du = _lib.swiglu_bwd(dh, g2, u2)
+        return dg, du
+
+
+def swiglu(gate_out: torch.Tensor, up_out: torch.Tensor) -> torch.Tensor:
+    """``F.silu(gate_out) * up_out`` (bf16), with the result's int8 codes recorded for the next ConvRot layer
+    that receives it (``SwiGLU.forward``, ``mmdit.py:177-178``)."""
+    if gate_out.shape != up_out.shape:
+        raise ValueError(f"gate {tuple(gate_out.shape)} and up {tuple(up_out.shape)} differ in shape")
+    if gate_out.dtype != torch.bfloat16 or up_out.dtype != torch.bfloat16:
+        raise NotImplementedError("the fused SwiGLU runs bf16 tensors (the DiT dtype)")
+    K = gate_out.shape[-1]
+    h, q, s = _SwiGLUQuantFn.apply(_rows(gate_out, K), _rows(up_out, K))
+    h = h.reshape(gate_out.shape)
+    shared_input_quant.seed(h, q, s)
+    return h
+
+
+class _RmsModQuantFn(torch.autograd.Function):
+    """Forward: the modulated RMSNorm of ``mmdit.py:314-317`` with the codes of its output (one gfx950 pass).
+    Backward: the reference's own formula re-run on the saved inputs under autograd (``F.rms_norm`` and the
+    eager bf16 modulation), so the gradients are the reference's."""
+
+    @staticmethod
+    def forward(ctx, x2, norm_scale, mod_scale, mod_shift, eps, rows_per_batch):
+        h, q, s = _lib.rmsmod_rotquant(x2, norm_scale.float().contiguous(), eps, mod_scale, mod_shift,
+                                       rows_per_batch)
+        ctx.eps, ctx.rpb = eps, rows_per_batch
+        ctx.save_for_backward(x2, norm_scale, mod_scale, mod_shift)
+        ctx.mark_non_differentiable(q, s)
+        return h, q, s
+
+    @staticmethod
+    def backward(ctx, dh, _dq, _ds):
+        x2, ns, ms, mb = ctx.saved_tensors
+        M, K = x2.shape
+        B = ms.shape[0]
+        rpb = ctx.rpb if B > 1 else M
+        need = ctx.needs_input_grad[:4]
+        with torch.enable_grad():
+            leaves = [t.detach().requires_grad_(n) for t, n in zip((x2, ns, ms, mb), need)]
+            x3 = leaves[0].reshape(-1, rpb, K)
+            n = F.rms_norm(x3.float(), (K,), eps=ctx.eps, weight=leaves[1].float() + 1.0).to(x2.dtype)
+            h = (1 + leaves[2][:, None, :]) * n + leaves[3][:, None, :]
+            wrt = [t for t, n in zip(leaves, need) if n]
+            grads = torch.autograd.grad(h.reshape(M, K), wrt, dh) if wrt else ()
+        it = iter(grads)
+        return tuple(next(it) if n else None for n in need) + (None, None)
+
+
+def modulated_rmsnorm(norm: nn.Module, x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor) -> torch.Tensor:
+    """``(1 + scale) * norm(x) + shift`` for the reference's ``RMSNorm`` module ``norm`` (attributes ``scale``,
+    ``eps``; ``mmdit.py:146-161``), computed with its int8 codes in one pass and the codes recorded for the
+    ConvRot layers that receive the result.  ``x`` (B, L, K) or (M, K) bf16; ``scale`` / ``shift`` bf16 with one
+    entry per batch row of ``x`` broadcast over the tokens ((B, 1, K), as ``DoubleSharedModulation`` yields) or
+    a single entry."""
+    if x.dtype != torch.bfloat16 or scale.dtype != torch.bfloat16 or shift.dtype != torch.bfloat16:
+        raise NotImplementedError("the fused modulated RMSNorm runs bf16 tensors (the DiT dtype)")
+    K = x.shape[-1]
+    if scale.shape != shift.shape or scale.shape[-1] != K:
+        raise ValueError(f"scale {tuple(scale.shape)} / shift {tuple(shift.shape)} do not match {K} features")
+    x2 = _rows(x, K)
+    M = x2.shape[0]
+    ms, mb = scale.reshape(-1, K), shift.reshape(-1, K)
+    B = ms.shape[0]
+    if B > 1:
+        if x.dim() < 2 or x.shape[0] != B or scale.numel() // K != B or any(d != 1 for d in scale.shape[1:-1]):
+            raise ValueError(f"scale {tuple(scale.shape)} does not broadcast over x {tuple(x.shape)} per batch row")
+    # the kernel reads both with one row stride (the chunks of one modulation tensor share theirs)
+    if not (ms.stride(1) == 1 and mb.stride(1) == 1 and ms.stride(0) == mb.stride(0) and ms.stride(0) % 8 == 0
+            and ms.data_ptr() % 16 == 0 and mb.data_ptr() % 16 == 0):
+        ms, mb = ms.contiguous(), mb.contiguous()
+    h, q, s = _RmsModQuantFn.apply(x2, norm.scale, ms, mb, float(norm.eps), M // B)
+    h = h.reshape(x.shape)
+    shared_input_quant.seed(h, q, s)
+    return h
+
+
+# ----------------------------------------------------------------------------------------------------------
+# In-place patch of a DiT's blocks
+# ----------------------------------------------------------------------------------------------------------
+def _convrot(m) -> bool:
+    return isinstance(m, ConvRotLinear) or isinstance(getattr(m, "base", None), ConvRotLinear)
+
+
+def _fused_swiglu_forward(self, x):
+    # SwiGLU.forward (mmdit.py:177-178) with the product and its codes from one pass
+    return self.down(swiglu(self.gate(x), self.up(x)))
+
+
+def _fused_block_forward(self, x, vec, freqs, mask=None):
+    # SingleStreamBlock.forward (mmdit.py:310-319) with both modulated norms and their codes from one pass
+    prescale, preshift, pregate, postscale, postshift, postgate = self.mod(vec)
+    x = x + pregate * self.attn(modulated_rmsnorm(self.prenorm, x, prescale, preshift), freqs, mask)
+    x = x + postgate * self.mlp(modulated_rmsnorm(self.postnorm, x, postscale, postshift))
+    return x
+
+
+def fuse_producers(dit) -> int:
+    """Patch the blocks of ``dit.blocks`` in place so their quantized linears' inputs come from the fused
+    producers: a block with ``mod / prenorm / postnorm / attn / mlp`` (``SingleStreamBlock``,
+    ``mmdit.py:294-319``) whose attention and MLP input linears are ConvRot gets the fused modulated RMSNorm;
+    an MLP with ``gate / up / down`` (``SwiGLU``) whose ``down`` is ConvRot gets the fused product.  Call after
+    ``quantize_dit_convrot`` and ``inject_lora``.  Returns the number of forwards patched."""
+    n = 0
+    for blk in dit.blocks:
+        mlp = getattr(blk, "mlp", None)
+        if mlp is not None and all(hasattr(mlp, a) for a in ("gate", "up", "down")) and _convrot(mlp.down):
+            mlp.forward = types.MethodType(_fused_swiglu_forward, mlp)
+            n += 1
+        attn = getattr(blk, "attn", None)
+        if (all(hasattr(blk, a) for a in ("mod", "prenorm", "postnorm", "attn", "mlp"))
+                and all(hasattr(nm, "scale") and hasattr(nm, "eps") for nm in (blk.prenorm, blk.postnorm))
+                and _convrot(getattr(attn, "wq", None)) and _convrot(getattr(mlp, "gate", None))):
+            blk.forward = types.MethodType(_fused_block_forward, blk)
+            n += 1
+    return n

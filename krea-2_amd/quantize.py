@@ -43,9 +43,13 @@ class _SharedInputQuant:
         self.val = None
         self.misses = 0
 
+    @staticmethod
+    def _key(x: torch.Tensor):
+        return (x._version, x.data_ptr(), tuple(x.shape), tuple(x.stride()), x.device,
+                torch.cuda.current_stream(x.device).cuda_stream)
+
     def lookup(self, x: torch.Tensor, x2: torch.Tensor):
-        key = (x._version, x.data_ptr(), tuple(x.shape), tuple(x.stride()), x.device,
-               torch.cuda.current_stream(x.device).cuda_stream)
+        key = self._key(x)
         if self.enabled and self.ref is not None and self.ref() is x and self.key == key:
             return self.val
         self.misses += 1
@@ -53,6 +57,12 @@ class _SharedInputQuant:
         if self.enabled:
             self.ref, self.key, self.val = weakref.ref(x), key, (qx, sx)
         return qx, sx
+
+    def seed(self, x: torch.Tensor, qx: torch.Tensor, sx: torch.Tensor) -> None:
+        """Record codes a producer-fused kernel computed for ``x`` (exactly those ``rotquant`` gives), so the
+        ConvRot layers that receive ``x`` next skip their own rotate/quant."""
+        if self.enabled:
+            self.ref, self.key, self.val = weakref.ref(x), self._key(x), (qx, sx)
 
 
 shared_input_quant = _SharedInputQuant()

@@ -302,3 +302,63 @@ def fp8_linear(x_bf16, wq, scale_bf16, bias=None):
     w = wq.to(torch.bfloat16) * scale_bf16.to(torch.bfloat16)
     b = bias.to(torch.bfloat16) if bias is not None else None
     return F.linear(x_bf16, w, b)
+
+
+# ----------------------------------------------------------------------------------------------------------
+# Producers of the quantized linears' inputs (fused into rotate/quant by the kernels)
+# ----------------------------------------------------------------------------------------------------------
+def _sigmoid_f32(g) -> np.ndarray:
+    g = np.asarray(g, dtype=np.float32)
+    with np.errstate(over="ignore"):
+        return np.float32(1.0) / (np.float32(1.0) + np.exp(-g))
+
+
+def swiglu(g, u) -> np.ndarray:
+    """``F.silu(self.gate(x)) * self.up(x)`` of ``SwiGLU.forward`` (reference ``mmdit.py:177-178``) on bf16
+    tensors: ``F.silu`` computes ``g / (1 + exp(-g))`` in float32 and returns bf16, the product rounds to bf16
+    again.  ``g``, ``u`` float32 arrays holding bf16 values; returns float32 holding the bf16 result ``h``."""
+    g = np.asarray(g, dtype=np.float32)
+    u = np.asarray(u, dtype=np.float32)
+    with np.errstate(over="ignore"):
+        s = bf16_round(g / (np.float32(1.0) + np.exp(-g)))
+    return bf16_round(s * u)
+
+
+def swiglu_backward(dh, g, u):
+    """Autograd of :func:`swiglu` with the reference's eager bf16 roundings: the product's backward gives
+    ``du = bf16(dh * s)`` and ``ds = bf16(dh * u)`` (``s = bf16(silu(g))``), and silu's backward gives
+    ``dg = bf16((ds * sig) * (1 + g (1 - sig)))`` with ``sig = 1 / (1 + exp(-g))`` in float32 — the
+    derivative of ``g * sig(g)``.  Returns ``(dg, du)`` as float32 holding bf16 values."""
+    dh = np.asarray(dh, dtype=np.float32)
+    g = np.asarray(g, dtype=np.float32)
+    u = np.asarray(u, dtype=np.float32)
+    sig = _sigmoid_f32(g)
+    with np.errstate(over="ignore"):
+        s = bf16_round(g / (np.float32(1.0) + np.exp(-g)))
+    du = bf16_round(dh * s)
+    ds = bf16_round(dh * u)
+    dg = bf16_round((ds * sig) * (np.float32(1.0) + g * (np.float32(1.0) - sig)))
+    return dg, du
+
+
+def rmsmod(x, norm_scale, eps: float, mod_scale, mod_shift, rows_per_batch: int) -> np.ndarray:
+    """The modulated RMSNorm that feeds ``attn`` and ``mlp`` in ``SingleStreamBlock.forward`` (reference
+    ``mmdit.py:314-317``), with ``RMSNorm.forward`` (``mmdit.py:156-161``):
+
+    ``n = bf16((x * rsqrt(mean(x^2) + eps)) * (scale + 1))`` in float32 over the whole row (``F.rms_norm`` on
+    ``x.float()`` with weight ``scale.float() + 1``, then ``.to(x.dtype)``), and
+    ``h = bf16(bf16(bf16(1 + p) * n) + b)`` — each eager bf16 op rounds — with ``p``, ``b`` the modulation
+    scale / shift entry of the row's batch (``row // rows_per_batch``; one entry for every row when there
+    is one).  ``x`` float32 (M,K) holding bf16 values, ``norm_scale`` float32 (K,), ``mod_scale`` /
+    ``mod_shift`` float32 (B,K) holding bf16 values.  Returns float32 holding the bf16 result ``h``."""
+    x = np.asarray(x, dtype=np.float32)
+    M, K = x.shape
+    w1 = np.asarray(norm_scale, dtype=np.float32) + np.float32(1.0)
+    ms = np.asarray(mod_scale, dtype=np.float32).reshape(-1, K)
+    mb = np.asarray(mod_shift, dtype=np.float32).reshape(-1, K)
+    b = np.zeros(M, dtype=np.int64) if ms.shape[0] == 1 else np.arange(M) // int(rows_per_batch)
+    mean = np.sum(x * x, axis=1, dtype=np.float32) / np.float32(K)
+    r = np.float32(1.0) / np.sqrt(mean + np.float32(eps))
+    n = bf16_round((x * r[:, None]) * w1[None, :])
+    p1 = bf16_round(np.float32(1.0) + ms[b])
+    return bf16_round(bf16_round(p1 * n) + mb[b])

@@ -275,3 +275,87 @@ def test_fp8_weight_quant_known_answer():
     q, s = orc.fp8_weight_quant(w)
     assert float(s[0, 0]) == 1.0
     assert q.float().tolist()[0] == [448.0, 1.0, -3.25, 0.1015625, 16.0, -448.0, 0.0, 2.5]
+
+
+# ---------------------------------------------------------------------------------------------- producers
+def _bf16(a):
+    return torch.from_numpy(np.asarray(a, np.float32)).to(torch.bfloat16)
+
+
+def _ulp_diff(a, b):
+    """Distance in bf16 steps between two float32 arrays holding bf16 values (same sign assumed near 0)."""
+    ia = orc.bf16_bits(a).astype(np.int32)
+    ib = orc.bf16_bits(b).astype(np.int32)
+    ia = np.where(ia & 0x8000, 0x8000 - ia, ia)   # sign-magnitude -> ordered integers
+    ib = np.where(ib & 0x8000, 0x8000 - ib, ib)
+    return np.abs(ia - ib)
+
+
+def test_swiglu_closed_forms():
+    """silu(0) = 0; silu(g) rounds to g for g >= 16 (exp(-g) < 2^-23 of 1) and to -0 for g <= -104 (exp
+    overflows); u = 0 gives 0; the product is rounded to bf16 once more (3 * 0.73046875 -> 2.1875)."""
+    g = np.array([0.0, 16.0, 24.0, -120.0, 1.0, 1.0], np.float32)
+    u = np.array([5.0, 3.0, -2.0, 7.0, 0.0, 3.0], np.float32)
+    h = orc.swiglu(g, u)
+    assert h.tolist()[:5] == [0.0, 48.0, -48.0, 0.0, 0.0]
+    assert h[5] == orc.bf16_round(np.float32(3.0) * np.float32(0.73046875))  # bf16(silu(1)) = 0.73046875
+    assert orc.swiglu(np.float32([1.0]), np.float32([1.0]))[0] == np.float32(0.73046875)
+
+
+def test_swiglu_matches_torch_eager_bf16():
+    """Against torch's CPU ``F.silu(g) * u`` on bf16 tensors (its own exp): within one bf16 step, and equal
+    almost everywhere (a rounding-order mistake would move far more than 0.1% of the elements)."""
+    rng = np.random.default_rng(21)
+    g = orc.bf16_round(rng.standard_normal((64, 512)).astype(np.float32) * 3)
+    u = orc.bf16_round(rng.standard_normal((64, 512)).astype(np.float32))
+    ref = (torch.nn.functional.silu(_bf16(g)) * _bf16(u)).float().numpy()
+    d = _ulp_diff(orc.swiglu(g, u), ref)
+    assert d.max() <= 1 and (d == 0).mean() > 0.999
+
+
+def test_swiglu_backward_matches_torch_autograd_bf16():
+    rng = np.random.default_rng(22)
+    g = orc.bf16_round(rng.standard_normal((32, 512)).astype(np.float32) * 3)
+    u = orc.bf16_round(rng.standard_normal((32, 512)).astype(np.float32))
+    dh = orc.bf16_round(rng.standard_normal((32, 512)).astype(np.float32) * 1e-3)
+    gt, ut = _bf16(g).requires_grad_(True), _bf16(u).requires_grad_(True)
+    (torch.nn.functional.silu(gt) * ut).backward(_bf16(dh))
+    dg, du = orc.swiglu_backward(dh, g, u)
+    d_u = _ulp_diff(du, ut.grad.float().numpy())
+    d_g = _ulp_diff(dg, gt.grad.float().numpy())
+    assert d_u.max() <= 1 and (d_u == 0).mean() > 0.999
+    assert d_g.max() <= 2 and (d_g == 0).mean() > 0.99
+
+
+def test_rmsmod_closed_forms():
+    """A row of +-c with c a power of two has rms c, so n = sign * (scale + 1) exactly (eps = 0); p = -1
+    zeroes the modulated norm and leaves the shift; p = b = 0 gives n; the batch entry of row m is m // L."""
+    K = 256
+    x = np.full((2, K), 4.0, np.float32)
+    x[:, ::2] = -4.0
+    ns = np.zeros(K, np.float32)
+    ns[:4] = [0.5, -0.25, 1.0, 0.0]
+    zero = np.zeros((1, K), np.float32)
+    n = orc.rmsmod(x, ns, 0.0, zero, zero, 2)
+    assert np.array_equal(n, np.sign(x) * (ns + 1.0)[None, :])
+    b = orc.bf16_round(np.linspace(-2, 2, K, dtype=np.float32))[None, :]
+    assert np.array_equal(orc.rmsmod(x, ns, 0.0, -np.ones((1, K), np.float32), b, 2), np.repeat(b, 2, 0))
+    ms = np.stack([np.zeros(K, np.float32), np.ones(K, np.float32)])       # batch 1 doubles its rows
+    h = orc.rmsmod(np.tile(x, (2, 1)), ns, 0.0, ms, np.zeros((2, K), np.float32), 2)
+    assert np.array_equal(h[2:], orc.bf16_round(2 * h[:2]))
+
+
+def test_rmsmod_matches_torch_eager_bf16():
+    """Against torch's CPU ``(1 + p) * F.rms_norm(x.float(), eps, weight=scale + 1).to(bf16) + b`` on bf16
+    tensors shaped as in the block (x (B,L,K), p / b (B,1,K)): within one bf16 step, almost all equal."""
+    rng = np.random.default_rng(23)
+    B, L, K, eps = 2, 48, 768, 1e-5
+    x = orc.bf16_round(rng.standard_normal((B * L, K)).astype(np.float32) * 2)
+    ns = (rng.standard_normal(K) * 0.1).astype(np.float32)
+    p = orc.bf16_round(rng.standard_normal((B, K)).astype(np.float32) * 0.3)
+    b = orc.bf16_round(rng.standard_normal((B, K)).astype(np.float32) * 0.3)
+    xt = _bf16(x).reshape(B, L, K)
+    n = torch.nn.functional.rms_norm(xt.float(), (K,), eps=eps, weight=torch.from_numpy(ns) + 1.0)
+    ref = ((1 + _bf16(p)[:, None, :]) * n.to(torch.bfloat16) + _bf16(b)[:, None, :]).float().reshape(B * L, K)
+    d = _ulp_diff(orc.rmsmod(x, ns, eps, p, b, L), ref.numpy())
+    assert d.max() <= 1 and (d == 0).mean() > 0.999
