@@ -301,6 +301,55 @@ def run_cfg3(k2, steps, dev, settle_s=0.0):
             "dx_tflops": round(ops_fwd / ((ms - ms_fwd) * 1e-3) / 1e12, 1)}
 
 
+def run_producers(k2, steps, dev):
+    """The two producer-fused rotate/quant kernels at cfg4's image-stream shapes (M = 2 x 4096 tokens): the
+    modulated RMSNorm of the block input (K = 3072, per-batch modulation) and the SwiGLU product that feeds
+    the down projection (K = 12288).  Each is timed fused (one kernel: h and its codes) and as the reference
+    computes it (torch's eager ops, mmdit.py:156-161,177-178,314-317) followed by rotate/quant of h.  Inputs
+    rotate over 4 tensors so that every call reads them from HBM; bytes are the fused kernel's algorithmic
+    traffic: RMSNorm 2MK in + 2MK h + MK codes + 4M scales, SwiGLU 4MK in + 2MK h + MK codes + 4M."""
+    L = k2._lib
+    F_ = torch.nn.functional
+    B, Lt, K, KH = 2, 4096, 3072, 12288
+    M = B * Lt
+    g = torch.Generator().manual_seed(11)
+    xs = [torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev) for _ in range(4)]
+    ns = (torch.randn(K, generator=g) * 0.1).to(dev)
+    vec = (torch.randn(B, 1, 6 * K, generator=g) * 0.3).to(torch.bfloat16).to(dev)
+    ps, sh = vec[..., :K], vec[..., K:2 * K]
+    gus = [(torch.randn(M, KH, generator=g) * 3).to(torch.bfloat16).to(dev) for _ in range(2)] + \
+          [torch.randn(M, KH, generator=g).to(torch.bfloat16).to(dev) for _ in range(2)]
+    pairs = [(gus[0], gus[2]), (gus[1], gus[3]), (gus[2], gus[0]), (gus[3], gus[1])]
+
+    def rms_fused():
+        for x in xs:
+            L.rmsmod_rotquant(x, ns, 1e-5, ps.reshape(B, K), sh.reshape(B, K), Lt)
+
+    def rms_ref():
+        for x in xs:
+            n = F_.rms_norm(x.view(B, Lt, K).float(), (K,), eps=1e-5, weight=ns + 1.0).to(torch.bfloat16)
+            L.rotquant(((1 + ps) * n + sh).view(M, K))
+
+    def swi_fused():
+        for gt, ut in pairs:
+            L.swiglu_rotquant(gt, ut)
+
+    def swi_ref():
+        for gt, ut in pairs:
+            L.rotquant(F_.silu(gt) * ut)
+
+    out = {}
+    for name, fused, ref, nbytes in (("rmsnorm_mod", rms_fused, rms_ref, 5 * M * K + 4 * M),
+                                     ("swiglu", swi_fused, swi_ref, 7 * M * KH + 4 * M)):
+        tf = sorted(time_loop(fused, steps) for _ in range(5))[2] / 4
+        tr = sorted(time_loop(ref, steps) for _ in range(5))[2] / 4
+        gbs = nbytes / (tf * 1e-3) / 1e9
+        out[name] = {"M": M, "K": K if name == "rmsnorm_mod" else KH, "fused_ms": round(tf, 4),
+                     "unfused_ms": round(tr, 4), "fused_GBps": round(gbs, 1),
+                     "fused_pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 2)}
+    return out
+
+
 def run_cfg4(k2, steps, dev, settle_s=0.0):
     """Summed forward time of one double-stream block's quantized linears (image + text stream, plus the
     per-stream adaLN modulation at M=2), each a LoRALinear (r=16) over a W8A8 ConvRot base."""
@@ -497,6 +546,7 @@ def main():
     extra["gemm_pct_of_mfma_probe"] = round(100 * gemm_tops / probe, 2)
     extra["cfg3"] = run_cfg3(k2, max(5, a.steps // 2), dev, a.settle / 2)
     extra["cfg4"] = run_cfg4(k2, max(5, a.steps // 2), dev, a.settle / 2)
+    extra["producers_cfg4_image"] = run_producers(k2, max(5, a.steps // 2), dev)
     cpu = None
     if not a.no_cpu:
         cpu = cpu_baseline(cfg, res["x"], res["W"], res["b"], res["A"], res["B"])

@@ -43,9 +43,23 @@ struct ProdArgs {
 
 __device__ __forceinline__ float bf16r(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
 
-__device__ __forceinline__ float silu_f32(float g) { return __fdiv_rn(g, 1.f + expf(-g)); }
+// Two values rounded to bf16 by one v_cvt_pk_bf16_f32 (round to nearest even), unpacked in place.
+__device__ __forceinline__ void bf16r2(float& a, float& b) {
+  const uint32_t u = pack_bf16x2(a, b);
+  a = __uint_as_float(u << 16);
+  b = __uint_as_float(u & 0xffff0000u);
+}
 
-template <int PROD, int WPR, int kNCH>
+// sigmoid(g) = 1 / (1 + exp(-g)) with exp(-g) = 2^(-g log2 e) on v_exp_f32 and the reciprocal on v_rcp_f32:
+// a few float32 ulp from the correctly rounded quotient, which the bf16 rounding of the result hides except
+// in rare near-ties (the reference's own exp differs from the oracle's by as much).
+__device__ __forceinline__ float sigmoid_f32(float g) {
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(g * -1.44269504088896341f));
+}
+
+__device__ __forceinline__ float silu_f32(float g) { return g * sigmoid_f32(g); }
+
+template <int PROD, int WPR, int kNCH, bool kTail>
 __global__ __launch_bounds__(256) void prodquant_kernel(ProdArgs a) {
   constexpr int T = 64 * WPR;
   constexpr int CW = T * 16;
@@ -62,17 +76,37 @@ __global__ __launch_bounds__(256) void prodquant_kernel(ProdArgs a) {
   const int K = a.K;
   const int64_t rr = row_ok ? row : 0;
 
+  // Loads are unconditional from clamped (always valid) addresses, which keeps the kernel free of branches
+  // and lets each chunk's operands die before the next chunk's arrive; lanes past K hold zeros (their
+  // Hadamard blocks enter the row absmax).
   float v[kNCH][16];
 #pragma unroll
-  for (int c = 0; c < kNCH; ++c) load16<__bf16>(a.x0 + rr * a.ld0 + c * CW + off, row_ok && c * CW + off < K, v[c]);
+  for (int c = 0; c < kNCH; ++c) {
+    const int col = c * CW + off;
+    const bool ok = !kTail || col < K;
+    load16<__bf16>(a.x0 + rr * a.ld0 + (ok ? col : 0), true, v[c]);
+    if (kTail) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[c][i] = ok ? v[c][i] : 0.f;
+    }
+  }
 
   if (PROD == PROD_SWIGLU) {
 #pragma unroll
     for (int c = 0; c < kNCH; ++c) {
+      const int col = c * CW + off;
       float u[16];
-      load16<__bf16>(a.x1 + rr * a.ld1 + c * CW + off, row_ok && c * CW + off < K, u);
+      load16<__bf16>(a.x1 + rr * a.ld1 + (!kTail || col < K ? col : 0), true, u);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) v[c][i] = bf16r(bf16r(silu_f32(v[c][i])) * u[i]);
+      for (int i = 0; i < 16; i += 2) {   // silu(0) * u = 0 past K
+        float s0 = silu_f32(v[c][i]), s1 = silu_f32(v[c][i + 1]);
+        bf16r2(s0, s1);
+        float h0 = s0 * u[i], h1 = s1 * u[i + 1];
+        bf16r2(h0, h1);
+        v[c][i] = h0;
+        v[c][i + 1] = h1;
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
   } else {
     float ss = 0.f;
@@ -93,19 +127,34 @@ __global__ __launch_bounds__(256) void prodquant_kernel(ProdArgs a) {
     const int64_t b = rr / a.rpb;
     const uint16_t* ms = a.mscale + b * a.ldm;
     const uint16_t* mb = a.mshift + b * a.ldm;
+    // Per chunk: the norm weight (f32) and the two modulation vectors (bf16, kept packed) are loaded and
+    // consumed before the next chunk's, so at most one chunk of them is live (occupancy).
 #pragma unroll
     for (int c = 0; c < kNCH; ++c) {
       const int col = c * CW + off;
-      const bool ok = row_ok && col < K;
-      float w[16], p[16], sh[16];
-      load16<float>(a.nw + (ok ? col : 0), ok, w);
-      load16<__bf16>(reinterpret_cast<const __bf16*>(ms) + (ok ? col : 0), ok, p);
-      load16<__bf16>(reinterpret_cast<const __bf16*>(mb) + (ok ? col : 0), ok, sh);
+      const bool ok = !kTail || col < K;
+      const int cc = ok ? col : 0;
+      // unconditional loads from a clamped (always valid) address; lanes past K are zeroed below
+      float w[16];
+      load16<float>(a.nw + cc, true, w);
+      const uint4 pv0 = reinterpret_cast<const uint4*>(ms + cc)[0], pv1 = reinterpret_cast<const uint4*>(ms + cc)[1];
+      const uint4 bv0 = reinterpret_cast<const uint4*>(mb + cc)[0], bv1 = reinterpret_cast<const uint4*>(mb + cc)[1];
+      const uint32_t pw[8] = {pv0.x, pv0.y, pv0.z, pv0.w, pv1.x, pv1.y, pv1.z, pv1.w};
+      const uint32_t bw[8] = {bv0.x, bv0.y, bv0.z, bv0.w, bv1.x, bv1.y, bv1.z, bv1.w};
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float n = bf16r((v[c][i] * rinv) * (w[i] + 1.f));
-        v[c][i] = bf16r(bf16r(bf16r(1.f + p[i]) * n) + sh[i]);
+      for (int i = 0; i < 16; i += 2) {   // element pairs share each bf16 conversion
+        float n0 = (v[c][i] * rinv) * (w[i] + 1.f), n1 = (v[c][i + 1] * rinv) * (w[i + 1] + 1.f);
+        bf16r2(n0, n1);
+        float p0 = 1.f + __uint_as_float(pw[i >> 1] << 16), p1 = 1.f + __uint_as_float(pw[i >> 1] & 0xffff0000u);
+        bf16r2(p0, p1);
+        float m0 = p0 * n0, m1 = p1 * n1;
+        bf16r2(m0, m1);
+        float h0 = m0 + __uint_as_float(bw[i >> 1] << 16), h1 = m1 + __uint_as_float(bw[i >> 1] & 0xffff0000u);
+        bf16r2(h0, h1);
+        v[c][i] = !kTail || ok ? h0 : 0.f;   // blocks past K must stay zero: they enter the row absmax
+        v[c][i + 1] = !kTail || ok ? h1 : 0.f;
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
@@ -148,16 +197,23 @@ __global__ __launch_bounds__(256) void prodquant_kernel(ProdArgs a) {
   }
 }
 
-template <int PROD, int WPR>
-void launch_prod_wpr(const ProdArgs& a, hipStream_t st) {
+template <int PROD, int WPR, bool kTail>
+void launch_prod_nch(const ProdArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)((a.M + (4 / WPR) - 1) / (4 / WPR)));
   const int nch = (a.K + 1024 * WPR - 1) / (1024 * WPR);
   switch (nch) {
-    case 1: hipLaunchKernelGGL((prodquant_kernel<PROD, WPR, 1>), grid, dim3(256), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((prodquant_kernel<PROD, WPR, 2>), grid, dim3(256), 0, st, a); break;
-    case 3: hipLaunchKernelGGL((prodquant_kernel<PROD, WPR, 3>), grid, dim3(256), 0, st, a); break;
-    default: hipLaunchKernelGGL((prodquant_kernel<PROD, WPR, 4>), grid, dim3(256), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((prodquant_kernel<PROD, WPR, 1, kTail>), grid, dim3(256), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((prodquant_kernel<PROD, WPR, 2, kTail>), grid, dim3(256), 0, st, a); break;
+    case 3: hipLaunchKernelGGL((prodquant_kernel<PROD, WPR, 3, kTail>), grid, dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL((prodquant_kernel<PROD, WPR, 4, kTail>), grid, dim3(256), 0, st, a); break;
   }
+}
+
+// kTail: K is not a whole number of chunks, so some lanes' columns lie past K.
+template <int PROD, int WPR>
+void launch_prod_wpr(const ProdArgs& a, hipStream_t st) {
+  if (a.K % (1024 * WPR)) launch_prod_nch<PROD, WPR, true>(a, st);
+  else launch_prod_nch<PROD, WPR, false>(a, st);
 }
 
 template <int PROD>
@@ -191,8 +247,8 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const uint4* __restrict
         const float d = bf16_bits_to_f32((aw[j] >> (16 * e)) & 0xffffu);
         const float x = bf16_bits_to_f32((bw[j] >> (16 * e)) & 0xffffu);
         const float up = bf16_bits_to_f32((cw[j] >> (16 * e)) & 0xffffu);
-        const float sig = __fdiv_rn(1.f, 1.f + expf(-x));
-        const float sl = bf16r(__fdiv_rn(x, 1.f + expf(-x)));
+        const float sig = sigmoid_f32(x);
+        const float sl = bf16r(x * sig);   // the forward's silu_f32, bit for bit
         ru[e] = d * sl;
         const float ds = bf16r(d * up);
         rg[e] = (ds * sig) * (1.f + x * (1.f - sig));

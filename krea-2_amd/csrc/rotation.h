@@ -67,17 +67,26 @@ __device__ __forceinline__ void store16_bf16(uint16_t* p, const float (&v)[16]) 
   reinterpret_cast<uint4*>(p)[1] = make_uint4(h[4], h[5], h[6], h[7]);
 }
 
-__device__ __forceinline__ float wave_max(float m) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-  return m;
+// Wave-wide reductions, result in every lane: DPP inside each 16-lane row (quad_perm xor1, xor2,
+// row_half_mirror, row_mirror), then the four row results through readlane.  The operation order is
+// fixed, so the sum is deterministic.
+template <bool kMax>
+__device__ __forceinline__ float wave_reduce(float m) {
+  auto op = [](float a, float b) { return kMax ? fmaxf(a, b) : a + b; };
+  m = op(m, dpp_f<0xB1>(m));
+  m = op(m, dpp_f<0x4E>(m));
+  m = op(m, dpp_f<0x141>(m));
+  m = op(m, dpp_f<0x140>(m));
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 48));
+  return op(op(r0, r1), op(r2, r3));
 }
 
-__device__ __forceinline__ float wave_sum(float m) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) m += __shfl_xor(m, o, 64);
-  return m;
-}
+__device__ __forceinline__ float wave_max(float m) { return wave_reduce<true>(m); }
+
+__device__ __forceinline__ float wave_sum(float m) { return wave_reduce<false>(m); }
 
 // The seven butterfly stages of one chunk: strides 1, 2, 4, 8 in-lane, then 16, 32, 64 across lanes.
 // c1, c2, c8 are the cross-lane multipliers (-1 on the lane holding the upper element of each pair).

@@ -4,7 +4,8 @@
   restatement of the reference's eager ops (``mmdit.py:156-161,177-178,314-317``) and equal to it almost
   everywhere (the exp / reduction orders differ only in the last float32 bits); the int8 codes and scales
   bit-exact against the oracle's rotate/quant of the kernel's own ``h`` and against ``k2q_rotquant(h)``.
-* ``k2q_swiglu_bwd``: within one (du) / two (dg) bf16 steps of the oracle's autograd restatement.
+* ``k2q_swiglu_bwd``: within two bf16 steps of the oracle's autograd restatement (each output is two roundings
+  deep), equal almost everywhere.
 * ``fuse_producers`` on a restated reference block (``mmdit.py:104-115,146-212,294-319``): outputs and gradients
   against the same block without fusion, one rotate/quant per block left (the attention output), and a
   checkpointed backward equal to a plain one.
@@ -71,8 +72,14 @@ def test_swiglu_rotquant(k2, dev, M, K, strided):
         gd, ud = _bf16((M, K), g, 3.0).to(dev), _bf16((M, K), g).to(dev)
     h, q, s = k2._lib.swiglu_rotquant(gd, ud)
     torch.cuda.synchronize()
-    d = _steps(_np(h), orc.swiglu(_np(gd), _np(ud)))
-    assert d.max() <= 1 and (d == 0).mean() > 0.999
+    # bf16(silu(g)) may sit one step off the oracle's where exp / reciprocal differ in the last float32 bits
+    # at a rounding boundary; h = bf16(s u) then moves by up to a step of the product plus one of its own
+    gn, un = _np(gd), _np(ud)
+    ho = orc.swiglu(gn, un)
+    so = orc.swiglu(gn, np.ones_like(un))                      # bf16(silu(g))
+    hk = _np(h)
+    assert np.all(np.abs(hk - ho) <= (np.abs(so * un) + np.abs(ho)) * 2.0 ** -7)
+    assert (hk == ho).mean() > 0.999
     _check_codes(k2, h, q, s)
 
 
@@ -126,7 +133,7 @@ def test_swiglu_bwd(k2, dev, M, K):
     torch.cuda.synchronize()
     og, ou = orc.swiglu_backward(_np(dh), _np(gd), _np(ud))
     d_u, d_g = _steps(_np(du), ou), _steps(_np(dg), og)
-    assert d_u.max() <= 1 and (d_u == 0).mean() > 0.999
+    assert d_u.max() <= 2 and (d_u == 0).mean() > 0.999    # du = bf16(dh * bf16(silu(g))): two roundings
     assert d_g.max() <= 2 and (d_g == 0).mean() > 0.99
 
 
