@@ -99,6 +99,26 @@ int k2q_gemm_w8a8(const int8_t* qx, const float* sx, const int8_t* qw, const flo
                   const float* u, const float* lora_b, int64_t r, float lora_scale,
                   int64_t M, int64_t N, int64_t K, uint16_t* y, void* ws, int64_t ws_bytes, void* stream);
 
+/* Grouped W8A8 forward: the linears that read one input (wq/wk/wv/gate of Attention.forward, mmdit.py:199,
+ * each an Fp8Linear.forward + LoRA add, quantize.py:49-51 and lora.py:47-48) as one launch over the shared
+ * codes qx / sx.  Segment i is k2q_gemm_w8a8 of its own weights into its own output y (M x N, row stride N)
+ * with its factors u[:, u_col .. u_col + r) (u: M rows of ldu f32, r as for k2q_gemm_w8a8; lora_b NULL: no
+ * adapter on that segment); the outputs are bit-identical to nseg separate k2q_gemm_w8a8 calls.
+ * 1 <= nseg <= 4, every N a multiple of 256, M > 8.  ws: k2q_gemm_w8a8_ws_bytes(M, sum of N, K). */
+typedef struct {
+  const int8_t* qw;       /* N x K int8 codes */
+  const float* sw;        /* N f32 scales */
+  const float* bias;      /* N f32, nullable */
+  const float* lora_b;    /* N x r f32, nullable */
+  uint16_t* y;            /* M x N bf16 */
+  int64_t N;
+  int64_t u_col;          /* first column of this segment's factors in u */
+  float lora_scale;
+} k2q_w8a8_segment;
+int k2q_gemm_w8a8_grouped(const int8_t* qx, const float* sx, int64_t M, int64_t K, const k2q_w8a8_segment* seg,
+                          int64_t nseg, const float* u, int64_t r, int64_t ldu, void* ws, int64_t ws_bytes,
+                          void* stream);
+
 /* W4A8 variant: per-group int32 partials scaled by the bf16 group scales. */
 int k2q_gemm_w4a8(const int8_t* qx, const float* sx, const uint8_t* qw4, const uint16_t* sw4,
                   const float* bias, const float* u, const float* lora_b, int64_t r, float lora_scale,

@@ -30,6 +30,17 @@ _i64 = ctypes.c_int64
 _int = ctypes.c_int
 _f32 = ctypes.c_float
 
+
+class W8A8Segment(ctypes.Structure):
+    """``k2q_w8a8_segment`` of ``include/k2q.h``: one linear of a grouped forward."""
+    _fields_ = [("qw", ctypes.c_void_p), ("sw", ctypes.c_void_p), ("bias", ctypes.c_void_p),
+                ("lora_b", ctypes.c_void_p), ("y", ctypes.c_void_p), ("N", ctypes.c_int64),
+                ("u_col", ctypes.c_int64), ("lora_scale", ctypes.c_float)]
+
+
+GROUP_MAX = 4          # segments per grouped launch
+GROUP_ALIGN = 256      # each segment's out_features: a multiple of the GEMM tile
+
 _SIGNATURES = {
     "k2q_version": ([], ctypes.c_char_p),
     "k2q_check_device": ([], _int),
@@ -44,6 +55,7 @@ _SIGNATURES = {
     "k2q_lora_grads": ([_p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p], _int),
     "k2q_gemm_w8a8_ws_bytes": ([_i64, _i64, _i64], _i64),
     "k2q_gemm_w8a8": ([_p, _p, _p, _p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p, _i64, _p], _int),
+    "k2q_gemm_w8a8_grouped": ([_p, _p, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _i64, _p], _int),
     "k2q_gemm_w4a8": ([_p, _p, _p, _p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p], _int),
     "k2q_gemm_w8a8_acc": ([_p, _p, _i64, _i64, _i64, _p, _p, _i64, _p], _int),
     "k2q_gemm_w4a8_f32": ([_p, _p, _p, _i64, _i64, _i64, _p, _p], _int),
@@ -386,6 +398,62 @@ def gemm_w8a8(qx, sx, qw, sw, bias=None, u=None, lora_b=None, lora_scale: float 
     _check(lib.k2q_gemm_w8a8(_ptr(qx), _ptr(sx), _ptr(qw), _ptr(sw), _ptr(bias), _ptr(u), _ptr(lora_b), r,
                              float(lora_scale), M, N, K, _ptr(y), _ptr(ws), nws, _stream(dev)), "k2q_gemm_w8a8")
     return y
+
+
+def gemm_w8a8_grouped(qx, sx, segments, u=None):
+    """Several W8A8 linears that read the same codes in one launch.  ``segments``: sequence of
+    ``(q_w, s_w, bias, lora_b, u_col, lora_scale)`` (bias, lora_b nullable; a segment with ``lora_b`` uses
+    columns ``u_col .. u_col + r`` of ``u``, (M, ldu) f32 with r = ``lora_b.shape[1]``).  Returns one bf16
+    (M, N_i) output per segment, each equal to :func:`gemm_w8a8` of that segment."""
+    _need(qx, "q_x", torch.int8, 2)
+    dev = qx.device
+    M, K = qx.shape
+    _need(sx, "s_x", torch.float32, 1, dev)
+    if sx.shape[0] != M:
+        raise ValueError("s_x length != rows of q_x")
+    _check_k(K)
+    if not 1 <= len(segments) <= GROUP_MAX:
+        raise ValueError(f"a grouped launch takes 1..{GROUP_MAX} segments, got {len(segments)}")
+    if M <= 8:
+        raise ValueError("grouped launches need M > 8 (skinny M runs the per-linear GEMV)")
+    r, ldu = 0, 0
+    if u is not None:
+        if u.dtype != torch.float32 or u.dim() != 2 or u.shape[0] != M or u.stride(1) != 1 or u.data_ptr() % 16 \
+                or u.stride(0) % 4 or u.device != dev:
+            raise ValueError("u must be (M, ldu) f32 with contiguous 16-byte aligned rows")
+        ldu = u.stride(0)
+    arr = (W8A8Segment * len(segments))()
+    outs, keep = [], []
+    for i, (qw, sw, bias, lb, u_col, scale) in enumerate(segments):
+        _need(qw, f"q_w[{i}]", torch.int8, 2, dev)
+        N = qw.shape[0]
+        if qw.shape[1] != K or N % GROUP_ALIGN:
+            raise ValueError(f"segment {i}: q_w {tuple(qw.shape)} needs K={K} and N a multiple of {GROUP_ALIGN}")
+        _need(sw, f"s_w[{i}]", torch.float32, 1, dev)
+        if sw.shape[0] != N:
+            raise ValueError(f"segment {i}: s_w length != N")
+        if bias is not None:
+            _need(bias, f"bias[{i}]", torch.float32, 1, dev)
+            if bias.shape[0] != N:
+                raise ValueError(f"segment {i}: bias length != N")
+        if lb is not None:
+            _need(lb, f"lora_b[{i}]", torch.float32, 2, dev)
+            if u is None or lb.shape[0] != N:
+                raise ValueError(f"segment {i}: lora_b needs u and N rows")
+            if r and lb.shape[1] != r:
+                raise ValueError("every segment's adapter must have the same rank")
+            r = lb.shape[1]
+            _check_rank(r)
+            if u_col < 0 or u_col + r > ldu or u_col % 4:
+                raise ValueError(f"segment {i}: factor columns {u_col}..{u_col + r} outside u")
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        outs.append(y)
+        keep.extend([qw, sw, bias, lb])
+        arr[i] = W8A8Segment(_ptr(qw), _ptr(sw), _ptr(bias), _ptr(lb), _ptr(y), N, int(u_col or 0), float(scale))
+    _device_check(dev)
+    _check(load().k2q_gemm_w8a8_grouped(_ptr(qx), _ptr(sx), M, K, ctypes.cast(arr, ctypes.c_void_p), len(segments),
+                                        _ptr(u), r, ldu, None, 0, _stream(dev)), "k2q_gemm_w8a8_grouped")
+    return outs
 
 
 def gemm_w4a8(qx, sx, q4, s4, bias=None, u=None, lora_b=None, lora_scale: float = 1.0) -> torch.Tensor:

@@ -33,6 +33,21 @@ constexpr int BT = 256;     // tile rows (A) and columns (B)
 constexpr int BKB = 128;    // reduction bytes per stage
 constexpr int TILE_BYTES = BT * BKB;
 
+// One segment of a grouped forward (EPI_W8): linears that read the same input, their weight rows stacked
+// along A.  Each segment starts on a 256-row tile boundary, so a tile lies in one segment and takes its
+// operands, output and LoRA factors from it.
+constexpr int MAX_SEG = 4;
+struct GemmSeg {
+  const uint8_t* a;        // the segment's weight codes, rows x kbytes
+  const float* sw;         // its per-row scales
+  const float* bias;       // nullable
+  const float* lora_ra;    // its lora_b (rows x r f32); nullable: no adapter on this segment
+  void* out;               // its output, row stride ldo
+  int64_t start, rows, ldo;   // first A-row of the segment in the stacked numbering, rows, output stride
+  int64_t rb_off;          // column of its factors in lora_rb
+  float lora_scale;
+};
+
 struct GemmArgs {
   const uint8_t* a;   // A operand, rows_a x kbytes, row stride lda_b bytes
   const uint8_t* b;   // B operand, rows_b x kbytes
@@ -46,7 +61,10 @@ struct GemmArgs {
   const float* lora_ra;  // per-A-row LoRA factors: lora_b (rows_a x r f32) for the forward epilogues, the
                          // LoRA A itself (r x rows_a f32, so column a holds row a's factors) for EPI_DX/DXLIN
   int r;
+  int ldr;            // row stride of lora_rb in elements (r unless the factors of several segments share rows)
   float lora_scale;
+  int nseg;           // 0: one linear; else rows_a stacks nseg segments (EPI_W8)
+  GemmSeg seg[MAX_SEG];
   // Split schedule for the last, partly filled round of tiles: tiles 0 .. dp_tiles-1 run over the full
   // reduction; each of the sk_rem remainder tiles dp_tiles + i is cut into sk_s pieces (piece q covers
   // reduction slice q / sk_rem) whose accumulators go to part, and a fixup launch adds them.
@@ -325,7 +343,7 @@ __global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(GW / 4, G
 // One output tile (linear id lid) over reduction stages kbeg .. kbeg+nk-1, then its epilogue (MODE_TILE,
 // MODE_FIXUP) or its parked accumulators (MODE_PIECE).
 template <int EPI, int MODE>
-__device__ __forceinline__ void gemm_tile(const GemmArgs& p, int64_t lid, int kbeg, int nk) {
+__device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int kbeg, int nk) {
   constexpr bool BF16 = (EPI == EPI_DX || EPI == EPI_LIN || EPI == EPI_DXLIN);
   constexpr bool SCALED = (EPI == EPI_W8 || EPI == EPI_LIN);   // per-row scale / bias epilogue
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // [2][A stage | B stage], then epilogue
@@ -334,11 +352,39 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int64_t lid, int kb
   int tid = (int)threadIdx.x;
   asm volatile("" : "+v"(tid));
 
-  const int64_t tiles_a = (p.rows_a + BT - 1) / BT;
-  const int64_t tiles_b = (p.rows_b + BT - 1) / BT;
+  const int64_t tiles_a = (p0.rows_a + BT - 1) / BT;
+  const int64_t tiles_b = (p0.rows_b + BT - 1) / BT;
   int64_t ta, tb;
   group_coords(lid, tiles_a, tiles_b, ta, tb);
-  const int64_t A0 = ta * BT, B0 = tb * BT;
+  int64_t A0 = ta * BT;
+  const int64_t B0 = tb * BT;
+  // A grouped forward: the tile's segment supplies the operands (workgroup-uniform, scalar registers); A0
+  // becomes the row within the segment.  Constant segment indices keep every field a plain argument load.
+  // Grouped launches run full-K tiles only (no split pieces), so the piece and fixup kernels, at their
+  // register limit, carry none of this.
+  GemmArgs p = p0;
+  if constexpr (EPI == EPI_W8 && MODE == MODE_TILE) {
+    if (p0.nseg > 0) {
+      int s = 0;
+#pragma unroll
+      for (int i = 1; i < MAX_SEG; ++i) s = (i < p0.nseg && A0 >= p0.seg[i].start) ? i : s;
+#pragma unroll
+      for (int i = 0; i < MAX_SEG; ++i) {
+        if (i != s) continue;
+        const GemmSeg& g = p0.seg[i];
+        p.a = g.a;
+        p.sw = g.sw;
+        p.bias = g.bias;
+        p.lora_ra = g.lora_ra;
+        p.lora_rb = g.lora_ra ? p0.lora_rb + g.rb_off : nullptr;
+        p.lora_scale = g.lora_scale;
+        p.out = g.out;
+        p.rows_a = g.rows;
+        p.ldo = g.ldo;
+        A0 -= g.start;
+      }
+    }
+  }
 
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -560,7 +606,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int64_t lid, int kb
       ra = ra < p.rows_a ? ra : p.rows_a - 1;
       rb = rb < p.rows_b ? rb : p.rows_b - 1;
       pra = RA_T ? p.lora_ra + (int64_t)(8 * shalf) * p.rows_a + ra : p.lora_ra + ra * p.r + 8 * shalf;
-      prb = p.lora_rb + rb * p.r + 8 * shalf;
+      prb = p.lora_rb + rb * p.ldr + 8 * shalf;
       load_ra(0);
       lfb[0] = *reinterpret_cast<const v4f*>(prb);
       lfb[1] = *reinterpret_cast<const v4f*>(prb + 4);
@@ -981,6 +1027,7 @@ int launch_gemm(GemmArgs p, void* ws, int64_t ws_bytes, hipStream_t st) {
       hipFuncSetAttribute((const void*)gemm_nt_kernel<EPI, MODE_FIXUP>, hipFuncAttributeMaxDynamicSharedMemorySize,
                           lds) != hipSuccess)
     return K2Q_ELAUNCH;
+  if (p.ldr == 0) p.ldr = p.r;
   const int64_t tiles = ((p.rows_a + BT - 1) / BT) * ((p.rows_b + BT - 1) / BT);
   if (tiles > 0x7fffffff) return K2Q_EUNSUPPORTED;
   SplitPlan q = split_plan(tiles, (int)(p.kbytes / SBK), k2q_cu_count());
@@ -1054,6 +1101,50 @@ extern "C" int k2q_gemm_w8a8(const int8_t* qx, const float* sx, const int8_t* qw
   p.sx = sx; p.sw = sw; p.bias = bias;
   p.lora_rb = u; p.lora_ra = lora_b; p.r = u ? (int)r : 0; p.lora_scale = lora_scale;
   return launch_gemm<EPI_W8>(p, ws, ws_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int k2q_gemm_w8a8_grouped(const int8_t* qx, const float* sx, int64_t M, int64_t K,
+                                     const k2q_w8a8_segment* seg, int64_t nseg, const float* u, int64_t r,
+                                     int64_t ldu, void* ws, int64_t ws_bytes, void* stream) {
+  if (!qx || !sx || !seg || nseg < 1 || nseg > MAX_SEG || M <= K2Q_GEMV_MAX_M) return K2Q_EINVAL;
+  if (K < K2Q_HADAMARD || K % K2Q_HADAMARD || !k2q_aligned(qx, 16)) return K2Q_EINVAL;
+  bool any_lora = false;
+  int64_t start = 0;
+  GemmArgs p{};
+  for (int64_t i = 0; i < nseg; ++i) {
+    const k2q_w8a8_segment& g = seg[i];
+    if (!g.qw || !g.sw || !g.y || g.N < BT || g.N % BT) return K2Q_EINVAL;
+    if (!k2q_aligned(g.qw, 16) || !k2q_aligned(g.sw, 16) || !k2q_aligned(g.y, 16)) return K2Q_EINVAL;
+    if (g.bias && !k2q_aligned(g.bias, 16)) return K2Q_EINVAL;
+    if (g.lora_b) {
+      if (!u || !k2q_aligned(g.lora_b, 16) || g.u_col < 0 || g.u_col + r > ldu || g.u_col % 4) return K2Q_EINVAL;
+      any_lora = true;
+    }
+    GemmSeg& s = p.seg[i];
+    s.a = reinterpret_cast<const uint8_t*>(g.qw);
+    s.sw = g.sw;
+    s.bias = g.bias;
+    s.lora_ra = g.lora_b;
+    s.out = g.y;
+    s.start = start;
+    s.rows = g.N;
+    s.ldo = g.N;
+    s.rb_off = g.u_col;
+    s.lora_scale = g.lora_scale;
+    start += g.N;
+  }
+  if (any_lora && (r < 16 || r > 128 || r % 16 || ldu % 4 || !k2q_aligned(u, 16))) return K2Q_EINVAL;
+  p.nseg = (int)nseg;
+  p.a = p.seg[0].a;   // unused by the tiles (each takes its segment's), set for completeness
+  p.b = reinterpret_cast<const uint8_t*>(qx);
+  p.rows_a = start; p.rows_b = M; p.kbytes = K; p.lda_b = K; p.ldb_b = K;
+  p.sx = sx;
+  p.lora_rb = any_lora ? u : nullptr;
+  p.r = any_lora ? (int)r : 0;
+  p.ldr = (int)ldu;
+  (void)ws;
+  (void)ws_bytes;   // full-K tiles only: the split schedule's kernels take no segments
+  return launch_gemm<EPI_W8>(p, nullptr, 0, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int k2q_gemm_w8a8_acc(const int8_t* qx, const int8_t* qw, int64_t M, int64_t N, int64_t K,

@@ -15,6 +15,7 @@ calls them directly.
 from __future__ import annotations
 
 import types
+import weakref
 
 import torch
 import torch.nn as nn
@@ -164,5 +165,149 @@ def fuse_producers(dit) -> int:
                 and all(hasattr(nm, "scale") and hasattr(nm, "eps") for nm in (blk.prenorm, blk.postnorm))
                 and _convrot(getattr(attn, "wq", None)) and _convrot(getattr(mlp, "gate", None))):
             blk.forward = types.MethodType(_fused_block_forward, blk)
+            n += 1
+    return n
+
+
+# ----------------------------------------------------------------------------------------------------------
+# Linears that read one tensor, computed in one grouped launch
+# ----------------------------------------------------------------------------------------------------------
+def _lora_state(m):
+    """(A, B, effective scale) of a member's adapter as its forward would apply it now, or None (exact base)."""
+    if isinstance(m, ConvRotLinear) or m.scale_mul == 0.0:
+        return None
+    return m.lora_A, m.lora_B, float(m.scale * m.scale_mul)
+
+
+def _state_key(st):
+    if st is None:
+        return None
+    A, B, sc = st
+    return (id(A), A._version, id(B), B._version, sc)
+
+
+class _GroupedFn(torch.autograd.Function):
+    """Forward: one LoRA down-projection over the stacked adapters (``u = x [A_0; A_1; ..]^T``) and one grouped
+    GEMM (``k2q_gemm_w8a8_grouped``) giving every member's output, each bit-identical to the member's own
+    fused forward.  Backward: per member, the LoRA gradients and ``dX`` as ``_ConvRotLinearFn`` computes them;
+    the members' ``dX`` are added (the accumulation autograd performs at the shared input)."""
+
+    @staticmethod
+    def forward(ctx, x2, qx, sx, bases, scales, *ab):
+        As, Bs = ab[0::2], ab[1::2]
+        u = _lib.lora_down(x2, torch.cat(As) if len(As) > 1 else As[0]) if As else None
+        r = As[0].shape[0] if As else 0
+        segs, li = [], 0
+        for base, sc in zip(bases, scales):
+            if sc is None:
+                segs.append((base.qweight, base.weight_scale, base._bias_f32(), None, 0, 0.0))
+            else:
+                segs.append((base.qweight, base.weight_scale, base._bias_f32(), Bs[li], li * r, sc))
+                li += 1
+        ys = _lib.gemm_w8a8_grouped(qx, sx, segs, u)
+        ctx.bases, ctx.scales, ctx.r, ctx.nl = bases, scales, r, len(As)
+        ctx.save_for_backward(x2 if As else None, u, *As, *Bs)
+        return tuple(ys)
+
+    @staticmethod
+    def backward(ctx, *dys):
+        x2, u, *ab = ctx.saved_tensors
+        nl, r = ctx.nl, ctx.r
+        As, Bs = ab[:nl], ab[nl:]
+        grads = [None] * (2 * nl)
+        dx, li = None, 0
+        for i, (base, sc) in enumerate(zip(ctx.bases, ctx.scales)):
+            dy, has = dys[i], sc is not None
+            if dy is not None:
+                dy = dy.contiguous()
+                if dy.dtype != torch.bfloat16:
+                    dy = dy.to(torch.bfloat16)
+                g = None
+                if has:
+                    need_a, need_b = ctx.needs_input_grad[5 + 2 * li], ctx.needs_input_grad[6 + 2 * li]
+                    u_i = u[:, li * r:(li + 1) * r].contiguous() if need_b else None
+                    g, grads[2 * li], grads[2 * li + 1] = _lib.lora_grads(dy, x2 if need_a else None, u_i, Bs[li], sc)
+                if ctx.needs_input_grad[0]:
+                    d = _lib.gemm_dx(dy, base.qweight, base.weight_scale, w4=False, g=g,
+                                     lora_a=As[li] if has else None)
+                    dx = d if dx is None else dx + d
+            li += int(has)
+        return (dx, None, None, None, None, *grads)
+
+
+class _SiblingGroup:
+    """Linears that receive the same tensor (``wq / wk / wv / gate`` of ``Attention.forward``, ``mmdit.py:199``).
+    The first member called with a tensor computes every member's output in one grouped launch and keeps the
+    others; each later member called with that same tensor (same object, version, pointer, shape, strides and
+    stream) and an unchanged adapter takes its output.  Anything else runs the member's own forward."""
+
+    def __init__(self, members):
+        self.members = list(members)
+        self.ref = self.key = None
+        self.kept = {}
+
+    @staticmethod
+    def _key(x):
+        return (x._version, x.data_ptr(), tuple(x.shape), tuple(x.stride()), x.device,
+                torch.cuda.current_stream(x.device).cuda_stream)
+
+    def call(self, idx: int, x: torch.Tensor):
+        key = self._key(x)
+        if self.ref is not None and self.ref() is x and self.key == key and idx in self.kept:
+            out, sk = self.kept.pop(idx)
+            if sk == _state_key(_lora_state(self.members[idx])):
+                return out
+        K = x.shape[-1]
+        if x.dtype != torch.bfloat16 or x.numel() // max(K, 1) <= 8:
+            return None
+        x2 = _rows(x, K)
+        with torch.no_grad():
+            qx, sx = shared_input_quant.lookup(x, x2)
+        states = [_lora_state(m) for m in self.members]
+        bases = tuple(m if isinstance(m, ConvRotLinear) else m.base for m in self.members)
+        ab = [t for st in states if st is not None for t in st[:2]]
+        ys = _GroupedFn.apply(x2, qx, sx, bases, tuple(None if st is None else st[2] for st in states), *ab)
+        lead = x.shape[:-1]
+        outs = [y.reshape(*lead, b.out_features) for y, b in zip(ys, bases)]
+        self.ref, self.key = weakref.ref(x), key
+        self.kept = {i: (o, _state_key(st)) for i, (o, st) in enumerate(zip(outs, states)) if i != idx}
+        return outs[idx]
+
+
+def _grouped_member_forward(self, x):
+    group, idx = self._k2q_group
+    out = group.call(idx, x)
+    return out if out is not None else type(self).forward(self, x)
+
+
+def _groupable(m) -> bool:
+    base = m if isinstance(m, ConvRotLinear) else getattr(m, "base", None)
+    if not isinstance(base, ConvRotLinear) or base.mode != "w8a8" or base.out_features % _lib.GROUP_ALIGN:
+        return False
+    return base is m or (hasattr(m, "_fusable") and m._fusable())
+
+
+def group_siblings(dit, groups=(("attn", ("wq", "wk", "wv", "gate")),)) -> int:
+    """Make the ConvRot linears that read one tensor run as one grouped launch, in place: for every block of
+    ``dit.blocks`` and every ``(parent, names)`` of ``groups`` (default: the attention inputs of
+    ``mmdit.py:199``, where one launch replaces four; ``mlp.gate / up`` already fill the GPU on their own),
+    patch the members' forwards.  Members must be w8a8 ConvRot bases (or adapters over them with the fused
+    rank rules), ``out_features`` multiples of 256, one adapter rank.  Call after ``quantize_dit_convrot`` and
+    ``inject_lora``.  Returns the number of groups formed."""
+    n = 0
+    for blk in dit.blocks:
+        for parent_name, names in groups:
+            parent = getattr(blk, parent_name, None)
+            mods = [getattr(parent, nm, None) for nm in names] if parent is not None else []
+            if not mods or len(mods) > _lib.GROUP_MAX or not all(m is not None and _groupable(m) for m in mods):
+                continue
+            bases = [m if isinstance(m, ConvRotLinear) else m.base for m in mods]
+            ranks = {m.rank for m in mods if not isinstance(m, ConvRotLinear)}
+            if len({b.in_features for b in bases}) != 1 or len(ranks) > 1:
+                continue
+            group = _SiblingGroup(mods)
+            for i, m in enumerate(mods):
+                m._k2q_group = (group, i)
+                m.forward = types.MethodType(_grouped_member_forward, m)
             n += 1
     return n

@@ -15,10 +15,9 @@ import copy
 import numpy as np
 import pytest
 import torch
-import torch.nn as nn
-import torch.nn.functional as F
 
 from oracle import convrot as orc
+from restated_block import FEAT, Dit
 
 pytestmark = pytest.mark.gpu
 
@@ -138,81 +137,6 @@ def test_swiglu_bwd(k2, dev, M, K):
 
 
 # ------------------------------------------------------------------------------------------- patched block
-FEAT, HEADS, KVHEADS, HID = 512, 4, 2, 1024
-
-
-class RMSNorm(nn.Module):          # mmdit.py:146-161 (eager)
-    def __init__(self, n, eps=1e-5):
-        super().__init__()
-        self.features, self.eps = n, eps
-        self.scale = nn.Parameter(torch.zeros(n))
-
-    def forward(self, x):
-        t = F.rms_norm(x.float(), (self.features,), eps=self.eps, weight=self.scale.float() + 1.0)
-        return t.to(x.dtype)
-
-
-class Modulation(nn.Module):       # DoubleSharedModulation, mmdit.py:104-115
-    def __init__(self, d):
-        super().__init__()
-        self.lin = nn.Parameter(torch.zeros(6 * d))
-
-    def forward(self, vec):
-        return (vec + self.lin).chunk(6, dim=-1)
-
-
-class Attention(nn.Module):        # mmdit.py:181-212 without QK-norm / RoPE (they touch no Linear)
-    def __init__(self):
-        super().__init__()
-        hd = FEAT // HEADS
-        self.wq = nn.Linear(FEAT, FEAT, bias=False)
-        self.wk = nn.Linear(FEAT, hd * KVHEADS, bias=False)
-        self.wv = nn.Linear(FEAT, hd * KVHEADS, bias=False)
-        self.gate = nn.Linear(FEAT, FEAT, bias=False)
-        self.wo = nn.Linear(FEAT, FEAT, bias=False)
-
-    def forward(self, qkv, freqs=None, mask=None):
-        B, L, _ = qkv.shape
-        hd = FEAT // HEADS
-        q = self.wq(qkv).view(B, L, HEADS, hd).transpose(1, 2)
-        k = self.wk(qkv).view(B, L, KVHEADS, hd).transpose(1, 2).repeat_interleave(HEADS // KVHEADS, 1)
-        v = self.wv(qkv).view(B, L, KVHEADS, hd).transpose(1, 2).repeat_interleave(HEADS // KVHEADS, 1)
-        gate = self.gate(qkv)
-        o = F.scaled_dot_product_attention(q.float(), k.float(), v.float()).to(qkv.dtype)
-        o = o.transpose(1, 2).reshape(B, L, FEAT)
-        return self.wo(o * torch.sigmoid(gate))
-
-
-class SwiGLU(nn.Module):           # mmdit.py:164-178
-    def __init__(self):
-        super().__init__()
-        self.gate = nn.Linear(FEAT, HID, bias=False)
-        self.up = nn.Linear(FEAT, HID, bias=False)
-        self.down = nn.Linear(HID, FEAT, bias=False)
-
-    def forward(self, x):
-        return self.down(F.silu(self.gate(x)) * self.up(x))
-
-
-class Block(nn.Module):            # SingleStreamBlock, mmdit.py:294-319
-    def __init__(self):
-        super().__init__()
-        self.mod = Modulation(FEAT)
-        self.prenorm, self.postnorm = RMSNorm(FEAT), RMSNorm(FEAT)
-        self.attn, self.mlp = Attention(), SwiGLU()
-
-    def forward(self, x, vec, freqs, mask=None):
-        prescale, preshift, pregate, postscale, postshift, postgate = self.mod(vec)
-        x = x + pregate * self.attn((1 + prescale) * self.prenorm(x) + preshift, freqs, mask)
-        x = x + postgate * self.mlp((1 + postscale) * self.postnorm(x) + postshift)
-        return x
-
-
-class Dit(nn.Module):
-    def __init__(self):
-        super().__init__()
-        self.blocks = nn.ModuleList([Block(), Block()])
-
 
 def _build(k2, dev):
     g = torch.Generator().manual_seed(3)
