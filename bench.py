@@ -350,6 +350,39 @@ def run_producers(k2, steps, dev):
     return out
 
 
+def run_grouped(k2, steps, dev):
+    """The attention inputs of a Krea 2 block (wq 6144->6144, wk / wv 6144->1536, gate 6144->6144, all reading
+    one tensor, mmdit.py:199), each a LoRALinear (r=16) over a W8A8 ConvRot base, at M = 4608 (1024^2) and
+    16896 (2048^2): the four layers called one after another (the shared input quantized once) against the
+    same four after group_siblings (one grouped GEMM and one stacked LoRA down-projection)."""
+    import types
+
+    from krea2_amd import fused
+
+    out = {}
+    Ns = (6144, 1536, 1536, 6144)
+    K = 6144
+    for M in (4608, 16896):
+        attn = types.SimpleNamespace(**{n: make_layer(k2, K, N, 16, dev, seed=N + i)
+                                        for i, (n, N) in enumerate(zip(("wq", "wk", "wv", "gate"), Ns))})
+        mods = [attn.wq, attn.wk, attn.wv, attn.gate]
+        x = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).to(torch.bfloat16).to(dev)
+
+        def calls():
+            for m in mods:
+                m(x)
+
+        with torch.no_grad():
+            t_sep = sorted(time_loop(calls, steps) for _ in range(5))[2]
+            assert fused.group_siblings(types.SimpleNamespace(blocks=[types.SimpleNamespace(attn=attn)])) == 1
+            t_grp = sorted(time_loop(calls, steps) for _ in range(5))[2]
+        ops = 2.0 * M * K * sum(Ns)
+        out[f"M{M}"] = {"separate_ms": round(t_sep, 4), "grouped_ms": round(t_grp, 4),
+                        "separate_tops": round(ops / (t_sep * 1e-3) / 1e12, 1),
+                        "grouped_tops": round(ops / (t_grp * 1e-3) / 1e12, 1)}
+    return out
+
+
 def run_cfg4(k2, steps, dev, settle_s=0.0):
     """Summed forward time of one double-stream block's quantized linears (image + text stream, plus the
     per-stream adaLN modulation at M=2), each a LoRALinear (r=16) over a W8A8 ConvRot base."""
@@ -547,6 +580,7 @@ def main():
     extra["cfg3"] = run_cfg3(k2, max(5, a.steps // 2), dev, a.settle / 2)
     extra["cfg4"] = run_cfg4(k2, max(5, a.steps // 2), dev, a.settle / 2)
     extra["producers_cfg4_image"] = run_producers(k2, max(5, a.steps // 2), dev)
+    extra["grouped_attn_inputs"] = run_grouped(k2, max(5, a.steps // 2), dev)
     cpu = None
     if not a.no_cpu:
         cpu = cpu_baseline(cfg, res["x"], res["W"], res["b"], res["A"], res["B"])

@@ -10,7 +10,8 @@ results (same rounding points), and the codes equal a separate rotate/quant of t
 
 :func:`fuse_producers` patches a DiT's blocks in place (call it after ``quantize_dit_convrot`` and
 ``inject_lora``); :func:`modulated_rmsnorm` and :func:`swiglu` are the two operations for model code that
-calls them directly.
+calls them directly.  :func:`group_siblings` makes the linears that read one tensor (``wq / wk / wv / gate``)
+run as one grouped GEMM launch.
 """
 from __future__ import annotations
 
