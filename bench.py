@@ -383,6 +383,65 @@ def run_grouped(k2, steps, dev):
     return out
 
 
+def run_krea_block(k2, steps, dev):
+    """The quantized-linear work of one Krea 2 single-stream block at 1024^2 (M = 4608, width 6144, 48 heads
+    of 128 with 12 KV heads, SwiGLU 16384; mmdit.py:164-212,294-319), LoRA r=16 on all eight linears: the
+    modulated RMSNorm, wq/wk/wv/gate, wo, the second modulated RMSNorm, mlp.gate/up, the SwiGLU product and
+    mlp.down, with the residual adds and gates.  Attention itself is left out: `q * sigmoid(gate)` stands in
+    for `attention(q, k, v) * sigmoid(gate)` (same shapes into wo), so the time is the linears, their
+    producers and the elementwise glue.  Timed forward (no_grad) and forward + backward, as the reference
+    computes the producers (torch eager ops, every linear quantizing its own input or hitting the
+    shared-input cache) against fuse_producers' kernels plus group_siblings' grouped attention inputs."""
+    import types
+
+    from krea2_amd import fused
+
+    F_ = torch.nn.functional
+    M, D, KV, HID, r = 4608, 6144, 1536, 16384, 16
+    g = torch.Generator().manual_seed(21)
+
+    def norm():
+        return types.SimpleNamespace(scale=(torch.randn(D, generator=g) * 0.1).to(torch.bfloat16).to(dev), eps=1e-5)
+
+    attn = types.SimpleNamespace(wq=make_layer(k2, D, D, r, dev, 1), wk=make_layer(k2, D, KV, r, dev, 2),
+                                 wv=make_layer(k2, D, KV, r, dev, 3), gate=make_layer(k2, D, D, r, dev, 4),
+                                 wo=make_layer(k2, D, D, r, dev, 5))
+    mlp = types.SimpleNamespace(gate=make_layer(k2, D, HID, r, dev, 6), up=make_layer(k2, D, HID, r, dev, 7),
+                                down=make_layer(k2, HID, D, r, dev, 8))
+    pre, post = norm(), norm()
+    lin = (torch.randn(6 * D, generator=g) * 0.1).to(torch.bfloat16).to(dev)
+    vec = (torch.randn(1, 1, 6 * D, generator=g) * 0.3).to(torch.bfloat16).to(dev)
+    x0 = torch.randn(1, M, D, generator=g).to(torch.bfloat16).to(dev)
+    dy = (torch.randn(1, M, D, generator=g) * 1e-2).to(torch.bfloat16).to(dev)
+
+    def rms(nm, x):
+        return F_.rms_norm(x.float(), (D,), eps=nm.eps, weight=nm.scale.float() + 1.0).to(x.dtype)
+
+    def block(x, fuse):
+        ps, sh, pg, qs, qsh, qg = (vec + lin).chunk(6, dim=-1)
+        h = fused.modulated_rmsnorm(pre, x, ps, sh) if fuse else (1 + ps) * rms(pre, x) + sh
+        q, _k, _v, gt = attn.wq(h), attn.wk(h), attn.wv(h), attn.gate(h)
+        x = x + pg * attn.wo(q * torch.sigmoid(gt))
+        h = fused.modulated_rmsnorm(post, x, qs, qsh) if fuse else (1 + qs) * rms(post, x) + qsh
+        a, b = mlp.gate(h), mlp.up(h)
+        return x + qg * mlp.down(fused.swiglu(a, b) if fuse else F_.silu(a) * b)
+
+    def fwd_bwd(fuse):
+        x = x0.clone().requires_grad_(True)
+        block(x, fuse).backward(dy)
+
+    out = {}
+    for fuse in (False, True):
+        if fuse:
+            fused.group_siblings(types.SimpleNamespace(blocks=[types.SimpleNamespace(attn=attn)]))
+        with torch.no_grad():
+            t_f = sorted(time_loop(lambda: block(x0, fuse), steps) for _ in range(3))[1]
+        t_fb = sorted(time_loop(lambda: fwd_bwd(fuse), max(3, steps // 2)) for _ in range(3))[1]
+        out["fused" if fuse else "reference_ops"] = {"fwd_ms": round(t_f, 4), "fwd_bwd_ms": round(t_fb, 4)}
+    out["shape"] = f"M={M} width={D} kv={KV} hidden={HID} r={r}; attention excluded"
+    return out
+
+
 def run_cfg4(k2, steps, dev, settle_s=0.0):
     """Summed forward time of one double-stream block's quantized linears (image + text stream, plus the
     per-stream adaLN modulation at M=2), each a LoRALinear (r=16) over a W8A8 ConvRot base."""
@@ -581,6 +640,7 @@ def main():
     extra["cfg4"] = run_cfg4(k2, max(5, a.steps // 2), dev, a.settle / 2)
     extra["producers_cfg4_image"] = run_producers(k2, max(5, a.steps // 2), dev)
     extra["grouped_attn_inputs"] = run_grouped(k2, max(5, a.steps // 2), dev)
+    extra["krea_block_linears"] = run_krea_block(k2, max(5, a.steps // 2), dev)
     cpu = None
     if not a.no_cpu:
         cpu = cpu_baseline(cfg, res["x"], res["W"], res["b"], res["A"], res["B"])

@@ -62,7 +62,10 @@ int k2q_quant_weight_i4(const void* w, int w_dtype, int64_t N, int64_t K,
  *   n = bf16((x * rsqrt(mean_k x^2 + eps)) * (norm_scale + 1)),  h = bf16(bf16(bf16(1 + p) * n) + b),
  *   p / b = bf16 mod_scale / mod_shift at entry (row / rows_per_batch) * ld_mod (ld_mod 0: one entry).
  * k2q_swiglu_bwd is the autograd of the SwiGLU product (n bf16 elements, n % 8 == 0):
- *   du = bf16(dh * bf16(silu(g))),  dg = bf16((bf16(dh * u) * sig) * (1 + g (1 - sig))),  sig = sigmoid(g). */
+ *   du = bf16(dh * bf16(silu(g))),  dg = bf16((bf16(dh * u) * sig) * (1 + g (1 - sig))),  sig = sigmoid(g).
+ * k2q_rmsmod_bwd is the autograd of the modulated RMSNorm for x (x, dh, dx contiguous M x K bf16, K % 8 == 0):
+ *   g = bf16(dh * bf16(1 + p)) * (norm_scale + 1),  r = rsqrt(mean_k x^2 + eps),
+ *   dx = bf16(g r - x (r^3 / K) sum_k g x),  p indexed as in k2q_rmsmod_rotquant. */
 int k2q_swiglu_rotquant(const uint16_t* gate, int64_t ldg, const uint16_t* up, int64_t ldu, int64_t M, int64_t K,
                         uint16_t* h, int8_t* q, float* s, void* stream);
 int k2q_rmsmod_rotquant(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, const float* norm_scale, float eps,
@@ -70,6 +73,8 @@ int k2q_rmsmod_rotquant(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, co
                         int64_t rows_per_batch, uint16_t* h, int8_t* q, float* s, void* stream);
 int k2q_swiglu_bwd(const uint16_t* dh, const uint16_t* gate, const uint16_t* up, int64_t n, uint16_t* dgate,
                    uint16_t* dup, void* stream);
+int k2q_rmsmod_bwd(const uint16_t* dh, const uint16_t* x, int64_t M, int64_t K, const float* norm_scale, float eps,
+                   const uint16_t* mod_scale, int64_t ld_mod, int64_t rows_per_batch, uint16_t* dx, void* stream);
 
 /* LoRA down-projection u = x.f32 @ A^T (lora.py:47, first product).  When the rows alone do not fill the
  * GPU, K is cut into slices whose partials meet in ws (k2q_lora_down_ws_bytes(M, K, r) bytes; 0 means none

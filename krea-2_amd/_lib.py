@@ -49,6 +49,7 @@ _SIGNATURES = {
     "k2q_swiglu_rotquant": ([_p, _i64, _p, _i64, _i64, _i64, _p, _p, _p, _p], _int),
     "k2q_rmsmod_rotquant": ([_p, _i64, _i64, _i64, _p, _f32, _p, _p, _i64, _i64, _p, _p, _p, _p], _int),
     "k2q_swiglu_bwd": ([_p, _p, _p, _i64, _p, _p, _p], _int),
+    "k2q_rmsmod_bwd": ([_p, _p, _i64, _i64, _p, _f32, _p, _i64, _i64, _p, _p], _int),
     "k2q_lora_down_ws_bytes": ([_i64, _i64, _i64], _i64),
     "k2q_lora_down": ([_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _p], _int),
     "k2q_lora_grads_ws_bytes": ([_i64, _i64, _i64, _i64], _i64),
@@ -248,6 +249,36 @@ def rmsmod_rotquant(x: torch.Tensor, norm_scale: torch.Tensor, eps: float, mod_s
                                       _ptr(mod_shift), ldm, rows_per_batch if B > 1 else M, _ptr(h), _ptr(q),
                                       _ptr(s), _stream(dev)), "k2q_rmsmod_rotquant")
     return h, q, s
+
+
+def rmsmod_bwd(dh: torch.Tensor, x: torch.Tensor, norm_scale: torch.Tensor, eps: float, mod_scale: torch.Tensor,
+               rows_per_batch: int) -> torch.Tensor:
+    """Input gradient of :func:`rmsmod_rotquant`'s ``h`` for ``x``: ``dx`` (M,K) bf16.  ``dh``, ``x`` (M,K) bf16
+    contiguous; ``norm_scale`` (K,) f32; ``mod_scale`` (B,K) bf16 rows indexed as in the forward."""
+    _need(dh, "dh", torch.bfloat16, 2)
+    dev = dh.device
+    _need(x, "x", torch.bfloat16, 2, dev)
+    if dh.shape != x.shape:
+        raise ValueError("dh and x differ in shape")
+    M, K = x.shape
+    if M < 1 or K % 8 or K > 16384:
+        raise ValueError(f"x {tuple(x.shape)}: K must be a multiple of 8 up to 16384")
+    _need(norm_scale, "norm_scale", torch.float32, 1, dev)
+    if norm_scale.shape[0] != K:
+        raise ValueError("norm_scale length != K")
+    if mod_scale.dtype != torch.bfloat16 or mod_scale.dim() != 2 or mod_scale.shape[1] != K or \
+            mod_scale.stride(1) != 1 or mod_scale.data_ptr() % 16 or mod_scale.device != dev:
+        raise ValueError(f"mod_scale must be a (B, {K}) bf16 tensor with contiguous 16-byte aligned rows")
+    B = mod_scale.shape[0]
+    ldm = 0 if B == 1 else mod_scale.stride(0)
+    rows_per_batch = int(rows_per_batch)
+    if B > 1 and (ldm % 8 or rows_per_batch * B != M):
+        raise ValueError(f"rows_per_batch={rows_per_batch} does not split {M} rows into {B} entries")
+    _device_check(dev)
+    dx = torch.empty_like(x)
+    _check(load().k2q_rmsmod_bwd(_ptr(dh), _ptr(x), M, K, _ptr(norm_scale), float(eps), _ptr(mod_scale), ldm,
+                                 rows_per_batch if B > 1 else M, _ptr(dx), _stream(dev)), "k2q_rmsmod_bwd")
+    return dx
 
 
 def swiglu_bwd(dh: torch.Tensor, g: torch.Tensor, u: torch.Tensor):

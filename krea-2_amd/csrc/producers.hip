@@ -261,7 +261,142 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const uint4* __restrict
   }
 }
 
+// Input gradient of the modulated RMSNorm (the autograd of the forward's eager ops for x alone):
+//   dn = bf16(dh * bf16(1 + p)),  g = dn * (w + 1),  r = rsqrt(mean x^2 + eps),
+//   dx = bf16(g r - x (r^3 / K) sum_k(g x)).
+// A team of 64 * WPR lanes owns a row; lane t handles the 8-element chunks at 8 t + 8 T c, c < kNCH, held
+// packed (bf16 pairs) between the two row reductions.
+template <int WPR, int kNCH>
+__global__ __launch_bounds__(256) void rmsmod_bwd_kernel(const uint16_t* __restrict__ dh, const uint16_t* __restrict__ x,
+                                                         int64_t M, int K, const float* __restrict__ nw, float eps,
+                                                         const uint16_t* __restrict__ mscale, int64_t ldm, int64_t rpb,
+                                                         uint16_t* __restrict__ dx) {
+  constexpr int T = 64 * WPR;
+  constexpr int ROWS = 4 / WPR;
+  __shared__ float sred[2][4];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * ROWS + wave / WPR;
+  const int t = (wave % WPR) * 64 + lane;
+  const bool row_ok = row < M;
+  const int64_t rr = row_ok ? row : 0;
+  const uint16_t* ms = mscale + (rr / rpb) * ldm;
+
+  uint4 xv[kNCH], dv[kNCH];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < kNCH; ++c) {
+    const int col = 8 * t + 8 * T * c;
+    const bool ok = col < K;
+    xv[c] = ok ? *reinterpret_cast<const uint4*>(x + rr * K + col) : make_uint4(0, 0, 0, 0);
+    dv[c] = ok ? *reinterpret_cast<const uint4*>(dh + rr * K + col) : make_uint4(0, 0, 0, 0);
+    const uint32_t w[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float a = __uint_as_float(w[j] << 16), b = __uint_as_float(w[j] & 0xffff0000u);
+      ss += a * a;
+      ss += b * b;
+    }
+  }
+  ss = wave_sum(ss);
+  if (WPR > 1) {
+    if (lane == 0) sred[0][wave] = ss;
+    __syncthreads();
+    const int w0 = (wave / WPR) * WPR;
+    ss = 0.f;
+#pragma unroll
+    for (int w = 0; w < WPR; ++w) ss += sred[0][w0 + w];
+  }
+  const float r = __fdiv_rn(1.f, __fsqrt_rn(__fdiv_rn(ss, (float)K) + eps));
+
+  // g = bf16(dh * p1) * (w + 1), kept in f32 (8 per chunk) for the final pass
+  float gv[kNCH][8];
+  float dot = 0.f;
+#pragma unroll
+  for (int c = 0; c < kNCH; ++c) {
+    const int col = 8 * t + 8 * T * c;
+    const int cc = col < K ? col : 0;
+    float w[8];
+    const float4 w0 = *reinterpret_cast<const float4*>(nw + cc), w1 = *reinterpret_cast<const float4*>(nw + cc + 4);
+    w[0] = w0.x; w[1] = w0.y; w[2] = w0.z; w[3] = w0.w; w[4] = w1.x; w[5] = w1.y; w[6] = w1.z; w[7] = w1.w;
+    const uint4 pv = *reinterpret_cast<const uint4*>(ms + cc);
+    const uint32_t pw[4] = {pv.x, pv.y, pv.z, pv.w};
+    const uint32_t dw[4] = {dv[c].x, dv[c].y, dv[c].z, dv[c].w};
+    const uint32_t xw[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float p0 = 1.f + __uint_as_float(pw[j] << 16), p1 = 1.f + __uint_as_float(pw[j] & 0xffff0000u);
+      bf16r2(p0, p1);
+      float n0 = __uint_as_float(dw[j] << 16) * p0, n1 = __uint_as_float(dw[j] & 0xffff0000u) * p1;
+      bf16r2(n0, n1);
+      const float g0 = n0 * (w[2 * j] + 1.f), g1 = n1 * (w[2 * j + 1] + 1.f);
+      gv[c][2 * j] = g0;
+      gv[c][2 * j + 1] = g1;
+      dot += g0 * __uint_as_float(xw[j] << 16);
+      dot += g1 * __uint_as_float(xw[j] & 0xffff0000u);
+    }
+  }
+  dot = wave_sum(dot);
+  if (WPR > 1) {
+    if (lane == 0) sred[1][wave] = dot;
+    __syncthreads();
+    const int w0 = (wave / WPR) * WPR;
+    dot = 0.f;
+#pragma unroll
+    for (int w = 0; w < WPR; ++w) dot += sred[1][w0 + w];
+  }
+  if (!row_ok) return;
+  const float c3 = __fdiv_rn(r * r * r * dot, (float)K);
+#pragma unroll
+  for (int c = 0; c < kNCH; ++c) {
+    const int col = 8 * t + 8 * T * c;
+    if (col >= K) continue;
+    const uint32_t xw[4] = {xv[c].x, xv[c].y, xv[c].z, xv[c].w};
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float d0 = gv[c][2 * j] * r - __uint_as_float(xw[j] << 16) * c3;
+      const float d1 = gv[c][2 * j + 1] * r - __uint_as_float(xw[j] & 0xffff0000u) * c3;
+      o[j] = pack_bf16x2(d0, d1);
+    }
+    *reinterpret_cast<uint4*>(dx + row * K + col) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+template <int WPR>
+void launch_rmsmod_bwd(const uint16_t* dh, const uint16_t* x, int64_t M, int K, const float* nw, float eps,
+                       const uint16_t* ms, int64_t ldm, int64_t rpb, uint16_t* dx, hipStream_t st) {
+  const dim3 grid((unsigned)((M + (4 / WPR) - 1) / (4 / WPR)));
+  const int nch = (K + 512 * WPR - 1) / (512 * WPR);
+#define K2Q_RMB(N)                                                                                            \
+  case N:                                                                                                     \
+    hipLaunchKernelGGL((rmsmod_bwd_kernel<WPR, N>), grid, dim3(256), 0, st, dh, x, M, K, nw, eps, ms, ldm, rpb, dx); \
+    break;
+  switch (nch) {
+    K2Q_RMB(1) K2Q_RMB(2) K2Q_RMB(3) K2Q_RMB(4) K2Q_RMB(5) K2Q_RMB(6) K2Q_RMB(7)
+    default: hipLaunchKernelGGL((rmsmod_bwd_kernel<WPR, 8>), grid, dim3(256), 0, st, dh, x, M, K, nw, eps, ms, ldm,
+                                rpb, dx); break;
+  }
+#undef K2Q_RMB
+}
+
 }  // namespace
+
+extern "C" int k2q_rmsmod_bwd(const uint16_t* dh, const uint16_t* x, int64_t M, int64_t K, const float* norm_scale,
+                              float eps, const uint16_t* mod_scale, int64_t ld_mod, int64_t rows_per_batch,
+                              uint16_t* dx, void* stream) {
+  if (M < 1 || K < 8 || K % 8) return K2Q_EINVAL;
+  if (K > 16384) return K2Q_EUNSUPPORTED;
+  if (!dh || !x || !norm_scale || !mod_scale || !dx || !k2q_aligned(dh, 16) || !k2q_aligned(x, 16) ||
+      !k2q_aligned(norm_scale, 16) || !k2q_aligned(mod_scale, 16) || !k2q_aligned(dx, 16) || ld_mod < 0 ||
+      ld_mod % 8 || rows_per_batch < 1 || !(eps >= 0.f))
+    return K2Q_EINVAL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (K <= 4096) launch_rmsmod_bwd<1>(dh, x, M, (int)K, norm_scale, eps, mod_scale, ld_mod, rows_per_batch, dx, st);
+  else if (K <= 8192) launch_rmsmod_bwd<2>(dh, x, M, (int)K, norm_scale, eps, mod_scale, ld_mod, rows_per_batch, dx, st);
+  else launch_rmsmod_bwd<4>(dh, x, M, (int)K, norm_scale, eps, mod_scale, ld_mod, rows_per_batch, dx, st);
+  return k2q_launch_status();
+}
 
 extern "C" int k2q_swiglu_rotquant(const uint16_t* gate, int64_t ldg, const uint16_t* up, int64_t ldu, int64_t M,
                                    int64_t K, uint16_t* h, int8_t* q, float* s, void* stream) {

@@ -71,8 +71,9 @@ def swiglu(gate_out: torch.Tensor, up_out: torch.Tensor) -> torch.Tensor:
 
 class _RmsModQuantFn(torch.autograd.Function):
     """Forward: the modulated RMSNorm of ``mmdit.py:314-317`` with the codes of its output (one gfx950 pass).
-    Backward: the reference's own formula re-run on the saved inputs under autograd (``F.rms_norm`` and the
-    eager bf16 modulation), so the gradients are the reference's."""
+    Backward: when only ``x`` needs a gradient (LoRA training: the norm and modulation are frozen and the
+    conditioning vector comes from frozen layers), ``k2q_rmsmod_bwd``; otherwise the reference's own formula
+    re-run on the saved inputs under autograd (``F.rms_norm`` and the eager bf16 modulation)."""
 
     @staticmethod
     def forward(ctx, x2, norm_scale, mod_scale, mod_shift, eps, rows_per_batch):
@@ -90,6 +91,12 @@ class _RmsModQuantFn(torch.autograd.Function):
         B = ms.shape[0]
         rpb = ctx.rpb if B > 1 else M
         need = ctx.needs_input_grad[:4]
+        if need[0] and not any(need[1:]):
+            dh = dh.contiguous()
+            if dh.dtype != torch.bfloat16:
+                dh = dh.to(torch.bfloat16)
+            dx = _lib.rmsmod_bwd(dh, x2.contiguous(), ns.float().contiguous(), ctx.eps, ms, rpb)
+            return dx, None, None, None, None, None
         with torch.enable_grad():
             leaves = [t.detach().requires_grad_(n) for t, n in zip((x2, ns, ms, mb), need)]
             x3 = leaves[0].reshape(-1, rpb, K)

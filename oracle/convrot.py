@@ -362,3 +362,23 @@ def rmsmod(x, norm_scale, eps: float, mod_scale, mod_shift, rows_per_batch: int)
     n = bf16_round((x * r[:, None]) * w1[None, :])
     p1 = bf16_round(np.float32(1.0) + ms[b])
     return bf16_round(bf16_round(p1 * n) + mb[b])
+
+
+def rmsmod_backward_x(dh, x, norm_scale, eps: float, mod_scale, rows_per_batch: int) -> np.ndarray:
+    """The input gradient of :func:`rmsmod` for ``x`` under the reference's eager ops: the modulation's
+    product backward rounds ``dn = bf16(dh * bf16(1 + p))`` (bf16 tensors), the cast ``.to(x.dtype)`` passes it
+    to float32, and ``F.rms_norm``'s backward (``mmdit.py:158-160``) with ``g = dn * (scale + 1)`` is
+    ``dx = g r - x (r^3 / K) sum_k(g x)``, ``r = rsqrt(mean(x^2) + eps)``, rounded to bf16 at the end.
+    Evaluated in float64 here (the kernels' float32 differs by rounding only)."""
+    x = np.asarray(x, dtype=np.float32)
+    M, K = x.shape
+    dh = np.asarray(dh, dtype=np.float32)
+    ms = np.asarray(mod_scale, dtype=np.float32).reshape(-1, K)
+    b = np.zeros(M, dtype=np.int64) if ms.shape[0] == 1 else np.arange(M) // int(rows_per_batch)
+    p1 = bf16_round(np.float32(1.0) + ms[b])
+    g = bf16_round(dh * p1).astype(np.float64) * (np.asarray(norm_scale, np.float32) + np.float32(1.0))[None, :]
+    x64 = x.astype(np.float64)
+    r = 1.0 / np.sqrt((x64 * x64).mean(axis=1) + eps)
+    dot = (g * x64).sum(axis=1)
+    dx = g * r[:, None] - x64 * (r ** 3 * dot / K)[:, None]
+    return bf16_round(dx.astype(np.float32))

@@ -359,3 +359,24 @@ def test_rmsmod_matches_torch_eager_bf16():
     ref = ((1 + _bf16(p)[:, None, :]) * n.to(torch.bfloat16) + _bf16(b)[:, None, :]).float().reshape(B * L, K)
     d = _ulp_diff(orc.rmsmod(x, ns, eps, p, b, L), ref.numpy())
     assert d.max() <= 1 and (d == 0).mean() > 0.999
+
+
+def test_rmsmod_backward_x_matches_torch_autograd():
+    """Against torch's CPU autograd of the reference formula (bf16 tensors, ``F.rms_norm`` on float32):
+    close in relative Frobenius norm and equal in most elements; a dropped bf16 rounding of ``dn`` or a
+    missing ``+1`` on the norm weight fails it."""
+    rng = np.random.default_rng(24)
+    B, L, K, eps = 2, 32, 512, 1e-5
+    x = orc.bf16_round(rng.standard_normal((B * L, K)).astype(np.float32) * 2)
+    ns = (rng.standard_normal(K) * 0.1).astype(np.float32)
+    p = orc.bf16_round(rng.standard_normal((B, K)).astype(np.float32) * 0.3)
+    b = orc.bf16_round(rng.standard_normal((B, K)).astype(np.float32) * 0.3)
+    dh = orc.bf16_round(rng.standard_normal((B * L, K)).astype(np.float32) * 1e-2)
+    xt = _bf16(x).reshape(B, L, K).requires_grad_(True)
+    n = torch.nn.functional.rms_norm(xt.float(), (K,), eps=eps, weight=torch.from_numpy(ns) + 1.0)
+    h = (1 + _bf16(p)[:, None, :]) * n.to(torch.bfloat16) + _bf16(b)[:, None, :]
+    h.backward(_bf16(dh).reshape(B, L, K))
+    ref = xt.grad.float().reshape(B * L, K).numpy()
+    dx = orc.rmsmod_backward_x(dh, x, ns, eps, p, L)
+    assert np.linalg.norm(dx - ref) / np.linalg.norm(ref) < 1e-3     # unrounded dn: 2.8e-3
+    assert (_ulp_diff(dx, ref) == 0).mean() > 0.99                    # unrounded dn: 73% equal
