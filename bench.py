@@ -293,12 +293,16 @@ def run_cfg3(k2, steps, dev, settle_s=0.0):
         ms = time_loop(step, steps)
         with torch.no_grad():
             ms_fwd = time_loop(lambda: layer(x), steps)
+        k2.set_dx_weight_cache(layer, True)     # the frozen base's effective weight kept between backwards
+        ms_cached = time_loop(step, steps)
+        k2.set_dx_weight_cache(layer, False)
     finally:
         k2.quantize.shared_input_quant.enabled = prev
     ops_fwd = 2.0 * c["M"] * c["N"] * c["K"]
     return {"step_ms": round(ms, 4), "fwd_ms": round(ms_fwd, 4), "bwd_ms": round(ms - ms_fwd, 4),
             "fwd_tops": round(ops_fwd / (ms_fwd * 1e-3) / 1e12, 1),
-            "dx_tflops": round(ops_fwd / ((ms - ms_fwd) * 1e-3) / 1e12, 1)}
+            "dx_tflops": round(ops_fwd / ((ms - ms_fwd) * 1e-3) / 1e12, 1),
+            "step_ms_dx_weight_cached": round(ms_cached, 4)}
 
 
 def run_producers(k2, steps, dev):

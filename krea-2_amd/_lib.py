@@ -545,12 +545,38 @@ def gemm_w4a8_f32(qx, q4, s4) -> torch.Tensor:
 # ----------------------------------------------------------------------------------------------------------
 # (4) input gradient
 # ----------------------------------------------------------------------------------------------------------
+def dx_weight(qw, sw, *, w4: bool = False) -> torch.Tensor:
+    """The effective weight of the straight-through forward, ``bf16(2^-7 W_hat R)^T`` (K,N): what
+    :func:`gemm_dx` builds on every call unless it is handed one (``wt=``)."""
+    dev = qw.device
+    if w4:
+        _need(qw, "q_w4", torch.uint8, 2, dev)
+        N, K = qw.shape[0], qw.shape[1] * 2
+        _need(sw, "s_w4", torch.bfloat16, 2, dev)
+        if sw.shape != (K // INT4_GROUP, N):
+            raise ValueError("s_w4 shape mismatch")
+    else:
+        _need(qw, "q_w", torch.int8, 2, dev)
+        N, K = qw.shape
+        _need(sw, "s_w", torch.float32, 1, dev)
+        if sw.shape[0] != N:
+            raise ValueError("s_w length mismatch")
+    _check_k(K)
+    if N % 64:
+        raise ValueError(f"out_features={N} must be a multiple of 64 for the input-gradient GEMM")
+    _device_check(dev)
+    wt = torch.empty((K, N), dtype=torch.bfloat16, device=dev)
+    _check(load().k2q_dx_prep_eff(None if w4 else _ptr(qw), None if w4 else _ptr(sw), _ptr(qw) if w4 else None,
+                                  _ptr(sw) if w4 else None, N, K, _ptr(wt), _stream(dev)), "k2q_dx_prep_eff")
+    return wt
+
+
 def gemm_dx(dy, qw, sw, *, w4: bool = False, g=None, lora_a=None, split: bool = True,
-            fold_rotation: bool = True) -> torch.Tensor:
+            fold_rotation: bool = True, wt=None) -> torch.Tensor:
     """``dx = bf16(2^-7 (dy W_hat) R + g lora_A)`` (M,K); ``dy`` (M,N) bf16, ``g`` (M,r) f32 already
     scaled (``lora_scale * dy @ lora_B``), ``lora_a`` (r,K) f32.  ``fold_rotation`` (default) builds the
-    effective weight ``bf16(2^-7 W_hat R)^T`` and runs the plain GEMM; otherwise ``bf16(W_hat)^T`` and the
-    GEMM with the inverse rotation in its epilogue."""
+    effective weight ``bf16(2^-7 W_hat R)^T`` (or takes it as ``wt``, from :func:`dx_weight`) and runs the
+    plain GEMM; otherwise ``bf16(W_hat)^T`` and the GEMM with the inverse rotation in its epilogue."""
     _need(dy, "dy", torch.bfloat16, 2)
     dev = dy.device
     M, N = dy.shape
@@ -581,11 +607,18 @@ def gemm_dx(dy, qw, sw, *, w4: bool = False, g=None, lora_a=None, split: bool = 
         _check_rank(r)
     _device_check(dev)
     st = _stream(dev)
-    wt = torch.empty((K, N), dtype=torch.bfloat16, device=dev)
     lib = load()
-    prep = lib.k2q_dx_prep_eff if fold_rotation else lib.k2q_dx_prep
-    _check(prep(None if w4 else _ptr(qw), None if w4 else _ptr(sw), _ptr(qw) if w4 else None,
-                _ptr(sw) if w4 else None, N, K, _ptr(wt), st), "k2q_dx_prep")
+    if wt is not None:
+        if not fold_rotation:
+            raise ValueError("a prebuilt effective weight needs fold_rotation=True")
+        _need(wt, "wt", torch.bfloat16, 2, dev)
+        if wt.shape != (K, N):
+            raise ValueError(f"wt must be (K, N) = {(K, N)}, got {tuple(wt.shape)}")
+    else:
+        wt = torch.empty((K, N), dtype=torch.bfloat16, device=dev)
+        prep = lib.k2q_dx_prep_eff if fold_rotation else lib.k2q_dx_prep
+        _check(prep(None if w4 else _ptr(qw), None if w4 else _ptr(sw), _ptr(qw) if w4 else None,
+                    _ptr(sw) if w4 else None, N, K, _ptr(wt), st), "k2q_dx_prep")
     dx = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
     ws, nws = _workspace(lib.k2q_gemm_dx_ws_bytes(M, N, K) if split else 0, dev)
     gemm = lib.k2q_gemm_dx_lin if fold_rotation else lib.k2q_gemm_dx

@@ -237,7 +237,7 @@ class _GroupedFn(torch.autograd.Function):
                     g, grads[2 * li], grads[2 * li + 1] = _lib.lora_grads(dy, x2 if need_a else None, u_i, Bs[li], sc)
                 if ctx.needs_input_grad[0]:
                     d = _lib.gemm_dx(dy, base.qweight, base.weight_scale, w4=False, g=g,
-                                     lora_a=As[li] if has else None)
+                                     lora_a=As[li] if has else None, wt=base.cached_dx_weight())
                     dx = d if dx is None else dx + d
             li += int(has)
         return (dx, None, None, None, None, *grads)

@@ -75,12 +75,13 @@ class _ConvRotLinearFn(torch.autograd.Function):
     Deterministic (no atomics, fixed reduction order), so checkpoint recompute reproduces the forward."""
 
     @staticmethod
-    def forward(ctx, x2, lora_A, lora_B, qweight, wscale, bias, w4, lora_scale, qx, sx):
+    def forward(ctx, x2, lora_A, lora_B, qweight, wscale, bias, w4, lora_scale, qx, sx, owner):
         u = _lib.lora_down(x2, lora_A) if lora_A is not None else None
         gemm = _lib.gemm_w4a8 if w4 else _lib.gemm_w8a8
         y = gemm(qx, sx, qweight, wscale, bias, u, lora_B, lora_scale)
         ctx.w4 = w4
         ctx.lora_scale = lora_scale
+        ctx.owner = owner
         ctx.save_for_backward(x2 if lora_A is not None else None, u, lora_A, lora_B, qweight, wscale)
         return y
 
@@ -96,8 +97,9 @@ class _ConvRotLinearFn(torch.autograd.Function):
                                         u if ctx.needs_input_grad[2] else None, B, ctx.lora_scale)
         dx = None
         if ctx.needs_input_grad[0]:
-            dx = _lib.gemm_dx(dy, qweight, wscale, w4=ctx.w4, g=g, lora_a=A if g is not None else None)
-        return dx, dA, dB, None, None, None, None, None, None, None
+            dx = _lib.gemm_dx(dy, qweight, wscale, w4=ctx.w4, g=g, lora_a=A if g is not None else None,
+                              wt=ctx.owner.cached_dx_weight())
+        return dx, dA, dB, None, None, None, None, None, None, None, None
 
 
 class ConvRotLinear(nn.Module):
@@ -115,6 +117,8 @@ class ConvRotLinear(nn.Module):
         if mode not in MODES:
             raise ValueError(f"mode must be one of {MODES}, got {mode!r}")
         self.mode = mode
+        self.cache_dx_weight = False   # keep the backward's effective weight between calls (see below)
+        self._dx_cache = None
         if lin is None:  # filled by from_quantized
             return
         w = lin.weight.data
@@ -171,6 +175,22 @@ class ConvRotLinear(nn.Module):
     def weight(self) -> torch.Tensor:  # device probe for LoRALinear (quantize.py:44-46)
         return self.qweight
 
+    def cached_dx_weight(self) -> torch.Tensor | None:
+        """With ``cache_dx_weight`` on, the effective weight ``bf16(2^-7 W_hat R)^T`` that the input-gradient
+        GEMM reads (K x N bf16, 2 bytes per weight), built once and reused while the codes and scales are the
+        same tensors (pointer, version, device); otherwise None and every backward builds it.  The frozen
+        base never changes during LoRA training, so the cache trades 2 bytes per weight of HBM (24 GB for
+        the 12.2e9 block weights) for the per-call weight pass; it defeats block swap's paging."""
+        if not getattr(self, "cache_dx_weight", False):
+            self._dx_cache = None
+            return None
+        q, s = self.qweight, self.wscale
+        key = (q.data_ptr(), q._version, s.data_ptr(), s._version, q.device)
+        if self._dx_cache is None or self._dx_cache[0] != key:
+            self._dx_cache = None
+            self._dx_cache = (key, _lib.dx_weight(q, self.weight_scale, w4=self.mode == "w4a8"))
+        return self._dx_cache[1]
+
     @property
     def weight_scale(self) -> torch.Tensor:
         """The scales as floats: f32 (N,) for w8a8, bf16 (K/64, N) for w4a8 (views, no copy)."""
@@ -202,7 +222,7 @@ class ConvRotLinear(nn.Module):
         with torch.no_grad():
             qx, sx = shared_input_quant.lookup(x, x2)
         y = _ConvRotLinearFn.apply(x2, lora_A, lora_B, self.qweight, self.weight_scale, self._bias_f32(),
-                                   self.mode == "w4a8", float(lora_scale), qx, sx)
+                                   self.mode == "w4a8", float(lora_scale), qx, sx, self)
         return y.reshape(*lead, self.out_features)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
@@ -225,6 +245,22 @@ def quantize_dit_convrot(dit, mode: str = "w8a8") -> int:
     for mod, name, child in targets:
         setattr(mod, name, ConvRotLinear(child, mode))
     return len(targets)
+
+
+def set_dx_weight_cache(model: nn.Module, enable: bool = True) -> int:
+    """Turn the input-gradient weight cache of every :class:`ConvRotLinear` in ``model`` on or off (off also
+    frees the cached weights).  On, each layer keeps ``bf16(2^-7 W_hat R)^T`` (2 bytes per weight) after its
+    first backward instead of rebuilding it on every call.  The cache follows the codes' pointer and version:
+    block swap's re-pointering rebuilds it; an edit through ``.data`` does not, so turn it off and on again
+    after one.  Returns the number of layers set."""
+    n = 0
+    for m in model.modules():
+        if isinstance(m, ConvRotLinear):
+            m.cache_dx_weight = bool(enable)
+            if not enable:
+                m._dx_cache = None
+            n += 1
+    return n
 
 
 # ----------------------------------------------------------------------------------------------------------

@@ -426,6 +426,37 @@ def test_module_backward_matches_oracle(k2, dev, mode):
     assert base.qweight.grad is None
 
 
+@pytest.mark.parametrize("mode", ["w8a8", "w4a8"])
+def test_dx_weight_cache(k2, dev, mode):
+    """With the input-gradient weight cache on, dX and the LoRA grads are bit-identical to the uncached
+    backward, the cached weight is reused across calls and rebuilt when the codes are re-pointered (block
+    swap's `p.data = ...`); turning it off frees it."""
+    _, base, lora = _layers(k2, dev, K=512, N=256, r=16, mode=mode)
+    x = make_x(160, 512, seed=21).to(dev)
+    dy = (torch.randn(160, 256, generator=torch.Generator().manual_seed(5)) * 1e-3).to(torch.bfloat16).to(dev)
+
+    def grads():
+        lora.lora_A.grad = lora.lora_B.grad = None
+        xr = x.clone().requires_grad_(True)
+        lora(xr).backward(dy)
+        return xr.grad.clone(), lora.lora_A.grad.clone(), lora.lora_B.grad.clone()
+
+    ref = grads()
+    assert base._dx_cache is None
+    assert k2.set_dx_weight_cache(lora, True) == 1
+    first = grads()
+    w1 = base._dx_cache[1]
+    second = grads()
+    assert base._dx_cache[1] is w1                               # reused
+    base.qweight.data = base.qweight.data.clone()                # re-pointered as block swap does
+    third = grads()
+    assert base._dx_cache[1] is not w1 and torch.equal(base._dx_cache[1], w1)
+    for got in (first, second, third):
+        assert all(torch.equal(a, b) for a, b in zip(got, ref))
+    k2.set_dx_weight_cache(lora, False)
+    assert base._dx_cache is None and base.cached_dx_weight() is None
+
+
 def test_deterministic_and_checkpoint_recompute(k2, dev):
     _, _, lora = _layers(k2, dev)
     x = make_x(512, 512, seed=14).to(dev)
