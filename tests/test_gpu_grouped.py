@@ -181,3 +181,31 @@ def test_group_member_with_changed_adapter_runs_alone(k2, dev):
     assert torch.equal(k, attn.wk.base(x))
     assert (v.float() - ref_v.float()).abs().max() <= ref_v.float().abs().max() * 2 ** -7
     assert (q.float() - ref_q.float()).abs().max() <= ref_q.float().abs().max() * 2 ** -7
+
+
+@pytest.mark.timeout(300)
+def test_producers_and_grouping_together(k2, dev):
+    """fuse_producers and group_siblings on the same blocks: the patched block forward feeds the grouped
+    attention inputs the codes its fused RMSNorm produced (no rotate/quant for them), outputs and gradients
+    stay within the bf16 bars of the plain block, and a checkpointed backward equals a plain one bit for bit."""
+    from krea2_amd.quantize import shared_input_quant
+    dit, ad = _build(k2, dev)
+    fdit = copy.deepcopy(dit)
+    fad = {k: fdit.get_submodule(k) for k in ad}
+    assert k2.fuse_producers(fdit) == 4 and k2.group_siblings(fdit) == 2
+    g = torch.Generator().manual_seed(8)
+    B, Lt = 2, 128
+    x = (torch.randn(B, Lt, FEAT, generator=g)).to(torch.bfloat16).to(dev)
+    vec = (torch.randn(B, 1, 6 * FEAT, generator=g) * 0.3).to(torch.bfloat16).to(dev)
+    dy = (torch.randn(B, Lt, FEAT, generator=g) * 1e-2).to(torch.bfloat16).to(dev)
+    y0, dx0, gr0 = _step(dit, ad, x, vec, dy)
+    m0 = shared_input_quant.misses
+    y1, dx1, gr1 = _step(fdit, fad, x, vec, dy)
+    assert shared_input_quant.misses - m0 == 2    # only the attention output (wo's input), once per block
+    assert _rel(y1, y0) < 1e-2 and _rel(dx1, dx0) < 1e-2
+    for k in gr0:
+        assert _rel(gr1[k][0], gr0[k][0]) < 2e-2 and _rel(gr1[k][1], gr0[k][1]) < 2e-2, k
+    y2, dx2, gr2 = _step(fdit, fad, x, vec, dy, ckpt=True)
+    assert torch.equal(y2, y1) and torch.equal(dx2, dx1)
+    for k in gr1:
+        assert torch.equal(gr2[k][0], gr1[k][0]) and torch.equal(gr2[k][1], gr1[k][1]), k
