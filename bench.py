@@ -482,8 +482,9 @@ def run_cfg4(k2, steps, dev, settle_s=0.0):
 
 def profile_pass(k2, dev):
     """Fixed launches for rocprofv3 counter passes: cfg2 rotate/quant, LoRA down, GEMM, 3 times each; the cfg3
-    input-gradient GEMM (with its LoRA term) 3 times; then a plain 256 MiB device copy (Tensor.copy_) 3 times,
-    the calibration point for FETCH/WRITE_SIZE."""
+    input-gradient GEMM (with its LoRA term) 3 times; the two producer kernels at cfg4's image-stream shapes
+    and the grouped attention-input GEMM (M = 4608, 6144 -> 6144 | 1536 | 1536 | 6144, r = 16) 3 times each;
+    then a plain 256 MiB device copy (Tensor.copy_) 3 times, the calibration point for FETCH/WRITE_SIZE."""
     L = k2._lib
     c = CONFIGS[2]
     x, W, b, A, B = synth(c["M"], c["K"], c["N"], c["r"], c["bias"])
@@ -501,6 +502,30 @@ def profile_pass(k2, dev):
     g = (torch.randn(c3["M"], c3["r"], generator=g3) * 1e-3).to(dev)
     for _ in range(3):
         L.gemm_dx(dy, qw3, sw3, g=g, lora_a=A3)
+    del qw3, dy, A3, g
+    # the producer kernels at cfg4's image-stream shapes and the grouped attention-input GEMM at M = 4608
+    Mi, Ki, Kh = 8192, 3072, 12288
+    xi = torch.randn(Mi, Ki, generator=g3).to(torch.bfloat16).to(dev)
+    ns = (torch.randn(Ki, generator=g3) * 0.1).to(dev)
+    mod = (torch.randn(2, Ki, generator=g3) * 0.3).to(torch.bfloat16).to(dev)
+    gt = (torch.randn(Mi, Kh, generator=g3) * 3).to(torch.bfloat16).to(dev)
+    ut = torch.randn(Mi, Kh, generator=g3).to(torch.bfloat16).to(dev)
+    for _ in range(3):
+        L.rmsmod_rotquant(xi, ns, 1e-5, mod, mod, Mi // 2)
+        L.swiglu_rotquant(gt, ut)
+    del xi, gt, ut
+    Mg, Kg, r = 4608, 6144, 16
+    qg = torch.randint(-127, 128, (Mg, Kg), generator=g3, dtype=torch.int8).to(dev)
+    sg = (torch.rand(Mg, generator=g3) * 0.05).to(dev)
+    ug = torch.randn(Mg, 4 * r, generator=g3).to(dev)
+    segs = []
+    for i, Ng in enumerate((6144, 1536, 1536, 6144)):
+        segs.append((torch.randint(-127, 128, (Ng, Kg), generator=g3, dtype=torch.int8).to(dev),
+                     (torch.rand(Ng, generator=g3) * 0.01).to(dev), None,
+                     (torch.randn(Ng, r, generator=g3) * 0.01).to(dev), i * r, 1.0))
+    for _ in range(3):
+        L.gemm_w8a8_grouped(qg, sg, segs, ug)
+    del qg, segs, ug
     src = torch.ones(1 << 28, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     for _ in range(3):
