@@ -446,6 +446,45 @@ def run_krea_block(k2, steps, dev):
     return out
 
 
+def run_reference_gpu(k2, res, steps, dev):
+    """The reference's own quantized linear + adapter (``Fp8Linear.forward``, quantize.py:48-51: a bf16
+    dequantization of the fp8 weight on every call, then ``F.linear``; ``LoRALinear.forward``, lora.py:47-48:
+    two fp32 products and a bf16 add) restated with torch ops and run on this GPU at cfg2 (torch's own
+    kernels, hipBLASLt for the products), beside this package's fp8 base (``Fp8Linear`` on the gfx950 kernels:
+    dequantization kernel and bf16 MFMA GEMM with the fused adapter).  Same inputs as the headline step."""
+    F_ = torch.nn.functional
+    x, W, A, B = res["x"].to(dev), res["W"].to(dev), res["A"].to(dev), res["B"].to(dev)
+    M, K, N = x.shape[0], x.shape[1], W.shape[0]
+    w = W.float()
+    scale = w.abs().amax(dim=1, keepdim=True).clamp(min=1e-8) / 448.0          # quantize.py:36
+    wq = (w / scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)             # quantize.py:37
+    sc = scale.to(torch.bfloat16)
+    del w
+
+    def ref():
+        wd = wq.to(torch.bfloat16) * sc.to(torch.bfloat16)                     # quantize.py:49
+        out = F_.linear(x, wd, None)                                           # quantize.py:51
+        delta = (x.to(A.dtype) @ A.t()) @ B.t()                                 # lora.py:47
+        return out + 1.0 * delta.to(out.dtype)                                 # lora.py:48
+
+    lin = torch.nn.Linear(K, N, bias=False, dtype=torch.bfloat16, device=dev)
+    with torch.no_grad():
+        lin.weight.copy_(W)
+    fp8 = k2.LoRALinear(k2.Fp8Linear(lin), A.shape[0], float(A.shape[0]))
+    del lin
+    with torch.no_grad():
+        fp8.lora_A.copy_(A)
+        fp8.lora_B.copy_(B)
+        t_ref = sorted(time_loop(ref, steps) for _ in range(3))[1]
+        t_fp8 = sorted(time_loop(lambda: fp8(x), steps) for _ in range(3))[1]
+    ops = 2.0 * M * N * K
+    return {"reference_fp8_path": {"ms": round(t_ref, 4), "tops": round(ops / (t_ref * 1e-3) / 1e12, 1),
+                                   "path": "Fp8Linear.forward + LoRALinear.forward restated with torch ops on the GPU"},
+            "k2q_fp8_path": {"ms": round(t_fp8, 4), "tops": round(ops / (t_fp8 * 1e-3) / 1e12, 1),
+                             "path": "krea2_amd Fp8Linear + LoRALinear (same numerics, gfx950 kernels)"},
+            "convrot_speedup_vs_reference": round(t_ref / res["ms_step"], 2)}
+
+
 def run_cfg4(k2, steps, dev, settle_s=0.0):
     """Summed forward time of one double-stream block's quantized linears (image + text stream, plus the
     per-stream adaLN modulation at M=2), each a LoRALinear (r=16) over a W8A8 ConvRot base."""
@@ -665,6 +704,7 @@ def main():
     probe = mfma_probe(k2, dev)
     extra["mfma_probe_int8_tops"] = round(probe, 1)
     extra["gemm_pct_of_mfma_probe"] = round(100 * gemm_tops / probe, 2)
+    extra["reference_path_gpu_cfg2"] = run_reference_gpu(k2, res, max(5, a.steps // 2), dev)
     extra["cfg3"] = run_cfg3(k2, max(5, a.steps // 2), dev, a.settle / 2)
     extra["cfg4"] = run_cfg4(k2, max(5, a.steps // 2), dev, a.settle / 2)
     extra["producers_cfg4_image"] = run_producers(k2, max(5, a.steps // 2), dev)
