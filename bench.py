@@ -298,11 +298,30 @@ def run_cfg3(k2, steps, dev, settle_s=0.0):
         k2.set_dx_weight_cache(layer, False)
     finally:
         k2.quantize.shared_input_quant.enabled = prev
+
+    # The reference's step on the same GPU: Fp8Linear.forward (quantize.py:48-51) + LoRALinear.forward
+    # (lora.py:47-48) restated with torch ops, its autograd through the dequantized bf16 weight.
+    F_ = torch.nn.functional
+    w = (torch.randn(c["N"], c["K"], generator=torch.Generator().manual_seed(3)) * 0.02).to(dev)
+    scale = w.abs().amax(dim=1, keepdim=True).clamp(min=1e-8) / 448.0
+    wq, sc = (w / scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn), scale.to(torch.bfloat16)
+    A = layer.lora_A.detach().clone().requires_grad_(True)
+    B = layer.lora_B.detach().clone().requires_grad_(True)
+    del w
+
+    def ref_step():
+        x.grad = A.grad = B.grad = None
+        out = F_.linear(x, wq.to(torch.bfloat16) * sc)
+        out = out + ((x.to(A.dtype) @ A.t()) @ B.t()).to(out.dtype)
+        out.backward(dy)
+
+    ms_ref = time_loop(ref_step, steps)
     ops_fwd = 2.0 * c["M"] * c["N"] * c["K"]
     return {"step_ms": round(ms, 4), "fwd_ms": round(ms_fwd, 4), "bwd_ms": round(ms - ms_fwd, 4),
             "fwd_tops": round(ops_fwd / (ms_fwd * 1e-3) / 1e12, 1),
             "dx_tflops": round(ops_fwd / ((ms - ms_fwd) * 1e-3) / 1e12, 1),
-            "step_ms_dx_weight_cached": round(ms_cached, 4)}
+            "step_ms_dx_weight_cached": round(ms_cached, 4),
+            "reference_fp8_step_ms_gpu": round(ms_ref, 4)}
 
 
 def run_producers(k2, steps, dev):
