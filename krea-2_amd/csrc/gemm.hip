@@ -702,7 +702,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
       for (int ib = 0; ib < WB; ++ib)
         ctile_put(ctile, WBR * wb + 32 * ib, 128 * wa + 32 * ia, lane, __builtin_bit_cast(v16f, acc[ia][ib]));
     lds_barrier();
-    // Pass C: wave w stores tile rows 32w .. 32w+31, two rows (2 x 512 B) per instruction.
+    // Pass C: wave w stores tile rows 32w .. 32w+31, two rows (2 x 512 B) per instruction.  Non-temporal:
+    // the output is not read again by this launch, and streaming it keeps the operand strips in L2.
     uint16_t* out = static_cast<uint16_t*>(p.out);
     const int chunk = lane & 31;
     const int64_t col = A0 + 8 * chunk;
@@ -713,7 +714,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
       for (int i = 0; i < RPW / 2; ++i) {
         const int row = RPW * wave + 2 * i + (lane >> 5);
         const v4u v = *reinterpret_cast<const v4u*>(ctile + row * CROW + 16 * chunk);
-        if (col_ok && B0 + row < p.rows_b) *reinterpret_cast<v4u*>(out + (B0 + row) * p.ldo + col) = v;
+        if (col_ok && B0 + row < p.rows_b) __builtin_nontemporal_store(v, reinterpret_cast<v4u*>(out + (B0 + row) * p.ldo + col));
       }
     } else {                       // ragged widths: element stores
       for (int i = 0; i < RPW / 2; ++i) {
