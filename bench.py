@@ -687,8 +687,8 @@ def main():
     a = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus > 1 or world > 1:
-        print("bench.py measures one MI355X: this build has no multi-GPU path (per-token rows shard with no "
-              "communication; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one MI355X: this build has no multi-GPU path (the per-token rows of the path "
+              "shard over GPUs with no communication). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
