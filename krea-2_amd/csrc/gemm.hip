@@ -959,7 +959,7 @@ __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) 
       const uint8_t* c = reinterpret_cast<const uint8_t*>(ctile) + (t >> 5) * W4_CROW + 8 * cq;
 #pragma unroll 4
       for (int row = t >> 5; row < rows; row += 8) {
-        *reinterpret_cast<v2u*>(o) = *reinterpret_cast<const v2u*>(c);
+        __builtin_nontemporal_store(*reinterpret_cast<const v2u*>(c), reinterpret_cast<v2u*>(o));   // as in pass C
         o += 8 * p.N;
         c += 8 * W4_CROW;
       }

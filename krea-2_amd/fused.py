@@ -247,7 +247,8 @@ class _SiblingGroup:
     """Linears that receive the same tensor (``wq / wk / wv / gate`` of ``Attention.forward``, ``mmdit.py:199``).
     The first member called with a tensor computes every member's output in one grouped launch and keeps the
     others; each later member called with that same tensor (same object, version, pointer, shape, strides and
-    stream) and an unchanged adapter takes its output.  Anything else runs the member's own forward."""
+    stream) and an unchanged adapter takes its output.  Anything else runs the member's own forward.  Kept
+    outputs a member never asks for stay referenced until the group's next launch replaces them."""
 
     def __init__(self, members):
         self.members = list(members)
