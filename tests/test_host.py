@@ -293,3 +293,68 @@ def test_quantized_base_load_rejects_mismatches(k2, tmp_path):
         k2.load_quantized_base(_tiny_dit(), g)
     with pytest.raises(ValueError):
         k2.save_quantized_base(_tiny_dit(), str(tmp_path / "none.safetensors"))
+
+
+def test_new_entry_points_reject_bad_arguments_without_gpu(k2):
+    """The producer, producer-backward and grouped entry points return K2Q_EINVAL / K2Q_EUNSUPPORTED for invalid
+    shapes and pointers before touching the device."""
+    lib = k2._lib.load()
+    buf = ctypes.create_string_buffer(8192 + 16)
+    p = (ctypes.addressof(buf) + 15) // 16 * 16
+    assert lib.k2q_swiglu_rotquant(p, 128, p, 128, 4, 100, p, p, p, None) == -1      # K % 128
+    assert lib.k2q_swiglu_rotquant(p, 64, p, 128, 4, 128, p, p, p, None) == -1       # row stride < K
+    assert lib.k2q_swiglu_rotquant(p, 32768, p, 32768, 4, 32768, p, p, p, None) == -4  # K too large
+    assert lib.k2q_rmsmod_rotquant(p, 128, 4, 128, p, 1e-5, p, p, 0, 0, p, p, p, None) == -1   # rows per batch
+    assert lib.k2q_rmsmod_rotquant(p, 128, 4, 128, p, -1.0, p, p, 0, 4, p, p, p, None) == -1   # eps
+    assert lib.k2q_rmsmod_rotquant(p, 128, 4, 128, p, 1e-5, p + 2, p, 0, 4, p, p, p, None) == -1  # misaligned
+    assert lib.k2q_rmsmod_bwd(p, p, 4, 12, p, 1e-5, p, 0, 4, p, None) == -1             # K % 8
+    assert lib.k2q_rmsmod_bwd(p, p, 4, 32768, p, 1e-5, p, 0, 4, p, None) == -4          # K too large
+    assert lib.k2q_swiglu_bwd(p, p, p, 12, p, p, None) == -1                           # n % 8
+    seg = (k2._lib.W8A8Segment * 5)()
+    for s in seg:
+        s.qw = s.sw = s.y = p
+        s.N, s.u_col, s.lora_scale = 256, 0, 1.0
+    assert lib.k2q_gemm_w8a8_grouped(p, p, 64, 128, ctypes.cast(seg, ctypes.c_void_p), 5, None, 0, 0,
+                                     None, 0, None) == -1                                # > 4 segments
+    assert lib.k2q_gemm_w8a8_grouped(p, p, 8, 128, ctypes.cast(seg, ctypes.c_void_p), 1, None, 0, 0,
+                                     None, 0, None) == -1                                # M <= 8
+    seg[0].N = 384
+    assert lib.k2q_gemm_w8a8_grouped(p, p, 64, 128, ctypes.cast(seg, ctypes.c_void_p), 1, None, 0, 0,
+                                     None, 0, None) == -1                                # N % 256
+
+
+def test_fusion_walkers_leave_unquantized_blocks_alone(k2):
+    """fuse_producers / group_siblings patch only blocks whose linears are ConvRot (w8a8 for grouping):
+    plain nn.Linear blocks are left untouched, and the host-side checks of the fused ops raise before any
+    launch."""
+    dit = _Dit()
+    assert k2.fuse_producers(dit) == 0 and k2.group_siblings(dit) == 0
+    assert "forward" not in vars(dit.blocks[0].attn.wq) and "forward" not in vars(dit.blocks[0])
+    x = torch.zeros(2, 8, 256, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        k2.swiglu(x, x[..., :128])
+    with pytest.raises(NotImplementedError):
+        k2.swiglu(x.float(), x.float())
+    norm = nn.Module()
+    norm.scale, norm.eps = nn.Parameter(torch.zeros(256)), 1e-5
+    sc = torch.zeros(3, 1, 256, dtype=torch.bfloat16)                    # 3 entries for a batch of 2
+    with pytest.raises(ValueError):
+        k2.modulated_rmsnorm(norm, x, sc, sc)
+    with pytest.raises(ValueError):
+        k2.modulated_rmsnorm(norm, x, sc[:2], sc[:2, :, :128])
+    with pytest.raises(RuntimeError):                                    # valid shapes, CPU: refuses
+        k2.modulated_rmsnorm(norm, x, sc[:2], sc[:2])
+
+
+def test_grouped_wrapper_validates_before_launch(k2):
+    L = k2._lib
+    q = torch.zeros(64, 256, dtype=torch.int8)
+    s = torch.zeros(64)
+    seg = (torch.zeros(384, 256, dtype=torch.int8), torch.zeros(384), None, None, 0, 1.0)
+    with pytest.raises(ValueError):                                      # N % 256
+        L.gemm_w8a8_grouped(q, s, [seg])
+    ok = (torch.zeros(256, 256, dtype=torch.int8), torch.zeros(256), None, torch.zeros(256, 16), 0, 1.0)
+    with pytest.raises(ValueError):                                      # an adapter without u
+        L.gemm_w8a8_grouped(q, s, [ok])
+    with pytest.raises(ValueError):                                      # u columns out of range
+        L.gemm_w8a8_grouped(q, s, [ok[:4] + (8, 1.0)], torch.zeros(64, 16))
