@@ -245,3 +245,42 @@ def test_fusions_at_krea_width(k2, dev):
     assert torch.equal(y2, y1) and torch.equal(dx2, dx1)
     for k in gr1:
         assert torch.equal(gr2[k][0], gr1[k][0]) and torch.equal(gr2[k][1], gr1[k][1]), k
+
+
+@pytest.mark.timeout(300)
+def test_block_forward_replays_in_a_hip_graph(k2, dev):
+    """A fused, grouped block forward (producers, grouped attention inputs, every ConvRot GEMM and LoRA
+    kernel) captured once in a HIP graph and replayed three times on new input data, with eager work and
+    synchronizations between the replays: every replay equals the eager forward bit for bit."""
+    dit, _ = _build(k2, dev)
+    assert k2.fuse_producers(dit) == 4 and k2.group_siblings(dit) == 2
+    g = torch.Generator().manual_seed(10)
+    B, Lt = 2, 128
+    vec = (torch.randn(B, 1, 6 * FEAT, generator=g) * 0.3).to(torch.bfloat16).to(dev)
+    xs = [torch.randn(B, Lt, FEAT, generator=g).to(torch.bfloat16).to(dev) for _ in range(3)]
+
+    def fwd(x):
+        h = x
+        for blk in dit.blocks:
+            h = blk(h, vec, None)
+        return h
+
+    static_x = xs[0].clone()
+    with torch.no_grad():
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                fwd(static_x)                      # warm-up on the capture stream
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            static_y = fwd(static_x)
+        for x in xs:
+            static_x.copy_(x)
+            graph.replay()
+            torch.cuda.synchronize()
+            got = static_y.clone()
+            ref = fwd(x.clone())                   # eager, between the replays
+            torch.cuda.synchronize()
+            assert torch.equal(got, ref)
