@@ -1,0 +1,102 @@
+"""Seeded shape sweep of the producer-fused kernels, their backward kernels and the grouped GEMM: ragged M,
+K with and without a partial chunk (K a multiple of 128 that is not a multiple of the 1024 / 2048 / 4096
+chunk width), row strides above K, one to four segments.  The bars are those of the dedicated tests: codes
+and scales bit-exact against rotate/quant of the kernel's own h, h within the stated bf16 steps of the
+oracle, grouped outputs bit-identical to the per-segment GEMM."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import convrot as orc
+
+pytestmark = pytest.mark.gpu
+
+_RNG = np.random.default_rng(2024)
+_K = [128, 384, 1152, 3072, 4992, 6144, 9088, 12288, 16384]
+_PROD_CASES = [(int(_RNG.integers(1, 700)), int(k), int(_RNG.integers(0, 3))) for k in _RNG.choice(_K, 12)]
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _codes_match(k2, h, q, s):
+    q2, s2, _ = k2._lib.rotquant(h)
+    assert torch.equal(q2, q) and torch.equal(s2, s)
+    qo, so, _ = orc.rotquant(_np(h))
+    assert np.array_equal(q.cpu().numpy(), qo) and np.array_equal(s.cpu().numpy(), so)
+
+
+@pytest.mark.parametrize("M,K,pad", _PROD_CASES)
+def test_swiglu_sweep(k2, dev, M, K, pad):
+    g = torch.Generator().manual_seed(M * 7 + K)
+    ld = K + 128 * pad
+    buf = (torch.randn(M, 2 * ld, generator=g) * 3).to(torch.bfloat16).to(dev)
+    gt, ut = buf[:, :K], buf[:, ld:ld + K]
+    h, q, s = k2._lib.swiglu_rotquant(gt, ut)
+    dh = (torch.randn(M, K, generator=g) * 1e-2).to(torch.bfloat16).to(dev)
+    dg, du = k2._lib.swiglu_bwd(dh, gt.contiguous(), ut.contiguous())
+    torch.cuda.synchronize()
+    gn, un = _np(gt), _np(ut)
+    ho, so = orc.swiglu(gn, un), orc.swiglu(gn, np.ones_like(un))
+    hk = _np(h)
+    assert np.all(np.abs(hk - ho) <= (np.abs(so * un) + np.abs(ho)) * 2.0 ** -7)
+    assert (hk == ho).mean() > 0.999
+    _codes_match(k2, h, q, s)
+    og, ou = orc.swiglu_backward(_np(dh), gn, un)
+    assert np.linalg.norm(_np(dg) - og) <= 1e-2 * np.linalg.norm(og)
+    assert np.linalg.norm(_np(du) - ou) <= 1e-2 * np.linalg.norm(ou)
+
+
+@pytest.mark.parametrize("M,K,pad", _PROD_CASES)
+def test_rmsmod_sweep(k2, dev, M, K, pad):
+    g = torch.Generator().manual_seed(M * 11 + K)
+    B = 1 + pad % 2 + (M % 3 == 0)
+    Mb = max(B, M - M % B)
+    L = Mb // B
+    ld = K + 128 * pad
+    x = (torch.randn(Mb, ld, generator=g) * 2).to(torch.bfloat16).to(dev)[:, :K]
+    ns = (torch.randn(K, generator=g) * 0.1).to(dev)
+    vec = (torch.randn(B, 1, 6 * K, generator=g) * 0.3).to(torch.bfloat16).to(dev)
+    ms, mb = vec[..., :K].reshape(B, K), vec[..., K:2 * K].reshape(B, K)
+    h, q, s = k2._lib.rmsmod_rotquant(x, ns, 1e-5, ms, mb, L)
+    dh = (torch.randn(Mb, K, generator=g) * 1e-2).to(torch.bfloat16).to(dev)
+    dx = k2._lib.rmsmod_bwd(dh, x.contiguous(), ns, 1e-5, ms, L)
+    torch.cuda.synchronize()
+    xn = _np(x)
+    ho = orc.rmsmod(xn, _np(ns), 1e-5, _np(ms), _np(mb), L)
+    zero = np.zeros_like(_np(ms))
+    n = orc.rmsmod(xn, _np(ns), 1e-5, zero, zero, L)
+    rows = np.arange(Mb) // L if B > 1 else np.zeros(Mb, np.int64)
+    prod = orc.bf16_round(orc.bf16_round(1.0 + _np(ms))[rows] * n)
+    hk = _np(h)
+    assert np.all(np.abs(hk - ho) <= (np.abs(prod) + np.abs(ho)) * 2.0 ** -7)
+    assert (hk == ho).mean() > 0.999
+    _codes_match(k2, h, q, s)
+    ref = orc.rmsmod_backward_x(_np(dh), xn, _np(ns), 1e-5, _np(ms), L)
+    assert np.linalg.norm(_np(dx) - ref) <= 1e-3 * np.linalg.norm(ref)
+
+
+_GROUP_CASES = [(int(_RNG.integers(9, 1200)), int(_RNG.choice([128, 640, 3072, 6144])),
+                 tuple(int(256 * v) for v in _RNG.integers(1, 9, size=int(_RNG.integers(1, 5)))),
+                 int(_RNG.choice([16, 32, 64]))) for _ in range(10)]
+
+
+@pytest.mark.parametrize("M,K,Ns,r", _GROUP_CASES)
+def test_grouped_sweep(k2, dev, M, K, Ns, r):
+    L = k2._lib
+    g = torch.Generator().manual_seed(M + K + sum(Ns))
+    qx = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8).to(dev)
+    sx = (torch.rand(M, generator=g) * 0.05 + 1e-3).to(dev)
+    u = torch.randn(M, len(Ns) * r, generator=g).to(dev)
+    segs = []
+    for i, N in enumerate(Ns):
+        qw = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev)
+        sw = (torch.rand(N, generator=g) * 0.01 + 1e-4).to(dev)
+        b = (torch.randn(N, generator=g) * 0.1).to(dev) if i % 2 else None
+        lb = (torch.randn(N, r, generator=g) * 0.05).to(dev) if (i + M) % 3 else None
+        segs.append((qw, sw, b, lb, i * r, 0.5 + i))
+    ys = L.gemm_w8a8_grouped(qx, sx, segs, u)
+    for (qw, sw, b, lb, c, sc), y in zip(segs, ys):
+        uc = u[:, c:c + r].contiguous() if lb is not None else None
+        assert torch.equal(y, L.gemm_w8a8(qx, sx, qw, sw, b, uc, lb, sc, split=False))
