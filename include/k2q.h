@@ -109,7 +109,8 @@ int k2q_gemm_w8a8(const int8_t* qx, const float* sx, const int8_t* qw, const flo
  * codes qx / sx.  Segment i is k2q_gemm_w8a8 of its own weights into its own output y (M x N, row stride N)
  * with its factors u[:, u_col .. u_col + r) (u: M rows of ldu f32, r as for k2q_gemm_w8a8; lora_b NULL: no
  * adapter on that segment); the outputs are bit-identical to nseg separate k2q_gemm_w8a8 calls.
- * 1 <= nseg <= 4, every N a multiple of 256, M > 8.  ws: k2q_gemm_w8a8_ws_bytes(M, sum of N, K). */
+ * 1 <= nseg <= 4, every N a multiple of 256, M > 8.  The launch runs full-K tiles only: ws / ws_bytes are
+ * accepted for symmetry with k2q_gemm_w8a8 and not used (pass NULL, 0). */
 typedef struct {
   const int8_t* qw;       /* N x K int8 codes */
   const float* sw;        /* N f32 scales */
