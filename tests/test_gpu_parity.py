@@ -172,7 +172,8 @@ def _forward_case(k2, dev, M, K, N, r, w4, bias, seed):
 
 @pytest.mark.parametrize("M,K,N,r,bias", [(256, 256, 256, 0, False), (300, 384, 260, 16, True),
                                           (512, 3072, 1024, 32, True), (257, 1024, 512, 64, False),
-                                          (64, 512, 128, 128, True)])
+                                          (64, 512, 128, 128, True), (384, 768, 512, 48, True),
+                                          (130, 512, 384, 112, False)])
 def test_forward_w8a8(k2, dev, M, K, N, r, bias):
     y, u, ref = _forward_case(k2, dev, M, K, N, r, False, bias, seed=M + N)
     assert rel_frob(y.float().cpu().numpy(), ref["y64"]) < REL_FROB_TOL
@@ -183,7 +184,7 @@ def test_forward_w8a8(k2, dev, M, K, N, r, bias):
 
 
 @pytest.mark.parametrize("M,K,N,r,bias", [(256, 256, 128, 0, False), (300, 384, 260, 16, True),
-                                          (512, 3072, 1024, 32, False)])
+                                          (512, 3072, 1024, 32, False), (256, 768, 384, 48, True)])
 def test_forward_w4a8(k2, dev, M, K, N, r, bias):
     y, _, ref = _forward_case(k2, dev, M, K, N, r, True, bias, seed=M + N + 7)
     assert rel_frob(y.float().cpu().numpy(), ref["y64"]) < 4e-3
