@@ -14,8 +14,9 @@
  *          sw4 K/64 x N bf16 group scales, group-major (scales of one group are contiguous over n)
  *   u      M x r   f32 LoRA down-projection x A^T;  lora_a r x K f32, lora_b N x r f32
  *   y      M x N   bf16,  dy M x N bf16,  dx M x K bf16
- * Constraints checked before any launch: K % 128 == 0 (Hadamard block), r % 16 == 0 and r <= 128 when
- * a LoRA term is present, pointers 16-byte aligned, M, N >= 1.
+ * Constraints checked before any launch: K % 128 == 0 (Hadamard block), r % 16 == 0 and 16 <= r <=
+ * K2Q_MAX_RANK when a LoRA term is present (ranks run in chunks of 128 inside; a caller pads other ranks
+ * with zero factor rows, which changes no result), pointers 16-byte aligned, M, N >= 1.
  */
 #ifndef K2Q_H
 #define K2Q_H
@@ -31,6 +32,8 @@ extern "C" {
 #define K2Q_EARCH (-2)       /* current device is not gfx950 */
 #define K2Q_ELAUNCH (-3)     /* kernel launch reported an error */
 #define K2Q_EUNSUPPORTED (-4)/* shape outside what the kernels implement (e.g. K too large) */
+
+#define K2Q_MAX_RANK 4096    /* largest LoRA rank any entry point takes */
 
 #define K2Q_DTYPE_BF16 0
 #define K2Q_DTYPE_F32 1

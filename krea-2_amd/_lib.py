@@ -23,7 +23,8 @@ DTYPE_BF16 = 0
 DTYPE_F32 = 1
 HADAMARD_BLOCK = 128
 INT4_GROUP = 64
-MAX_RANK = 128
+MAX_RANK = 4096        # K2Q_MAX_RANK: ranks run in chunks of 128 inside the library
+RANK_ALIGN = 16        # the kernels take ranks in multiples of 16 (callers pad with zero factor rows)
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -155,8 +156,9 @@ def _check_k(K: int) -> None:
 
 
 def _check_rank(r: int) -> None:
-    if r < 16 or r > MAX_RANK or r % 16:
-        raise ValueError(f"LoRA rank {r} must be a multiple of 16 in [16, {MAX_RANK}] for the fused path")
+    if r < RANK_ALIGN or r > MAX_RANK or r % RANK_ALIGN:
+        raise ValueError(f"LoRA rank {r} must be a multiple of {RANK_ALIGN} in [{RANK_ALIGN}, {MAX_RANK}] "
+                         "(pad the factors with zero ranks)")
 
 
 # ----------------------------------------------------------------------------------------------------------

@@ -1060,9 +1060,12 @@ int check_common(int64_t M, int64_t N, int64_t K) {
   return K2Q_OK;
 }
 
+// The epilogues take the LoRA term 16 ranks at a time, so any multiple of 16 up to K2Q_MAX_RANK works.
+bool rank_ok(int64_t r) { return r >= 16 && r <= K2Q_MAX_RANK && r % 16 == 0; }
+
 int check_lora(const float* u, const float* lb, int64_t r) {
   if (!u) return K2Q_OK;
-  if (!lb || r < 16 || r > 128 || r % 16) return K2Q_EINVAL;
+  if (!lb || !rank_ok(r)) return K2Q_EINVAL;
   if (!k2q_aligned(u, 16) || !k2q_aligned(lb, 16)) return K2Q_EINVAL;
   return K2Q_OK;
 }
@@ -1134,7 +1137,7 @@ extern "C" int k2q_gemm_w8a8_grouped(const int8_t* qx, const float* sx, int64_t 
     s.lora_scale = g.lora_scale;
     start += g.N;
   }
-  if (any_lora && (r < 16 || r > 128 || r % 16 || ldu % 4 || !k2q_aligned(u, 16))) return K2Q_EINVAL;
+  if (any_lora && (!rank_ok(r) || ldu % 4 || !k2q_aligned(u, 16))) return K2Q_EINVAL;
   p.nseg = (int)nseg;
   p.a = p.seg[0].a;   // unused by the tiles (each takes its segment's), set for completeness
   p.b = reinterpret_cast<const uint8_t*>(qx);

@@ -26,11 +26,12 @@ __device__ __forceinline__ void split8(v4f p, v4f q, v8bf& hi, v8bf& lo) {
 // from global memory in MFMA layout (lane l: row l%16 of x or of A, 8 contiguous k at 8*(l/16) of each
 // 32-wide step), double-buffered so one batch of loads is in flight while the previous one is multiplied.
 // The wave partials meet in LDS and are added in the fixed order wave 0 + 1 + 2 + 3 (deterministic).
-// out: u (M x 16RT) when gridDim.y == 1, else the partial slices [gridDim.y][M][16RT].
+// out: u (M rows of row stride ldo, columns 0 .. 16RT) when gridDim.y == 1, else the partial slices
+// [gridDim.y][M][ldo].
 template <int RT, int TT>
 __global__ __launch_bounds__(256) void lora_down_kernel(const uint16_t* __restrict__ x, int64_t M, int64_t ldx,
                                                         const float* __restrict__ a, int64_t K, int kslice,
-                                                        float* __restrict__ out) {
+                                                        int64_t ldo, float* __restrict__ out) {
   constexpr int UNR = RT <= 2 ? 2 : 1;   // 32-wide k steps per load batch
   constexpr int R = 16 * RT;
   __shared__ float part[3][TT][RT][4][64];
@@ -109,7 +110,7 @@ __global__ __launch_bounds__(256) void lora_down_kernel(const uint16_t* __restri
   }
   __syncthreads();
   if (wave != 0) return;
-  float* o = out + (int64_t)blockIdx.y * M * R;
+  float* o = out + (int64_t)blockIdx.y * M * ldo;
   // C layout (16x16): lane l owns column (rank) l%16 and rows 4*(l/16) + i.
 #pragma unroll
   for (int t = 0; t < TT; ++t)
@@ -119,7 +120,7 @@ __global__ __launch_bounds__(256) void lora_down_kernel(const uint16_t* __restri
       for (int i = 0; i < 4; ++i) {
         const float v = ((acc[t][j][i] + part[0][t][j][i][lane]) + part[1][t][j][i][lane]) + part[2][t][j][i][lane];
         const int64_t m = m0 + 16 * t + 4 * (lane >> 4) + i;
-        if (m < M) o[m * R + 16 * j + (lane & 15)] = v;
+        if (m < M) o[m * ldo + 16 * j + (lane & 15)] = v;
       }
 }
 
@@ -127,7 +128,8 @@ __global__ __launch_bounds__(256) void lora_down_kernel(const uint16_t* __restri
 // x K-slice blockIdx.y of LD_NW * 32 * NS columns; wave w keeps the split fragments of its 32*NS columns of A in
 // registers for the whole row range (A is read once per workgroup) and walks the 16-row tiles, the next tile's
 // x fragments in flight while the current one is multiplied.  Per tile the 8 wave partials meet in LDS and
-// are added in wave order (deterministic); out gets u (one slice) or the slice partial [slice][M][16RT].
+// are added in wave order (deterministic); out gets u (one slice; rows of stride ldo) or the slice partial
+// [slice][M][ldo].
 constexpr int LD_NW = 8;   // waves per workgroup
 template <int RT>
 struct LdShape {
@@ -139,7 +141,8 @@ template <int RT>
 __global__ __launch_bounds__(64 * LD_NW) void lora_down_as_kernel(const uint16_t* __restrict__ x, int64_t M,
                                                                   int64_t ldx, const float* __restrict__ a, int64_t K,
                                                                   int64_t a_kstride, float a_scale,
-                                                                  int64_t rows_per_wg, float* __restrict__ out) {
+                                                                  int64_t rows_per_wg, int64_t ldo,
+                                                                  float* __restrict__ out) {
   constexpr int NS = LdShape<RT>::NS;
   constexpr int R = 16 * RT;
   __shared__ float red[2][LD_NW][RT][4][64];
@@ -209,7 +212,7 @@ __global__ __launch_bounds__(64 * LD_NW) void lora_down_as_kernel(const uint16_t
 #pragma unroll
       for (int ww = 1; ww < LD_NW; ++ww) v += red[buf][ww][jt][i][ln];
       const int64_t m = m_beg + 16 * (int64_t)t + 4 * (ln >> 4) + i;
-      if (m < m_end) out[(int64_t)blockIdx.y * M * R + m * R + 16 * jt + (ln & 15)] = v;
+      if (m < m_end) out[((int64_t)blockIdx.y * M + m) * ldo + 16 * jt + (ln & 15)] = v;
     }
   };
   v4i x0[NS], x1[NS];
@@ -222,14 +225,17 @@ __global__ __launch_bounds__(64 * LD_NW) void lora_down_as_kernel(const uint16_t
   }
 }
 
-// u = sum of the K-slice partials in slice order (deterministic); n4 = M*r/4 float4 elements.
-__global__ __launch_bounds__(256) void lora_reduce_kernel(const v4f* __restrict__ part, int ks, int64_t n4,
-                                                          v4f* __restrict__ u) {
+// u = sum of the K-slice partials in slice order (deterministic).  part: [ks][M][4 r4] f32; u: M rows of
+// ldu4 float4s, of which the first r4 are written.
+__global__ __launch_bounds__(256) void lora_reduce_kernel(const v4f* __restrict__ part, int ks, int64_t M, int64_t r4,
+                                                          int64_t ldu4, v4f* __restrict__ u) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t n4 = M * r4;
   if (i >= n4) return;
   v4f s = part[i];
   for (int p = 1; p < ks; ++p) s += part[p * n4 + i];
-  u[i] = s;
+  const int64_t m = i / r4;
+  u[m * ldu4 + (i - m * r4)] = s;
 }
 
 // Launch plan: TT row tiles per workgroup (fewer for tiny M), and K cut into ks slices (K % (128 ks) == 0,
@@ -257,13 +263,14 @@ LoraPlan lora_plan(int64_t M, int64_t K, int64_t r) {
 
 template <int RT>
 void launch_lora_down(int tt, dim3 grid, hipStream_t st, const uint16_t* x, int64_t M, int64_t ldx, const float* a,
-                      int64_t K, int kslice, float* out) {
+                      int64_t K, int kslice, int64_t ldo, float* out) {
   if (tt == 4)
-    hipLaunchKernelGGL((lora_down_kernel<RT, (RT <= 4 ? 4 : 2)>), grid, dim3(256), 0, st, x, M, ldx, a, K, kslice, out);
+    hipLaunchKernelGGL((lora_down_kernel<RT, (RT <= 4 ? 4 : 2)>), grid, dim3(256), 0, st, x, M, ldx, a, K, kslice, ldo,
+                       out);
   else if (tt == 2)
-    hipLaunchKernelGGL((lora_down_kernel<RT, 2>), grid, dim3(256), 0, st, x, M, ldx, a, K, kslice, out);
+    hipLaunchKernelGGL((lora_down_kernel<RT, 2>), grid, dim3(256), 0, st, x, M, ldx, a, K, kslice, ldo, out);
   else
-    hipLaunchKernelGGL((lora_down_kernel<RT, 1>), grid, dim3(256), 0, st, x, M, ldx, a, K, kslice, out);
+    hipLaunchKernelGGL((lora_down_kernel<RT, 1>), grid, dim3(256), 0, st, x, M, ldx, a, K, kslice, ldo, out);
 }
 
 // wt[k][n] = bf16(W_hat[n][k]) for a 64 x 64 tile; W_hat = s_w[n] q[n][k] (int8) or
@@ -399,8 +406,6 @@ __global__ __launch_bounds__(256) void rot_dequant_t_kernel(const int8_t* __rest
   }
 }
 
-}  // namespace
-
 // A-stationary plan: K cut into workgroup spans (slices), rows split so that slices x row groups ~ CUs.
 struct AsPlan {
   int64_t slices, groups, rows;
@@ -422,15 +427,35 @@ AsPlan as_plan(int64_t M, int64_t K, int64_t r) {
 
 template <int RT>
 void launch_as(const AsPlan& p, hipStream_t st, const uint16_t* x, int64_t M, int64_t ldx, const float* a, int64_t K,
-               int64_t a_kstride, float a_scale, float* out) {
+               int64_t a_kstride, float a_scale, int64_t ldo, float* out) {
   hipLaunchKernelGGL(lora_down_as_kernel<RT>, dim3((unsigned)p.groups, (unsigned)p.slices), dim3(64 * LD_NW), 0, st,
-                     x, M, ldx, a, K, a_kstride, a_scale, p.rows, out);
+                     x, M, ldx, a, K, a_kstride, a_scale, p.rows, ldo, out);
 }
 
+// Ranks run in chunks of at most LORA_CHUNK (the kernels' largest rank tile); chunk c covers factor rows
+// [c LORA_CHUNK, ..) and writes its columns of u.  The chunks run one after another on the stream and share
+// one workspace, so the workspace holds the largest chunk's slice partials.
+constexpr int64_t LORA_CHUNK = 128;
+constexpr int64_t LORA_MAX_RANK = 4096;
+
+bool rank_ok(int64_t r) { return r >= 16 && r <= LORA_MAX_RANK && r % 16 == 0; }
+
+int64_t chunk_ws_bytes(int64_t M, int64_t K, int64_t rc) {
+  const AsPlan p = as_plan(M, K, rc);
+  return p.slices > 1 ? p.slices * M * rc * 4 : 0;
+}
+
+}  // namespace
+
 extern "C" int64_t k2q_lora_down_ws_bytes(int64_t M, int64_t K, int64_t r) {
-  if (M < 1 || K < 128 || K % 128 || r < 16 || r > 128 || r % 16) return 0;
-  const AsPlan p = as_plan(M, K, r);
-  return p.slices > 1 ? p.slices * M * r * 4 : 0;
+  if (M < 1 || K < 128 || K % 128 || !rank_ok(r)) return 0;
+  int64_t b = 0;
+  for (int64_t c0 = 0; c0 < r; c0 += LORA_CHUNK) {
+    const int64_t rc = r - c0 < LORA_CHUNK ? r - c0 : LORA_CHUNK;
+    const int64_t bc = chunk_ws_bytes(M, K, rc);
+    b = bc > b ? bc : b;
+  }
+  return b;
 }
 
 extern "C" int k2q_lora_down(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const float* lora_a,
@@ -438,20 +463,21 @@ extern "C" int k2q_lora_down(const uint16_t* x, int64_t M, int64_t K, int64_t ld
   return lora_down_impl(x, M, K, ldx, lora_a, 1, 1.f, r, ws, ws_bytes, u, static_cast<hipStream_t>(stream));
 }
 
-// The transposed-factor form needs the A-stationary path (one K slice, or a workspace for the slices).
-int lora_down_impl(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const float* lora_a, int64_t a_kstride,
-                   float a_scale, int64_t r, void* ws, int64_t ws_bytes, float* u, hipStream_t st) {
-  if (!x || !lora_a || !u || M < 1 || K < 128 || K % 128 || ldx < K || ldx % 8) return K2Q_EINVAL;
-  if (r < 16 || r > 128 || r % 16) return K2Q_EINVAL;
-  if (!k2q_aligned(x, 16) || !k2q_aligned(lora_a, 16) || !k2q_aligned(u, 16) || (ws && !k2q_aligned(ws, 16)))
-    return K2Q_EINVAL;
-  const AsPlan q = as_plan(M, K, r);
-  if (q.slices == 1 || (ws && ws_bytes >= q.slices * M * r * 4)) {
+namespace {
+
+// One chunk of rc <= LORA_CHUNK ranks: factor a (rows at stride K, or columns at stride a_kstride), output
+// columns of u at row stride ldu.  The transposed-factor form needs the A-stationary path (one K slice, or a
+// workspace for the slices).
+int lora_down_chunk(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const float* a, int64_t a_kstride,
+                    float a_scale, int64_t rc, void* ws, int64_t ws_bytes, float* u, int64_t ldu, hipStream_t st) {
+  const AsPlan q = as_plan(M, K, rc);
+  if (q.slices == 1 || (ws && ws_bytes >= q.slices * M * rc * 4)) {
     if (q.groups > 0x7fffffff || q.slices > 0xffff) return K2Q_EUNSUPPORTED;
     float* out = q.slices > 1 ? static_cast<float*>(ws) : u;
-    switch (r / 16) {
+    const int64_t ldo = q.slices > 1 ? rc : ldu;
+    switch (rc / 16) {
 #define K2Q_AS_CASE(RT) \
-  case RT: launch_as<RT>(q, st, x, M, ldx, lora_a, K, a_kstride, a_scale, out); break;
+  case RT: launch_as<RT>(q, st, x, M, ldx, a, K, a_kstride, a_scale, ldo, out); break;
       K2Q_AS_CASE(1) K2Q_AS_CASE(2) K2Q_AS_CASE(3) K2Q_AS_CASE(4)
       K2Q_AS_CASE(5) K2Q_AS_CASE(6) K2Q_AS_CASE(7) K2Q_AS_CASE(8)
 #undef K2Q_AS_CASE
@@ -459,35 +485,46 @@ int lora_down_impl(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const f
         return K2Q_EINVAL;
     }
     if (q.slices > 1) {
-      const int64_t n4 = M * r / 4;
+      const int64_t n4 = M * rc / 4;
       hipLaunchKernelGGL(lora_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st,
-                         static_cast<const v4f*>(ws), (int)q.slices, n4, reinterpret_cast<v4f*>(u));
+                         static_cast<const v4f*>(ws), (int)q.slices, M, rc / 4, ldu / 4, reinterpret_cast<v4f*>(u));
     }
     return k2q_launch_status();
   }
   // No room for the slice partials: the row-tiled kernel over the whole of K in one launch.
   if (a_kstride != 1) return K2Q_EINVAL;
-  LoraPlan p = lora_plan(M, K, r);
-  p.ks = 1;
+  const LoraPlan p = lora_plan(M, K, rc);
   if (p.row_blocks > 0x7fffffff) return K2Q_EUNSUPPORTED;
-  const dim3 grid((unsigned)p.row_blocks, (unsigned)p.ks);
-  float* out = p.ks > 1 ? static_cast<float*>(ws) : u;
-  const int kslice = (int)(K / p.ks);
-  switch (r / 16) {
+  const dim3 grid((unsigned)p.row_blocks, 1u);
+  switch (rc / 16) {
 #define K2Q_LD_CASE(RT) \
-  case RT: launch_lora_down<RT>(p.tt, grid, st, x, M, ldx, lora_a, K, kslice, out); break;
+  case RT: launch_lora_down<RT>(p.tt, grid, st, x, M, ldx, a, K, (int)K, ldu, u); break;
     K2Q_LD_CASE(1) K2Q_LD_CASE(2) K2Q_LD_CASE(3) K2Q_LD_CASE(4)
     K2Q_LD_CASE(5) K2Q_LD_CASE(6) K2Q_LD_CASE(7) K2Q_LD_CASE(8)
 #undef K2Q_LD_CASE
     default:
       return K2Q_EINVAL;
   }
-  if (p.ks > 1) {
-    const int64_t n4 = M * r / 4;
-    hipLaunchKernelGGL(lora_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st,
-                       static_cast<const v4f*>(ws), p.ks, n4, reinterpret_cast<v4f*>(u));
-  }
   return k2q_launch_status();
+}
+
+}  // namespace
+
+// u (M x r, row stride r) = x (a_scale F)^T for any rank r that is a multiple of 16, as consecutive chunks of at
+// most LORA_CHUNK ranks.
+int lora_down_impl(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const float* lora_a, int64_t a_kstride,
+                   float a_scale, int64_t r, void* ws, int64_t ws_bytes, float* u, hipStream_t st) {
+  if (!x || !lora_a || !u || M < 1 || K < 128 || K % 128 || ldx < K || ldx % 8) return K2Q_EINVAL;
+  if (!rank_ok(r)) return K2Q_EINVAL;
+  if (!k2q_aligned(x, 16) || !k2q_aligned(lora_a, 16) || !k2q_aligned(u, 16) || (ws && !k2q_aligned(ws, 16)))
+    return K2Q_EINVAL;
+  for (int64_t c0 = 0; c0 < r; c0 += LORA_CHUNK) {
+    const int64_t rc = r - c0 < LORA_CHUNK ? r - c0 : LORA_CHUNK;
+    const float* a = a_kstride == 1 ? lora_a + c0 * K : lora_a + c0;
+    const int rc_status = lora_down_chunk(x, M, K, ldx, a, a_kstride, a_scale, rc, ws, ws_bytes, u + c0, r, st);
+    if (rc_status) return rc_status;
+  }
+  return K2Q_OK;
 }
 
 extern "C" int k2q_dx_prep_eff(const int8_t* qw, const float* sw, const uint8_t* qw4, const uint16_t* sw4,

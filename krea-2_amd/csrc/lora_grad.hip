@@ -74,7 +74,7 @@ __device__ __forceinline__ void wg_wait_vmcnt() {
 
 // out (+ slice offset) = scale * P^T Q over the rows [mchunk*blockIdx.y, +mchunk) of M.
 //   pth/ptl: R x Mp bf16 (P^T hi and lo, zero past M, Mp a multiple of 32); q: M x C bf16, row stride ldq.
-//   trans == 0: out[j][c] (R x C); trans == 1: out[c][j] (C x R).  With gridDim.y > 1 the partial of slice
+//   trans == 0: out[j][c] (R x C); trans == 1: out[c][j] (C rows of stride ldt).  With gridDim.y > 1 the partial of slice
 //   blockIdx.y goes to out + blockIdx.y * R * C in the [j][c] layout, unscaled (wgrad_reduce finishes it).
 // Both operands arrive by LDS-DMA (global_load_lds_dwordx4) through a WG_NST-slot ring, one s_waitcnt and
 // one s_barrier per stage (no __syncthreads: its fence would drain the prefetches).  Q rows past M are read
@@ -83,7 +83,7 @@ template <int RT>
 __global__ __launch_bounds__(256) void wgrad_kernel(const uint16_t* __restrict__ pth, const uint16_t* __restrict__ ptl,
                                                     int64_t M, int64_t Mp, const uint16_t* __restrict__ q, int64_t C,
                                                     int64_t ldq, int64_t mchunk, float scale, int trans,
-                                                    float* __restrict__ out) {
+                                                    int64_t ldt, float* __restrict__ out) {
   using S = WgShape<RT>;
   constexpr int R = 16 * RT;
   __shared__ __attribute__((aligned(16))) uint8_t ring[WG_NST * S::STAGE];
@@ -191,15 +191,15 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const uint16_t* __restrict__
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[(int64_t)(j + i) * C + c] = f * acc[jt][kt][i];
       } else {
-        *reinterpret_cast<v4f*>(o + c * R + j) = scale * acc[jt][kt];
+        *reinterpret_cast<v4f*>(o + c * ldt + j) = scale * acc[jt][kt];
       }
     }
   }
 }
 
-// out = scale * sum over slices (slice order) of part[s][j][c]; layout [j][c] or (trans) [c][j].
+// out = scale * sum over slices (slice order) of part[s][j][c]; layout [j][c] or (trans) [c][j] with row stride ldt.
 __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restrict__ part, int S, int64_t R, int64_t C,
-                                                           float scale, int trans, float* __restrict__ out) {
+                                                           float scale, int trans, int64_t ldt, float* __restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;   // index into [j][c]
   if (i >= R * C) return;
   float v = part[i];
@@ -207,7 +207,7 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restri
   v *= scale;
   if (trans) {
     const int64_t j = i / C, c = i % C;
-    out[c * R + j] = v;
+    out[c * ldt + j] = v;
   } else {
     out[i] = v;
   }
@@ -230,6 +230,16 @@ WgradPlan wgrad_plan(int64_t M, int64_t C) {
 
 int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
 
+// Ranks run in chunks of at most GRAD_CHUNK (the wgrad kernel's largest rank tile), one after another on the
+// stream; dA's chunk c is rows [c GRAD_CHUNK, ..) of dA, dB's chunk c columns [c GRAD_CHUNK, ..) of dB.
+constexpr int64_t GRAD_CHUNK = 128;
+constexpr int64_t GRAD_MAX_RANK = 4096;
+
+bool grad_shape_ok(int64_t M, int64_t N, int64_t K, int64_t r) {
+  return M >= 1 && N >= 128 && N % 128 == 0 && K >= 128 && K % 128 == 0 && r >= 16 && r <= GRAD_MAX_RANK &&
+         r % 16 == 0;
+}
+
 struct GradLayout {
   int64_t ld, pt, part_a, part_b, total;   // byte offsets into the workspace
   int64_t mp;
@@ -242,32 +252,34 @@ GradLayout grad_layout(int64_t M, int64_t N, int64_t K, int64_t r) {
   L.pa = wgrad_plan(M, K);
   L.pb = wgrad_plan(M, N);
   int64_t off = 0;
+  const int64_t rc = r < GRAD_CHUNK ? r : GRAD_CHUNK;   // ranks of the largest chunk (chunks share the partials)
   L.ld = off;     off += align256(k2q_lora_down_ws_bytes(M, N, r));
   L.pt = off;     off += 4 * align256(r * L.mp * 2);
-  L.part_a = off; off += L.pa.slices > 1 ? align256(L.pa.slices * r * K * 4) : 0;
-  L.part_b = off; off += L.pb.slices > 1 ? align256(L.pb.slices * r * N * 4) : 0;
+  L.part_a = off; off += L.pa.slices > 1 ? align256(L.pa.slices * rc * K * 4) : 0;
+  L.part_b = off; off += L.pb.slices > 1 ? align256(L.pb.slices * rc * N * 4) : 0;
   L.total = off;
   return L;
 }
 
 template <int RT>
 void launch_wgrad(const WgradPlan& p, hipStream_t st, const uint16_t* pth, const uint16_t* ptl, int64_t M, int64_t Mp,
-                  const uint16_t* q, int64_t C, float scale, int trans, float* part, float* out) {
+                  const uint16_t* q, int64_t C, float scale, int trans, int64_t ldt, float* part, float* out) {
   const dim3 grid((unsigned)p.kblocks, (unsigned)p.slices);
   float* o = p.slices > 1 ? part : out;
-  hipLaunchKernelGGL(wgrad_kernel<RT>, grid, dim3(256), 0, st, pth, ptl, M, Mp, q, C, C, p.mchunk, scale, trans, o);
+  hipLaunchKernelGGL(wgrad_kernel<RT>, grid, dim3(256), 0, st, pth, ptl, M, Mp, q, C, C, p.mchunk, scale, trans, ldt,
+                     o);
   if (p.slices > 1) {
     const int64_t n = (int64_t)16 * RT * C;
     hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, part,
-                       (int)p.slices, (int64_t)16 * RT, C, scale, trans, out);
+                       (int)p.slices, (int64_t)16 * RT, C, scale, trans, ldt, out);
   }
 }
 
 void wgrad(int rt, const WgradPlan& p, hipStream_t st, const uint16_t* pth, const uint16_t* ptl, int64_t M,
-           int64_t Mp, const uint16_t* q, int64_t C, float scale, int trans, float* part, float* out) {
+           int64_t Mp, const uint16_t* q, int64_t C, float scale, int trans, int64_t ldt, float* part, float* out) {
   switch (rt) {
 #define K2Q_WG_CASE(RT) \
-  case RT: launch_wgrad<RT>(p, st, pth, ptl, M, Mp, q, C, scale, trans, part, out); break;
+  case RT: launch_wgrad<RT>(p, st, pth, ptl, M, Mp, q, C, scale, trans, ldt, part, out); break;
     K2Q_WG_CASE(1) K2Q_WG_CASE(2) K2Q_WG_CASE(3) K2Q_WG_CASE(4)
     K2Q_WG_CASE(5) K2Q_WG_CASE(6) K2Q_WG_CASE(7) K2Q_WG_CASE(8)
 #undef K2Q_WG_CASE
@@ -284,14 +296,14 @@ void split_t(hipStream_t st, const float* P, int64_t M, int64_t r, int64_t Mp, u
 }  // namespace
 
 extern "C" int64_t k2q_lora_grads_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t r) {
-  if (M < 1 || N < 128 || N % 128 || K < 128 || K % 128 || r < 16 || r > 128 || r % 16) return 0;
+  if (!grad_shape_ok(M, N, K, r)) return 0;
   return grad_layout(M, N, K, r).total;
 }
 
 extern "C" int k2q_lora_grads(const uint16_t* dy, const uint16_t* x, const float* u, const float* lora_b, int64_t r,
                               float scale, int64_t M, int64_t N, int64_t K, float* g, float* dA, float* dB, void* ws,
                               int64_t ws_bytes, void* stream) {
-  if (M < 1 || N < 128 || N % 128 || K < 128 || K % 128 || r < 16 || r > 128 || r % 16) return K2Q_EINVAL;
+  if (!grad_shape_ok(M, N, K, r)) return K2Q_EINVAL;
   if (!dy || !lora_b || !g || !ws || (dA && !x) || (dB && !u)) return K2Q_EINVAL;
   if (!k2q_aligned(dy, 16) || !k2q_aligned(lora_b, 16) || !k2q_aligned(g, 16) || !k2q_aligned(ws, 256) ||
       (x && !k2q_aligned(x, 16)) || (u && !k2q_aligned(u, 16)) || (dA && !k2q_aligned(dA, 16)) ||
@@ -311,14 +323,16 @@ extern "C" int k2q_lora_grads(const uint16_t* dy, const uint16_t* x, const float
   const int64_t ld_bytes = k2q_lora_down_ws_bytes(M, N, r);
   int rc = lora_down_impl(dy, M, N, N, lora_b, r, scale, r, ld_bytes ? w + L.ld : nullptr, ld_bytes, g, st);
   if (rc) return rc;
-  const int rt = (int)(r / 16);
-  if (dA) {
-    split_t(st, g, M, r, L.mp, pt[0], pt[1]);
-    wgrad(rt, L.pa, st, pt[0], pt[1], M, L.mp, x, K, 1.f, 0, reinterpret_cast<float*>(w + L.part_a), dA);
-  }
-  if (dB) {
-    split_t(st, u, M, r, L.mp, pt[2], pt[3]);
-    wgrad(rt, L.pb, st, pt[2], pt[3], M, L.mp, dy, N, scale, 1, reinterpret_cast<float*>(w + L.part_b), dB);
+  if (dA) split_t(st, g, M, r, L.mp, pt[0], pt[1]);
+  if (dB) split_t(st, u, M, r, L.mp, pt[2], pt[3]);
+  for (int64_t c0 = 0; c0 < r; c0 += GRAD_CHUNK) {
+    const int rt = (int)((r - c0 < GRAD_CHUNK ? r - c0 : GRAD_CHUNK) / 16);
+    if (dA)
+      wgrad(rt, L.pa, st, pt[0] + c0 * L.mp, pt[1] + c0 * L.mp, M, L.mp, x, K, 1.f, 0, 0,
+            reinterpret_cast<float*>(w + L.part_a), dA + c0 * K);
+    if (dB)
+      wgrad(rt, L.pb, st, pt[2] + c0 * L.mp, pt[3] + c0 * L.mp, M, L.mp, dy, N, scale, 1, r,
+            reinterpret_cast<float*>(w + L.part_b), dB + c0);
   }
   return k2q_launch_status();
 }

@@ -20,7 +20,6 @@ import weakref
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
 from . import _lib
 from .quantize import ConvRotLinear, shared_input_quant
@@ -71,9 +70,9 @@ def swiglu(gate_out: torch.Tensor, up_out: torch.Tensor) -> torch.Tensor:
 
 class _RmsModQuantFn(torch.autograd.Function):
     """Forward: the modulated RMSNorm of ``mmdit.py:314-317`` with the codes of its output (one gfx950 pass).
-    Backward: when only ``x`` needs a gradient (LoRA training: the norm and modulation are frozen and the
-    conditioning vector comes from frozen layers), ``k2q_rmsmod_bwd``; otherwise the reference's own formula
-    re-run on the saved inputs under autograd (``F.rms_norm`` and the eager bf16 modulation)."""
+    Backward: the input gradient ``k2q_rmsmod_bwd``.  Only ``x`` can need one: in LoRA training the norm scale
+    and the modulation tensors are frozen (the conditioning vector is ``tproj(t)``, ``mmdit.py:446``), and
+    :func:`modulated_rmsnorm` refuses them as gradient inputs before launching anything."""
 
     @staticmethod
     def forward(ctx, x2, norm_scale, mod_scale, mod_shift, eps, rows_per_batch):
@@ -87,25 +86,15 @@ class _RmsModQuantFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dh, _dq, _ds):
         x2, ns, ms, mb = ctx.saved_tensors
-        M, K = x2.shape
-        B = ms.shape[0]
-        rpb = ctx.rpb if B > 1 else M
-        need = ctx.needs_input_grad[:4]
-        if need[0] and not any(need[1:]):
-            dh = dh.contiguous()
-            if dh.dtype != torch.bfloat16:
-                dh = dh.to(torch.bfloat16)
-            dx = _lib.rmsmod_bwd(dh, x2.contiguous(), ns.float().contiguous(), ctx.eps, ms, rpb)
-            return dx, None, None, None, None, None
-        with torch.enable_grad():
-            leaves = [t.detach().requires_grad_(n) for t, n in zip((x2, ns, ms, mb), need)]
-            x3 = leaves[0].reshape(-1, rpb, K)
-            n = F.rms_norm(x3.float(), (K,), eps=ctx.eps, weight=leaves[1].float() + 1.0).to(x2.dtype)
-            h = (1 + leaves[2][:, None, :]) * n + leaves[3][:, None, :]
-            wrt = [t for t, n in zip(leaves, need) if n]
-            grads = torch.autograd.grad(h.reshape(M, K), wrt, dh) if wrt else ()
-        it = iter(grads)
-        return tuple(next(it) if n else None for n in need) + (None, None)
+        if not ctx.needs_input_grad[0]:
+            return None, None, None, None, None, None
+        M = x2.shape[0]
+        rpb = ctx.rpb if ms.shape[0] > 1 else M
+        dh = dh.contiguous()
+        if dh.dtype != torch.bfloat16:
+            dh = dh.to(torch.bfloat16)
+        dx = _lib.rmsmod_bwd(dh, x2.contiguous(), ns.float().contiguous(), ctx.eps, ms, rpb)
+        return dx, None, None, None, None, None
 
 
 def modulated_rmsnorm(norm: nn.Module, x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor) -> torch.Tensor:
@@ -119,6 +108,10 @@ def modulated_rmsnorm(norm: nn.Module, x: torch.Tensor, scale: torch.Tensor, shi
     K = x.shape[-1]
     if scale.shape != shift.shape or scale.shape[-1] != K:
         raise ValueError(f"scale {tuple(scale.shape)} / shift {tuple(shift.shape)} do not match {K} features")
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (norm.scale, scale, shift)):
+        raise NotImplementedError("the fused modulated RMSNorm computes the gradient of its input only; the norm "
+                                  "scale and the modulation must be frozen (as in LoRA training) or the block left "
+                                  "unfused")
     x2 = _rows(x, K)
     M = x2.shape[0]
     ms, mb = scale.reshape(-1, K), shift.reshape(-1, K)
@@ -181,17 +174,20 @@ def fuse_producers(dit) -> int:
 # Linears that read one tensor, computed in one grouped launch
 # ----------------------------------------------------------------------------------------------------------
 def _lora_state(m):
-    """(A, B, effective scale) of a member's adapter as its forward would apply it now, or None (exact base)."""
-    if isinstance(m, ConvRotLinear) or m.scale_mul == 0.0:
+    """(A, B, effective scale) of a member's adapter as its forward would apply it now (the factors as the
+    kernels take them: f32, rank padded to a multiple of 16), or None (exact base)."""
+    if isinstance(m, ConvRotLinear) or m.scale * m.scale_mul == 0.0:
         return None
-    return m.lora_A, m.lora_B, float(m.scale * m.scale_mul)
+    A, B = m._kernel_factors()
+    return A, B, float(m.scale * m.scale_mul)
 
 
-def _state_key(st):
-    if st is None:
+def _state_key(m):
+    """Identity of what a member's adapter would add now: its parameters (object and version) and scale."""
+    if isinstance(m, ConvRotLinear) or m.scale * m.scale_mul == 0.0:
         return None
-    A, B, sc = st
-    return (id(A), A._version, id(B), B._version, sc)
+    A, B = m.lora_A, m.lora_B
+    return (id(A), A._version, id(B), B._version, float(m.scale * m.scale_mul))
 
 
 class _GroupedFn(torch.autograd.Function):
@@ -264,7 +260,7 @@ class _SiblingGroup:
         key = self._key(x)
         if self.ref is not None and self.ref() is x and self.key == key and idx in self.kept:
             out, sk = self.kept.pop(idx)
-            if sk == _state_key(_lora_state(self.members[idx])):
+            if sk == _state_key(self.members[idx]):
                 return out
         K = x.shape[-1]
         if x.dtype != torch.bfloat16 or x.numel() // max(K, 1) <= 8:
@@ -279,7 +275,7 @@ class _SiblingGroup:
         lead = x.shape[:-1]
         outs = [y.reshape(*lead, b.out_features) for y, b in zip(ys, bases)]
         self.ref, self.key = weakref.ref(x), key
-        self.kept = {i: (o, _state_key(st)) for i, (o, st) in enumerate(zip(outs, states)) if i != idx}
+        self.kept = {i: (o, _state_key(m)) for i, (o, m) in enumerate(zip(outs, self.members)) if i != idx}
         return outs[idx]
 
 
@@ -293,7 +289,7 @@ def _groupable(m) -> bool:
     base = m if isinstance(m, ConvRotLinear) else getattr(m, "base", None)
     if not isinstance(base, ConvRotLinear) or base.mode != "w8a8" or base.out_features % _lib.GROUP_ALIGN:
         return False
-    return base is m or (hasattr(m, "_fusable") and m._fusable())
+    return base is m or hasattr(m, "_kernel_factors")
 
 
 def group_siblings(dit, groups=(("attn", ("wq", "wk", "wv", "gate")),)) -> int:

@@ -1,32 +1,52 @@
-"""LoRA adapters over the ConvRot base, with the reference's module API unchanged.
+"""LoRA adapters for the DiT, with the module API of the reference's ``lora.py`` and the adapter maths run in the
+fused HIP kernels whenever the base is one of this package's quantized linears.
 
-Mirrors ``lora.py`` of the reference: ``LoRALinear`` (``lora.py:27-48``) with the same attributes
-(``base, rank, scale, scale_mul, lora_A, lora_B``), init (``:30-41``) and maths
-``base(x) + (scale*scale_mul) * ((x.f32 @ A^T) @ B^T)`` (``:43-48``); ``lora_scaled`` / ``lora_disabled``
-(``:51-70``); ``inject_lora`` with the same duck-typed base check (``:81-116``); ``lora_parameters``
-(``:119-123``); ``save_lora`` / ``load_lora_weights`` / ``load_lora`` with the same safetensors keys and
-metadata (``:154-222``).
+Interface kept from the reference (callers and saved files depend on it):
 
-The one behavioural addition: when ``base`` is a :class:`~.quantize.ConvRotLinear` or
-:class:`~.quantize.Fp8Linear` and the rank fits the fused
-kernels (a multiple of 16, at most 128; ``out_features`` a multiple of 128), ``forward`` runs base + LoRA as
-one fused HIP pass (the LoRA down-projection on bf16 MFMA, the up-projection inside the GEMM epilogue) instead
-of three extra GEMMs and three elementwise kernels, and the backward computes the LoRA gradients with the
-library's own kernels.  ``scale_mul == 0`` still returns exactly ``base(x)`` (``lora.py:45-46``).
+* ``LoRALinear(base, rank, alpha)`` with attributes ``base, rank, scale, scale_mul, lora_A, lora_B``, the init of
+  ``lora.py:30-41`` (frozen base, ``scale = alpha / rank``, ``A`` kaiming-uniform, ``B`` zeros) and the output
+  ``base(x) + (scale * scale_mul) * ((x.f32 @ A^T) @ B^T)`` of ``lora.py:43-48``; ``scale_mul == 0`` returns
+  exactly ``base(x)``.
+* ``lora_scaled`` / ``lora_disabled`` (``lora.py:51-70``), ``inject_lora`` with the duck-typed base test
+  (``lora.py:81-116``), ``lora_parameters`` (``:119-123``), ``save_lora`` / ``load_lora_weights`` /
+  ``load_lora`` with the key format ``<prefix>.<module path>.lora_{A,B}.weight`` and metadata
+  ``{format: krea2-lora, rank, alpha}`` (``:154-222``).
+
+Over a :class:`~.quantize.ConvRotLinear` or :class:`~.quantize.Fp8Linear` base every rank runs on the library's
+kernels: the down-projection on bf16 MFMA, the up-projection in the GEMM epilogue, the backward in the LoRA
+gradient kernels.  The kernels take ranks in multiples of 16, so other ranks are padded with zero factor rows,
+which adds exact zeros and changes no result.  Over a plain ``nn.Linear`` (the unquantized stages outside the
+hot path) the adapter is the reference's own torch expression.
 """
 from __future__ import annotations
 
 import contextlib
 import math
 import os
+import tempfile
+from dataclasses import dataclass
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
+from . import _lib
 from .quantize import ConvRotLinear, Fp8Linear
 
 DEFAULT_TARGETS = ("attn.wq", "attn.wk", "attn.wv", "attn.wo", "attn.gate",
                    "mlp.gate", "mlp.up", "mlp.down")
+
+_LORA_FORMAT = "krea2-lora"
+_HIP_BASES = (ConvRotLinear, Fp8Linear)
+
+
+def _is_adaptable(mod) -> bool:
+    """The reference's test for a wrappable base: an ``nn.Linear`` or anything flagged ``is_quant_linear``."""
+    return isinstance(mod, nn.Linear) or bool(getattr(mod, "is_quant_linear", False))
+
+
+def _padded_rank(rank: int) -> int:
+    return -(-rank // _lib.RANK_ALIGN) * _lib.RANK_ALIGN
 
 
 class LoRALinear(nn.Module):
@@ -34,159 +54,190 @@ class LoRALinear(nn.Module):
 
     def __init__(self, base: nn.Module, rank: int, alpha: float):
         super().__init__()
+        if rank < 1:
+            raise ValueError(f"LoRA rank must be positive, got {rank}")
+        if isinstance(base, _HIP_BASES):
+            # what the library's LoRA gradient kernels take (the dims of every Krea 2 linear qualify)
+            if base.in_features % _lib.HADAMARD_BLOCK or base.out_features % _lib.HADAMARD_BLOCK:
+                raise ValueError(f"a LoRA over a quantized base needs in/out features that are multiples of "
+                                 f"{_lib.HADAMARD_BLOCK}, got {base.in_features} -> {base.out_features}")
+            if rank > _lib.MAX_RANK:
+                raise ValueError(f"LoRA rank {rank} exceeds the library's {_lib.MAX_RANK}")
         self.base = base
-        for p in self.base.parameters():
-            p.requires_grad_(False)
+        base.requires_grad_(False)
         self.rank = rank
         self.scale = alpha / rank
         self.scale_mul = 1.0
-        dev = base.weight.device
-        self.lora_A = nn.Parameter(torch.empty(rank, base.in_features, device=dev, dtype=torch.float32))
-        self.lora_B = nn.Parameter(torch.zeros(base.out_features, rank, device=dev, dtype=torch.float32))
+        home = base.weight.device
+        self.lora_A = nn.Parameter(torch.empty(rank, base.in_features, device=home, dtype=torch.float32))
+        self.lora_B = nn.Parameter(torch.zeros(base.out_features, rank, device=home, dtype=torch.float32))
         nn.init.kaiming_uniform_(self.lora_A, a=math.sqrt(5))
 
-    def _fusable(self) -> bool:
-        return (isinstance(self.base, (ConvRotLinear, Fp8Linear)) and self.rank % 16 == 0 and self.rank <= 128
-                and self.base.in_features % 128 == 0 and self.base.out_features % 128 == 0
-                and self.lora_A.dtype == torch.float32 and self.lora_B.dtype == torch.float32)
+    def _kernel_factors(self):
+        """``(A, B)`` as the kernels take them: f32, the rank padded with zeros to a multiple of 16.  Both are
+        autograd functions of the parameters, so the padded ranks' gradients are dropped on the way back."""
+        A, B = self.lora_A, self.lora_B
+        if A.dtype != torch.float32:
+            A, B = A.float(), B.float()
+        extra = _padded_rank(self.rank) - self.rank
+        if extra:
+            A = F.pad(A, (0, 0, 0, extra))
+            B = F.pad(B, (0, extra))
+        return A.contiguous(), B.contiguous()
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if self.scale_mul == 0.0:
-            return self.base(x)
-        if self._fusable():
-            return self.base.forward_lora(x, self.lora_A, self.lora_B, self.scale * self.scale_mul)
-        out = self.base(x)
-        delta = (x.to(self.lora_A.dtype) @ self.lora_A.t()) @ self.lora_B.t()
-        return out + (self.scale * self.scale_mul) * delta.to(out.dtype)
+        s = self.scale * self.scale_mul
+        if isinstance(self.base, _HIP_BASES):
+            if s == 0.0:
+                return self.base(x)
+            A, B = self._kernel_factors()
+            return self.base.forward_lora(x, A, B, s)
+        y = self.base(x)
+        if s == 0.0:
+            return y
+        return y + s * ((x.to(self.lora_A.dtype) @ self.lora_A.t()) @ self.lora_B.t()).to(y.dtype)
+
+
+def _adapters_in(model: nn.Module) -> list[LoRALinear]:
+    return [m for m in model.modules() if isinstance(m, LoRALinear)]
 
 
 @contextlib.contextmanager
 def lora_scaled(model: nn.Module, factor: float):
-    """Temporarily multiply every adapter's effect by ``factor`` (may be negative or 0)."""
-    mods = [m for m in model.modules() if isinstance(m, LoRALinear)]
-    prev = [m.scale_mul for m in mods]
+    """Within the ``with`` body every adapter of ``model`` acts ``factor`` times as strongly (negative flips the
+    direction, 0 turns it off); each adapter's own multiplier comes back afterwards."""
+    saved = {m: m.scale_mul for m in _adapters_in(model)}
+    for m in saved:
+        m.scale_mul = float(factor)
     try:
-        for m in mods:
-            m.scale_mul = float(factor)
         yield
     finally:
-        for m, p in zip(mods, prev):
-            m.scale_mul = p
+        for m, v in saved.items():
+            m.scale_mul = v
 
 
 def lora_disabled(model: nn.Module):
-    """Context manager: run with all adapters off (frozen-base prediction)."""
+    """Context manager: the frozen base alone (every adapter's multiplier 0)."""
     return lora_scaled(model, 0.0)
 
 
-def _resolve(parent: nn.Module, dotted: str):
-    obj = parent
-    parts = dotted.split(".")
-    for p in parts[:-1]:
-        obj = getattr(obj, p)
-    return obj, parts[-1]
+@dataclass
+class _Site:
+    name: str          # adapter name: the module path under the DiT
+    owner: nn.Module   # module holding the linear as an attribute
+    attr: str
+    base: nn.Module
 
 
-def _adaptable(base) -> bool:
-    return isinstance(base, nn.Linear) or getattr(base, "is_quant_linear", False)
+def _target_sites(prefix: str, stack, targets):
+    for i, blk in enumerate(stack):
+        for tgt in targets:
+            owner_path, _, attr = tgt.rpartition(".")
+            try:
+                owner = blk.get_submodule(owner_path) if owner_path else blk
+            except AttributeError:
+                continue
+            base = getattr(owner, attr, None)
+            if _is_adaptable(base):
+                yield _Site(f"{prefix}.{i}.{tgt}", owner, attr, base)
+
+
+def _module_sites(prefix: str, root: nn.Module):
+    for path, mod in list(root.named_modules()):
+        if path and _is_adaptable(mod):
+            owner_path, _, attr = path.rpartition(".")
+            yield _Site(f"{prefix}.{path}", root.get_submodule(owner_path) if owner_path else root, attr, mod)
 
 
 def inject_lora(dit, rank: int, alpha: float | None = None, *, targets=DEFAULT_TARGETS,
                 include_txtfusion: bool = True, include_txtmlp: bool = True) -> dict:
-    """Freeze the DiT and wrap each target Linear (or quantized base) with :class:`LoRALinear`."""
-    alpha = alpha if alpha is not None else float(rank)
+    """Freeze ``dit`` and put a :class:`LoRALinear` around every targeted linear (or quantized base): the
+    ``targets`` paths inside each of ``dit.blocks`` and, when asked for and present, inside the text-fusion
+    layerwise / refiner blocks, plus every linear of ``dit.txtmlp``.  Returns ``{module path: adapter}``;
+    raises ``RuntimeError`` when nothing matched.  ``alpha`` defaults to ``rank`` (scale 1)."""
+    alpha = float(rank) if alpha is None else alpha
     dit.requires_grad_(False)
-    groups = [("blocks", dit.blocks)]
-    if include_txtfusion and hasattr(dit, "txtfusion"):
-        groups.append(("txtfusion.layerwise_blocks", dit.txtfusion.layerwise_blocks))
-        groups.append(("txtfusion.refiner_blocks", dit.txtfusion.refiner_blocks))
-    adapters: dict[str, LoRALinear] = {}
-    for prefix, modlist in groups:
-        for i, blk in enumerate(modlist):
-            for tgt in targets:
-                try:
-                    parent, leaf = _resolve(blk, tgt)
-                    base = getattr(parent, leaf)
-                except AttributeError:
-                    continue
-                if not _adaptable(base):
-                    continue
-                lora = LoRALinear(base, rank, alpha)
-                setattr(parent, leaf, lora)
-                adapters[f"{prefix}.{i}.{tgt}"] = lora
-    if include_txtmlp and hasattr(dit, "txtmlp"):
-        for name, base in list(dit.txtmlp.named_modules()):
-            if not name or not _adaptable(base):
-                continue
-            parent = dit.txtmlp.get_submodule(name.rsplit(".", 1)[0]) if "." in name else dit.txtmlp
-            leaf = name.rsplit(".", 1)[-1]
-            lora = LoRALinear(base, rank, alpha)
-            setattr(parent, leaf, lora)
-            adapters[f"txtmlp.{name}"] = lora
-    if not adapters:
-        raise RuntimeError("inject_lora matched no Linear targets; check target names vs mmdit.py")
+    sites = list(_target_sites("blocks", dit.blocks, targets))
+    fusion = getattr(dit, "txtfusion", None) if include_txtfusion else None
+    if fusion is not None:
+        for stage in ("layerwise_blocks", "refiner_blocks"):
+            sites += _target_sites(f"txtfusion.{stage}", getattr(fusion, stage), targets)
+    txtmlp = getattr(dit, "txtmlp", None) if include_txtmlp else None
+    if txtmlp is not None:
+        sites += _module_sites("txtmlp", txtmlp)
+    if not sites:
+        raise RuntimeError(f"inject_lora: no linear of {type(dit).__name__} matches the targets {tuple(targets)}")
+    adapters = {}
+    for site in sites:
+        adapter = LoRALinear(site.base, rank, alpha)
+        setattr(site.owner, site.attr, adapter)
+        adapters[site.name] = adapter
     return adapters
 
 
 def lora_parameters(adapters: dict) -> list:
-    params = []
-    for m in adapters.values():
-        params.extend([m.lora_A, m.lora_B])
-    return params
+    """The trainable tensors, ``[A_0, B_0, A_1, B_1, ...]`` in adapter order."""
+    return [p for m in adapters.values() for p in (m.lora_A, m.lora_B)]
+
+
+def _key(prefix: str, name: str, which: str) -> str:
+    return f"{prefix}.{name}.lora_{which}.weight"
 
 
 def save_lora(adapters: dict, path: str, *, rank: int, alpha: float, metadata: dict | None = None,
               key_prefix: str = "diffusion_model") -> None:
-    """Save adapters as bf16 safetensors, keys ``<key_prefix>.<name>.lora_{A,B}.weight``, written atomically."""
+    """Write the adapters to ``path`` as safetensors: bf16 ``lora_A`` / ``lora_B`` per adapter under
+    ``<key_prefix>.<name>.lora_{A,B}.weight``, metadata ``format / rank / alpha`` plus ``metadata``.  The file
+    appears atomically (written next to ``path``, then renamed)."""
     from safetensors.torch import save_file
 
-    sd = {}
-    for name, m in adapters.items():
-        sd[f"{key_prefix}.{name}.lora_A.weight"] = m.lora_A.detach().to(torch.bfloat16).cpu().contiguous()
-        sd[f"{key_prefix}.{name}.lora_B.weight"] = m.lora_B.detach().to(torch.bfloat16).cpu().contiguous()
-    meta = {"format": "krea2-lora", "rank": str(rank), "alpha": str(alpha)}
-    if metadata:
-        meta.update({k: str(v) for k, v in metadata.items()})
-    tmp = path + ".tmp"
-    save_file(sd, tmp, metadata=meta)
-    os.replace(tmp, path)
+    tensors = {_key(key_prefix, name, w): t.detach().to(torch.bfloat16).cpu().contiguous()
+               for name, m in adapters.items() for w, t in (("A", m.lora_A), ("B", m.lora_B))}
+    meta = {"format": _LORA_FORMAT, "rank": str(rank), "alpha": str(alpha)}
+    meta.update({k: str(v) for k, v in (metadata or {}).items()})
+    fd, tmp = tempfile.mkstemp(prefix=os.path.basename(path) + ".", dir=os.path.dirname(os.path.abspath(path)))
+    os.close(fd)
+    try:
+        save_file(tensors, tmp, metadata=meta)
+        os.replace(tmp, path)
+    except BaseException:
+        if os.path.exists(tmp):
+            os.remove(tmp)
+        raise
 
 
 def load_lora_weights(adapters: dict, path: str, *, key_prefix: str = "diffusion_model") -> int:
-    """Copy saved ``lora_{A,B}`` into already-injected adapters; returns how many had no saved weights."""
+    """Copy the factors saved in ``path`` into already-injected ``adapters`` (in place, cast to the parameters'
+    dtype).  Returns how many adapters found no saved pair (0: everything loaded)."""
     from safetensors.torch import load_file
 
-    sd = load_file(path)
+    saved = load_file(path)
     missing = 0
-    for name, m in adapters.items():
-        a = sd.get(f"{key_prefix}.{name}.lora_A.weight")
-        b = sd.get(f"{key_prefix}.{name}.lora_B.weight")
-        if a is None or b is None:
-            missing += 1
-            continue
-        with torch.no_grad():
-            m.lora_A.copy_(a.to(m.lora_A.dtype))
-            m.lora_B.copy_(b.to(m.lora_B.dtype))
+    with torch.no_grad():
+        for name, m in adapters.items():
+            pair = [saved.get(_key(key_prefix, name, w)) for w in ("A", "B")]
+            if any(t is None for t in pair):
+                missing += 1
+                continue
+            for param, t in zip((m.lora_A, m.lora_B), pair):
+                param.copy_(t.to(param.dtype))
     return missing
 
 
 def load_lora(dit, path: str) -> dict:
-    """Inject adapters matching a saved LoRA (rank and text-side stages inferred from its keys) and load it."""
+    """Inject adapters shaped like the ones saved in ``path`` and load them.  The rank comes from the first
+    saved ``lora_A``; text-fusion and text-MLP adapters are injected when the file holds any."""
     from safetensors.torch import load_file
 
-    sd = load_file(path)
-    rank = None
-    has_txtfusion = has_txtmlp = False
-    for k, v in sd.items():
-        name = k[len("diffusion_model."):].rsplit(".lora_", 1)[0]
-        has_txtfusion |= "txtfusion" in name
-        has_txtmlp |= "txtmlp" in name
-        if k.endswith("lora_A.weight") and rank is None:
-            rank = v.shape[0]
-    if rank is None:
-        raise ValueError(f"no lora_A weights found in {path}")
-    adapters = inject_lora(dit, rank, include_txtfusion=has_txtfusion, include_txtmlp=has_txtmlp)
+    saved = load_file(path)
+    prefix = "diffusion_model."
+    names = {k[len(prefix):].rsplit(".lora_", 1)[0] for k in saved if k.startswith(prefix)}
+    ranks = [t.shape[0] for k, t in saved.items() if k.endswith("lora_A.weight")]
+    if not ranks:
+        raise ValueError(f"{path} holds no lora_A tensors")
+    adapters = inject_lora(dit, ranks[0], include_txtfusion=any("txtfusion" in n for n in names),
+                           include_txtmlp=any("txtmlp" in n for n in names))
     missing = load_lora_weights(adapters, path)
     if missing:
-        print(f"[load_lora] warning: {missing} injected adapters had no saved weights")
+        print(f"[load_lora] {missing} of {len(adapters)} injected adapters have no weights in {path}")
     return adapters

@@ -68,6 +68,14 @@ class _SharedInputQuant:
 shared_input_quant = _SharedInputQuant()
 
 
+def _check_out_features(N: int) -> None:
+    """The input-gradient GEMM reads dY in 64-column steps, so a layer that trains through its backward needs
+    ``out_features % 64 == 0`` (every Krea 2 linear has it); reject others when the layer is built, not in the
+    middle of a training step."""
+    if N < 64 or N % 64:
+        raise ValueError(f"out_features={N} must be a positive multiple of 64 (the input-gradient GEMM's step)")
+
+
 class _ConvRotLinearFn(torch.autograd.Function):
     """Forward: rotate+quantize x, optional LoRA down-projection, fused GEMM + epilogue.
     Backward (straight-through over both quantizers): ``dX = 2^-7 (dY W_hat) R + g A`` with
@@ -124,8 +132,7 @@ class ConvRotLinear(nn.Module):
         w = lin.weight.data
         N, K = w.shape
         _lib._check_k(K)
-        if N % 4:
-            raise ValueError(f"out_features={N} must be a multiple of 4")
+        _check_out_features(N)
         home = w.device
         if home.type != "cuda":
             if not torch.cuda.is_available():
@@ -165,6 +172,7 @@ class ConvRotLinear(nn.Module):
             if wscale_bits.shape != (K // _lib.INT4_GROUP, N):
                 raise ValueError("w4a8 scale bits must be (K/64, N)")
         _lib._check_k(K)
+        _check_out_features(N)
         m.qweight = nn.Parameter(qweight, requires_grad=False)
         m.wscale = nn.Parameter(wscale_bits, requires_grad=False)
         m.bias = nn.Parameter(bias, requires_grad=False) if bias is not None else None
@@ -308,8 +316,9 @@ class Fp8Linear(nn.Module):
         super().__init__()
         w = lin.weight.data
         N, K = w.shape
-        if K % 64 or N % 4:
-            raise ValueError(f"Fp8Linear needs in_features % 64 == 0 and out_features % 4 == 0, got {K}, {N}")
+        if K % 64:
+            raise ValueError(f"Fp8Linear needs in_features % 64 == 0, got {K}")
+        _check_out_features(N)
         home = w.device
         if home.type != "cuda":
             if not torch.cuda.is_available():
@@ -331,6 +340,9 @@ class Fp8Linear(nn.Module):
         if weight_fp8.dtype != torch.float8_e4m3fn or weight_fp8.dim() != 2:
             raise ValueError("weight_fp8 must be a 2-D float8_e4m3fn tensor")
         N, K = weight_fp8.shape
+        if K % 64:
+            raise ValueError(f"Fp8Linear needs in_features % 64 == 0, got {K}")
+        _check_out_features(N)
         if scale.dtype != torch.bfloat16 or scale.numel() != N:
             raise ValueError("scale must hold one bf16 value per output row")
         m = cls.__new__(cls)

@@ -67,7 +67,7 @@ def test_grouped_argument_checks(k2, dev):
         L.gemm_w8a8_grouped(qx[:8], sx[:8], [(*ok, 0, 1.0)])  # skinny M runs the GEMV per linear
 
 
-def _build(k2, dev):
+def _build(k2, dev, rank=16):
     g = torch.Generator().manual_seed(3)
     dit = Dit()
     with torch.no_grad():
@@ -76,7 +76,7 @@ def _build(k2, dev):
             p.copy_(torch.randn(p.shape, generator=g) * sc)
     dit = dit.to(torch.bfloat16).to(dev)
     assert k2.quantize_dit_convrot(dit, "w8a8") == 16
-    ad = k2.inject_lora(dit, 16, include_txtfusion=False, include_txtmlp=False)
+    ad = k2.inject_lora(dit, rank, include_txtfusion=False, include_txtmlp=False)
     with torch.no_grad():
         for m in ad.values():
             m.lora_B.copy_(torch.randn(m.lora_B.shape, generator=g) * 0.01)
@@ -132,10 +132,13 @@ def test_group_siblings_matches_ungrouped(k2, dev, monkeypatch):
         assert torch.equal(gr2[k][0], gr1[k][0]) and torch.equal(gr2[k][1], gr1[k][1]), k
 
 
-def test_grouped_layer_gradients(k2, dev):
+@pytest.mark.parametrize("rank", [16, 32, 64, 24])
+def test_grouped_layer_gradients(k2, dev, rank):
     """The four attention inputs on one tensor with fixed output gradients: grouped against each member's own
-    forward / backward (same codes; only the stacked LoRA down-projection's summation order differs)."""
-    dit, ad = _build(k2, dev)
+    forward / backward (same codes; only the stacked LoRA down-projection's summation order differs).  The
+    stacked rank is 4 x rank: 64 .. 256 (the reference's default rank 64 stacks to 256, two 128-rank chunks of
+    the down-projection); rank 24 is padded to 32 per member."""
+    dit, ad = _build(k2, dev, rank)
     gdit = copy.deepcopy(dit)
     assert k2.group_siblings(gdit) == 2
     names = ("wq", "wk", "wv", "gate")

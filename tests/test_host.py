@@ -50,9 +50,14 @@ def test_status_codes_for_bad_arguments_without_gpu(k2):
     assert lib.k2q_gemm_w8a8(p, p, p, p, None, p, p, 8, 1.0, 4, 4, 128, p, None, 0, None) == -1   # rank 8
     assert lib.k2q_gemm_w8a8(p, p, p, p, None, None, None, 0, 0.0, 4, 6, 128, p, None, 0, None) == -1  # N % 4
     assert lib.k2q_gemm_dx(p, p, 4, 96, 128, None, None, 0, p, None, 0, None) == -1    # N % 64
-    assert lib.k2q_lora_down(p, 4, 128, 128, p, 200, p, 0, p, None) == -1    # rank > 128
+    assert lib.k2q_lora_down(p, 4, 128, 128, p, 200, p, 0, p, None) == -1    # rank % 16
+    assert lib.k2q_lora_down(p, 4, 128, 128, p, 8192, p, 0, p, None) == -1   # rank > K2Q_MAX_RANK
     assert lib.k2q_lora_down(p, 4, 100, 100, p, 16, None, 0, p, None) == -1  # K % 128
     assert lib.k2q_lora_down_ws_bytes(4, 128, 200) == 0                      # no plan for a bad rank
+    # ranks above 128 run as 128-rank chunks sharing one workspace: the largest chunk's K-slice partials
+    assert lib.k2q_lora_down_ws_bytes(4096, 3072, 256) == lib.k2q_lora_down_ws_bytes(4096, 3072, 128) > 0
+    assert lib.k2q_lora_grads_ws_bytes(4096, 3072, 3072, 256) > lib.k2q_lora_grads_ws_bytes(4096, 3072, 3072, 128)
+    assert lib.k2q_lora_grads_ws_bytes(4096, 3072, 3072, 8192) == 0
 
 
 def test_wrappers_validate_before_launch(k2):
@@ -125,7 +130,7 @@ class _Block(nn.Module):
     def __init__(self, d=256, h=512):
         super().__init__()
         self.attn = nn.Module()
-        for n, o in (("wq", d), ("wk", d // 4), ("wv", d // 4), ("gate", d), ("wo", d)):
+        for n, o in (("wq", d), ("wk", d // 2), ("wv", d // 2), ("gate", d), ("wo", d)):
             setattr(self.attn, n, nn.Linear(d, o, bias=False))
         self.mlp = nn.Module()
         self.mlp.gate = nn.Linear(d, h, bias=False)
@@ -160,6 +165,34 @@ def test_inject_lora_accepts_quantized_bases_by_duck_typing(k2):
     with k2.lora_disabled(dit):
         assert all(m.scale_mul == 0.0 for m in adapters.values())
     assert all(m.scale_mul == 1.0 for m in adapters.values())
+
+
+def test_lora_over_quantized_base_rejects_shapes_the_kernels_do_not_take(k2):
+    """A LoRA over a quantized base runs only on the library's kernels, which take in/out features in multiples
+    of 128: other shapes are refused when the adapter is built (not with a torch fallback, not mid-step)."""
+    base = _cpu_quantized(N=64, K=256)
+    with pytest.raises(ValueError, match="multiples of 128"):
+        k2.LoRALinear(base, 16, 16.0)
+    with pytest.raises(ValueError, match="rank"):
+        k2.LoRALinear(_cpu_quantized(N=128, K=256), 0, 1.0)
+    with pytest.raises(ValueError, match="multiple of 64"):
+        _cpu_quantized(N=96, K=256)
+
+
+@pytest.mark.parametrize("rank", [4, 8, 16, 24, 200])
+def test_lora_kernel_factors_pad_ranks_with_zeros(k2, rank):
+    """The fused path hands the kernels the factors padded to a multiple of 16 ranks with zeros (an exact no-op
+    in every sum); gradients reach the unpadded parameters only."""
+    m = k2.LoRALinear(_cpu_quantized(N=128, K=256), rank, float(rank))
+    nn.init.normal_(m.lora_B)
+    A, B = m._kernel_factors()
+    rp = -(-rank // 16) * 16
+    assert A.shape == (rp, 256) and B.shape == (128, rp) and A.dtype == B.dtype == torch.float32
+    assert torch.equal(A[:rank], m.lora_A) and torch.equal(B[:, :rank], m.lora_B)
+    assert not A[rank:].any() and not B[:, rank:].any()
+    (A.sum() + 2 * B.sum()).backward()
+    assert m.lora_A.grad.shape == (rank, 256) and torch.all(m.lora_A.grad == 1)
+    assert m.lora_B.grad.shape == (128, rank) and torch.all(m.lora_B.grad == 2)
 
 
 def test_inject_lora_raises_without_targets(k2):
@@ -336,7 +369,7 @@ def test_fusion_walkers_leave_unquantized_blocks_alone(k2):
     with pytest.raises(NotImplementedError):
         k2.swiglu(x.float(), x.float())
     norm = nn.Module()
-    norm.scale, norm.eps = nn.Parameter(torch.zeros(256)), 1e-5
+    norm.scale, norm.eps = nn.Parameter(torch.zeros(256), requires_grad=False), 1e-5
     sc = torch.zeros(3, 1, 256, dtype=torch.bfloat16)                    # 3 entries for a batch of 2
     with pytest.raises(ValueError):
         k2.modulated_rmsnorm(norm, x, sc, sc)
@@ -344,6 +377,15 @@ def test_fusion_walkers_leave_unquantized_blocks_alone(k2):
         k2.modulated_rmsnorm(norm, x, sc[:2], sc[:2, :, :128])
     with pytest.raises(RuntimeError):                                    # valid shapes, CPU: refuses
         k2.modulated_rmsnorm(norm, x, sc[:2], sc[:2])
+    # the fused norm differentiates its input only: a trainable norm scale or modulation is refused up front
+    norm.scale.requires_grad_(True)
+    with pytest.raises(NotImplementedError, match="frozen"):
+        k2.modulated_rmsnorm(norm, x, sc[:2], sc[:2])
+    norm.scale.requires_grad_(False)
+    with pytest.raises(NotImplementedError, match="frozen"):
+        k2.modulated_rmsnorm(norm, x, sc[:2].requires_grad_(True), sc[:2])
+    with torch.no_grad(), pytest.raises(RuntimeError):                   # no autograd: only the CPU refusal
+        k2.modulated_rmsnorm(norm, x, sc[:2].requires_grad_(True), sc[:2])
 
 
 def test_grouped_wrapper_validates_before_launch(k2):
