@@ -10,11 +10,20 @@ on; ``cpu_baseline`` times the CPU oracle (a port of the same arithmetic) on a b
 Before the W warmup steps, ``--settle`` seconds of untimed steps let the GPU clocks leave their ramp-up
 state (``extra.settle_s`` reports it).
 
-    python bench.py [--steps K] [--warmup W] [--settle S] [--config 2] [--all] [--no-cpu]
+Every BASELINE.json configuration gets its own record in ``extra`` (``cfg0`` .. ``cfg4``): GPU ms and TOPS,
+the roofline fraction of its dominant kernel against the peak that bounds it (int8 MFMA for the forward GEMMs,
+bf16 MFMA for the input-gradient GEMM, HBM for rotate/quant and the M=2 GEMV), and two CPU paths timed in the
+same process on the host's cores: the oracle (this build's arithmetic restated on the CPU) and the reference's
+own ``Fp8Linear`` + ``LoRALinear`` maths restated with torch CPU ops.
+
+    python bench.py [--steps K] [--warmup W] [--settle S] [--config 2] [--no-cpu]
+    python bench.py --profile-pass          # fixed launches for rocprofv3 counter passes
+    python bench.py --pmc-summary DIR       # traffic table from two rocprofv3 --pmc runs over --profile-pass
 """
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import platform
@@ -273,8 +282,9 @@ def _no_input_reuse(k2):
     return prev
 
 
-def run_cfg3(k2, steps, dev, settle_s=0.0):
-    """Forward + backward (dX through the frozen base with the inverse rotation, dA, dB) of one layer."""
+def run_cfg3(k2, steps, dev, settle_s=0.0, cpu=False):
+    """Forward + backward (dX through the frozen base with the inverse rotation, dA, dB) of one layer; with
+    ``cpu``, the CPU paths of the same step (:func:`cpu_cfg3`)."""
     c = CFG3
     layer = make_layer(k2, c["K"], c["N"], c["r"], dev, seed=3)
     g = torch.Generator().manual_seed(4)
@@ -316,12 +326,35 @@ def run_cfg3(k2, steps, dev, settle_s=0.0):
         out.backward(dy)
 
     ms_ref = time_loop(ref_step, steps)
+    # The backward's kernels alone: the input-gradient GEMM (bf16 MFMA, with its LoRA term) on the layer's
+    # effective weight, and the per-call pass that builds that weight (HBM: N K int8 in, 2 N K bf16 out).
+    L = k2._lib
+    base = layer.base
+    wt = L.dx_weight(base.qweight, base.weight_scale)
+    gg = (torch.randn(c["M"], c["r"], generator=g) * 1e-3).to(dev)
+    A_ = layer.lora_A.detach()
+    ms_dx = sorted(time_loop(lambda: L.gemm_dx(dy, base.qweight, base.weight_scale, g=gg, lora_a=A_, wt=wt), steps)
+                   for _ in range(3))[1]
+    ms_prep = sorted(time_loop(lambda: L.dx_weight(base.qweight, base.weight_scale), steps) for _ in range(3))[1]
+    del wt
     ops_fwd = 2.0 * c["M"] * c["N"] * c["K"]
-    return {"step_ms": round(ms, 4), "fwd_ms": round(ms_fwd, 4), "bwd_ms": round(ms - ms_fwd, 4),
-            "fwd_tops": round(ops_fwd / (ms_fwd * 1e-3) / 1e12, 1),
-            "dx_tflops": round(ops_fwd / ((ms - ms_fwd) * 1e-3) / 1e12, 1),
+    dx_tflops = ops_fwd / (ms_dx * 1e-3) / 1e12
+    prep_gbs = 3.0 * c["N"] * c["K"] / (ms_prep * 1e-3) / 1e9
+    fwd_tops = ops_fwd / (ms_fwd * 1e-3) / 1e12
+    return {"workload": c["name"], "ms": round(ms, 4), "step_ms": round(ms, 4), "fwd_ms": round(ms_fwd, 4),
+            "bwd_ms": round(ms - ms_fwd, 4), "fwd_tops": round(fwd_tops, 1),
+            "tops": round(2 * ops_fwd / (ms * 1e-3) / 1e12, 1),
+            "dx_gemm_ms": round(ms_dx, 4), "dx_gemm_tflops": round(dx_tflops, 1),
+            "dx_weight_pass_ms": round(ms_prep, 4),
+            "roofline": roofline_entry("gemm_nt_kernel<EPI_DXLIN> (input gradient)", "mfma", dx_tflops,
+                                       BF16_PEAK_TFLOPS, "TFLOP/s"),
+            "fwd_roofline": roofline_entry("forward (rotate/quant + LoRA down + W8A8 GEMM)", "mfma", fwd_tops,
+                                           INT8_PEAK_TOPS, "TOPS"),
+            "dx_weight_roofline": roofline_entry("rot_dequant_t_kernel (effective weight)", "hbm", prep_gbs,
+                                                 HBM_PEAK_GBS, "GB/s"),
             "step_ms_dx_weight_cached": round(ms_cached, 4),
-            "reference_fp8_step_ms_gpu": round(ms_ref, 4)}
+            "reference_fp8_step_ms_gpu": round(ms_ref, 4),
+            **({"cpu": cpu_cfg3(*_layer_tensors(layer, 3, c["K"], c["N"]))} if cpu else {})}
 
 
 def run_producers(k2, steps, dev):
@@ -504,16 +537,19 @@ def run_reference_gpu(k2, res, steps, dev):
             "convrot_speedup_vs_reference": round(t_ref / res["ms_step"], 2)}
 
 
-def run_cfg4(k2, steps, dev, settle_s=0.0):
+def run_cfg4(k2, steps, dev, settle_s=0.0, cpu=False):
     """Summed forward time of one double-stream block's quantized linears (image + text stream, plus the
-    per-stream adaLN modulation at M=2), each a LoRALinear (r=16) over a W8A8 ConvRot base."""
+    per-stream adaLN modulation at M=2), each a LoRALinear (r=16) over a W8A8 ConvRot base; with ``cpu``, the
+    CPU paths of the same ten linears (:func:`cpu_cfg4`)."""
     total_ops = 0.0
-    layers = []
+    layers, seeds = [], []
     for sname, M in CFG4_STREAMS:
         for lname, K, N in CFG4_LINEARS:
             layers.append((f"{sname}.{lname}", make_layer(k2, K, N, 16, dev, seed=K + N + M), M, K, N))
+            seeds.append(K + N + M)
         K, N, Ma = CFG4_ADALN
         layers.append((f"{sname}.adaln", make_layer(k2, K, N, 16, dev, seed=7 + M), Ma, K, N))
+        seeds.append(7 + M)
     # One input tensor per linear: in the block each linear reads a different activation, so nothing here
     # may reuse another linear's quantized input.
     xs = {}
@@ -535,7 +571,21 @@ def run_cfg4(k2, steps, dev, settle_s=0.0):
                 per[name] = round(time_loop(lambda: layer(xs[name]), max(3, steps // 2)), 4)
     finally:
         k2.quantize.shared_input_quant.enabled = prev
-    return {"block_linears_ms": round(ms, 4), "tops": round(total_ops / (ms * 1e-3) / 1e12, 1), "per_linear_ms": per}
+    tops = total_ops / (ms * 1e-3) / 1e12
+    K, N, Ma = CFG4_ADALN
+    adaln_ms = min(per[f"{sname}.adaln"] for sname, _ in CFG4_STREAMS)
+    adaln_gbs = (N * K + 4 * N + 2 * Ma * K + 2 * Ma * N) / (adaln_ms * 1e-3) / 1e9
+    return {"workload": "cfg4: one double-stream block's quantized linears at 1024^2, CFG batch 2 (image M=8192, "
+                        "text M=1024; qkv, out, up, down + adaLN at M=2), W8A8, LoRA r=16 on each",
+            "ms": round(ms, 4), "block_linears_ms": round(ms, 4), "tops": round(tops, 1),
+            "roofline": roofline_entry("the ten linears' launches (W8A8 GEMMs, GEMV, rotate/quant, LoRA)", "mfma",
+                                       tops, INT8_PEAK_TOPS, "TOPS"),
+            "adaln_roofline": roofline_entry("adaLN linear at M=2 (rotate/quant, LoRA down, GEMV: weight read once)",
+                                             "hbm", adaln_gbs,
+                                             HBM_PEAK_GBS, "GB/s"),
+            "per_linear_ms": per,
+            **({"cpu": cpu_cfg4([(M, K, N, *_layer_tensors(layer, sd, K, N))
+                                 for (_, layer, M, K, N), sd in zip(layers, seeds)])} if cpu else {})}
 
 
 def profile_pass(k2, dev):
@@ -659,15 +709,226 @@ def power_pass(k2, dev, seconds=4.0):
           flush=True)
 
 
+TRAFFIC_JSON = ROOT / "profiles" / "traffic_cfg2.json"
+
+
+def kernel_sources_sha() -> str:
+    """sha1 over the kernel sources (krea-2_amd/csrc): a traffic profile describes the kernels it was measured
+    on, so it is used only while the sources are the same."""
+    h = hashlib.sha1()
+    for f in sorted((ROOT / "krea-2_amd" / "csrc").glob("*")):
+        if f.suffix in (".hip", ".h"):
+            h.update(f.name.encode())
+            h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
 def measured_traffic(kernel_key: str):
     """HBM bytes per launch of a kernel from the committed rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE,
-    copy-calibrated), or None when no summary exists."""
-    path = ROOT / "profiles" / "traffic_cfg2.json"
+    copy-calibrated) and whether it applies: ``(bytes, True)`` when the summary was made from the current kernel
+    sources, ``(None, False)`` when it is stale or missing."""
     try:
-        data = json.loads(path.read_text())
-        return data["kernels"][kernel_key]["traffic_bytes"]
+        data = json.loads(TRAFFIC_JSON.read_text())
+        if data.get("kernel_sources_sha") != kernel_sources_sha():
+            return None, False
+        return data["kernels"][kernel_key]["traffic_bytes"], True
     except (OSError, KeyError, ValueError):
-        return None
+        return None, False
+
+
+# Kernels of --profile-pass: (label, kernel-name substring, grid threads, algorithmic read, algorithmic write).
+def _profiled_kernels():
+    M2, K2, N2, r2 = 16896, 3072, 12288, 32
+    M3, K3, N3, r3 = 4608, 12288, 3072, 64
+    Mi, Ki, Kh = 8192, 3072, 12288
+    Mg, Kg, Ng, rg = 4608, 6144, 15360, 16
+    copy = 1 << 28
+    return [
+        ("gemm_nt_kernel<EPI_W8> cfg2", "gemm_nt_kernel<0, 0>", 124928,
+         M2 * K2 + N2 * K2 + 4 * M2 + 4 * N2 + 4 * M2 * r2 + 4 * N2 * r2, 2 * M2 * N2),
+        ("rotquant_kernel cfg2", "rotquant_kernel", 1081344, 2 * M2 * K2, M2 * K2 + 4 * M2),
+        ("lora_down_as_kernel<2> cfg2", "lora_down_as_kernel<2>", None, 2 * M2 * K2 + 4 * r2 * K2, 3 * 4 * M2 * r2),
+        ("lora_reduce_kernel cfg2", "lora_reduce_kernel", 135168, 3 * 4 * M2 * r2, 4 * M2 * r2),
+        ("gemm_nt_kernel<EPI_DXLIN> cfg3 (input gradient)", "gemm_nt_kernel<4, 0>", 110592,
+         2 * M3 * N3 + 2 * K3 * N3 + 4 * M3 * r3 + 4 * r3 * K3, 2 * M3 * K3),
+        ("rot_dequant_t_kernel cfg3 (effective weight)", "rot_dequant_t_kernel<false>", 1179648, N3 * K3 + 4 * N3,
+         2 * K3 * N3),
+        ("prodquant_kernel<RMSMOD> cfg4 image (M=8192, K=3072)", "prodquant_kernel<1, 1, 3, false>", 524288,
+         2 * Mi * Ki, 2 * Mi * Ki + Mi * Ki + 4 * Mi),
+        ("prodquant_kernel<SWIGLU> cfg4 image (M=8192, K=12288)", "prodquant_kernel<0, 4, 3, false>", 2097152,
+         4 * Mi * Kh, 2 * Mi * Kh + Mi * Kh + 4 * Mi),
+        ("gemm_nt_kernel<EPI_W8> grouped attention inputs (M=4608)", "gemm_nt_kernel<0, 0>", 110592,
+         Mg * Kg + Ng * Kg + 4 * Mg + 4 * Ng + 4 * Mg * 4 * rg + 4 * Ng * rg, 2 * Mg * Ng),
+        ("copy 256 MiB (hipMemcpy device to device)", "copyBuffer", 131072, copy, copy),
+    ]
+
+
+def pmc_summary(fetch_dir: str, write_dir: str) -> None:
+    """Bytes per dispatch from two ``rocprofv3 --pmc FETCH_SIZE`` / ``--pmc WRITE_SIZE`` runs over
+    ``--profile-pass`` (KiB counters, median over the dispatches), each scaled by what the counter reads for the
+    pass's 256 MiB device copy; writes ``profiles/traffic_cfg2.json`` (stamped with the kernel sources' sha1)
+    and prints the markdown table."""
+    import csv
+    import statistics
+
+    def load(d):
+        out = {}
+        for f in Path(d).glob("**/*counter_collection.csv"):
+            for row in csv.DictReader(open(f)):
+                out.setdefault((row["Kernel_Name"], int(row["Grid_Size"])), []).append(float(row["Counter_Value"]))
+        return out
+
+    F_, W_ = load(fetch_dir), load(write_dir)
+
+    def find(sub, grid, d):
+        for (n, g), v in d.items():
+            if sub in n and (grid is None or g == grid):
+                return v
+        raise KeyError((sub, grid))
+
+    copy = 1 << 28
+    ff = copy / (statistics.median(find("copyBuffer", 131072, F_)) * 1024)
+    wf = copy / (statistics.median(find("copyBuffer", 131072, W_)) * 1024)
+    out = {"kernel_sources_sha": kernel_sources_sha(),
+           "calibration": {"copy_bytes": copy, "fetch_factor": ff, "write_factor": wf}, "kernels": {}}
+    lines = ["| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM read bytes | HBM write bytes | "
+             "algorithmic read / write bytes |", "|---|---|---|---|---|---|---|"]
+    for label, sub, grid, ar, aw in _profiled_kernels():
+        f, w = find(sub, grid, F_), find(sub, grid, W_)
+        fk, wk = statistics.median(f), statistics.median(w)
+        rb, wb = fk * 1024 * ff, wk * 1024 * wf
+        out["kernels"][label] = {"dispatches": len(f), "fetch_kib": fk, "write_kib": wk, "read_bytes": rb,
+                                 "write_bytes": wb, "traffic_bytes": rb + wb, "algorithmic_read": ar,
+                                 "algorithmic_write": aw}
+        lines.append(f"| {label} | {len(f)} | {fk:.0f} | {wk:.0f} | {rb / 1e6:.1f} MB | {wb / 1e6:.1f} MB | "
+                     f"{ar / 1e6:.1f} MB / {aw / 1e6:.1f} MB |")
+    TRAFFIC_JSON.write_text(json.dumps(out, indent=1) + "\n")
+    print(f"fetch factor {ff:.4f}, write factor {wf:.4f}, kernel sources {out['kernel_sources_sha']}")
+    print("\n".join(lines))
+
+
+# ----------------------------------------------------------------------------------------------------------
+# Per-config CPU paths (bounded samples, timed on this host's cores)
+# ----------------------------------------------------------------------------------------------------------
+def _median_time(fn, budget_s, min_runs=3, max_runs=30):
+    import numpy as np
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < min_runs or (time.perf_counter() < t_end and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
+
+
+def _layer_tensors(layer, seed, K, N):
+    """CPU copies of a bench layer's operands: the W8A8 codes and scales the GPU quantizer made (offline weight
+    preparation; equal to the oracle's quant_weight_i8 bit for bit, which the GPU tests check), the bf16 weight
+    (regenerated from the layer's seed, as make_layer drew it) and the LoRA factors."""
+    g = torch.Generator().manual_seed(seed)
+    W = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    return (layer.base.qweight.cpu().numpy(), layer.base.weight_scale.cpu().numpy(), W,
+            layer.lora_A.detach().cpu(), layer.lora_B.detach().cpu())
+
+
+def cpu_cfg3(qw, sw, W, A, B, rows=128, budget_s=2.0):
+    """cfg3's training step on the CPU for ``rows`` of the 4608 tokens: the oracle's forward + backward (the
+    ConvRot arithmetic) and the reference's own step restated (``Fp8Linear.forward`` + ``LoRALinear.forward``
+    under torch autograd, quantize.py:48-51, lora.py:47-48).  ms are scaled to the full M."""
+    from oracle import convrot as orc
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    c = CFG3
+    M, K, N = c["M"], c["K"], c["N"]
+    g = torch.Generator().manual_seed(33)
+    x = torch.randn(rows, K, generator=g).to(torch.bfloat16)
+    dy = (torch.randn(rows, N, generator=g) * 1e-3).to(torch.bfloat16)
+    xs, dys, An, Bn = x.float().numpy(), dy.float().numpy(), A.numpy(), B.numpy()
+
+    def oracle_step():
+        orc.forward(xs, qw, sw, lora_A=An, lora_B=Bn, lora_scale=1.0, fast=True)
+        orc.backward(dys, xs, qw, sw, lora_A=An, lora_B=Bn, lora_scale=1.0)
+
+    wq, sc = orc.fp8_weight_quant(W.float().numpy())
+    Ar, Br = A.clone().requires_grad_(True), B.clone().requires_grad_(True)
+
+    def ref_step():
+        xr = x.clone().requires_grad_(True)
+        out = torch.nn.functional.linear(xr, wq.to(torch.bfloat16) * sc.to(torch.bfloat16))
+        out = out + ((xr.to(torch.float32) @ Ar.t()) @ Br.t()).to(out.dtype)
+        out.backward(dy)
+
+    ops = 2.0 * 2.0 * M * N * K      # forward GEMM + input-gradient GEMM
+    res = {}
+    for name, fn in (("oracle", oracle_step), ("reference_fp8", ref_step)):
+        t, n = _median_time(fn, budget_s)
+        ms = t * 1e3 * M / rows
+        res[name] = {"ms": round(ms, 2), "tops": round(ops / (ms * 1e-3) / 1e12, 4), "cores": torch.get_num_threads(),
+                     "kind": "port", "sample": f"{rows} of {M} rows, forward + backward, median of {n} runs, "
+                                               "ms scaled to M"}
+    return res
+
+
+def cpu_cfg4(items, rows=128, budget_s=0.3):
+    """cfg4's ten block linears on the CPU: each linear's forward (oracle ConvRot W8A8 + LoRA r=16, and the
+    reference's Fp8Linear + LoRALinear restated) on up to ``rows`` tokens, scaled to the stream's M and summed.
+    ``items``: (M, K, N, qw, sw, W, A, B) per linear, as :func:`_layer_tensors` gives them."""
+    from oracle import convrot as orc
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    tot = {"oracle": 0.0, "reference_fp8": 0.0}
+    ops = 0.0
+    for M, K, N, qw, sw, W, A, B in items:
+        n = min(rows, M)
+        x = torch.randn(n, K, generator=torch.Generator().manual_seed(M + K)).to(torch.bfloat16)
+        xs, An, Bn = x.float().numpy(), A.numpy(), B.numpy()
+        wq, sc = orc.fp8_weight_quant(W.float().numpy())
+        t_o, _ = _median_time(lambda: orc.forward(xs, qw, sw, lora_A=An, lora_B=Bn, lora_scale=1.0, fast=True),
+                              budget_s)
+
+        def ref():
+            out = orc.fp8_linear(x, wq, sc)
+            return out + ((x.float() @ A.t()) @ B.t()).to(out.dtype)
+
+        t_r, _ = _median_time(ref, budget_s)
+        tot["oracle"] += t_o * M / n
+        tot["reference_fp8"] += t_r * M / n
+        ops += 2.0 * M * N * K
+    return {name: {"ms": round(t * 1e3, 2), "tops": round(ops / t / 1e12, 4), "cores": torch.get_num_threads(),
+                   "kind": "port",
+                   "sample": f"each linear on up to {rows} of its M rows (adaLN: both), median of >= 3 runs, "
+                             "ms scaled to M and summed"} for name, t in tot.items()}
+
+
+def roofline_entry(kernel, bound, achieved, peak, unit):
+    return {"kernel": kernel, "bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4)}
+
+
+def forward_record(cfg, res, cpu=None, cpu_ref=None):
+    """One BASELINE forward config (rotate/quant + LoRA down-projection + GEMM with the fused epilogue)."""
+    gemm_tops = res["ops"] / (res["ms_gemm"] * 1e-3) / 1e12
+    rot_gbs = res["rot_bytes"] / (res["ms_rot_stream"] * 1e-3) / 1e9
+    rec = {"workload": cfg["name"], "ms": round(res["ms_step"], 4), "tops": round(res["tops"], 1),
+           "pct_int8_peak": round(100 * res["tops"] / INT8_PEAK_TOPS, 2),
+           "gemm_ms": round(res["ms_gemm"], 4), "lora_down_ms": round(res["ms_lora"], 4),
+           "rotquant_ms_in_step": round(res["ms_rot"], 4),
+           "roofline": roofline_entry("gemm_w4_kernel" if cfg["w4"] else "gemm_nt_kernel<EPI_W8>", "mfma", gemm_tops,
+                                      INT8_PEAK_TOPS, "TOPS"),
+           "rotquant_roofline": roofline_entry("rotquant_kernel (4 inputs streamed from HBM)", "hbm", rot_gbs,
+                                               HBM_PEAK_GBS, "GB/s")}
+    rec["rotquant_roofline"]["ms"] = round(res["ms_rot_stream"], 4)
+    if cpu is not None:
+        rec["cpu"] = {"oracle": cpu, "reference_fp8": cpu_ref}
+    return rec
+
+
+_T0 = time.perf_counter()
+
+
+def progress(what: str) -> None:
+    """One line per finished leg on stderr (stdout carries only the JSON line)."""
+    print(f"[bench {time.perf_counter() - _T0:6.1f} s] {what}", file=sys.stderr, flush=True)
 
 
 def main():
@@ -679,12 +940,16 @@ def main():
                     help="seconds of untimed steps before the warmup steps, so the clocks leave their ramp-up "
                          "state (0 disables)")
     ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
-    ap.add_argument("--all", action="store_true", help="also report configs 0 and 1 (stderr)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--profile-pass", action="store_true", help="fixed launches for rocprofv3 counter runs")
     ap.add_argument("--power", action="store_true",
                     help="GEMM vs hipBLASLt int8 vs bf16 at the cfg2 shape with board power / clock samples")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="write profiles/traffic_cfg2.json from two rocprofv3 --pmc runs over --profile-pass")
     a = ap.parse_args()
+    if a.pmc_summary:
+        pmc_summary(*a.pmc_summary)
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus > 1 or world > 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (the per-token rows of the path "
@@ -705,6 +970,7 @@ def main():
         return
     cfg = CONFIGS[a.config]
     res = run_config(k2, cfg, a.steps, a.warmup, dev, a.settle)
+    progress(f"cfg{a.config} forward timed")
 
     gemm_tops = res["ops"] / (res["ms_gemm"] * 1e-3) / 1e12
     rot_gbs = res["rot_bytes"] / (res["ms_rot_stream"] * 1e-3) / 1e9
@@ -724,15 +990,37 @@ def main():
     extra["mfma_probe_int8_tops"] = round(probe, 1)
     extra["gemm_pct_of_mfma_probe"] = round(100 * gemm_tops / probe, 2)
     extra["reference_path_gpu_cfg2"] = run_reference_gpu(k2, res, max(5, a.steps // 2), dev)
-    extra["cfg3"] = run_cfg3(k2, max(5, a.steps // 2), dev, a.settle / 2)
-    extra["cfg4"] = run_cfg4(k2, max(5, a.steps // 2), dev, a.settle / 2)
+    progress("MFMA probe and the reference's GPU path timed")
+    cpu = cpu_ref = None
+    if not a.no_cpu:
+        cpu = cpu_baseline(cfg, res["x"], res["W"], res["b"], res["A"], res["B"])
+        cpu_ref = cpu_reference_path(cfg, res["x"], res["W"], res["b"], res["A"], res["B"])
+        extra["cpu_reference_fp8_path"] = cpu_ref
+        progress("CPU paths of the headline config timed")
+    # every BASELINE.json configuration: GPU time, roofline fraction, CPU paths
+    extra[f"cfg{a.config}"] = forward_record(cfg, res, cpu, cpu_ref)
+    for c in sorted(CONFIGS):
+        if c == a.config:
+            continue
+        rc = run_config(k2, CONFIGS[c], a.steps, a.warmup, dev, a.settle / 2)
+        cc = ccr = None
+        if not a.no_cpu:
+            cc = cpu_baseline(CONFIGS[c], rc["x"], rc["W"], rc["b"], rc["A"], rc["B"], budget_s=3.0, rows=512)
+            ccr = cpu_reference_path(CONFIGS[c], rc["x"], rc["W"], rc["b"], rc["A"], rc["B"], budget_s=2.0, rows=512)
+        extra[f"cfg{c}"] = forward_record(CONFIGS[c], rc, cc, ccr)
+        del rc
+        progress(f"cfg{c} timed")
+    extra["cfg3"] = run_cfg3(k2, max(5, a.steps // 2), dev, a.settle / 2, cpu=not a.no_cpu)
+    progress("cfg3 timed")
+    extra["cfg4"] = run_cfg4(k2, max(5, a.steps // 2), dev, a.settle / 2, cpu=not a.no_cpu)
+    progress("cfg4 timed")
     extra["producers_cfg4_image"] = run_producers(k2, max(5, a.steps // 2), dev)
     extra["grouped_attn_inputs"] = run_grouped(k2, max(5, a.steps // 2), dev)
     extra["krea_block_linears"] = run_krea_block(k2, max(5, a.steps // 2), dev)
-    cpu = None
-    if not a.no_cpu:
-        cpu = cpu_baseline(cfg, res["x"], res["W"], res["b"], res["A"], res["B"])
-        extra["cpu_reference_fp8_path"] = cpu_reference_path(cfg, res["x"], res["W"], res["b"], res["A"], res["B"])
+    progress("producers, grouped attention inputs and the Krea 2 block timed")
+    traffic, fresh = measured_traffic("gemm_nt_kernel<EPI_W8> cfg2") if a.config == 2 and not cfg["w4"] else (None, False)
+    extra["traffic_profile"] = ("profiles/traffic_cfg2.json, measured on these kernel sources" if fresh else
+                                "no PMC profile of these kernel sources: traffic omitted")
     line = {
         "metric": METRIC,
         "value": round(res["tops"], 2),
@@ -751,20 +1039,11 @@ def main():
                    "weights": "int4 g64" if cfg["w4"] else "int8 per-channel", "hadamard_block": 128},
         "roofline": {"bound": "mfma", "kernel": "gemm_nt_kernel<EPI_W8>" if not cfg["w4"] else "gemm_w4_kernel",
                      "achieved": round(gemm_tops, 1), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
-                     "frac": round(gemm_tops / INT8_PEAK_TOPS, 4),
-                     "traffic": measured_traffic("gemm_nt_kernel<EPI_W8> cfg2") if a.config == 2 else None},
+                     "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": traffic},
         "cpu_baseline": cpu,
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
-    if a.all:
-        for c in (0, 1):
-            if c == a.config:
-                continue
-            r2 = run_config(k2, CONFIGS[c], a.steps, a.warmup, dev, a.settle / 2)
-            print(json.dumps({"config": CONFIGS[c]["name"], "ms_step": round(r2["ms_step"], 4),
-                              "tops": round(r2["tops"], 1), "gemm_ms": round(r2["ms_gemm"], 4),
-                              "rotquant_ms": round(r2["ms_rot_stream"], 4)}), file=sys.stderr, flush=True)
 
 
 if __name__ == "__main__":
