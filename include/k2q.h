@@ -32,6 +32,7 @@ extern "C" {
 #define K2Q_EARCH (-2)       /* current device is not gfx950 */
 #define K2Q_ELAUNCH (-3)     /* kernel launch reported an error */
 #define K2Q_EUNSUPPORTED (-4)/* shape outside what the kernels implement (e.g. K too large) */
+#define K2Q_ESCRATCH (-5)    /* the shape needs more than the library's K2Q_SCRATCH_BYTES of device scratch */
 
 #define K2Q_MAX_RANK 4096    /* largest LoRA rank any entry point takes */
 
@@ -94,6 +95,18 @@ int64_t k2q_lora_grads_ws_bytes(int64_t M, int64_t N, int64_t K, int64_t r);
 int k2q_lora_grads(const uint16_t* dy, const uint16_t* x, const float* u, const float* lora_b, int64_t r,
                    float scale, int64_t M, int64_t N, int64_t K, float* g, float* dA, float* dB, void* ws,
                    int64_t ws_bytes, void* stream);
+
+/* k2q_lora_grads without a workspace argument; allocates nothing.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving or training loops,
+ * harnesses that forbid it).  The workspace comes from a device array inside the library, K2Q_SCRATCH_BYTES per
+ * GPU, held until the process ends; a shape whose k2q_lora_grads_ws_bytes exceeds it returns K2Q_ESCRATCH
+ * before any launch (cfg3's M = 4608, N = 3072, K = 12288, r = 64 needs ~38 MB).  Every call on one GPU shares
+ * that GPU's scratch: calls that overlap on one GPU (two streams, two threads) race.  Results are bit-identical
+ * to k2q_lora_grads. */
+#define K2Q_SCRATCH_BYTES ((int64_t)64 << 20)
+int k2q_lora_grads_noalloc(const uint16_t* dy, const uint16_t* x, const float* u, const float* lora_b, int64_t r,
+                           float scale, int64_t M, int64_t N, int64_t K, float* g, float* dA, float* dB,
+                           void* stream);
 
 /* (2)+(3) W8A8 GEMM with the fused epilogue, replacing F.linear(x, W_deq, b) of quantize.py:49-51 and
  * the LoRA add of lora.py:47-48:

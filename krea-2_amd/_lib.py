@@ -18,7 +18,8 @@ LIB_PATH = Path(__file__).resolve().parent / "libk2q.so"
 
 K2Q_OK = 0
 _STATUS = {-1: "K2Q_EINVAL (bad shape, null or misaligned pointer)", -2: "K2Q_EARCH (device is not gfx950)",
-           -3: "K2Q_ELAUNCH (kernel launch failed)", -4: "K2Q_EUNSUPPORTED (shape outside the kernels)"}
+           -3: "K2Q_ELAUNCH (kernel launch failed)", -4: "K2Q_EUNSUPPORTED (shape outside the kernels)",
+           -5: "K2Q_ESCRATCH (the shape needs more device scratch than the library holds)"}
 DTYPE_BF16 = 0
 DTYPE_F32 = 1
 HADAMARD_BLOCK = 128
@@ -55,6 +56,7 @@ _SIGNATURES = {
     "k2q_lora_down": ([_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _p], _int),
     "k2q_lora_grads_ws_bytes": ([_i64, _i64, _i64, _i64], _i64),
     "k2q_lora_grads": ([_p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p], _int),
+    "k2q_lora_grads_noalloc": ([_p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p, _p, _p], _int),
     "k2q_gemm_w8a8_ws_bytes": ([_i64, _i64, _i64], _i64),
     "k2q_gemm_w8a8": ([_p, _p, _p, _p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p, _i64, _p], _int),
     "k2q_gemm_w8a8_grouped": ([_p, _p, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _i64, _p], _int),
@@ -380,6 +382,53 @@ def lora_grads(dy, x, u, lora_b, lora_scale: float):
     _check(lib.k2q_lora_grads(_ptr(dy), _ptr(x), _ptr(u), _ptr(lora_b), r, float(lora_scale), M, N, K, _ptr(g),
                               _ptr(dA), _ptr(dB), _ptr(ws), nws, _stream(dev)), "k2q_lora_grads")
     return g, dA, dB
+
+
+SCRATCH_BYTES = 64 << 20     # K2Q_SCRATCH_BYTES: the library's own device scratch per GPU
+
+
+def lora_grads_noalloc(dy, x, u, lora_b, lora_scale: float, g, dA=None, dB=None) -> None:
+    """:func:`lora_grads` into caller-provided outputs with nothing allocated, by the library or here: the
+    workspace is the library's device scratch (``SCRATCH_BYTES`` per GPU, shared by every call on that GPU, so
+    calls that overlap on one GPU race).  ``g`` (M,r), ``dA`` (r,K) and ``dB`` (N,r) f32 contiguous, the last two
+    optional (with ``x`` / ``u``).  Raises before any launch when the shape needs more scratch than that."""
+    _need(dy, "dy", torch.bfloat16, 2)
+    dev = dy.device
+    M, N = dy.shape
+    _need(lora_b, "lora_B", torch.float32, 2, dev)
+    r = lora_b.shape[1]
+    if lora_b.shape[0] != N:
+        raise ValueError(f"lora_B has {lora_b.shape[0]} rows, dy has {N} columns")
+    _check_rank(r)
+    if N % HADAMARD_BLOCK:
+        raise ValueError(f"out_features={N} must be a multiple of {HADAMARD_BLOCK} for the LoRA gradients")
+    _need(g, "g", torch.float32, 2, dev)
+    if g.shape != (M, r):
+        raise ValueError(f"g must be {(M, r)}, got {tuple(g.shape)}")
+    K = HADAMARD_BLOCK
+    if (x is None) != (dA is None):
+        raise ValueError("x and dA go together")
+    if (u is None) != (dB is None):
+        raise ValueError("u and dB go together")
+    if x is not None:
+        _need(x, "x", torch.bfloat16, 2, dev)
+        K = x.shape[1]
+        _check_k(K)
+        _need(dA, "dA", torch.float32, 2, dev)
+        if x.shape[0] != M or dA.shape != (r, K):
+            raise ValueError("x / dA shapes do not match dy and the rank")
+    if u is not None:
+        _need(u, "u", torch.float32, 2, dev)
+        _need(dB, "dB", torch.float32, 2, dev)
+        if u.shape != (M, r) or dB.shape != (N, r):
+            raise ValueError("u / dB shapes do not match dy and the rank")
+    need = load().k2q_lora_grads_ws_bytes(M, N, K, r)
+    if need > SCRATCH_BYTES:
+        raise ValueError(f"the LoRA gradients of M={M}, N={N}, K={K}, r={r} need {need} bytes of workspace, more than "
+                         f"the library's {SCRATCH_BYTES}-byte scratch: use lora_grads")
+    _device_check(dev)
+    _check(load().k2q_lora_grads_noalloc(_ptr(dy), _ptr(x), _ptr(u), _ptr(lora_b), r, float(lora_scale), M, N, K,
+                                         _ptr(g), _ptr(dA), _ptr(dB), _stream(dev)), "k2q_lora_grads_noalloc")
 
 
 # ----------------------------------------------------------------------------------------------------------

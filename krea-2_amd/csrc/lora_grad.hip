@@ -13,6 +13,8 @@
 // through a transposing split first (R x M rows of hi and lo) and reaches LDS the same way.  Each workgroup
 // owns 256 columns and one slice of M; the slices' partials are added in slice order by a second kernel
 // (deterministic).
+#include <mutex>
+
 #include "k2q_common.h"
 
 namespace {
@@ -335,4 +337,44 @@ extern "C" int k2q_lora_grads(const uint16_t* dy, const uint16_t* x, const float
             reinterpret_cast<float*>(w + L.part_b), dB + c0);
   }
   return k2q_launch_status();
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// k2q_lora_grads_noalloc: the same gradients with the workspace taken from the library's own device scratch,
+// for callers that cannot allocate.  The scratch is a file-scope device array (one copy per GPU, resident until
+// the process ends); host code reaches it only through the per-device address hipGetSymbolAddress returns.
+// Nothing in it needs to start at zero (the transposes zero their own padding, every partial is written before
+// it is read).  All calls on one GPU share it: calls that overlap on one GPU race.
+static __device__ __align__(256) uint8_t scratch[K2Q_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_mu;
+void* scratch_ptr[MAX_DEVICES];
+
+// The current device's address of `scratch`, looked up once per device (with that device current).
+void* scratch_for_current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return nullptr;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    scratch_ptr[dev] = ptr;
+  }
+  return scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" int k2q_lora_grads_noalloc(const uint16_t* dy, const uint16_t* x, const float* u, const float* lora_b,
+                                      int64_t r, float scale, int64_t M, int64_t N, int64_t K, float* g, float* dA,
+                                      float* dB, void* stream) {
+  if (!grad_shape_ok(M, N, K, r)) return K2Q_EINVAL;
+  const int64_t need = grad_layout(M, N, K, r).total;
+  if (need > K2Q_SCRATCH_BYTES) return K2Q_ESCRATCH;
+  void* ws = scratch_for_current_device();
+  if (!ws) return K2Q_ELAUNCH;
+  return k2q_lora_grads(dy, x, u, lora_b, r, scale, M, N, K, g, dA, dB, ws, need, stream);
 }
