@@ -169,19 +169,42 @@ def cpu_reference_path(cfg, x, W, b, A, B, budget_s=6.0, rows=2048):
             "sample": f"{rows} of {cfg['M']} rows, median of {len(times)} runs ({t * 1e3:.0f} ms each)"}
 
 
+PROBE_LIB = ROOT / "krea-2_amd" / "libk2q_probe.so"
+_probe = {}
+
+
+def mfma_probe_i8(iters: int, workgroups: int, dev) -> int:
+    """Launches the register-only int8 MFMA loop of ``libk2q_probe.so`` (krea-2_amd/csrc/probe.hip, a measurement
+    aid built beside the product library) on the current stream; returns the int8 operations it performs."""
+    import ctypes
+    if "lib" not in _probe:
+        lib = ctypes.CDLL(str(PROBE_LIB))
+        lib.k2q_mfma_probe_i8_ops.argtypes, lib.k2q_mfma_probe_i8_ops.restype = [ctypes.c_int64] * 2, ctypes.c_int64
+        lib.k2q_mfma_probe_i8.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
+        lib.k2q_mfma_probe_i8.restype = ctypes.c_int
+        _probe["lib"] = lib
+    lib = _probe["lib"]
+    out = _probe.get(dev)
+    if out is None or out.numel() < workgroups * 512:
+        out = _probe[dev] = torch.empty(workgroups * 512, dtype=torch.int32, device=dev)
+    rc = lib.k2q_mfma_probe_i8(iters, workgroups, out.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
+    if rc != 0:
+        raise RuntimeError(f"k2q_mfma_probe_i8 failed with status {rc}")
+    return lib.k2q_mfma_probe_i8_ops(iters, workgroups)
+
+
 def mfma_probe(k2, dev, seconds=1.0):
     """Sustained int8 MFMA rate of this board in this run (register-only v_mfma_i32_32x32x32_i8 loop, two
     waves per SIMD on every CU, pseudo-random operands): the same-run ceiling the GEMM is compared with."""
-    L = k2._lib
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     iters = 2000
-    settle(lambda: L.mfma_probe_i8(iters, cus, dev), 0.5)
+    settle(lambda: mfma_probe_i8(iters, cus, dev), 0.5)
     s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ops, n, t_end = 0, 0, time.perf_counter() + seconds
     s_ev.record()
     while time.perf_counter() < t_end:
         for _ in range(4):
-            ops += L.mfma_probe_i8(iters, cus, dev)
+            ops += mfma_probe_i8(iters, cus, dev)
         n += 4
         torch.cuda.synchronize()
     e_ev.record()

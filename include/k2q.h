@@ -141,6 +141,22 @@ int k2q_gemm_w8a8_grouped(const int8_t* qx, const float* sx, int64_t M, int64_t 
                           int64_t nseg, const float* u, int64_t r, int64_t ldu, void* ws, int64_t ws_bytes,
                           void* stream);
 
+/* One quantized linear + LoRA forward in one call: Fp8Linear.forward + the adapter add of LoRALinear.forward
+ * (quantize.py:48-51, lora.py:43-48) with the ConvRot arithmetic, i.e. the launches of k2q_rotquant (skipped when
+ * codes_ready: qx / sx already hold x's codes, e.g. from a producer kernel), k2q_lora_down (when lora_a) and
+ * k2q_gemm_w8a8 / k2q_gemm_w4a8 issued from one call.  wmode K2Q_WMODE_W8: qw int8 N x K, sw f32 N;
+ * K2Q_WMODE_W4: qw packed int4 N x K/2, sw bf16 K/64 x N.  x: M rows of ldx bf16; qx (M x K int8), sx (M f32)
+ * and u (M x r f32, the LoRA factors the backward reuses) are caller buffers the call fills; y M x N bf16.
+ * M <= 8: one launch computes the codes and u, then the GEMV (two launches for the linear).
+ * ws: k2q_linear_fwd_ws_bytes bytes, used by the down-projection and the GEMM one after the other. */
+#define K2Q_WMODE_W8 0
+#define K2Q_WMODE_W4 1
+int64_t k2q_linear_fwd_ws_bytes(int wmode, int64_t M, int64_t N, int64_t K, int64_t r);
+int k2q_linear_fwd(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, int8_t* qx, float* sx, int codes_ready,
+                   const float* lora_a, const float* lora_b, int64_t r, float lora_scale, float* u, int wmode,
+                   const void* qw, const void* sw, const float* bias, int64_t N, uint16_t* y, void* ws,
+                   int64_t ws_bytes, void* stream);
+
 /* W4A8 variant: per-group int32 partials scaled by the bf16 group scales. */
 int k2q_gemm_w4a8(const int8_t* qx, const float* sx, const uint8_t* qw4, const uint16_t* sw4,
                   const float* bias, const float* u, const float* lora_b, int64_t r, float lora_scale,
@@ -191,11 +207,6 @@ int k2q_gemm_bf16(const uint16_t* x, const uint16_t* w, const float* bias, const
 int k2q_gemm_dx_lin(const uint16_t* dy, const uint16_t* wt, int64_t M, int64_t N, int64_t K, const float* g,
                     const float* lora_a, int64_t r, uint16_t* dx, void* ws, int64_t ws_bytes, void* stream);
 
-/* Same-run MFMA ceiling (no counterpart in the reference; a measurement aid for bench.py): a loop of
- * iters x 64 v_mfma_i32_32x32x32_i8 per wave, 8 waves per workgroup, register operands only.
- * k2q_mfma_probe_i8_ops gives the int8 operations one launch performs; out holds workgroups*512 int32. */
-int64_t k2q_mfma_probe_i8_ops(int64_t iters, int64_t workgroups);
-int k2q_mfma_probe_i8(int64_t iters, int64_t workgroups, int32_t* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -61,6 +61,9 @@ _SIGNATURES = {
     "k2q_gemm_w8a8": ([_p, _p, _p, _p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p, _i64, _p], _int),
     "k2q_gemm_w8a8_grouped": ([_p, _p, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _i64, _p], _int),
     "k2q_gemm_w4a8": ([_p, _p, _p, _p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p], _int),
+    "k2q_linear_fwd_ws_bytes": ([_int, _i64, _i64, _i64, _i64], _i64),
+    "k2q_linear_fwd": ([_p, _i64, _i64, _i64, _p, _p, _int, _p, _p, _i64, _f32, _p, _int, _p, _p, _p, _i64, _p, _p,
+                        _i64, _p], _int),
     "k2q_gemm_w8a8_acc": ([_p, _p, _i64, _i64, _i64, _p, _p, _i64, _p], _int),
     "k2q_gemm_w4a8_f32": ([_p, _p, _p, _i64, _i64, _i64, _p, _p], _int),
     "k2q_quant_weight_fp8": ([_p, _int, _i64, _i64, _p, _p, _p], _int),
@@ -68,8 +71,6 @@ _SIGNATURES = {
     "k2q_gemm_bf16_ws_bytes": ([_i64, _i64, _i64], _i64),
     "k2q_gemm_bf16": ([_p, _p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p, _i64, _p], _int),
     "k2q_gemm_dx_lin": ([_p, _p, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _p], _int),
-    "k2q_mfma_probe_i8_ops": ([_i64, _i64], _i64),
-    "k2q_mfma_probe_i8": ([_i64, _i64, _p, _p], _int),
     "k2q_dx_prep": ([_p, _p, _p, _p, _i64, _i64, _p, _p], _int),
     "k2q_dx_prep_eff": ([_p, _p, _p, _p, _i64, _i64, _p, _p], _int),
     "k2q_gemm_dx_ws_bytes": ([_i64, _i64, _i64], _i64),
@@ -482,6 +483,42 @@ def gemm_w8a8(qx, sx, qw, sw, bias=None, u=None, lora_b=None, lora_scale: float 
     return y
 
 
+WMODE_W8, WMODE_W4 = 0, 1
+
+
+def linear_fwd(x2, qx, sx, codes_ready: bool, A, B, lora_scale: float, qw, sw, bias, w4: bool):
+    """One quantized linear + LoRA forward in one library call (``k2q_linear_fwd``): rotate/quant of ``x2`` into
+    ``qx`` / ``sx`` (unless ``codes_ready``), ``u = x2 A^T`` (when ``A``), the GEMM with the fused epilogue.
+    Returns ``(y, u | None)``.  The module's per-call entry: the weights and factors come from the module (their
+    shapes fixed when it was built), so only the relations a foreign call needs are checked here, cheaply; the
+    library checks pointers and alignment again.  ``x2`` (M,K) bf16 rows of stride ``x2.stride(0)``."""
+    M, K = x2.shape
+    N = qw.shape[0]
+    dev = x2.device
+    if x2.dtype != torch.bfloat16 or x2.stride(1) != 1 or qw.device != dev or qx.shape != (M, K) or sx.shape != (M,):
+        raise ValueError("linear_fwd: x / code buffers do not match the layer")
+    r = 0
+    if A is not None:
+        r = A.shape[0]
+        if A.shape != (r, K) or B.shape != (N, r) or A.dtype != torch.float32 or B.dtype != torch.float32 \
+                or A.device != dev or not (A.is_contiguous() and B.is_contiguous()):
+            raise ValueError("linear_fwd: LoRA factors do not match the layer")
+        _check_rank(r)
+    if bias is not None and (bias.shape != (N,) or bias.dtype != torch.float32 or bias.device != dev):
+        raise ValueError("linear_fwd: bias does not match the layer")
+    _device_check(dev)
+    lib = load()
+    wmode = WMODE_W4 if w4 else WMODE_W8
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    u = torch.empty((M, r), dtype=torch.float32, device=dev) if r else None
+    nws = lib.k2q_linear_fwd_ws_bytes(wmode, M, N, K, r)
+    ws = torch.empty((nws,), dtype=torch.uint8, device=dev) if nws > 0 else None
+    _check(lib.k2q_linear_fwd(x2.data_ptr(), x2.stride(0), M, K, qx.data_ptr(), sx.data_ptr(), int(codes_ready),
+                              _ptr(A), _ptr(B), r, float(lora_scale), _ptr(u), wmode, qw.data_ptr(), sw.data_ptr(),
+                              _ptr(bias), N, y.data_ptr(), _ptr(ws), nws, _stream(dev)), "k2q_linear_fwd")
+    return y, u
+
+
 def gemm_w8a8_grouped(qx, sx, segments, u=None):
     """Several W8A8 linears that read the same codes in one launch.  ``segments``: sequence of
     ``(q_w, s_w, bias, lora_b, u_col, lora_scale)`` (bias, lora_b nullable; a segment with ``lora_b`` uses
@@ -774,23 +811,3 @@ def gemm_dx_fp8(dy, q, s, *, g=None, lora_a=None, split: bool = True) -> torch.T
     _check(lib.k2q_gemm_dx_lin(_ptr(dy), _ptr(wt), M, N, K, _ptr(g), _ptr(lora_a) if r else None, r, _ptr(dx),
                                _ptr(ws), nws, st), "k2q_gemm_dx_lin")
     return dx
-
-
-# ----------------------------------------------------------------------------------------------------------
-# Measurement aid
-# ----------------------------------------------------------------------------------------------------------
-def mfma_probe_i8(iters: int, workgroups: int, dev=None) -> int:
-    """Launches the register-only int8 MFMA loop on the current stream; returns the int8 operations it
-    performs (time it with events around the call)."""
-    dev = torch.device("cuda", torch.cuda.current_device()) if dev is None else dev
-    _device_check(dev)
-    lib = load()
-    out = _probe_out.get(dev)
-    if out is None or out.numel() < workgroups * 512:
-        out = torch.empty(workgroups * 512, dtype=torch.int32, device=dev)
-        _probe_out[dev] = out
-    _check(lib.k2q_mfma_probe_i8(iters, workgroups, _ptr(out), _stream(dev)), "k2q_mfma_probe_i8")
-    return lib.k2q_mfma_probe_i8_ops(iters, workgroups)
-
-
-_probe_out: dict = {}

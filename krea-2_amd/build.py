@@ -15,7 +15,11 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 INCLUDE = HERE.parent / "include"
 LIB = HERE / "libk2q.so"
-SOURCES = ("api.hip", "rotquant.hip", "producers.hip", "gemm.hip", "gemv.hip", "lora.hip", "lora_grad.hip", "fp8.hip", "probe.hip")
+SOURCES = ("api.hip", "rotquant.hip", "producers.hip", "gemm.hip", "gemv.hip", "lora.hip", "lora_grad.hip", "fp8.hip",
+           "linear.hip")
+# bench.py's same-run MFMA ceiling: a measurement aid, built into its own library, not into the product's
+PROBE_SOURCES = ("probe.hip",)
+PROBE_LIB = HERE / "libk2q_probe.so"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -35,21 +39,28 @@ def _compile(src: Path, obj: Path) -> None:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{r.stderr}")
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every kernel source for gfx950 and link ``libk2q.so``.  Always recompiles."""
-    objdir = HERE / "_build"
-    objdir.mkdir(exist_ok=True)
-    objs = [objdir / (Path(s).stem + ".o") for s in SOURCES]
-    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as ex:
-        list(ex.map(lambda so: _compile(CSRC / so[0], so[1]), zip(SOURCES, objs)))
-    tmp = LIB.with_suffix(".so.tmp")
+def _link(objs, lib: Path) -> None:
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, LIB)
+        raise RuntimeError(f"link of {lib.name} failed:\n{r.stderr}")
+    os.replace(tmp, lib)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every kernel source for gfx950 and link ``libk2q.so`` (and bench.py's ``libk2q_probe.so``).
+    Always recompiles."""
+    objdir = HERE / "_build"
+    objdir.mkdir(exist_ok=True)
+    srcs = SOURCES + PROBE_SOURCES
+    objs = {s: objdir / (Path(s).stem + ".o") for s in srcs}
+    with cf.ThreadPoolExecutor(max_workers=min(len(srcs), os.cpu_count() or 1)) as ex:
+        list(ex.map(lambda s: _compile(CSRC / s, objs[s]), srcs))
+    _link([objs[s] for s in SOURCES], LIB)
+    _link([objs[s] for s in PROBE_SOURCES], PROBE_LIB)
     if verbose:
-        print(f"built {LIB} ({LIB.stat().st_size} bytes)")
+        print(f"built {LIB} ({LIB.stat().st_size} bytes) and {PROBE_LIB.name}")
     return LIB
 
 

@@ -1,0 +1,161 @@
+// One quantized linear + LoRA forward per call: the C counterpart of Fp8Linear.forward followed by the adapter
+// add of LoRALinear.forward (reference quantize.py:48-51, lora.py:43-48), with the ConvRot arithmetic of the
+// other kernels.  The launches that make it up (rotate/quant, LoRA down-projection, GEMM with its epilogue) are
+// issued from here, so a caller pays one foreign call per linear.
+//
+// Skinny M (M <= K2Q_GEMV_MAX_M: the adaLN modulation linears run at M = batch) has one more fusion: a prologue
+// kernel computes a row's int8 codes and its LoRA factors u = x A^T in one launch (one workgroup per row), and
+// the GEMV follows, so the linear is two launches.  Its codes are bit-identical to k2q_rotquant (same butterfly
+// per 128-block, same quantizer); u is an f32 dot product per rank in a fixed order (x is bf16, so every product
+// is exact in f32; the sums differ from the MFMA down-projection only by f32 rounding).
+#include "rotation.h"
+
+namespace {
+
+using namespace k2q_rot;
+
+constexpr int SK_T = 256;       // lanes per row (four waves)
+constexpr int SK_CW = SK_T * 16;   // elements per chunk
+constexpr int SK_JB = 16;       // ranks per reduction batch
+
+// Row blockIdx.x of x: u[row, :] = x[row, :] A^T (when a != nullptr), then (when q != nullptr) the codes and scale
+// of the rotated row.  kNCH chunks of 4096 elements cover K.
+template <int kNCH>
+__global__ __launch_bounds__(SK_T) void skinny_prologue_kernel(const __bf16* __restrict__ x, int64_t ldx, int K,
+                                                               const float* __restrict__ a, int r,
+                                                               float* __restrict__ u, int8_t* __restrict__ q,
+                                                               float* __restrict__ s) {
+  __shared__ float red[4][SK_JB];
+  __shared__ float smax[4];
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const int64_t row = blockIdx.x;
+  const int off = lane_offset(t);
+  const __bf16* xr = x + row * ldx;
+  float v[kNCH][16];
+#pragma unroll
+  for (int c = 0; c < kNCH; ++c) {
+    const int col = c * SK_CW + off;
+    load16<__bf16>(xr + col, col < K, v[c]);
+  }
+
+  if (a) {
+    for (int j0 = 0; j0 < r; j0 += SK_JB) {
+      float p[SK_JB];
+#pragma unroll
+      for (int j = 0; j < SK_JB; ++j) p[j] = 0.f;
+#pragma unroll
+      for (int c = 0; c < kNCH; ++c) {
+        const int col = c * SK_CW + off;
+        if (col >= K) continue;
+#pragma unroll
+        for (int j = 0; j < SK_JB; ++j) {
+          const float4* ap = reinterpret_cast<const float4*>(a + (int64_t)(j0 + j) * K + col);
+#pragma unroll
+          for (int e4 = 0; e4 < 4; ++e4) {
+            const float4 w = ap[e4];
+            p[j] = __builtin_fmaf(v[c][4 * e4], w.x, p[j]);
+            p[j] = __builtin_fmaf(v[c][4 * e4 + 1], w.y, p[j]);
+            p[j] = __builtin_fmaf(v[c][4 * e4 + 2], w.z, p[j]);
+            p[j] = __builtin_fmaf(v[c][4 * e4 + 3], w.w, p[j]);
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < SK_JB; ++j) p[j] = wave_sum(p[j]);
+      if (lane == 0) {
+#pragma unroll
+        for (int j = 0; j < SK_JB; ++j) red[wave][j] = p[j];
+      }
+      __syncthreads();
+      if (t < SK_JB) u[row * r + j0 + t] = ((red[0][t] + red[1][t]) + red[2][t]) + red[3][t];
+      __syncthreads();
+    }
+  }
+  if (!q) return;
+
+  const int l = t & 15;
+  const float c1 = (l & 1) ? -1.f : 1.f;
+  const float c2 = (l & 2) ? -1.f : 1.f;
+  const float c8 = (l & 8) ? -1.f : 1.f;
+  const float sigma = c1 * c2 * c8;
+  float amax = 0.f;
+#pragma unroll
+  for (int c = 0; c < kNCH; ++c) {
+    rotate16(v[c], c1, c2, c8);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[c][i]));
+  }
+  amax = wave_max(amax);
+  if (lane == 0) smax[wave] = amax;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < 4; ++w) amax = fmaxf(amax, smax[w]);
+  amax = fmaxf(amax, 1e-8f);
+  const float inv = __fdiv_rn(127.f, amax);
+  if (t == 0) s[row] = __fdiv_rn(amax, 127.f);
+  const float mul = inv * sigma;
+  int8_t* qr = q + row * (int64_t)K;
+#pragma unroll
+  for (int c = 0; c < kNCH; ++c) {
+    const int col = c * SK_CW + off;
+    if (col < K) store_codes16(qr + col, v[c], mul);
+  }
+}
+
+int launch_skinny(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, const float* a, int64_t r, float* u, int8_t* q,
+                  float* s, hipStream_t st) {
+  const __bf16* xp = reinterpret_cast<const __bf16*>(x);
+  const int nch = (int)((K + SK_CW - 1) / SK_CW);
+  const dim3 grid((unsigned)M);
+  switch (nch) {
+    case 1: hipLaunchKernelGGL(skinny_prologue_kernel<1>, grid, dim3(SK_T), 0, st, xp, ldx, (int)K, a, (int)r, u, q, s); break;
+    case 2: hipLaunchKernelGGL(skinny_prologue_kernel<2>, grid, dim3(SK_T), 0, st, xp, ldx, (int)K, a, (int)r, u, q, s); break;
+    case 3: hipLaunchKernelGGL(skinny_prologue_kernel<3>, grid, dim3(SK_T), 0, st, xp, ldx, (int)K, a, (int)r, u, q, s); break;
+    case 4: hipLaunchKernelGGL(skinny_prologue_kernel<4>, grid, dim3(SK_T), 0, st, xp, ldx, (int)K, a, (int)r, u, q, s); break;
+    default: return K2Q_EUNSUPPORTED;
+  }
+  return k2q_launch_status();
+}
+
+}  // namespace
+
+extern "C" int64_t k2q_linear_fwd_ws_bytes(int wmode, int64_t M, int64_t N, int64_t K, int64_t r) {
+  if (M < 1 || N < 1 || K < K2Q_HADAMARD || K % K2Q_HADAMARD) return 0;
+  int64_t b = 0;
+  if (r > 0 && M > K2Q_GEMV_MAX_M) b = k2q_lora_down_ws_bytes(M, K, r);
+  if (wmode == K2Q_WMODE_W8) {
+    const int64_t g = k2q_gemm_w8a8_ws_bytes(M, N, K);
+    b = g > b ? g : b;
+  }
+  return b;
+}
+
+extern "C" int k2q_linear_fwd(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, int8_t* qx, float* sx,
+                              int codes_ready, const float* lora_a, const float* lora_b, int64_t r, float lora_scale,
+                              float* u, int wmode, const void* qw, const void* sw, const float* bias, int64_t N,
+                              uint16_t* y, void* ws, int64_t ws_bytes, void* stream) {
+  if (!x || !qx || !sx || !qw || !sw || !y || M < 1 || N < 1 || K < K2Q_HADAMARD || K % K2Q_HADAMARD) return K2Q_EINVAL;
+  if (K > 16384) return K2Q_EUNSUPPORTED;
+  if (ldx < K || ldx % 8 || !k2q_aligned(x, 16) || !k2q_aligned(qx, 16)) return K2Q_EINVAL;
+  if (wmode != K2Q_WMODE_W8 && wmode != K2Q_WMODE_W4) return K2Q_EINVAL;
+  if (lora_a && (!lora_b || !u || r < 16 || r > K2Q_MAX_RANK || r % 16 || !k2q_aligned(lora_a, 16) ||
+                 !k2q_aligned(u, 16)))
+    return K2Q_EINVAL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t rr = lora_a ? r : 0;
+  int rc = K2Q_OK;
+  if (M <= K2Q_GEMV_MAX_M) {
+    if (lora_a || !codes_ready)
+      rc = launch_skinny(x, ldx, M, K, lora_a, rr, u, codes_ready ? nullptr : qx, sx, st);
+  } else {
+    if (!codes_ready) rc = k2q_rotquant(x, K2Q_DTYPE_BF16, M, K, ldx, qx, sx, nullptr, stream);
+    if (!rc && lora_a) rc = lora_down_impl(x, M, K, ldx, lora_a, 1, 1.f, rr, ws, ws_bytes, u, st);
+  }
+  if (rc) return rc;
+  const float* uu = lora_a ? u : nullptr;
+  if (wmode == K2Q_WMODE_W8)
+    return k2q_gemm_w8a8(qx, sx, static_cast<const int8_t*>(qw), static_cast<const float*>(sw), bias, uu,
+                         lora_a ? lora_b : nullptr, rr, lora_scale, M, N, K, y, ws, ws_bytes, stream);
+  return k2q_gemm_w4a8(qx, sx, static_cast<const uint8_t*>(qw), static_cast<const uint16_t*>(sw), bias, uu,
+                       lora_a ? lora_b : nullptr, rr, lora_scale, M, N, K, y, stream);
+}

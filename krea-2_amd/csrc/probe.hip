@@ -3,6 +3,12 @@
 // pseudo-random int8 codes and cycles through all 64 pairs, so consecutive MFMAs see different operands
 // (the chip's power, and with it the clock, depends on how many operand bits toggle).  The number it gives
 // is the int8 MFMA rate this board sustains in the current run, for comparison with the GEMM.
+//
+// A measurement aid of bench.py, built into its own library (libk2q_probe.so), not part of the product's
+// C ABI (libk2q.so, include/k2q.h).  bench.py binds the two entry points with ctypes:
+//   int64_t k2q_mfma_probe_i8_ops(int64_t iters, int64_t workgroups)   int8 operations of one launch
+//   int k2q_mfma_probe_i8(int64_t iters, int64_t workgroups, int32_t* out, void* stream)
+//     iters x 64 MFMAs per wave, 8 waves per workgroup; out holds workgroups * 512 int32 checksums.
 #include "k2q_common.h"
 
 namespace {

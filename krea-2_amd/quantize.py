@@ -58,6 +58,19 @@ class _SharedInputQuant:
             self.ref, self.key, self.val = weakref.ref(x), key, (qx, sx)
         return qx, sx
 
+    def find(self, x: torch.Tensor):
+        """``(key, codes)``: the codes kept for exactly this tensor, or None; the key goes back to :meth:`keep`."""
+        key = self._key(x)
+        if self.enabled and self.ref is not None and self.ref() is x and self.key == key:
+            return key, self.val
+        self.misses += 1
+        return key, None
+
+    def keep(self, x: torch.Tensor, key, qx: torch.Tensor, sx: torch.Tensor) -> None:
+        """Record the codes a fused forward wrote for ``x`` (``key`` from :meth:`find`, taken before that call)."""
+        if self.enabled:
+            self.ref, self.key, self.val = weakref.ref(x), key, (qx, sx)
+
     def seed(self, x: torch.Tensor, qx: torch.Tensor, sx: torch.Tensor) -> None:
         """Record codes a producer-fused kernel computed for ``x`` (exactly those ``rotquant`` gives), so the
         ConvRot layers that receive ``x`` next skip their own rotate/quant."""
@@ -77,16 +90,15 @@ def _check_out_features(N: int) -> None:
 
 
 class _ConvRotLinearFn(torch.autograd.Function):
-    """Forward: rotate+quantize x, optional LoRA down-projection, fused GEMM + epilogue.
+    """Forward: one library call (``k2q_linear_fwd``): rotate+quantize x (unless its codes are given), LoRA
+    down-projection, fused GEMM + epilogue.
     Backward (straight-through over both quantizers): ``dX = 2^-7 (dY W_hat) R + g A`` with
     ``g = s dY B``; ``dA = g^T x``, ``dB = s dY^T u`` — the autograd of ``lora.py:47-48`` through a frozen base.
     Deterministic (no atomics, fixed reduction order), so checkpoint recompute reproduces the forward."""
 
     @staticmethod
-    def forward(ctx, x2, lora_A, lora_B, qweight, wscale, bias, w4, lora_scale, qx, sx, owner):
-        u = _lib.lora_down(x2, lora_A) if lora_A is not None else None
-        gemm = _lib.gemm_w4a8 if w4 else _lib.gemm_w8a8
-        y = gemm(qx, sx, qweight, wscale, bias, u, lora_B, lora_scale)
+    def forward(ctx, x2, lora_A, lora_B, qweight, wscale, bias, w4, lora_scale, qx, sx, codes_ready, owner):
+        y, u = _lib.linear_fwd(x2, qx, sx, codes_ready, lora_A, lora_B, lora_scale, qweight, wscale, bias, w4)
         ctx.w4 = w4
         ctx.lora_scale = lora_scale
         ctx.owner = owner
@@ -107,7 +119,7 @@ class _ConvRotLinearFn(torch.autograd.Function):
         if ctx.needs_input_grad[0]:
             dx = _lib.gemm_dx(dy, qweight, wscale, w4=ctx.w4, g=g, lora_a=A if g is not None else None,
                               wt=ctx.owner.cached_dx_weight())
-        return dx, dA, dB, None, None, None, None, None, None, None, None
+        return dx, dA, dB, None, None, None, None, None, None, None, None, None
 
 
 class ConvRotLinear(nn.Module):
@@ -225,12 +237,27 @@ class ConvRotLinear(nn.Module):
         x2 = x.reshape(-1, self.in_features)
         if not x2.is_contiguous() or x2.data_ptr() % 16:
             x2 = x2.contiguous()
-        if x2.shape[0] == 0:
+        M = x2.shape[0]
+        if M == 0:
             return x.new_empty(*lead, self.out_features)
-        with torch.no_grad():
-            qx, sx = shared_input_quant.lookup(x, x2)
-        y = _ConvRotLinearFn.apply(x2, lora_A, lora_B, self.qweight, self.weight_scale, self._bias_f32(),
-                                   self.mode == "w4a8", float(lora_scale), qx, sx, self)
+        key, codes = shared_input_quant.find(x)
+        ready = codes is not None
+        if ready:
+            qx, sx = codes
+        else:
+            qx = torch.empty((M, self.in_features), dtype=torch.int8, device=x2.device)
+            sx = torch.empty((M,), dtype=torch.float32, device=x2.device)
+        w4 = self.mode == "w4a8"
+        grad = torch.is_grad_enabled() and (x2.requires_grad or (lora_A is not None and
+                                                                  (lora_A.requires_grad or lora_B.requires_grad)))
+        if grad:
+            y = _ConvRotLinearFn.apply(x2, lora_A, lora_B, self.qweight, self.weight_scale, self._bias_f32(), w4,
+                                       float(lora_scale), qx, sx, ready, self)
+        else:   # nothing to differentiate: no autograd node, the one library call
+            y, _ = _lib.linear_fwd(x2, qx, sx, ready, lora_A, lora_B, float(lora_scale), self.qweight,
+                                   self.weight_scale, self._bias_f32(), w4)
+        if not ready:
+            shared_input_quant.keep(x, key, qx, sx)
         return y.reshape(*lead, self.out_features)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:

@@ -132,6 +132,12 @@ def test_lora_any_rank_runs_on_the_kernels(k2, dev, monkeypatch, mode, rank):
     layer.scale_mul = -0.75                                          # a slider setting (lora.py:37)
     s = layer.scale * layer.scale_mul
     calls = _count_calls(monkeypatch, k2._lib, ("lora_down", "lora_grads"))
+    real_fwd = k2._lib.linear_fwd
+
+    def fwd(x2, qx, sx, ready, A, B, *rest):
+        calls["lora_down"] += A is not None        # the one-call forward runs the down-projection inside
+        return real_fwd(x2, qx, sx, ready, A, B, *rest)
+    monkeypatch.setattr(k2._lib, "linear_fwd", fwd)
     x = synth_x(M, K, rank)
     dy = (torch.randn(M, N, generator=torch.Generator().manual_seed(rank)) * 1e-3).to(torch.bfloat16)
     xd = x.to(dev).requires_grad_(True)

@@ -1,0 +1,100 @@
+"""GPU tests of ``k2q_linear_fwd``: one library call per quantized linear + LoRA forward (the module's path).
+
+* M > 8: the call issues the same launches as the separate entry points (rotate/quant, LoRA down-projection,
+  GEMM), so codes, scales, u and y are bit-identical to calling them one by one.
+* M <= 8: one prologue launch computes the codes (bit-identical to ``k2q_rotquant``) and u (an f32 dot product
+  per rank: within f32 rounding of the down-projection kernel and of the float64 product), then the GEMV;
+  y within the forward bar of the oracle.
+* ``codes_ready``: codes computed elsewhere (a producer kernel) are used as given.
+* W4A8 through the same call.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import convrot as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_frob(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def _case(M, K, N, r, seed, dev, w4=False, bias=True):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g)
+    x[:, torch.randperm(K, generator=g)[: max(1, K // 100)]] *= 20
+    x = x.to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    b = torch.randn(N, generator=g) * 0.02 if bias else None
+    A = torch.randn(r, K, generator=g) * 0.01 if r else None
+    B = torch.randn(N, r, generator=g) * 0.01 if r else None
+    return x, w, b, A, B
+
+
+@pytest.mark.parametrize("M,K,N,r,w4", [(512, 3072, 1024, 32, False), (300, 640, 384, 0, False),
+                                        (1024, 12288, 3072, 16, False), (256, 512, 384, 48, True)])
+def test_one_call_equals_separate_launches(k2, dev, M, K, N, r, w4):
+    L = k2._lib
+    x, w, b, A, B = _case(M, K, N, r, M + K, dev, w4)
+    xd, wd = x.to(dev), w.to(dev)
+    bd = b.to(dev) if b is not None else None
+    Ad = A.to(dev) if A is not None else None
+    Bd = B.to(dev) if B is not None else None
+    qw, sw = L.quant_weight_i4(wd) if w4 else L.quant_weight_i8(wd)
+    qx = torch.empty(M, K, dtype=torch.int8, device=dev)
+    sx = torch.empty(M, device=dev)
+    y, u = L.linear_fwd(xd, qx, sx, False, Ad, Bd, 0.75, qw, sw, bd, w4)
+    q0, s0, _ = L.rotquant(xd)
+    u0 = L.lora_down(xd, Ad) if r else None
+    gemm = L.gemm_w4a8 if w4 else L.gemm_w8a8
+    y0 = gemm(q0, s0, qw, sw, bd, u0, Bd, 0.75)
+    assert torch.equal(qx, q0) and torch.equal(sx, s0) and torch.equal(y, y0)
+    if r:
+        assert torch.equal(u, u0)
+    # codes given (as a producer kernel leaves them): the call uses them as they are
+    y1, _ = L.linear_fwd(xd, q0, s0, True, Ad, Bd, 0.75, qw, sw, bd, w4)
+    assert torch.equal(y1, y0)
+
+
+@pytest.mark.parametrize("M,K,N,r", [(1, 3072, 18432, 16), (2, 3072, 18432, 16), (5, 12288, 3072, 64),
+                                     (8, 16384, 256, 128), (3, 640, 512, 0), (2, 6144, 2048, 256)])
+def test_skinny_prologue_codes_and_factors(k2, dev, M, K, N, r):
+    L = k2._lib
+    x, w, b, A, B = _case(M, K, N, r, 3 * M + K, dev)
+    xd = x.to(dev)
+    qw, sw = L.quant_weight_i8(w.to(dev))
+    Ad = A.to(dev) if A is not None else None
+    Bd = B.to(dev) if B is not None else None
+    qx = torch.full((M, K), 99, dtype=torch.int8, device=dev)
+    sx = torch.zeros(M, device=dev)
+    y, u = L.linear_fwd(xd, qx, sx, False, Ad, Bd, 1.0, qw, sw, b.to(dev), False)
+    q0, s0, _ = L.rotquant(xd)
+    assert torch.equal(qx, q0) and torch.equal(sx, s0)                       # bit-identical codes
+    if r:
+        u64 = orc.lora_down(x.float().numpy(), A.numpy())
+        assert rel_frob(u.cpu().numpy(), u64) < 1e-6
+    ref = orc.forward(x.float().numpy(), qw.cpu().numpy(), sw.cpu().numpy(), bias=b.numpy(),
+                      lora_A=None if A is None else A.numpy(), lora_B=None if B is None else B.numpy(), lora_scale=1.0)
+    assert rel_frob(y.float().cpu().numpy(), ref["y64"]) < 4e-3
+    # LoRA factors only (codes given)
+    if r:
+        y2, u2 = L.linear_fwd(xd, q0, s0, True, Ad, Bd, 1.0, qw, sw, b.to(dev), False)
+        assert torch.equal(u2, u) and torch.equal(y2, y)
+
+
+def test_skinny_w4(k2, dev):
+    L = k2._lib
+    M, K, N, r = 2, 3072, 1024, 16
+    x, w, b, A, B = _case(M, K, N, r, 77, dev, w4=True)
+    q4, s4 = L.quant_weight_i4(w.to(dev))
+    qx = torch.empty(M, K, dtype=torch.int8, device=dev)
+    sx = torch.empty(M, device=dev)
+    y, u = L.linear_fwd(x.to(dev), qx, sx, False, A.to(dev), B.to(dev), 1.0, q4, s4, b.to(dev), True)
+    qo, so = orc.quant_weight_i4(w.float().numpy())
+    ref = orc.forward(x.float().numpy(), qo, so, w4=True, bias=b.numpy(), lora_A=A.numpy(), lora_B=B.numpy(),
+                      lora_scale=1.0)
+    assert rel_frob(y.float().cpu().numpy(), ref["y64"]) < 4e-3

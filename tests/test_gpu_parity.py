@@ -830,10 +830,12 @@ def test_shared_input_quantized_once(k2, dev):
 
 
 def test_mfma_probe_runs_and_counts(k2, dev):
-    """The same-run MFMA ceiling bench.py reports: the probe writes one checksum per thread (not all equal:
-    the operands differ per lane) and reports 2*32^3 ops per MFMA, 64 MFMAs per wave and iteration."""
-    ops = k2._lib.mfma_probe_i8(3, 4, dev)
+    """The same-run MFMA ceiling bench.py reports (its own library, libk2q_probe.so): the probe writes one
+    checksum per thread (not all equal: the operands differ per lane) and reports 2*32^3 ops per MFMA, 64 MFMAs
+    per wave and iteration."""
+    import bench
+    ops = bench.mfma_probe_i8(3, 4, dev)
     torch.cuda.synchronize()
     assert ops == 4 * 8 * 3 * 64 * 2 * 32 * 32 * 32
-    out = k2._lib._probe_out[dev][: 4 * 512].cpu()
+    out = bench._probe[dev][: 4 * 512].cpu()
     assert len(set(out.tolist())) > 1
