@@ -162,10 +162,31 @@ int k2q_gemm_w4a8(const int8_t* qx, const float* sx, const uint8_t* qw4, const u
                   const float* bias, const float* u, const float* lora_b, int64_t r, float lora_scale,
                   int64_t M, int64_t N, int64_t K, uint16_t* y, void* stream);
 
+/* Output tile shapes of the MFMA GEMMs (A-rows x B-rows per workgroup).  Every entry point picks one per
+ * launch with a cost model (K2Q_TILE_AUTO); the debug entries below take a shape explicitly so tests can run
+ * each on any problem.  The result does not depend on the shape (int32 sums are exact; the f32 epilogue and
+ * the LoRA term are computed per element in the same order). */
+#define K2Q_TILE_AUTO (-1)
+#define K2Q_TILE_256x256 0
+#define K2Q_TILE_256x320 1
+#define K2Q_TILE_192x256 2
+#define K2Q_TILE_128x128 3
+#define K2Q_TILE_GEMV 4      /* M <= K2Q_GEMV_MAX_M: the GEMV, no tiles */
+
+/* The schedule k2q_gemm_w8a8 (and the W8 GEMM of k2q_linear_fwd) takes for an M x N x K problem on a GPU with
+ * `cus` compute units: returns the K2Q_TILE_* shape (or K2Q_TILE_GEMV), and in *split_pieces (nullable) the
+ * number of K-pieces its last round of 256x256 tiles is cut into (1 = none).  Host only: no device call. */
+int k2q_gemm_w8a8_plan(int64_t M, int64_t N, int64_t K, int cus, int* split_pieces);
+
 /* Debug entries: raw int32 accumulators acc[m,n] = sum_k qx[m,k] qw[n,k] (W8), and for W4 the f32
- * value sum_g sw4[n,g] * acc_g[m,n] without s_x, 2^-7, bias or LoRA. */
+ * value sum_g sw4[n,g] * acc_g[m,n] without s_x, 2^-7, bias or LoRA.  k2q_gemm_w8a8_tile is k2q_gemm_w8a8
+ * with the tile shape given (M <= 8 runs the GEMV whatever the shape). */
 int k2q_gemm_w8a8_acc(const int8_t* qx, const int8_t* qw, int64_t M, int64_t N, int64_t K,
-                      int32_t* acc, void* ws, int64_t ws_bytes, void* stream);   /* ws as k2q_gemm_w8a8 */
+                      int32_t* acc, void* ws, int64_t ws_bytes, int tile, void* stream);   /* ws as k2q_gemm_w8a8 */
+int k2q_gemm_w8a8_tile(const int8_t* qx, const float* sx, const int8_t* qw, const float* sw, const float* bias,
+                       const float* u, const float* lora_b, int64_t r, float lora_scale,
+                       int64_t M, int64_t N, int64_t K, uint16_t* y, void* ws, int64_t ws_bytes, int tile,
+                       void* stream);
 int k2q_gemm_w4a8_f32(const int8_t* qx, const uint8_t* qw4, const uint16_t* sw4,
                       int64_t M, int64_t N, int64_t K, float* out, void* stream);
 

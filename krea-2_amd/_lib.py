@@ -64,7 +64,9 @@ _SIGNATURES = {
     "k2q_linear_fwd_ws_bytes": ([_int, _i64, _i64, _i64, _i64], _i64),
     "k2q_linear_fwd": ([_p, _i64, _i64, _i64, _p, _p, _int, _p, _p, _i64, _f32, _p, _int, _p, _p, _p, _i64, _p, _p,
                         _i64, _p], _int),
-    "k2q_gemm_w8a8_acc": ([_p, _p, _i64, _i64, _i64, _p, _p, _i64, _p], _int),
+    "k2q_gemm_w8a8_acc": ([_p, _p, _i64, _i64, _i64, _p, _p, _i64, _int, _p], _int),
+    "k2q_gemm_w8a8_tile": ([_p, _p, _p, _p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p, _i64, _int, _p], _int),
+    "k2q_gemm_w8a8_plan": ([_i64, _i64, _i64, _int, ctypes.POINTER(_int)], _int),
     "k2q_gemm_w4a8_f32": ([_p, _p, _p, _i64, _i64, _i64, _p, _p], _int),
     "k2q_quant_weight_fp8": ([_p, _int, _i64, _i64, _p, _p, _p], _int),
     "k2q_dequant_fp8": ([_p, _p, _i64, _i64, _int, _p, _p], _int),
@@ -461,10 +463,25 @@ def _gemm_common(qx, sx, N, bias, u, lora_b):
     return dev, M, K, r
 
 
+TILES = {"auto": -1, "256x256": 0, "256x320": 1, "192x256": 2, "128x128": 3}   # K2Q_TILE_*
+_TILE_NAMES = {v: k for k, v in TILES.items()} | {4: "gemv"}
+
+
+def gemm_w8a8_plan(M: int, N: int, K: int, cus: int = 256) -> tuple[str, int]:
+    """The schedule ``k2q_gemm_w8a8`` takes for an M x N x K problem on a GPU with ``cus`` compute units:
+    (tile shape or "gemv", K-pieces of the last round of 256x256 tiles).  Host only."""
+    pieces = _int(0)
+    rc = load().k2q_gemm_w8a8_plan(M, N, K, cus, ctypes.byref(pieces))
+    if rc < 0:
+        _check(rc, "k2q_gemm_w8a8_plan")
+    return _TILE_NAMES[rc], pieces.value
+
+
 def gemm_w8a8(qx, sx, qw, sw, bias=None, u=None, lora_b=None, lora_scale: float = 1.0, *,
-              split: bool = True) -> torch.Tensor:
+              split: bool = True, tile: str = "auto") -> torch.Tensor:
     """``y = bf16(2^-7 s_x s_w acc + bias + lora_scale u lora_B^T)`` (M,N).  ``split=False`` runs every tile
-    over the full K (the result is the same; the split schedule only fills the GPU's last round)."""
+    over the full K (the result is the same; the split schedule only fills the GPU's last round); ``tile`` forces
+    an output tile shape (``TILES``; the result is the same)."""
     _need(qw, "q_w", torch.int8, 2)
     N = qw.shape[0]
     dev, M, K, r = _gemm_common(qx, sx, N, bias, u, lora_b)
@@ -478,8 +495,9 @@ def gemm_w8a8(qx, sx, qw, sw, bias=None, u=None, lora_b=None, lora_scale: float 
     y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     lib = load()
     ws, nws = _workspace(lib.k2q_gemm_w8a8_ws_bytes(M, N, K) if split else 0, dev)
-    _check(lib.k2q_gemm_w8a8(_ptr(qx), _ptr(sx), _ptr(qw), _ptr(sw), _ptr(bias), _ptr(u), _ptr(lora_b), r,
-                             float(lora_scale), M, N, K, _ptr(y), _ptr(ws), nws, _stream(dev)), "k2q_gemm_w8a8")
+    _check(lib.k2q_gemm_w8a8_tile(_ptr(qx), _ptr(sx), _ptr(qw), _ptr(sw), _ptr(bias), _ptr(u), _ptr(lora_b), r,
+                                  float(lora_scale), M, N, K, _ptr(y), _ptr(ws), nws, TILES[tile], _stream(dev)),
+           "k2q_gemm_w8a8")
     return y
 
 
@@ -593,8 +611,8 @@ def gemm_w4a8(qx, sx, q4, s4, bias=None, u=None, lora_b=None, lora_scale: float 
     return y
 
 
-def gemm_w8a8_acc(qx, qw, *, split: bool = True) -> torch.Tensor:
-    """Debug: raw int32 accumulators ``qx @ qw^T`` (M,N)."""
+def gemm_w8a8_acc(qx, qw, *, split: bool = True, tile: str = "auto") -> torch.Tensor:
+    """Debug: raw int32 accumulators ``qx @ qw^T`` (M,N), optionally with a forced tile shape (``TILES``)."""
     _need(qx, "q_x", torch.int8, 2)
     dev = qx.device
     _need(qw, "q_w", torch.int8, 2, dev)
@@ -607,7 +625,7 @@ def gemm_w8a8_acc(qx, qw, *, split: bool = True) -> torch.Tensor:
     acc = torch.empty((M, N), dtype=torch.int32, device=dev)
     lib = load()
     ws, nws = _workspace(lib.k2q_gemm_w8a8_ws_bytes(M, N, K) if split else 0, dev)
-    _check(lib.k2q_gemm_w8a8_acc(_ptr(qx), _ptr(qw), M, N, K, _ptr(acc), _ptr(ws), nws, _stream(dev)),
+    _check(lib.k2q_gemm_w8a8_acc(_ptr(qx), _ptr(qw), M, N, K, _ptr(acc), _ptr(ws), nws, TILES[tile], _stream(dev)),
            "k2q_gemm_w8a8_acc")
     return acc
 

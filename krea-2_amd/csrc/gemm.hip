@@ -29,9 +29,7 @@ namespace {
 
 enum { EPI_W8 = 0, EPI_ACC = 1, EPI_DX = 2, EPI_LIN = 3, EPI_DXLIN = 4 };
 
-constexpr int BT = 256;     // tile rows (A) and columns (B)
 constexpr int BKB = 128;    // reduction bytes per stage
-constexpr int TILE_BYTES = BT * BKB;
 
 // One segment of a grouped forward (EPI_W8): linears that read the same input, their weight rows stacked
 // along A.  Each segment starts on a 256-row tile boundary, so a tile lies in one segment and takes its
@@ -107,45 +105,6 @@ __device__ __forceinline__ void tile_coords(uint32_t tiles_a, uint32_t tiles_b, 
   ta = r / gsize;
 }
 
-// Global -> registers: thread t copies chunk (t & 7) of tile rows (t >> 3) + 32 i, i = 0..7.  `tile` is the
-// workgroup-uniform address of the tile's first row at the current stage; the per-thread offsets are
-// 32-bit (row-in-tile * ld + chunk), with rows past the end clamped onto the last row (in bounds; those
-// results are never stored).
-template <int NL>  // NL = tile rows / 32
-struct TileOffsets {
-  uint32_t o[NL];
-};
-
-template <int NL>
-__device__ __forceinline__ TileOffsets<NL> tile_offsets(int64_t row0, int64_t nrows, int64_t ld) {
-  const int t = threadIdx.x;
-  TileOffsets<NL> r;
-#pragma unroll
-  for (int i = 0; i < NL; ++i) {
-    int64_t rr = (t >> 3) + 32 * i;
-    rr = row0 + rr < nrows ? rr : nrows - 1 - row0;
-    r.o[i] = (uint32_t)(rr * ld) + 16u * (uint32_t)(t & 7);
-  }
-  return r;
-}
-
-template <int NL>
-__device__ __forceinline__ void g2r(const uint8_t* tile, const TileOffsets<NL>& off, v4i (&r)[NL]) {
-#pragma unroll
-  for (int i = 0; i < NL; ++i) r[i] = *reinterpret_cast<const v4i*>(tile + off.o[i]);
-}
-
-template <int NL>
-__device__ __forceinline__ void r2s(uint8_t* s, const v4i (&r)[NL]) {
-  const int t = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < NL; ++i) {
-    const int row = (t >> 3) + 32 * i;
-    const int pc = (t & 7) ^ swz(row);
-    *reinterpret_cast<v4i*>(s + row * BKB + 16 * pc) = r[i];
-  }
-}
-
 __device__ __forceinline__ v4i frag(const uint8_t* s, int row, int chunk) {
   return *reinterpret_cast<const v4i*>(s + row * BKB + 16 * (chunk ^ swz(row)));
 }
@@ -191,21 +150,6 @@ __device__ __forceinline__ v16f lora_block(const float* lora_ra, const float* lo
   return f;
 }
 
-// bf16 store of one 32 x 32 block: out[m][n..n+3], m = bcol0 + lane%32, n = arow0 + 8 j + 4 (lane/32).
-__device__ __forceinline__ void store_block(uint16_t* out, int64_t ldo, int64_t rows_a, int64_t rows_b,
-                                            int64_t arow0, int64_t bcol0, int lane, const v16f& f) {
-  const int h = lane >> 5, c32 = lane & 31;
-  const int64_t m = bcol0 + c32;
-  if (m >= rows_b) return;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t n = arow0 + 8 * j + 4 * h;
-    if (n >= rows_a) continue;
-    const v2u v = v2u{pack_bf16x2(f[4 * j], f[4 * j + 1]), pack_bf16x2(f[4 * j + 2], f[4 * j + 3])};
-    *reinterpret_cast<v2u*>(out + m * ldo + n) = v;
-  }
-}
-
 // Inverse rotation of one column slice: FWHT over the wave's 128 A-rows (one Hadamard block), times
 // 2^-7.  Row-index bits: i -> 0-1 (register e bits 0-1), h -> 2 (partner lane l^32), j -> 3-4 (e bits
 // 2-3), ia -> 5-6.  The order of the stages is free here: the result is held to a tolerance.
@@ -244,37 +188,68 @@ __device__ __forceinline__ void fwht128_rows(v16f (&f)[4], int h) {
 
 // ---------------------------------------------------------------------------------------------------------
 // Main-loop data movement: global -> LDS by the gfx950 LDS-DMA path (global_load_lds_dwordx4), no VGPR
-// staging.  A stage is 128 bytes of the reduction axis for the tile's 256 A-rows and 256 B-rows (32 KB
-// each, the frag()/swz() layout above); two stages alternate in LDS.  One DMA wave instruction fills 8
-// consecutive LDS rows (1 KB: lane l -> row l/8, physical chunk l%8) and each lane fetches the logical
-// chunk (l%8) ^ swz(row) of its row, so every instruction reads 8 whole 128-byte lines.  Measured on
-// MI355X (same box, random data) against 64-byte stages fetched as paired half lines through a 5-slot
-// ring: cfg2 GEMM 643.6 -> 626.6 us, cfg3 input-gradient GEMM 331.5 -> 323.1 us; in a copy-only loop with
-// the same waits and barriers, half lines, paired half lines and whole lines move 24, 31 and 35 B/clk/CU.
-// A stage is consumed after every wave's `s_waitcnt vmcnt` for it plus one lds_barrier() (the wave's LDS
-// operations, then s_barrier; not __syncthreads, whose full memory fence would drain the prefetches).
+// staging.  A stage is 128 bytes of the reduction axis for the tile's TA A-rows and TB B-rows (the
+// frag()/swz() layout above); two stages alternate in LDS.  One DMA wave instruction fills 8 consecutive LDS
+// rows (1 KB: lane l -> row l/8, physical chunk l%8) and each lane fetches the logical chunk (l%8) ^ swz(row)
+// of its row, so every instruction reads 8 whole 128-byte lines.  Measured on MI355X (same box, random data)
+// against 64-byte stages fetched as paired half lines through a 5-slot ring: cfg2 GEMM 643.6 -> 626.6 us,
+// cfg3 input-gradient GEMM 331.5 -> 323.1 us; in a copy-only loop with the same waits and barriers, half
+// lines, paired half lines and whole lines move 24, 31 and 35 B/clk/CU.  A stage is consumed after every
+// wave's `s_waitcnt vmcnt` for it plus one lds_barrier() (the wave's LDS operations, then s_barrier; not
+// __syncthreads, whose full memory fence would drain the prefetches).
 constexpr int SBK = 64;                   // unit of reduction lengths in the split plan (half a stage)
 constexpr int WBK = 128;                  // reduction bytes per stage
-constexpr int WSTAGE = 2 * BT * WBK;      // one stage of both operands: 64 KB
 
 #define K2Q_GPTR(p) ((__attribute__((address_space(1))) void*)(p))
 #define K2Q_LPTR(p) ((__attribute__((address_space(3))) void*)(p))
 
-// Epilogue LDS use (after the main loop has drained the ring): the bf16 output tile, 256 rows of CROW
-// bytes (256 values + 16 B of padding, which spreads a lane group's 8-byte writes over all banks), then
-// 3 x 256 floats of scales at SCALE_OFF, then the LoRA factor rows of one 16-rank chunk as bf16 (A-side
-// rows, then B-side rows, LROW bytes each: 48, so the 16 rows read by a lane group start 12 words apart and
-// cover all 64 banks).
-constexpr int CROW = 2 * BT + 16;
-constexpr int SCALE_OFF = BT * CROW;
-constexpr int LROW = 48;
-constexpr int LORA_OFF = SCALE_OFF + 3 * BT * 4;
-constexpr int EPI_BYTES = LORA_OFF + 2 * BT * LROW;
-constexpr int GEMM_LDS_BYTES = 2 * WSTAGE > EPI_BYTES ? 2 * WSTAGE : EPI_BYTES;
-static_assert(GEMM_LDS_BYTES <= 160 * 1024, "gfx950 LDS is 160 KB per workgroup");
+constexpr int GW = 8;                     // waves per workgroup (two per SIMD)
+constexpr int GT = 64 * GW;               // threads per workgroup
+constexpr int LROW = 48;                  // epilogue LoRA staging row (bytes; see TileCfg)
+
+// Output tile shapes.  A workgroup computes TA A-rows x TB B-rows with its 8 waves laid out WVA along A by
+// 8/WVA along B; each wave owns NA x NB blocks of 32 x 32 (v_mfma 32x32 accumulators).  Per stage a wave
+// issues DA + DB DMA instructions (8 rows each).  The epilogue stages the bf16 tile in LDS CROWS B-rows at a
+// time (rows of CROW bytes: TA values plus 16 bytes of padding, which spreads a lane group's 8-byte writes
+// over all banks), then 3 sets of scales, then the LoRA factor rows of one 16-rank chunk as bf16 (A-side rows,
+// then B-side rows, LROW bytes each: 48, so the 16 rows read by a lane group start 12 words apart and cover
+// all 64 banks).
+//   T256 256 x 256: the general tile (4 x 2 blocks per wave, 128 accumulator registers).
+//   T320 256 x 320: 2 x 5 blocks per wave; 10 % fewer global->LDS bytes per MAC, and M = 16896 (2048^2)
+//        splits into 52.8 tiles of 320 where 256-row tiles leave 12.4 rounds of the GPU: 10 rounds instead
+//        of 13.  Its epilogue stages 160 B-rows at a time.
+//   T192 192 x 256 and T128 128 x 128 (two workgroups per CU): for grids that leave most of a round idle.
+template <int TA_, int TB_, int WVA_, int WPC_>
+struct TileCfg {
+  static constexpr int TA = TA_, TB = TB_, WVA = WVA_, WVB = GW / WVA_, WPC = WPC_;   // WPC: workgroups per CU
+  static constexpr int NA = TA / (32 * WVA), NB = TB / (32 * WVB);
+  static constexpr int ARW = 32 * NA, BRW = 32 * NB;
+  static constexpr int DA = TA / 8 / GW, DB = TB / 8 / GW;
+  static constexpr int STAGE = (TA + TB) * WBK;
+  static constexpr int CROW = 2 * TA + 16;
+  static constexpr int CROWS = TB <= 256 ? TB : TB / 2;
+  static constexpr int SCALE_OFF = CROWS * CROW;
+  static constexpr int LORA_OFF = SCALE_OFF + (TB + 2 * TA) * 4;
+  static constexpr int EPI_BYTES = LORA_OFF + (TA + TB) * LROW;
+  static constexpr int LDS = 2 * STAGE > EPI_BYTES ? 2 * STAGE : EPI_BYTES;
+  static constexpr int NBR = (TB + GT / 2 - 1) / (GT / 2);   // LoRA B-side rows staged per thread
+  static_assert(NA * 32 * WVA == TA && NB * 32 * WVB == TB, "waves tile the output");
+  static_assert(DA * 8 * GW == TA && DB * 8 * GW == TB, "DMA rows cover the stage");
+  static_assert(TA <= GT / 2 && CROWS % BRW == 0 && TB % CROWS == 0, "epilogue staging");
+  static_assert(LDS * WPC <= 160 * 1024, "gfx950 LDS is 160 KB per CU");
+};
+using T256 = TileCfg<256, 256, 2, 1>;
+using T320 = TileCfg<256, 320, 4, 1>;
+using T192 = TileCfg<192, 256, 2, 1>;
+using T128 = TileCfg<128, 128, 2, 2>;
+enum { TILE_AUTO = -1, TILE_256 = 0, TILE_320 = 1, TILE_192 = 2, TILE_128 = 3, TILE_COUNT = 4 };
+static_assert(TILE_AUTO == K2Q_TILE_AUTO && TILE_256 == K2Q_TILE_256x256 && TILE_320 == K2Q_TILE_256x320 &&
+                  TILE_192 == K2Q_TILE_192x256 && TILE_128 == K2Q_TILE_128x128 && TILE_COUNT == K2Q_TILE_GEMV,
+              "tile ids of the C ABI");
 
 // One 32 x 32 block of f32 (MFMA C layout) into the LDS tile as bf16: lane l owns tile row mrow0 + l%32
 // and columns ncol0 + 8j + 4(l/32) .. +3.
+template <int CROW>
 __device__ __forceinline__ void ctile_put(uint8_t* ct, int mrow0, int ncol0, int lane, const v16f& f) {
   uint8_t* row = ct + (mrow0 + (lane & 31)) * CROW + 2 * (ncol0 + 4 * (lane >> 5));
 #pragma unroll
@@ -298,18 +273,6 @@ __device__ __forceinline__ void wait_vmcnt() {
 // to it); outstanding global loads, the LDS-DMA prefetches among them, are not waited for.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// Eight waves (two per SIMD) on a 256 x 256 tile: wave w covers A-rows 128*(w&1) .. +128 and B-rows
-// 64*(w>>1) .. +64 (4 x 2 MFMA blocks, 128 accumulator registers), so both waves of a SIMD issue LDS-DMA
-// and MFMAs and each can run while the other waits.
-#ifndef K2Q_GW
-#define K2Q_GW 8
-#endif
-constexpr int GW = K2Q_GW;              // waves per workgroup (8: two per SIMD; 4: one per SIMD)
-constexpr int GT = 64 * GW;             // threads per workgroup
-constexpr int WB = 16 / GW;             // 32-wide B blocks per wave
-constexpr int WBR = 32 * WB;            // B-rows per wave
-constexpr int WDMA = BT / 8 / GW;       // DMA instructions per wave, operand and stage (8 rows each)
-
 enum { MODE_TILE = 0, MODE_PIECE = 1, MODE_FIXUP = 2 };
 
 // MODE_TILE: full-K tiles 0 .. dp_tiles-1 with their epilogues; workgroup b takes tiles r * gridDim.x + b'
@@ -317,51 +280,54 @@ enum { MODE_TILE = 0, MODE_PIECE = 1, MODE_FIXUP = 2 };
 // workgroups than CUs and give each the same number of tiles.  MODE_PIECE: one piece of a remainder tile,
 // accumulators parked in part.  MODE_FIXUP: the pieces of remainder tile dp_tiles + blockIdx.x added in
 // slice order, then the epilogue.  Separate kernels, so the register allocation of the tile kernel is not
-// shared with the other paths.
-template <int EPI, int MODE>
+// shared with the other paths.  The split modes run T256 tiles only.
+template <int EPI, int MODE, class C>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int64_t lid, int kbeg, int nk);
 
-template <int EPI, int MODE>
-__global__ __launch_bounds__(GT, 1) __attribute__((amdgpu_waves_per_eu(GW / 4, GW / 4))) void gemm_nt_kernel(GemmArgs p) {
+template <int EPI, int MODE, class C>
+__global__ __launch_bounds__(GT, C::WPC) __attribute__((amdgpu_waves_per_eu(2 * C::WPC, 2 * C::WPC)))
+void gemm_nt_kernel(GemmArgs p) {
   const int64_t nk_full = p.kbytes / SBK;
   if constexpr (MODE == MODE_FIXUP) {
-    gemm_tile<EPI, MODE>(p, p.dp_tiles + blockIdx.x, 0, (int)nk_full);
+    gemm_tile<EPI, MODE, C>(p, p.dp_tiles + blockIdx.x, 0, (int)nk_full);
   } else if constexpr (MODE == MODE_PIECE) {   // pieces cover whole stage pairs
     const int sl = (int)blockIdx.x / p.sk_rem;
     const int np = (int)(nk_full / 2);
     const int kbeg = 2 * (sl * np / p.sk_s);
-    gemm_tile<EPI, MODE>(p, p.dp_tiles + (int)blockIdx.x % p.sk_rem, kbeg, 2 * ((sl + 1) * np / p.sk_s) - kbeg);
+    gemm_tile<EPI, MODE, C>(p, p.dp_tiles + (int)blockIdx.x % p.sk_rem, kbeg, 2 * ((sl + 1) * np / p.sk_s) - kbeg);
   } else {
     const int64_t me = xcd_remap((int)blockIdx.x, (int)gridDim.x);
     for (int64_t base = 0; base + me < p.dp_tiles; base += gridDim.x) {
       if (base > 0) lds_barrier();   // every wave is done with the previous tile's LDS
-      gemm_tile<EPI, MODE>(p, base + me, 0, (int)nk_full);
+      gemm_tile<EPI, MODE, C>(p, base + me, 0, (int)nk_full);
     }
   }
 }
 
 // One output tile (linear id lid) over reduction stages kbeg .. kbeg+nk-1, then its epilogue (MODE_TILE,
 // MODE_FIXUP) or its parked accumulators (MODE_PIECE).
-template <int EPI, int MODE>
+template <int EPI, int MODE, class C>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int kbeg, int nk) {
   constexpr bool BF16 = (EPI == EPI_DX || EPI == EPI_LIN || EPI == EPI_DXLIN);
   constexpr bool SCALED = (EPI == EPI_W8 || EPI == EPI_LIN);   // per-row scale / bias epilogue
+  constexpr int NA = C::NA, NB = C::NB, TA = C::TA, TB = C::TB;
+  static_assert(EPI != EPI_DX || C::ARW == 128, "the rotating epilogue runs a 128-row FWHT per wave");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // [2][A stage | B stage], then epilogue
   // The thread index through an empty asm: values derived from it are then computed per tile, not hoisted
   // out of the tile loop of MODE_TILE (where they would stay live through the main loop and spill).
   int tid = (int)threadIdx.x;
   asm volatile("" : "+v"(tid));
 
-  const int64_t tiles_a = (p0.rows_a + BT - 1) / BT;
-  const int64_t tiles_b = (p0.rows_b + BT - 1) / BT;
+  const int64_t tiles_a = (p0.rows_a + TA - 1) / TA;
+  const int64_t tiles_b = (p0.rows_b + TB - 1) / TB;
   int64_t ta, tb;
   group_coords(lid, tiles_a, tiles_b, ta, tb);
-  int64_t A0 = ta * BT;
-  const int64_t B0 = tb * BT;
+  int64_t A0 = ta * TA;
+  const int64_t B0 = tb * TB;
   // A grouped forward: the tile's segment supplies the operands (workgroup-uniform, scalar registers); A0
   // becomes the row within the segment.  Constant segment indices keep every field a plain argument load.
   // Grouped launches run full-K tiles only (no split pieces), so the piece and fixup kernels, at their
-  // register limit, carry none of this.
+  // register limit, carry none of this.  Segments start on multiples of TA (the launch checks it).
   GemmArgs p = p0;
   if constexpr (EPI == EPI_W8 && MODE == MODE_TILE) {
     if (p0.nseg > 0) {
@@ -388,100 +354,108 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
 
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wa = wave & 1, wb = wave >> 1;
+  const int wa = wave % C::WVA, wb = wave / C::WVA;
   const int h = lane >> 5, c32 = lane & 31;
 
-  v16i acc[4][WB];
+  v16i acc[NA][NB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < NA; ++i)
 #pragma unroll
-    for (int j = 0; j < WB; ++j) acc[i][j] = v16i{0};
+    for (int j = 0; j < NB; ++j) acc[i][j] = v16i{0};
 
   // Epilogue operands of this tile, fetched now so their latency hides under the main loop:
-  // thread t < 256 holds s_x of B-row B0+t (times 2^-7), s_w and bias of A-row A0+t.
+  // thread t < TB holds s_x of B-row B0+t (times 2^-7), thread t < TA s_w and bias of A-row A0+t.
   float pre_sx = 0.f, pre_sw = 0.f, pre_bi = 0.f;
   if constexpr (SCALED) {
-    const int t = tid & (BT - 1);
+    const int t = tid;
     const int64_t rb = B0 + t < p.rows_b ? B0 + t : p.rows_b - 1;
     const int64_t ra = A0 + t < p.rows_a ? A0 + t : p.rows_a - 1;
     if constexpr (EPI == EPI_W8) {
-      pre_sx = p.sx[rb] * 0.0078125f;  // 2^-7: the two unnormalised rotations
-      pre_sw = p.sw[ra];
+      if (t < TB) pre_sx = p.sx[rb] * 0.0078125f;  // 2^-7: the two unnormalised rotations
+      if (t < TA) pre_sw = p.sw[ra];
     } else {
       pre_sx = 1.f;                    // fma(acc, 1, bias) = acc + bias, rounded once
       pre_sw = 1.f;
     }
-    pre_bi = p.bias ? p.bias[ra] : 0.f;
+    if (t < TA) pre_bi = p.bias ? p.bias[ra] : 0.f;
   }
 
   // Per-lane source offsets (bytes from the tile's first row) of the DMA instructions: LDS rows
-  // 8 (WDMA wave + i) + lane/8; rows past the matrix end are clamped onto its last row (never stored).
-  uint32_t offa[WDMA], offb[WDMA];
+  // 8 (D wave + i) + lane/8; rows past the matrix end are clamped onto its last row (never stored).
+  uint32_t offa[C::DA], offb[C::DB];
 #pragma unroll
-  for (int i = 0; i < WDMA; ++i) {
-    const int lrow = 8 * (WDMA * wave + i) + (lane >> 3);
-    int64_t ra = lrow, rb = lrow;
+  for (int i = 0; i < C::DA; ++i) {
+    const int lrow = 8 * (C::DA * wave + i) + (lane >> 3);
+    int64_t ra = lrow;
     ra = A0 + ra < p.rows_a ? ra : p.rows_a - 1 - A0;
+    offa[i] = (uint32_t)(ra * p.lda_b) + 16u * (uint32_t)((lane & 7) ^ swz(lrow));
+  }
+#pragma unroll
+  for (int i = 0; i < C::DB; ++i) {
+    const int lrow = 8 * (C::DB * wave + i) + (lane >> 3);
+    int64_t rb = lrow;
     rb = B0 + rb < p.rows_b ? rb : p.rows_b - 1 - B0;
-    const uint32_t ch = 16u * (uint32_t)((lane & 7) ^ swz(lrow));
-    offa[i] = (uint32_t)(ra * p.lda_b) + ch;
-    offb[i] = (uint32_t)(rb * p.ldb_b) + ch;
+    offb[i] = (uint32_t)(rb * p.ldb_b) + 16u * (uint32_t)((lane & 7) ^ swz(lrow));
   }
   const uint8_t* gA = p.a + A0 * p.lda_b + (int64_t)kbeg * SBK;
   const uint8_t* gB = p.b + B0 * p.ldb_b + (int64_t)kbeg * SBK;
-  uint8_t* ldsw = smem + 1024 * WDMA * wave;   // this wave's DMA rows inside a stage
+  uint8_t* ldsa = smem + 1024 * C::DA * wave;            // this wave's DMA rows inside a stage
+  uint8_t* ldsb = smem + TA * WBK + 1024 * C::DB * wave;
 
   // DMA of stage st (128 reduction bytes) into LDS slot `slot`.
   auto issue = [&](int st, int slot) {
-    uint8_t* buf = ldsw + slot * WSTAGE;
 #pragma unroll
-    for (int i = 0; i < WDMA; ++i)
-      __builtin_amdgcn_global_load_lds(K2Q_GPTR(gA + (int64_t)st * WBK + offa[i]), K2Q_LPTR(buf + 1024 * i), 16, 0, 0);
+    for (int i = 0; i < C::DA; ++i)
+      __builtin_amdgcn_global_load_lds(K2Q_GPTR(gA + (int64_t)st * WBK + offa[i]),
+                                       K2Q_LPTR(ldsa + slot * C::STAGE + 1024 * i), 16, 0, 0);
 #pragma unroll
-    for (int i = 0; i < WDMA; ++i)
-      __builtin_amdgcn_global_load_lds(K2Q_GPTR(gB + (int64_t)st * WBK + offb[i]), K2Q_LPTR(buf + BT * WBK + 1024 * i),
-                                       16, 0, 0);
+    for (int i = 0; i < C::DB; ++i)
+      __builtin_amdgcn_global_load_lds(K2Q_GPTR(gB + (int64_t)st * WBK + offb[i]),
+                                       K2Q_LPTR(ldsb + slot * C::STAGE + 1024 * i), 16, 0, 0);
   };
   // Fragments of substep kk (32 reduction bytes) of the stage in LDS slot `slot`.
-  auto read_frags = [&](int slot, int kk, v4i (&fa)[4], v4i (&fb)[WB]) {
-    const uint8_t* tA = smem + slot * WSTAGE;
-    const uint8_t* tB = tA + BT * WBK;
+  auto read_frags = [&](int slot, int kk, v4i (&fa)[NA], v4i (&fb)[NB]) {
+    const uint8_t* tA = smem + slot * C::STAGE;
+    const uint8_t* tB = tA + TA * WBK;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fa[i] = frag(tA, 128 * wa + 32 * i + c32, 2 * kk + h);
+    for (int i = 0; i < NA; ++i) fa[i] = frag(tA, C::ARW * wa + 32 * i + c32, 2 * kk + h);
 #pragma unroll
-    for (int i = 0; i < WB; ++i) fb[i] = frag(tB, WBR * wb + 32 * i + c32, 2 * kk + h);
+    for (int i = 0; i < NB; ++i) fb[i] = frag(tB, C::BRW * wb + 32 * i + c32, 2 * kk + h);
   };
-  auto mfmas = [&](const v4i (&fa)[4], const v4i (&fb)[WB]) {
+  auto mfmas = [&](const v4i (&fa)[NA], const v4i (&fb)[NB]) {
 #pragma unroll
-    for (int ia = 0; ia < 4; ++ia)
+    for (int ia = 0; ia < NA; ++ia)
 #pragma unroll
-      for (int ib = 0; ib < WB; ++ib) mma<BF16>(fa[ia], fb[ib], acc[ia][ib]);
+      for (int ib = 0; ib < NB; ++ib) mma<BF16>(fa[ia], fb[ib], acc[ia][ib]);
   };
 
   // Software pipeline, per stage s (slot s & 1) in four substeps of 32 bytes:
-  //   substeps 0-2 : read the next substep's fragments | 8 MFMAs
+  //   substeps 0-2 : read the next substep's fragments | NA NB MFMAs
   //   end of stage : wait for stage s+1's DMA and for this wave's own fragment reads, s_barrier (every
   //                  wave is done with slot s & 1), DMA stage s+2 into it
-  //   substep 3    : read stage s+1 substep-0 fragments | 8 MFMAs, the DMA instructions interleaved
+  //   substep 3    : read stage s+1 substep-0 fragments | NA NB MFMAs, the DMA instructions interleaved
   // so fragments are always in registers before their MFMAs and each stage's DMA is in flight for one
   // stage before its wait.  The body has no branches: past the last stage the DMA re-loads the last stage
   // into the freed slot (never one still in use) and the extra fragment reads are discarded, which keeps
   // the count of outstanding DMA instructions fixed at the waits.  nk counts 64-byte halves and is even
   // (every reduction length is a multiple of 128 bytes).
-  constexpr int G = 2 * WDMA;   // DMA instructions per wave per stage
-  // Accumulator storage of a piece in part: 16-byte unit ((ia * WB + ib) * 4 + q) of thread t at byte
+  constexpr int G = C::DA + C::DB;   // DMA instructions per wave per stage
+  constexpr int NR = NA + NB;        // fragment reads per substep
+  constexpr int NM = NA * NB;        // MFMAs per substep
+  constexpr int NI = NR < NM ? NR : NM;
+  // Accumulator storage of a piece in part: 16-byte unit ((ia * NB + ib) * 4 + q) of thread t at byte
   // 8 KB * unit + 16 t, so each wave instruction moves 1 KB of consecutive bytes.  The per-unit base is
   // workgroup-uniform (scalar registers) and the thread offset a 32-bit vector register.
-  constexpr int64_t PIECE_BYTES = (int64_t)BT * BT * 4;
+  constexpr int64_t PIECE_BYTES = (int64_t)TA * TB * 4;
   const uint32_t toff = 16u * tid;
   if constexpr (MODE == MODE_FIXUP) {
     for (int sl = 0; sl < p.sk_s; ++sl) {
       const uint8_t* pc = reinterpret_cast<const uint8_t*>(p.part) + ((int64_t)sl * p.sk_rem + blockIdx.x) * PIECE_BYTES;
 #pragma unroll
-      for (int ia = 0; ia < 4; ++ia)
+      for (int ia = 0; ia < NA; ++ia)
 #pragma unroll
-        for (int ib = 0; ib < WB; ++ib) {
-          const uint8_t* u = pc + (int64_t)(ia * WB + ib) * 4 * GT * 16;
+        for (int ib = 0; ib < NB; ++ib) {
+          const uint8_t* u = pc + (int64_t)(ia * NB + ib) * 4 * GT * 16;
           const v4i q0 = *reinterpret_cast<const v4i*>(u + toff);
           const v4i q1 = *reinterpret_cast<const v4i*>(u + GT * 16 + toff);
           const v4i q2 = *reinterpret_cast<const v4i*>(u + 2 * GT * 16 + toff);
@@ -496,17 +470,18 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
         }
     }
   } else {
-    v4i f0a[4], f0b[WB], f1a[4], f1b[WB];
+    v4i f0a[NA], f0b[NB], f1a[NA], f1b[NB];
     const int ns = nk / 2;   // stages
     // MFMAs of one substep interleaved with the next substep's fragment reads.
-    auto sub = [&](const v4i (&fa)[4], const v4i (&fb)[WB]) {
+    auto sub = [&](const v4i (&fa)[NA], const v4i (&fb)[NB]) {
       mfmas(fa, fb);
 #pragma unroll
-      for (int i = 0; i < 4 + WB; ++i) {
+      for (int i = 0; i < NI; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, 4 * WB - (4 + WB), 0);
+      if constexpr (NM > NI) __builtin_amdgcn_sched_group_barrier(0x008, NM - NI, 0);
+      if constexpr (NR > NI) __builtin_amdgcn_sched_group_barrier(0x100, NR - NI, 0);
     };
     issue(0, 0);
     issue(ns > 1 ? 1 : 0, 1);
@@ -527,39 +502,41 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
       issue(st + 2 < ns ? st + 2 : ns - 1, sl);
       read_frags(sl ^ 1, 0, f0a, f0b);
       mfmas(f1a, f1b);
+      constexpr int GI = G < NM ? G : NM;
 #pragma unroll
-      for (int i = 0; i < G; ++i) {
+      for (int i = 0; i < GI; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
         __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM (LDS-DMA)
       }
+      if constexpr (G > GI) __builtin_amdgcn_sched_group_barrier(0x020, G - GI, 0);
 #pragma unroll
-      for (int i = 0; i < 4 + WB; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-      if constexpr (4 * WB > G) __builtin_amdgcn_sched_group_barrier(0x008, 4 * WB - G, 0);
+      for (int i = 0; i < NR; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      if constexpr (NM > GI) __builtin_amdgcn_sched_group_barrier(0x008, NM - GI, 0);
     }
     wait_vmcnt<0>();   // no LDS-DMA may still be in flight when the workgroup's LDS is released
   }
   if constexpr (MODE == MODE_PIECE) {   // park the accumulators for the fixup launch
     uint8_t* dst = reinterpret_cast<uint8_t*>(p.part) + (int64_t)blockIdx.x * PIECE_BYTES;
 #pragma unroll
-    for (int ia = 0; ia < 4; ++ia)
+    for (int ia = 0; ia < NA; ++ia)
 #pragma unroll
-      for (int ib = 0; ib < WB; ++ib)
+      for (int ib = 0; ib < NB; ++ib)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          *reinterpret_cast<v4i*>(dst + (int64_t)((ia * WB + ib) * 4 + q) * GT * 16 + toff) =
+          *reinterpret_cast<v4i*>(dst + (int64_t)((ia * NB + ib) * 4 + q) * GT * 16 + toff) =
               v4i{acc[ia][ib][4 * q], acc[ia][ib][4 * q + 1], acc[ia][ib][4 * q + 2], acc[ia][ib][4 * q + 3]};
     return;
   }
 
-  const int64_t a0 = A0 + 128 * wa;   // first A-row of this wave
-  const int64_t b0 = B0 + WBR * wb;   // first B-row of this wave
+  const int64_t a0 = A0 + C::ARW * wa;   // first A-row of this wave
+  const int64_t b0 = B0 + C::BRW * wb;   // first B-row of this wave
 
   if constexpr (EPI == EPI_ACC) {
     int32_t* out = static_cast<int32_t*>(p.out);
 #pragma unroll
-    for (int ia = 0; ia < 4; ++ia)
+    for (int ia = 0; ia < NA; ++ia)
 #pragma unroll
-      for (int ib = 0; ib < WB; ++ib) {
+      for (int ib = 0; ib < NB; ++ib) {
         const int64_t m = b0 + 32 * ib + c32;
         if (m >= p.rows_b) continue;
 #pragma unroll
@@ -578,19 +555,21 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
     //      FWHT, 2^-7)
     //   B  LoRA: bf16 MFMAs accumulate the adapter term straight onto those f32 values (the factor rows
     //      staged in LDS per 16-rank chunk); base + adapter is rounded to bf16 once
-    //   C  the bf16 tile goes to LDS (256 rows of CROW bytes), then out with coalesced 16-byte stores,
-    //      512 contiguous bytes per output row segment.
-    // This thread's share of the LoRA factor rows for the staging below (A-side row A0 + t/2, B-side row
-    // B0 + t/2, ranks 8 (t&1) .. +8 of each 16-rank chunk): the first chunk is fetched now, so its latency
-    // hides under pass A, and each later chunk while the previous one is multiplied.  The input-gradient
-    // epilogues read their A-side factors straight from LoRA A (r x rows_a): 8 loads of 4 bytes, rank by
-    // rank, consecutive threads on consecutive columns.
+    //   C  the bf16 tile goes to LDS (CROWS rows of CROW bytes at a time), then out with coalesced 16-byte
+    //      stores, 2 TA contiguous bytes per output row segment.
+    // This thread's share of the LoRA factor rows for the staging below (A-side row A0 + t/2 for t/2 < TA,
+    // B-side rows B0 + t/2 + 256 i, ranks 8 (t&1) .. +8 of each 16-rank chunk): the first chunk is fetched
+    // now, so its latency hides under pass A, and each later chunk while the previous one is multiplied.  The
+    // input-gradient epilogues read their A-side factors straight from LoRA A (r x rows_a): 8 loads of 4
+    // bytes, rank by rank, consecutive threads on consecutive columns.
     constexpr bool RA_T = (EPI == EPI_DX || EPI == EPI_DXLIN);
+    constexpr int NBR = C::NBR;
     const bool lora = p.lora_rb != nullptr && p.r > 0;
     const int srow = tid >> 1, shalf = tid & 1;
+    const bool a_side = srow < TA;
     const float* pra = nullptr;
-    const float* prb = nullptr;
-    v4f lfa[2], lfb[2];
+    const float* prb[NBR];
+    v4f lfa[2], lfb[NBR][2];
     auto load_ra = [&](int c0) {
       if constexpr (RA_T) {
         const float* q = pra + (int64_t)c0 * p.rows_a;
@@ -601,23 +580,33 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
         lfa[1] = *reinterpret_cast<const v4f*>(pra + c0 + 4);
       }
     };
+    auto load_rb = [&](int c0) {
+#pragma unroll
+      for (int i = 0; i < NBR; ++i) {
+        lfb[i][0] = *reinterpret_cast<const v4f*>(prb[i] + c0);
+        lfb[i][1] = *reinterpret_cast<const v4f*>(prb[i] + c0 + 4);
+      }
+    };
     if (lora) {
-      int64_t ra = A0 + srow, rb = B0 + srow;
+      int64_t ra = A0 + (a_side ? srow : 0);
       ra = ra < p.rows_a ? ra : p.rows_a - 1;
-      rb = rb < p.rows_b ? rb : p.rows_b - 1;
       pra = RA_T ? p.lora_ra + (int64_t)(8 * shalf) * p.rows_a + ra : p.lora_ra + ra * p.r + 8 * shalf;
-      prb = p.lora_rb + rb * p.ldr + 8 * shalf;
+#pragma unroll
+      for (int i = 0; i < NBR; ++i) {
+        int64_t rb = B0 + srow + (GT / 2) * i;
+        rb = rb < p.rows_b ? rb : p.rows_b - 1;
+        prb[i] = p.lora_rb + rb * p.ldr + 8 * shalf;
+      }
       load_ra(0);
-      lfb[0] = *reinterpret_cast<const v4f*>(prb);
-      lfb[1] = *reinterpret_cast<const v4f*>(prb + 4);
+      load_rb(0);
     }
     lds_barrier();   // every wave is done with the LDS ring
-    float* s_sx = reinterpret_cast<float*>(smem + SCALE_OFF);
-    float* s_sw = s_sx + BT;
-    float* s_bi = s_sw + BT;
+    float* s_sx = reinterpret_cast<float*>(smem + C::SCALE_OFF);
+    float* s_sw = s_sx + TB;
+    float* s_bi = s_sw + TA;
     if constexpr (SCALED) {
-      if (tid < BT) {
-        s_sx[tid] = pre_sx;
+      if (tid < TB) s_sx[tid] = pre_sx;
+      if (tid < TA) {
         s_sw[tid] = pre_sw;
         s_bi[tid] = pre_bi;
       }
@@ -626,17 +615,17 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
     uint8_t* ctile = smem;
     if constexpr (SCALED) {
 #pragma unroll
-      for (int ia = 0; ia < 4; ++ia) {
+      for (int ia = 0; ia < NA; ++ia) {
         v4f sw[4], bi[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int nl = 128 * wa + 32 * ia + 8 * j + 4 * h;
+          const int nl = C::ARW * wa + 32 * ia + 8 * j + 4 * h;
           sw[j] = *reinterpret_cast<const v4f*>(s_sw + nl);
           bi[j] = *reinterpret_cast<const v4f*>(s_bi + nl);
         }
 #pragma unroll
-        for (int ib = 0; ib < WB; ++ib) {
-          const float sxm = s_sx[WBR * wb + 32 * ib + c32];
+        for (int ib = 0; ib < NB; ++ib) {
+          const float sxm = s_sx[C::BRW * wb + 32 * ib + c32];
           v16f a;   // whole-vector conversions (element-wise bit casts of vector lanes have miscompiled here)
           if constexpr (BF16)
             a = __builtin_bit_cast(v16f, acc[ia][ib]);
@@ -650,78 +639,94 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
           acc[ia][ib] = __builtin_bit_cast(v16i, f);   // in place: the f32 tile reuses the accumulators
         }
       }
-    } else {  // EPI_DX: one 32-column slice (ib) at a time; the FWHT needs all 4 row slices of it.
+    } else if constexpr (EPI == EPI_DX) {  // one 32-column slice (ib) at a time; the FWHT needs all 4 row slices
 #pragma unroll
-      for (int ib = 0; ib < WB; ++ib) {
+      for (int ib = 0; ib < NB; ++ib) {
         v16f f[4];
 #pragma unroll
         for (int ia = 0; ia < 4; ++ia) f[ia] = __builtin_bit_cast(v16f, acc[ia][ib]);
-        if constexpr (EPI == EPI_DX) fwht128_rows(f, h);
+        fwht128_rows(f, h);
 #pragma unroll
         for (int ia = 0; ia < 4; ++ia) acc[ia][ib] = __builtin_bit_cast(v16i, f[ia]);
       }
-    }
+    }   // EPI_DXLIN: the accumulators are the f32 values already
     // Pin the dequantized tile in registers here: otherwise the compiler sinks pass A's arithmetic past the
     // LoRA branch (to the stores) and keeps its scale operands live across it, which spills.
 #pragma unroll
-    for (int ia = 0; ia < 4; ++ia)
+    for (int ia = 0; ia < NA; ++ia)
 #pragma unroll
-      for (int ib = 0; ib < WB; ++ib) asm volatile("" : "+v"(acc[ia][ib]));
+      for (int ib = 0; ib < NB; ++ib) asm volatile("" : "+v"(acc[ia][ib]));
     if (lora) {
-      // Per 16-rank chunk the workgroup stages the tile's 256 A-side and 256 B-side factor rows in LDS as
-      // bf16 (B side times lora_scale), each f32 read once: thread t converts 8 ranks of row t/2.
-      uint8_t* sla = smem + LORA_OFF;
-      uint8_t* slb = sla + BT * LROW;
+      // Per 16-rank chunk the workgroup stages the tile's TA A-side and TB B-side factor rows in LDS as
+      // bf16 (B side times lora_scale), each f32 read once: thread t converts 8 ranks of its rows.
+      uint8_t* sla = smem + C::LORA_OFF;
+      uint8_t* slb = sla + TA * LROW;
       for (int c0 = 0; c0 < p.r; c0 += 16) {
-        *reinterpret_cast<v8bf*>(sla + srow * LROW + 16 * shalf) = f32x8_to_bf16v(lfa[0], lfa[1], 1.f);
-        *reinterpret_cast<v8bf*>(slb + srow * LROW + 16 * shalf) = f32x8_to_bf16v(lfb[0], lfb[1], p.lora_scale);
+        if (a_side) *reinterpret_cast<v8bf*>(sla + srow * LROW + 16 * shalf) = f32x8_to_bf16v(lfa[0], lfa[1], 1.f);
+#pragma unroll
+        for (int i = 0; i < NBR; ++i) {
+          const int row = srow + (GT / 2) * i;
+          if (row < TB)
+            *reinterpret_cast<v8bf*>(slb + row * LROW + 16 * shalf) = f32x8_to_bf16v(lfb[i][0], lfb[i][1], p.lora_scale);
+        }
         const int cn = c0 + 16 < p.r ? c0 + 16 : c0;   // next chunk (the last re-reads its own)
         load_ra(cn);
-        lfb[0] = *reinterpret_cast<const v4f*>(prb + cn);
-        lfb[1] = *reinterpret_cast<const v4f*>(prb + cn + 4);
+        load_rb(cn);
         lds_barrier();
-        v8bf fa[4], fb[WB];
+        v8bf fa[NA], fb[NB];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          fa[i] = *reinterpret_cast<const v8bf*>(sla + (128 * wa + 32 * i + c32) * LROW + 16 * h);
+        for (int i = 0; i < NA; ++i)
+          fa[i] = *reinterpret_cast<const v8bf*>(sla + (C::ARW * wa + 32 * i + c32) * LROW + 16 * h);
 #pragma unroll
-        for (int i = 0; i < WB; ++i)
-          fb[i] = *reinterpret_cast<const v8bf*>(slb + (WBR * wb + 32 * i + c32) * LROW + 16 * h);
+        for (int i = 0; i < NB; ++i)
+          fb[i] = *reinterpret_cast<const v8bf*>(slb + (C::BRW * wb + 32 * i + c32) * LROW + 16 * h);
 #pragma unroll
-        for (int ia = 0; ia < 4; ++ia)
+        for (int ia = 0; ia < NA; ++ia)
 #pragma unroll
-          for (int ib = 0; ib < WB; ++ib)
+          for (int ib = 0; ib < NB; ++ib)
             acc[ia][ib] = __builtin_bit_cast(
                 v16i, __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ia], fb[ib], __builtin_bit_cast(v16f, acc[ia][ib]), 0, 0, 0));
         lds_barrier();   // every wave has its fragments before the next chunk overwrites them
       }
     }
-#pragma unroll
-    for (int ia = 0; ia < 4; ++ia)
-#pragma unroll
-      for (int ib = 0; ib < WB; ++ib)
-        ctile_put(ctile, WBR * wb + 32 * ib, 128 * wa + 32 * ia, lane, __builtin_bit_cast(v16f, acc[ia][ib]));
-    lds_barrier();
-    // Pass C: wave w stores tile rows 32w .. 32w+31, two rows (2 x 512 B) per instruction.  Non-temporal:
-    // the output is not read again by this launch, and streaming it keeps the operand strips in L2.
+    // Pass C, CROWS B-rows at a time: the waves owning those rows put their blocks into the LDS tile, then
+    // wave w stores tile rows RPW w .. RPW w + RPW - 1, two rows (2 x 2 TA bytes) per instruction.
+    // Non-temporal: the output is not read again by this launch, and streaming it keeps the operand strips
+    // in L2.
     uint16_t* out = static_cast<uint16_t*>(p.out);
+    constexpr int RPW = C::CROWS / GW;   // rows per wave per pass
+    constexpr int CPR = TA / 8;          // 16-byte chunks per row
     const int chunk = lane & 31;
     const int64_t col = A0 + 8 * chunk;
-    constexpr int RPW = BT / GW;   // rows per wave
-    if ((p.ldo & 7) == 0) {        // rows are 16-byte aligned: one 16-byte store per lane
-      const bool col_ok = col < p.rows_a;
-#pragma unroll 4
-      for (int i = 0; i < RPW / 2; ++i) {
-        const int row = RPW * wave + 2 * i + (lane >> 5);
-        const v4u v = *reinterpret_cast<const v4u*>(ctile + row * CROW + 16 * chunk);
-        if (col_ok && B0 + row < p.rows_b) __builtin_nontemporal_store(v, reinterpret_cast<v4u*>(out + (B0 + row) * p.ldo + col));
+#pragma unroll
+    for (int pass = 0; pass < TB / C::CROWS; ++pass) {
+      if (pass > 0) lds_barrier();       // the previous pass's rows have left the tile
+      const int rbeg = pass * C::CROWS;
+      if (C::BRW * wb >= rbeg && C::BRW * wb < rbeg + C::CROWS) {
+#pragma unroll
+        for (int ia = 0; ia < NA; ++ia)
+#pragma unroll
+          for (int ib = 0; ib < NB; ++ib)
+            ctile_put<C::CROW>(ctile, C::BRW * wb - rbeg + 32 * ib, C::ARW * wa + 32 * ia, lane,
+                               __builtin_bit_cast(v16f, acc[ia][ib]));
       }
-    } else {                       // ragged widths: element stores
-      for (int i = 0; i < RPW / 2; ++i) {
-        const int row = RPW * wave + 2 * i + (lane >> 5);
-        if (B0 + row >= p.rows_b) continue;
-        const uint16_t* src = reinterpret_cast<const uint16_t*>(ctile + row * CROW + 16 * chunk);
-        for (int e = 0; e < 8 && col + e < p.rows_a; ++e) out[(B0 + row) * p.ldo + col + e] = src[e];
+      lds_barrier();
+      const int64_t R0 = B0 + rbeg;
+      if ((p.ldo & 7) == 0) {        // rows are 16-byte aligned: one 16-byte store per lane
+        const bool col_ok = chunk < CPR && col < p.rows_a;
+#pragma unroll 4
+        for (int i = 0; i < RPW / 2; ++i) {
+          const int row = RPW * wave + 2 * i + (lane >> 5);
+          const v4u v = *reinterpret_cast<const v4u*>(ctile + row * C::CROW + 16 * (chunk < CPR ? chunk : 0));
+          if (col_ok && R0 + row < p.rows_b) __builtin_nontemporal_store(v, reinterpret_cast<v4u*>(out + (R0 + row) * p.ldo + col));
+        }
+      } else {                       // ragged widths: element stores
+        for (int i = 0; i < RPW / 2; ++i) {
+          const int row = RPW * wave + 2 * i + (lane >> 5);
+          if (R0 + row >= p.rows_b || chunk >= CPR) continue;
+          const uint16_t* src = reinterpret_cast<const uint16_t*>(ctile + row * C::CROW + 16 * chunk);
+          for (int e = 0; e < 8 && col + e < p.rows_a; ++e) out[(R0 + row) * p.ldo + col + e] = src[e];
+        }
       }
     }
   }
@@ -981,23 +986,24 @@ int launch_w4(const W4Args& p, hipStream_t st) {
   return k2q_launch_status();
 }
 
-// Split plan for the tiles of the last, partly filled round, in units of one reduction stage of one tile
-// (measured on MI355X): a full-K tile costs nk + 8 (epilogue); cutting the rem remainder tiles into s
-// pieces (one round of pieces when rem * s <= CUs) costs nk / s per piece plus ~12 (ramp and piece
-// store), and the fixup launch ~20 + 3 per piece read back.  The s with the lowest cost is taken if it
-// saves at least 10 %.
+// Split plan for the tiles of the last, partly filled round of T256 tiles, in units of one reduction stage of
+// one tile (measured on MI355X): a full-K tile costs nk + 8 (epilogue); cutting the rem remainder tiles into s
+// pieces (one round of pieces when rem * s <= CUs) costs nk / s per piece plus ~12 (ramp and piece store),
+// and the fixup launch ~20 + 3 per piece read back.  The s with the lowest cost is taken if it saves at least
+// 10 %.
 struct SplitPlan {
   int64_t dp_tiles;
   int rem, s;
+  double cost;   // stage units of a T256 tile
 };
 
 SplitPlan split_plan(int64_t tiles, int nk, int cus) {
-  SplitPlan q{tiles, 0, 1};
+  SplitPlan q{tiles, 0, 1, 0.0};
   const int64_t full = tiles / cus, rem = tiles - full * cus;
-  if (rem == 0) return q;
   const double tile = nk + 8.0;
-  const double t_full = (double)(full + 1) * tile;
-  double best = 0.9 * t_full;
+  q.cost = (double)((tiles + cus - 1) / cus) * tile;
+  if (rem == 0) return q;
+  double best = 0.9 * q.cost;
   for (int s = 2; s <= 8 && rem * s <= cus && nk / s >= 8; ++s) {
     const double t = (double)full * tile + (double)nk / s + 12.0 + 20.0 + 3.0 * s;
     if (t < best) {
@@ -1008,49 +1014,130 @@ SplitPlan split_plan(int64_t tiles, int nk, int cus) {
   if (q.s > 1) {
     q.dp_tiles = full * cus;
     q.rem = (int)rem;
+    q.cost = best;
   }
   return q;
 }
 
+// Tile shape of a launch: the one with the lowest estimated time, in units of one reduction stage of a T256 tile.
+// A round of `active` tiles over `slots` = CUs x workgroups-per-CU costs nk x c x (0.7 + 0.3 active / slots) +
+// epilogue: a partly filled round runs its stages faster (less HBM and L2 contention).  Per-stage costs relative
+// to T256, fitted to the MI355X timings of 17 launch shapes (M 1024..16896, N 1536..16384, K 3072..16384; the
+// fitted model picks the fastest measured shape on each): T320 1.25, T192 0.80, T128 0.60 with two workgroups
+// sharing a CU and 0.30 with a CU to itself; epilogues 8 (T256, T320), 7 (T192), 4 (T128).  T256 may instead cut
+// its last round's tiles along K (split_plan).  The rotating input-gradient epilogue runs 128 A-rows per wave
+// (T256 only); grouped launches need segments on tile boundaries (TA = 256 or 128).
+struct TileChoice {
+  int tile;
+  SplitPlan split;   // T256 only
+};
+
+template <class C>
+double tile_cost(int64_t rows_a, int64_t rows_b, int nk, int cus, double stage_cost, double alone_cost, double epi) {
+  const int64_t tiles = ((rows_a + C::TA - 1) / C::TA) * ((rows_b + C::TB - 1) / C::TB);
+  const int64_t slots = (int64_t)cus * C::WPC;
+  const int64_t full = tiles / slots, rem = tiles - full * slots;
+  auto round = [&](int64_t active) {
+    const double c = (C::WPC > 1 && active <= cus) ? alone_cost : stage_cost;
+    return nk * c * (0.7 + 0.3 * (double)active / (double)slots) + epi;
+  };
+  return (double)full * round(slots) + (rem ? round(rem) : 0.0);
+}
+
+TileChoice choose_tile(int epi, int64_t rows_a, int64_t rows_b, int64_t kbytes, bool grouped, int forced, int cus) {
+  const int nk = (int)(kbytes / SBK);
+  const int64_t tiles256 = ((rows_a + 255) / 256) * ((rows_b + 255) / 256);
+  TileChoice c{TILE_256, grouped ? SplitPlan{tiles256, 0, 1, 0.0} : split_plan(tiles256, nk, cus)};
+  if (forced >= 0) {
+    c.tile = forced;
+    if (forced != TILE_256) c.split = SplitPlan{0, 0, 1, 0.0};
+    return c;
+  }
+  if (epi == EPI_DX) return c;
+  double best = c.split.s > 1 ? c.split.cost : tile_cost<T256>(rows_a, rows_b, nk, cus, 1.0, 1.0, 8.0);
+  const double t320 = tile_cost<T320>(rows_a, rows_b, nk, cus, 1.25, 1.25, 8.0);
+  const double t192 = grouped ? 1e300 : tile_cost<T192>(rows_a, rows_b, nk, cus, 0.80, 0.80, 7.0);
+  const double t128 = tile_cost<T128>(rows_a, rows_b, nk, cus, 0.60, 0.30, 4.0);
+  if (t320 < best) { best = t320; c.tile = TILE_320; }
+  if (t192 < best) { best = t192; c.tile = TILE_192; }
+  if (t128 < best) { best = t128; c.tile = TILE_128; }
+  if (c.tile != TILE_256) c.split = SplitPlan{0, 0, 1, 0.0};
+  return c;
+}
+
+// Workspace for any schedule an entry may take: the T256 split plan's pieces (used when the launch runs T256
+// tiles, chosen or forced; other tile shapes leave it untouched).
 int64_t split_ws_bytes(int64_t rows_a, int64_t rows_b, int64_t kbytes) {
-  const int64_t tiles = ((rows_a + BT - 1) / BT) * ((rows_b + BT - 1) / BT);
+  const int64_t tiles = ((rows_a + 255) / 256) * ((rows_b + 255) / 256);
   const SplitPlan q = split_plan(tiles, (int)(kbytes / SBK), k2q_cu_count());
-  return q.s > 1 ? (int64_t)q.rem * q.s * BT * BT * 4 : 0;
+  return q.s > 1 ? (int64_t)q.rem * q.s * 256 * 256 * 4 : 0;
+}
+
+template <int EPI, int MODE, class C>
+int set_lds() {
+  return hipFuncSetAttribute((const void*)gemm_nt_kernel<EPI, MODE, C>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             C::LDS) == hipSuccess ? K2Q_OK : K2Q_ELAUNCH;
+}
+
+// Balanced persistent grid: as many rounds as the tiles need on this GPU's workgroup slots, and just enough
+// workgroups for that many rounds, each taking the same number of tiles (3168 T256 tiles on 256 CUs: 244
+// workgroups of 13), instead of a last round that leaves most CUs idle.
+template <int EPI, class C>
+int launch_tiles(const GemmArgs& p, hipStream_t st) {
+  if (int rc = set_lds<EPI, MODE_TILE, C>()) return rc;
+  const int64_t slots = (int64_t)k2q_cu_count() * C::WPC;
+  const int64_t rounds = (p.dp_tiles + slots - 1) / slots;
+  const int64_t nwg = (p.dp_tiles + rounds - 1) / rounds;
+  hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_TILE, C>), dim3((unsigned)nwg), dim3(GT), C::LDS, st, p);
+  return K2Q_OK;
 }
 
 template <int EPI>
-int launch_gemm(GemmArgs p, void* ws, int64_t ws_bytes, hipStream_t st) {
-  constexpr int lds = GEMM_LDS_BYTES;
-  if (hipFuncSetAttribute((const void*)gemm_nt_kernel<EPI, MODE_TILE>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          lds) != hipSuccess ||
-      hipFuncSetAttribute((const void*)gemm_nt_kernel<EPI, MODE_PIECE>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          lds) != hipSuccess ||
-      hipFuncSetAttribute((const void*)gemm_nt_kernel<EPI, MODE_FIXUP>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          lds) != hipSuccess)
-    return K2Q_ELAUNCH;
+int launch_gemm(GemmArgs p, void* ws, int64_t ws_bytes, hipStream_t st, int forced = TILE_AUTO) {
   if (p.ldr == 0) p.ldr = p.r;
-  const int64_t tiles = ((p.rows_a + BT - 1) / BT) * ((p.rows_b + BT - 1) / BT);
+  if (forced >= TILE_COUNT || (EPI == EPI_DX && forced >= 0 && forced != TILE_256)) return K2Q_EINVAL;
+  TileChoice c = choose_tile(EPI, p.rows_a, p.rows_b, p.kbytes, p.nseg > 0, forced, k2q_cu_count());
+  if (p.nseg > 0) {   // segments start on tile boundaries
+    const int ta = c.tile == TILE_192 ? 192 : c.tile == TILE_128 ? 128 : 256;
+    for (int i = 0; i < p.nseg; ++i)
+      if (p.seg[i].start % ta || p.seg[i].rows % ta) return K2Q_EINVAL;
+  }
+  if (c.tile != TILE_256) {
+    int64_t tiles;
+    if (c.tile == TILE_320) tiles = ((p.rows_a + 255) / 256) * ((p.rows_b + 319) / 320);
+    else if (c.tile == TILE_192) tiles = ((p.rows_a + 191) / 192) * ((p.rows_b + 255) / 256);
+    else tiles = ((p.rows_a + 127) / 128) * ((p.rows_b + 127) / 128);
+    if (tiles > 0x7fffffff) return K2Q_EUNSUPPORTED;
+    p.dp_tiles = tiles;
+    p.sk_rem = 0;
+    p.sk_s = 1;
+    int rc;
+    if constexpr (EPI == EPI_DX) {
+      rc = K2Q_EINVAL;
+    } else {
+      if (c.tile == TILE_320) rc = launch_tiles<EPI, T320>(p, st);
+      else if (c.tile == TILE_192) rc = launch_tiles<EPI, T192>(p, st);
+      else rc = launch_tiles<EPI, T128>(p, st);
+    }
+    return rc ? rc : k2q_launch_status();
+  }
+  SplitPlan q = c.split;
+  const int64_t tiles = ((p.rows_a + 255) / 256) * ((p.rows_b + 255) / 256);
   if (tiles > 0x7fffffff) return K2Q_EUNSUPPORTED;
-  SplitPlan q = split_plan(tiles, (int)(p.kbytes / SBK), k2q_cu_count());
-  if (q.s > 1 && (!ws || ws_bytes < (int64_t)q.rem * q.s * BT * BT * 4 || !k2q_aligned(ws, 16)))
-    q = SplitPlan{tiles, 0, 1};   // no room for the pieces: full-K tiles only
+  if (q.s > 1 && (!ws || ws_bytes < (int64_t)q.rem * q.s * 256 * 256 * 4 || !k2q_aligned(ws, 16)))
+    q = SplitPlan{tiles, 0, 1, 0.0};   // no room for the pieces: full-K tiles only
   p.dp_tiles = q.dp_tiles;
   p.sk_rem = q.rem;
   p.sk_s = q.s;
   p.part = static_cast<int32_t*>(ws);
+  int rc = K2Q_OK;
   // Pieces first: they fill the GPU for a short round, then the full tiles, then the fixup.
-  if (q.s > 1)
-    hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_PIECE>), dim3((unsigned)(q.rem * q.s)), dim3(GT), lds, st, p);
-  if (q.dp_tiles > 0) {
-    // Balanced grid: as many rounds as the tiles need on this GPU's CUs, and just enough workgroups for
-    // that many rounds, each taking the same number of tiles (3168 tiles on 256 CUs: 244 workgroups of
-    // 13), instead of a last round that leaves most CUs idle.
-    const int cus = k2q_cu_count();
-    const int64_t rounds = (q.dp_tiles + cus - 1) / cus;
-    const int64_t nwg = (q.dp_tiles + rounds - 1) / rounds;
-    hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_TILE>), dim3((unsigned)nwg), dim3(GT), lds, st, p);
+  if (q.s > 1) {
+    if ((rc = set_lds<EPI, MODE_PIECE, T256>()) || (rc = set_lds<EPI, MODE_FIXUP, T256>())) return rc;
+    hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_PIECE, T256>), dim3((unsigned)(q.rem * q.s)), dim3(GT), T256::LDS, st, p);
   }
-  if (q.s > 1) hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_FIXUP>), dim3((unsigned)q.rem), dim3(GT), lds, st, p);
+  if (q.dp_tiles > 0 && (rc = launch_tiles<EPI, T256>(p, st))) return rc;
+  if (q.s > 1) hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_FIXUP, T256>), dim3((unsigned)q.rem), dim3(GT), T256::LDS, st, p);
   return k2q_launch_status();
 }
 
@@ -1086,6 +1173,13 @@ extern "C" int k2q_gemm_w8a8(const int8_t* qx, const float* sx, const int8_t* qw
                              const float* bias, const float* u, const float* lora_b, int64_t r,
                              float lora_scale, int64_t M, int64_t N, int64_t K, uint16_t* y,
                              void* ws, int64_t ws_bytes, void* stream) {
+  return k2q_gemm_w8a8_tile(qx, sx, qw, sw, bias, u, lora_b, r, lora_scale, M, N, K, y, ws, ws_bytes, -1, stream);
+}
+
+extern "C" int k2q_gemm_w8a8_tile(const int8_t* qx, const float* sx, const int8_t* qw, const float* sw,
+                                  const float* bias, const float* u, const float* lora_b, int64_t r,
+                                  float lora_scale, int64_t M, int64_t N, int64_t K, uint16_t* y,
+                                  void* ws, int64_t ws_bytes, int tile, void* stream) {
   int rc = check_common(M, N, K);
   if (rc) return rc;
   if (!k2q_aligned(y, 16)) return K2Q_EINVAL;
@@ -1104,7 +1198,18 @@ extern "C" int k2q_gemm_w8a8(const int8_t* qx, const float* sx, const int8_t* qw
   p.out = y; p.ldo = N;
   p.sx = sx; p.sw = sw; p.bias = bias;
   p.lora_rb = u; p.lora_ra = lora_b; p.r = u ? (int)r : 0; p.lora_scale = lora_scale;
-  return launch_gemm<EPI_W8>(p, ws, ws_bytes, static_cast<hipStream_t>(stream));
+  return launch_gemm<EPI_W8>(p, ws, ws_bytes, static_cast<hipStream_t>(stream), tile);
+}
+
+extern "C" int k2q_gemm_w8a8_plan(int64_t M, int64_t N, int64_t K, int cus, int* split_pieces) {
+  if (M < 1 || N < 1 || K < K2Q_HADAMARD || K % K2Q_HADAMARD || cus < 1) return K2Q_EINVAL;
+  if (M <= K2Q_GEMV_MAX_M) {
+    if (split_pieces) *split_pieces = 1;
+    return K2Q_TILE_GEMV;
+  }
+  const TileChoice c = choose_tile(EPI_W8, N, M, K, false, TILE_AUTO, cus);
+  if (split_pieces) *split_pieces = c.tile == TILE_256 ? c.split.s : 1;
+  return c.tile;
 }
 
 extern "C" int k2q_gemm_w8a8_grouped(const int8_t* qx, const float* sx, int64_t M, int64_t K,
@@ -1117,7 +1222,7 @@ extern "C" int k2q_gemm_w8a8_grouped(const int8_t* qx, const float* sx, int64_t 
   GemmArgs p{};
   for (int64_t i = 0; i < nseg; ++i) {
     const k2q_w8a8_segment& g = seg[i];
-    if (!g.qw || !g.sw || !g.y || g.N < BT || g.N % BT) return K2Q_EINVAL;
+    if (!g.qw || !g.sw || !g.y || g.N < 256 || g.N % 256) return K2Q_EINVAL;
     if (!k2q_aligned(g.qw, 16) || !k2q_aligned(g.sw, 16) || !k2q_aligned(g.y, 16)) return K2Q_EINVAL;
     if (g.bias && !k2q_aligned(g.bias, 16)) return K2Q_EINVAL;
     if (g.lora_b) {
@@ -1152,7 +1257,7 @@ extern "C" int k2q_gemm_w8a8_grouped(const int8_t* qx, const float* sx, int64_t 
 }
 
 extern "C" int k2q_gemm_w8a8_acc(const int8_t* qx, const int8_t* qw, int64_t M, int64_t N, int64_t K,
-                                 int32_t* acc, void* ws, int64_t ws_bytes, void* stream) {
+                                 int32_t* acc, void* ws, int64_t ws_bytes, int tile, void* stream) {
   int rc = check_common(M, N, K);
   if (rc) return rc;
   if (!qx || !qw || !acc || !k2q_aligned(qx, 16) || !k2q_aligned(qw, 16) || !k2q_aligned(acc, 16))
@@ -1162,7 +1267,7 @@ extern "C" int k2q_gemm_w8a8_acc(const int8_t* qx, const int8_t* qw, int64_t M, 
   p.b = reinterpret_cast<const uint8_t*>(qx);
   p.rows_a = N; p.rows_b = M; p.kbytes = K; p.lda_b = K; p.ldb_b = K;
   p.out = acc; p.ldo = N;
-  return launch_gemm<EPI_ACC>(p, ws, ws_bytes, static_cast<hipStream_t>(stream));
+  return launch_gemm<EPI_ACC>(p, ws, ws_bytes, static_cast<hipStream_t>(stream), tile);
 }
 
 extern "C" int k2q_gemm_dx(const uint16_t* dy, const uint16_t* wt, int64_t M, int64_t N, int64_t K,

@@ -328,8 +328,8 @@ def test_gemm_split_schedule_bit_exact(k2, dev, M, N, K):
     qx_h = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
     qw_h = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
     qx, qw = torch.from_numpy(qx_h).to(dev), torch.from_numpy(qw_h).to(dev)
-    acc = k2._lib.gemm_w8a8_acc(qx, qw)
-    assert torch.equal(acc, k2._lib.gemm_w8a8_acc(qx, qw, split=False))
+    acc = k2._lib.gemm_w8a8_acc(qx, qw, tile="256x256")     # the split schedule runs 256 x 256 tiles
+    assert torch.equal(acc, k2._lib.gemm_w8a8_acc(qx, qw, split=False, tile="256x256"))
     rows = np.arange(M) if M <= 1024 else np.array([0, 1, 255, 256, M // 2, M - 257, M - 1])
     assert np.array_equal(acc.cpu().numpy()[rows], orc.gemm_acc_fast(qx_h[rows], qw_h))
     g = torch.Generator().manual_seed(1)
@@ -338,9 +338,10 @@ def test_gemm_split_schedule_bit_exact(k2, dev, M, N, K):
     bias = (torch.randn(N, generator=g) * 0.02).to(dev)
     u = torch.randn(M, 16, generator=g).to(dev)
     B = (torch.randn(N, 16, generator=g) * 0.01).to(dev)
-    y = k2._lib.gemm_w8a8(qx, sx, qw, sw, bias, u, B, 0.5)
-    y0 = k2._lib.gemm_w8a8(qx, sx, qw, sw, bias, u, B, 0.5, split=False)
+    y = k2._lib.gemm_w8a8(qx, sx, qw, sw, bias, u, B, 0.5, tile="256x256")
+    y0 = k2._lib.gemm_w8a8(qx, sx, qw, sw, bias, u, B, 0.5, split=False, tile="256x256")
     assert torch.equal(y.view(torch.int16), y0.view(torch.int16))
+    assert torch.equal(k2._lib.gemm_w8a8(qx, sx, qw, sw, bias, u, B, 0.5), y0)   # whatever tile is chosen
 
 
 def test_input_gradient_split_schedule(k2, dev):

@@ -60,6 +60,43 @@ def test_status_codes_for_bad_arguments_without_gpu(k2):
     assert lib.k2q_lora_grads_ws_bytes(4096, 3072, 3072, 8192) == 0
 
 
+# MI355X timings (us, one GEMM launch incl. epilogue) of each output tile shape on the shapes the chooser was
+# fitted to: (M, N, K) -> (fastest shape, its time, the 256x256 time).  The chooser must take the fastest.
+TILE_TIMINGS = {
+    (16896, 12288, 3072): ("256x320", 585.2, 609.1),     # cfg2
+    (4096, 3072, 3072): ("192x256", 42.7, 43.7),         # cfg0
+    (1024, 3072, 3072): ("128x128", 20.3, 36.8),         # cfg4 text out
+    (1024, 9216, 3072): ("192x256", 36.1, 39.7),         # cfg4 text qkv
+    (1024, 12288, 3072): ("192x256", 42.6, 43.1),        # cfg4 text up
+    (1024, 3072, 12288): ("128x128", 65.4, 67.2),        # cfg4 text down
+    (8192, 3072, 3072): ("192x256", 82.3, 84.4),         # cfg4 image out
+    (8192, 9216, 3072): ("256x320", 227.3, 228.6),       # cfg4 image qkv
+    (8192, 12288, 3072): ("256x256", 289.9, 289.9),      # cfg4 image up
+    (8192, 3072, 12288): ("192x256", 269.6, 287.2),      # cfg4 image down
+    (4608, 3072, 12288): ("256x256", 159.3, 159.3),      # cfg3 forward
+    (4608, 1536, 6144): ("128x128", 56.1, 67.4),         # d=6144 wk/wv, 2304+2304 tokens
+    (4608, 16384, 6144): ("256x320", 420.6, 422.1),      # d=6144 up
+    (16896, 6144, 6144): ("256x320", 547.6, 582.8),      # d=6144 wq, 16896 tokens
+}
+
+
+@pytest.mark.parametrize("shape", list(TILE_TIMINGS), ids=["x".join(map(str, s)) for s in TILE_TIMINGS])
+def test_gemm_plan_takes_the_fastest_measured_tile(k2, shape):
+    M, N, K = shape
+    tile, pieces = k2._lib.gemm_w8a8_plan(M, N, K, 256)
+    assert tile == TILE_TIMINGS[shape][0] and pieces >= 1
+
+
+def test_gemm_plan_edges(k2):
+    L = k2._lib
+    assert L.gemm_w8a8_plan(2, 18432, 3072) == ("gemv", 1)          # adaLN modulation: M <= 8
+    assert L.gemm_w8a8_plan(9, 512, 128)[0] in L.TILES
+    # a last round of 256x256 tiles that is cut along K: a GPU whose CUs the tiles fill a little over once
+    assert L.gemm_w8a8_plan(1024, 4608, 16384, 256) == ("256x256", 3)
+    with pytest.raises(RuntimeError):
+        L.gemm_w8a8_plan(4, 4, 100)
+
+
 def test_wrappers_validate_before_launch(k2):
     L = k2._lib
     with pytest.raises(ValueError):
