@@ -759,20 +759,41 @@ def measured_traffic(kernel_key: str):
         return None, False
 
 
-# Kernels of --profile-pass: (label, kernel-name substring, grid threads, algorithmic read, algorithmic write).
-def _profiled_kernels():
+# Output tile shapes of the GEMM kernel: plan name -> the TileCfg<TA, TB, waves along A, workgroups per CU> text
+# in the kernel's name, (TA, TB, workgroups per CU).
+_TILE_CFG = {"256x256": ("TileCfg<256, 256, 2, 1>", (256, 256, 1)), "256x320": ("TileCfg<256, 320, 4, 1>", (256, 320, 1)),
+             "192x256": ("TileCfg<192, 256, 2, 1>", (192, 256, 1)), "128x128": ("TileCfg<128, 128, 2, 2>", (128, 128, 2))}
+
+
+def _gemm_kernel(L, epi, M, N, K, grouped=False, cus=256):
+    """(kernel-name substrings, grid threads) of the one tile launch of a W8A8 GEMM (epi 0; K in int8 elements)
+    or of the input-gradient GEMM on the effective weight (epi 4; K in bytes: 2 x the bf16 reduction length) on
+    ``cus`` CUs, as the library schedules it: the shape the W8 plan picks for the same output and reduction bytes
+    (the two epilogues share the chooser), a balanced persistent grid of ceil(tiles / rounds) workgroups of 512
+    threads.  Split-K schedules are not profiled."""
+    tile, pieces = L.gemm_w8a8_plan(M, N, K, cus, grouped)
+    if pieces != 1:
+        raise ValueError(f"profiled GEMM {M}x{N}x{K} takes a split-K schedule")
+    name, (ta, tb, wpc) = _TILE_CFG[tile]
+    tiles = -(-N // ta) * -(-M // tb)
+    rounds = -(-tiles // (cus * wpc))
+    return (f"gemm_nt_kernel<{epi}, 0,", name), -(-tiles // rounds) * 512
+
+
+# Kernels of --profile-pass: (label, kernel-name substring(s), grid threads, algorithmic read, algorithmic write).
+def _profiled_kernels(L):
     M2, K2, N2, r2 = 16896, 3072, 12288, 32
     M3, K3, N3, r3 = 4608, 12288, 3072, 64
     Mi, Ki, Kh = 8192, 3072, 12288
     Mg, Kg, Ng, rg = 4608, 6144, 15360, 16
     copy = 1 << 28
     return [
-        ("gemm_nt_kernel<EPI_W8> cfg2", "gemm_nt_kernel<0, 0>", 124928,
+        ("gemm_nt_kernel<EPI_W8> cfg2", *_gemm_kernel(L, 0, M2, N2, K2),
          M2 * K2 + N2 * K2 + 4 * M2 + 4 * N2 + 4 * M2 * r2 + 4 * N2 * r2, 2 * M2 * N2),
         ("rotquant_kernel cfg2", "rotquant_kernel", 1081344, 2 * M2 * K2, M2 * K2 + 4 * M2),
         ("lora_down_as_kernel<2> cfg2", "lora_down_as_kernel<2>", None, 2 * M2 * K2 + 4 * r2 * K2, 3 * 4 * M2 * r2),
         ("lora_reduce_kernel cfg2", "lora_reduce_kernel", 135168, 3 * 4 * M2 * r2, 4 * M2 * r2),
-        ("gemm_nt_kernel<EPI_DXLIN> cfg3 (input gradient)", "gemm_nt_kernel<4, 0>", 110592,
+        ("gemm_nt_kernel<EPI_DXLIN> cfg3 (input gradient)", *_gemm_kernel(L, 4, M3, K3, 2 * N3),
          2 * M3 * N3 + 2 * K3 * N3 + 4 * M3 * r3 + 4 * r3 * K3, 2 * M3 * K3),
         ("rot_dequant_t_kernel cfg3 (effective weight)", "rot_dequant_t_kernel<false>", 1179648, N3 * K3 + 4 * N3,
          2 * K3 * N3),
@@ -780,13 +801,13 @@ def _profiled_kernels():
          2 * Mi * Ki, 2 * Mi * Ki + Mi * Ki + 4 * Mi),
         ("prodquant_kernel<SWIGLU> cfg4 image (M=8192, K=12288)", "prodquant_kernel<0, 4, 3, false>", 2097152,
          4 * Mi * Kh, 2 * Mi * Kh + Mi * Kh + 4 * Mi),
-        ("gemm_nt_kernel<EPI_W8> grouped attention inputs (M=4608)", "gemm_nt_kernel<0, 0>", 110592,
+        ("gemm_nt_kernel<EPI_W8> grouped attention inputs (M=4608)", *_gemm_kernel(L, 0, Mg, Ng, Kg, grouped=True),
          Mg * Kg + Ng * Kg + 4 * Mg + 4 * Ng + 4 * Mg * 4 * rg + 4 * Ng * rg, 2 * Mg * Ng),
         ("copy 256 MiB (hipMemcpy device to device)", "copyBuffer", 131072, copy, copy),
     ]
 
 
-def pmc_summary(fetch_dir: str, write_dir: str) -> None:
+def pmc_summary(k2, fetch_dir: str, write_dir: str) -> None:
     """Bytes per dispatch from two ``rocprofv3 --pmc FETCH_SIZE`` / ``--pmc WRITE_SIZE`` runs over
     ``--profile-pass`` (KiB counters, median over the dispatches), each scaled by what the counter reads for the
     pass's 256 MiB device copy; writes ``profiles/traffic_cfg2.json`` (stamped with the kernel sources' sha1)
@@ -804,8 +825,9 @@ def pmc_summary(fetch_dir: str, write_dir: str) -> None:
     F_, W_ = load(fetch_dir), load(write_dir)
 
     def find(sub, grid, d):
+        subs = (sub,) if isinstance(sub, str) else sub
         for (n, g), v in d.items():
-            if sub in n and (grid is None or g == grid):
+            if all(x in n for x in subs) and (grid is None or g == grid):
                 return v
         raise KeyError((sub, grid))
 
@@ -816,7 +838,7 @@ def pmc_summary(fetch_dir: str, write_dir: str) -> None:
            "calibration": {"copy_bytes": copy, "fetch_factor": ff, "write_factor": wf}, "kernels": {}}
     lines = ["| kernel | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM read bytes | HBM write bytes | "
              "algorithmic read / write bytes |", "|---|---|---|---|---|---|---|"]
-    for label, sub, grid, ar, aw in _profiled_kernels():
+    for label, sub, grid, ar, aw in _profiled_kernels(k2._lib):
         f, w = find(sub, grid, F_), find(sub, grid, W_)
         fk, wk = statistics.median(f), statistics.median(w)
         rb, wb = fk * 1024 * ff, wk * 1024 * wf
@@ -971,7 +993,8 @@ def main():
                     help="write profiles/traffic_cfg2.json from two rocprofv3 --pmc runs over --profile-pass")
     a = ap.parse_args()
     if a.pmc_summary:
-        pmc_summary(*a.pmc_summary)
+        import __graft_entry__ as ge
+        pmc_summary(ge.load_package(), *a.pmc_summary)
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus > 1 or world > 1:

@@ -175,8 +175,9 @@ int k2q_gemm_w4a8(const int8_t* qx, const float* sx, const uint8_t* qw4, const u
 
 /* The schedule k2q_gemm_w8a8 (and the W8 GEMM of k2q_linear_fwd) takes for an M x N x K problem on a GPU with
  * `cus` compute units: returns the K2Q_TILE_* shape (or K2Q_TILE_GEMV), and in *split_pieces (nullable) the
- * number of K-pieces its last round of 256x256 tiles is cut into (1 = none).  Host only: no device call. */
-int k2q_gemm_w8a8_plan(int64_t M, int64_t N, int64_t K, int cus, int* split_pieces);
+ * number of K-pieces its last round of 256x256 tiles is cut into (1 = none).  grouped != 0: the schedule of
+ * k2q_gemm_w8a8_grouped with N the segments' total out_features.  Host only: no device call. */
+int k2q_gemm_w8a8_plan(int64_t M, int64_t N, int64_t K, int cus, int grouped, int* split_pieces);
 
 /* Debug entries: raw int32 accumulators acc[m,n] = sum_k qx[m,k] qw[n,k] (W8), and for W4 the f32
  * value sum_g sw4[n,g] * acc_g[m,n] without s_x, 2^-7, bias or LoRA.  k2q_gemm_w8a8_tile is k2q_gemm_w8a8

@@ -66,7 +66,7 @@ _SIGNATURES = {
                         _i64, _p], _int),
     "k2q_gemm_w8a8_acc": ([_p, _p, _i64, _i64, _i64, _p, _p, _i64, _int, _p], _int),
     "k2q_gemm_w8a8_tile": ([_p, _p, _p, _p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p, _i64, _int, _p], _int),
-    "k2q_gemm_w8a8_plan": ([_i64, _i64, _i64, _int, ctypes.POINTER(_int)], _int),
+    "k2q_gemm_w8a8_plan": ([_i64, _i64, _i64, _int, _int, ctypes.POINTER(_int)], _int),
     "k2q_gemm_w4a8_f32": ([_p, _p, _p, _i64, _i64, _i64, _p, _p], _int),
     "k2q_quant_weight_fp8": ([_p, _int, _i64, _i64, _p, _p, _p], _int),
     "k2q_dequant_fp8": ([_p, _p, _i64, _i64, _int, _p, _p], _int),
@@ -467,11 +467,12 @@ TILES = {"auto": -1, "256x256": 0, "256x320": 1, "192x256": 2, "128x128": 3}   #
 _TILE_NAMES = {v: k for k, v in TILES.items()} | {4: "gemv"}
 
 
-def gemm_w8a8_plan(M: int, N: int, K: int, cus: int = 256) -> tuple[str, int]:
-    """The schedule ``k2q_gemm_w8a8`` takes for an M x N x K problem on a GPU with ``cus`` compute units:
-    (tile shape or "gemv", K-pieces of the last round of 256x256 tiles).  Host only."""
+def gemm_w8a8_plan(M: int, N: int, K: int, cus: int = 256, grouped: bool = False) -> tuple[str, int]:
+    """The schedule ``k2q_gemm_w8a8`` (``grouped``: ``k2q_gemm_w8a8_grouped``, N = the segments' total) takes for
+    an M x N x K problem on a GPU with ``cus`` compute units: (tile shape or "gemv", K-pieces of the last round
+    of 256x256 tiles).  Host only."""
     pieces = _int(0)
-    rc = load().k2q_gemm_w8a8_plan(M, N, K, cus, ctypes.byref(pieces))
+    rc = load().k2q_gemm_w8a8_plan(M, N, K, cus, int(grouped), ctypes.byref(pieces))
     if rc < 0:
         _check(rc, "k2q_gemm_w8a8_plan")
     return _TILE_NAMES[rc], pieces.value

@@ -1201,13 +1201,14 @@ extern "C" int k2q_gemm_w8a8_tile(const int8_t* qx, const float* sx, const int8_
   return launch_gemm<EPI_W8>(p, ws, ws_bytes, static_cast<hipStream_t>(stream), tile);
 }
 
-extern "C" int k2q_gemm_w8a8_plan(int64_t M, int64_t N, int64_t K, int cus, int* split_pieces) {
+extern "C" int k2q_gemm_w8a8_plan(int64_t M, int64_t N, int64_t K, int cus, int grouped, int* split_pieces) {
   if (M < 1 || N < 1 || K < K2Q_HADAMARD || K % K2Q_HADAMARD || cus < 1) return K2Q_EINVAL;
   if (M <= K2Q_GEMV_MAX_M) {
+    if (grouped) return K2Q_EINVAL;
     if (split_pieces) *split_pieces = 1;
     return K2Q_TILE_GEMV;
   }
-  const TileChoice c = choose_tile(EPI_W8, N, M, K, false, TILE_AUTO, cus);
+  const TileChoice c = choose_tile(EPI_W8, N, M, K, grouped != 0, TILE_AUTO, cus);
   if (split_pieces) *split_pieces = c.tile == TILE_256 ? c.split.s : 1;
   return c.tile;
 }

@@ -93,6 +93,9 @@ def test_gemm_plan_edges(k2):
     assert L.gemm_w8a8_plan(9, 512, 128)[0] in L.TILES
     # a last round of 256x256 tiles that is cut along K: a GPU whose CUs the tiles fill a little over once
     assert L.gemm_w8a8_plan(1024, 4608, 16384, 256) == ("256x256", 3)
+    # grouped launches take no 192-row tiles (segments start on 256- or 128-row boundaries)
+    assert L.gemm_w8a8_plan(4096, 3072, 3072) == ("192x256", 1)
+    assert L.gemm_w8a8_plan(4096, 3072, 3072, grouped=True)[0] != "192x256"
     with pytest.raises(RuntimeError):
         L.gemm_w8a8_plan(4, 4, 100)
 
