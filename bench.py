@@ -323,12 +323,12 @@ def run_cfg3(k2, steps, dev, settle_s=0.0, cpu=False):
     prev = _no_input_reuse(k2)
     try:
         settle(step, settle_s)
-        ms = time_loop(step, steps)
+        ms = time_loop(step, steps)             # the frozen base's effective weight resident (the default)
         with torch.no_grad():
             ms_fwd = time_loop(lambda: layer(x), steps)
-        k2.set_dx_weight_cache(layer, True)     # the frozen base's effective weight kept between backwards
-        ms_cached = time_loop(step, steps)
-        k2.set_dx_weight_cache(layer, False)
+        k2.set_dx_weight_cache(layer, False)    # every backward builds its effective weight
+        ms_per_call = time_loop(step, steps)
+        k2.set_dx_weight_cache(layer, True)
     finally:
         k2.quantize.shared_input_quant.enabled = prev
 
@@ -375,7 +375,7 @@ def run_cfg3(k2, steps, dev, settle_s=0.0, cpu=False):
                                            INT8_PEAK_TOPS, "TOPS"),
             "dx_weight_roofline": roofline_entry("rot_dequant_t_kernel (effective weight)", "hbm", prep_gbs,
                                                  HBM_PEAK_GBS, "GB/s"),
-            "step_ms_dx_weight_cached": round(ms_cached, 4),
+            "step_ms_dx_weight_per_call": round(ms_per_call, 4),
             "reference_fp8_step_ms_gpu": round(ms_ref, 4),
             **({"cpu": cpu_cfg3(*_layer_tensors(layer, 3, c["K"], c["N"]))} if cpu else {})}
 
@@ -466,11 +466,13 @@ def run_krea_block(k2, steps, dev):
     """The quantized-linear work of one Krea 2 single-stream block at 1024^2 (M = 4608, width 6144, 48 heads
     of 128 with 12 KV heads, SwiGLU 16384; mmdit.py:164-212,294-319), LoRA r=16 on all eight linears: the
     modulated RMSNorm, wq/wk/wv/gate, wo, the second modulated RMSNorm, mlp.gate/up, the SwiGLU product and
-    mlp.down, with the residual adds and gates.  Attention itself is left out: `q * sigmoid(gate)` stands in
-    for `attention(q, k, v) * sigmoid(gate)` (same shapes into wo), so the time is the linears, their
-    producers and the elementwise glue.  Timed forward (no_grad) and forward + backward, as the reference
+    mlp.down, with the residual adds and gates.  Attention itself is left out: each KV head's `k * v` added to
+    its four query heads, times `sigmoid(gate)`, stands in for `attention(q, k, v) * sigmoid(gate)` (same
+    shapes into wo, and gradients reach wq, wk, wv and gate as attention's do), so the time is the linears,
+    their producers and the elementwise glue.  Timed forward (no_grad) and forward + backward, as the reference
     computes the producers (torch eager ops, every linear quantizing its own input or hitting the
-    shared-input cache) against fuse_producers' kernels plus group_siblings' grouped attention inputs."""
+    shared-input cache) against fuse_producers' kernels plus group_siblings' groups (attention inputs and
+    SwiGLU gate / up: one grouped forward launch and one input-gradient GEMM each)."""
     import types
 
     from krea2_amd import fused
@@ -499,8 +501,10 @@ def run_krea_block(k2, steps, dev):
     def block(x, fuse):
         ps, sh, pg, qs, qsh, qg = (vec + lin).chunk(6, dim=-1)
         h = fused.modulated_rmsnorm(pre, x, ps, sh) if fuse else (1 + ps) * rms(pre, x) + sh
-        q, _k, _v, gt = attn.wq(h), attn.wk(h), attn.wv(h), attn.gate(h)
-        x = x + pg * attn.wo(q * torch.sigmoid(gt))
+        q, k, v, gt = attn.wq(h), attn.wk(h), attn.wv(h), attn.gate(h)
+        # attention stand-in: every KV head's k * v added to its 4 query heads (GQA 48 / 12 of 128)
+        o = (q.unflatten(-1, (KV // 128, -1, 128)) + (k * v).unflatten(-1, (KV // 128, 1, 128))).flatten(-3)
+        x = x + pg * attn.wo(o * torch.sigmoid(gt))
         h = fused.modulated_rmsnorm(post, x, qs, qsh) if fuse else (1 + qs) * rms(post, x) + qsh
         a, b = mlp.gate(h), mlp.up(h)
         return x + qg * mlp.down(fused.swiglu(a, b) if fuse else F_.silu(a) * b)
@@ -512,7 +516,7 @@ def run_krea_block(k2, steps, dev):
     out = {}
     for fuse in (False, True):
         if fuse:
-            fused.group_siblings(types.SimpleNamespace(blocks=[types.SimpleNamespace(attn=attn)]))
+            fused.group_siblings(types.SimpleNamespace(blocks=[types.SimpleNamespace(attn=attn, mlp=mlp)]))
         with torch.no_grad():
             t_f = sorted(time_loop(lambda: block(x0, fuse), steps) for _ in range(3))[1]
         t_fb = sorted(time_loop(lambda: fwd_bwd(fuse), max(3, steps // 2)) for _ in range(3))[1]

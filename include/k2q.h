@@ -229,6 +229,24 @@ int k2q_gemm_bf16(const uint16_t* x, const uint16_t* w, const float* bias, const
 int k2q_gemm_dx_lin(const uint16_t* dy, const uint16_t* wt, int64_t M, int64_t N, int64_t K, const float* g,
                     const float* lora_a, int64_t r, uint16_t* dx, void* ws, int64_t ws_bytes, void* stream);
 
+/* Grouped input gradient: the linears that read one input (wq/wk/wv/gate of Attention.forward, mmdit.py:199;
+ * gate/up of SwiGLU.forward, mmdit.py:178), whose input gradients autograd would add at the shared input, as
+ * one GEMM whose reduction runs over the segments in turn:
+ *   dx = bf16(sum_i dy_i wt_i^T + g A),
+ * segment i the gradient dy_i of linear i's output (M x N_i bf16, rows of ldy_i elements) and its effective
+ * weight wt_i (K x N_i bf16 from k2q_dx_prep_eff, row stride N_i); g (M x r f32, rows of ldg) and lora_a
+ * (r x K f32) the members' LoRA terms stacked along the rank (nullable).  1 <= nseg <= 4, every N_i a
+ * multiple of 64, ldy_i a multiple of 8, K % 64 == 0.  One f32 sum per output element, rounded once
+ * (separate k2q_gemm_dx_lin calls round each member's dx to bf16 before autograd adds them). */
+typedef struct {
+  const uint16_t* dy;     /* M x N bf16, row stride ldy */
+  int64_t ldy;
+  const uint16_t* wt;     /* K x N bf16, row stride N */
+  int64_t N;
+} k2q_dx_segment;
+int k2q_gemm_dx_grouped(const k2q_dx_segment* seg, int64_t nseg, int64_t M, int64_t K, const float* g, int64_t ldg,
+                        const float* lora_a, int64_t r, uint16_t* dx, void* stream);
+
 
 #ifdef __cplusplus
 }

@@ -33,6 +33,11 @@ _int = ctypes.c_int
 _f32 = ctypes.c_float
 
 
+class DxSegment(ctypes.Structure):
+    """``k2q_dx_segment`` of ``include/k2q.h``: one linear of a grouped input gradient."""
+    _fields_ = [("dy", ctypes.c_void_p), ("ldy", ctypes.c_int64), ("wt", ctypes.c_void_p), ("N", ctypes.c_int64)]
+
+
 class W8A8Segment(ctypes.Structure):
     """``k2q_w8a8_segment`` of ``include/k2q.h``: one linear of a grouped forward."""
     _fields_ = [("qw", ctypes.c_void_p), ("sw", ctypes.c_void_p), ("bias", ctypes.c_void_p),
@@ -77,6 +82,7 @@ _SIGNATURES = {
     "k2q_dx_prep_eff": ([_p, _p, _p, _p, _i64, _i64, _p, _p], _int),
     "k2q_gemm_dx_ws_bytes": ([_i64, _i64, _i64], _i64),
     "k2q_gemm_dx": ([_p, _p, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _p], _int),
+    "k2q_gemm_dx_grouped": ([_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _p], _int),
 }
 EXPORTS = tuple(_SIGNATURES)
 
@@ -731,6 +737,50 @@ def gemm_dx(dy, qw, sw, *, w4: bool = False, g=None, lora_a=None, split: bool = 
     gemm = lib.k2q_gemm_dx_lin if fold_rotation else lib.k2q_gemm_dx
     _check(gemm(_ptr(dy), _ptr(wt), M, N, K, _ptr(g), _ptr(lora_a) if r else None, r, _ptr(dx),
                 _ptr(ws), nws, st), "k2q_gemm_dx")
+    return dx
+
+
+def gemm_dx_grouped(segments, g=None, lora_a=None) -> torch.Tensor:
+    """Input gradient of linears that share their input, in one GEMM: ``dx = bf16(sum_i dy_i wt_i^T + g A)``.
+    ``segments``: ``(dy_i, wt_i)`` with ``dy_i`` (M, N_i) bf16 (row stride a multiple of 8, unit column
+    stride) and ``wt_i`` (K, N_i) bf16 from :func:`dx_weight`; ``g`` (M, r) f32 (row stride a multiple of 4)
+    and ``lora_a`` (r, K) f32 the members' LoRA terms stacked along the rank, or None."""
+    if not 1 <= len(segments) <= GROUP_MAX:
+        raise ValueError(f"a grouped input gradient takes 1..{GROUP_MAX} segments, got {len(segments)}")
+    dy0, wt0 = segments[0]
+    if not isinstance(dy0, torch.Tensor) or dy0.dim() != 2 or not isinstance(wt0, torch.Tensor) or wt0.dim() != 2:
+        raise ValueError("segments must be (dy (M, N_i), wt (K, N_i)) tensor pairs")
+    dev = dy0.device
+    M = dy0.shape[0]
+    K = wt0.shape[0]
+    arr = (DxSegment * len(segments))()
+    for i, (dy, wt) in enumerate(segments):
+        if dy.dtype != torch.bfloat16 or dy.dim() != 2 or dy.device != dev or dy.stride(1) != 1 \
+                or dy.stride(0) % 8 or dy.data_ptr() % 16:
+            raise ValueError(f"dy[{i}] must be (M, N) bf16 on {dev} with unit column stride and 16-byte rows")
+        _need(wt, f"wt[{i}]", torch.bfloat16, 2, dev)
+        N = dy.shape[1]
+        if dy.shape[0] != M or wt.shape != (K, N):
+            raise ValueError(f"segment {i}: dy {tuple(dy.shape)} / wt {tuple(wt.shape)} do not match M={M}, K={K}")
+        if N % 64:
+            raise ValueError(f"segment {i}: out_features={N} must be a multiple of 64")
+        arr[i] = DxSegment(dy.data_ptr(), dy.stride(0), wt.data_ptr(), N)
+    _check_k(K)
+    r, ldg = 0, 0
+    if g is not None:
+        if g.dtype != torch.float32 or g.dim() != 2 or g.device != dev or g.shape[0] != M or g.stride(1) != 1 \
+                or g.stride(0) % 4 or g.data_ptr() % 16:
+            raise ValueError("g must be (M, r) f32 with unit column stride and 16-byte rows")
+        _need(lora_a, "lora_A", torch.float32, 2, dev)
+        r, ldg = g.shape[1], g.stride(0)
+        if lora_a.shape != (r, K):
+            raise ValueError("lora_A must be (r, K) for g of r columns")
+        _check_rank(r)
+    _device_check(dev)
+    dx = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+    _check(load().k2q_gemm_dx_grouped(ctypes.addressof(arr), len(segments), M, K, _ptr(g), ldg,
+                                      _ptr(lora_a) if r else None, r, _ptr(dx), _stream(dev)),
+           "k2q_gemm_dx_grouped")
     return dx
 
 

@@ -46,6 +46,15 @@ struct GemmSeg {
   float lora_scale;
 };
 
+// One segment of a segmented reduction (EPI_DXLIN): stages end_prev .. end-1 of the reduction read A from a and
+// B from b with their own row strides.
+struct KSeg {
+  const uint8_t* a;
+  const uint8_t* b;
+  int64_t lda_b, ldb_b;
+  int end;                 // first stage (WBK reduction bytes) past this segment
+};
+
 struct GemmArgs {
   const uint8_t* a;   // A operand, rows_a x kbytes, row stride lda_b bytes
   const uint8_t* b;   // B operand, rows_b x kbytes
@@ -63,6 +72,8 @@ struct GemmArgs {
   float lora_scale;
   int nseg;           // 0: one linear; else rows_a stacks nseg segments (EPI_W8)
   GemmSeg seg[MAX_SEG];
+  int nks;            // 0: one reduction operand pair; else the reduction runs over nks segments (EPI_DXLIN)
+  KSeg ks[MAX_SEG];
   // Split schedule for the last, partly filled round of tiles: tiles 0 .. dp_tiles-1 run over the full
   // reduction; each of the sk_rem remainder tiles dp_tiles + i is cut into sk_s pieces (piece q covers
   // reduction slice q / sk_rem) whose accumulators go to part, and a fixup launch adds them.
@@ -273,14 +284,15 @@ __device__ __forceinline__ void wait_vmcnt() {
 // to it); outstanding global loads, the LDS-DMA prefetches among them, are not waited for.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-enum { MODE_TILE = 0, MODE_PIECE = 1, MODE_FIXUP = 2 };
+enum { MODE_TILE = 0, MODE_PIECE = 1, MODE_FIXUP = 2, MODE_KSEG = 3 };
 
 // MODE_TILE: full-K tiles 0 .. dp_tiles-1 with their epilogues; workgroup b takes tiles r * gridDim.x + b'
 // (b' its XCD-remapped id) for rounds r = 0, 1, ... while they exist, so the launch can use fewer
 // workgroups than CUs and give each the same number of tiles.  MODE_PIECE: one piece of a remainder tile,
 // accumulators parked in part.  MODE_FIXUP: the pieces of remainder tile dp_tiles + blockIdx.x added in
-// slice order, then the epilogue.  Separate kernels, so the register allocation of the tile kernel is not
-// shared with the other paths.  The split modes run T256 tiles only.
+// slice order, then the epilogue.  MODE_KSEG: MODE_TILE over a segmented reduction (the grouped input
+// gradient: the operand pair changes at segment boundaries).  Separate kernels, so the register allocation of
+// the tile kernel is not shared with the other paths.  The split modes run T256 tiles only.
 template <int EPI, int MODE, class C>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& p, int64_t lid, int kbeg, int nk);
 
@@ -383,34 +395,65 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
   // Per-lane source offsets (bytes from the tile's first row) of the DMA instructions: LDS rows
   // 8 (D wave + i) + lane/8; rows past the matrix end are clamped onto its last row (never stored).
   uint32_t offa[C::DA], offb[C::DB];
+  const uint8_t* gA;
+  const uint8_t* gB;
+  auto bind = [&](const uint8_t* a, const uint8_t* b, int64_t lda, int64_t ldb) {
 #pragma unroll
-  for (int i = 0; i < C::DA; ++i) {
-    const int lrow = 8 * (C::DA * wave + i) + (lane >> 3);
-    int64_t ra = lrow;
-    ra = A0 + ra < p.rows_a ? ra : p.rows_a - 1 - A0;
-    offa[i] = (uint32_t)(ra * p.lda_b) + 16u * (uint32_t)((lane & 7) ^ swz(lrow));
-  }
+    for (int i = 0; i < C::DA; ++i) {
+      const int lrow = 8 * (C::DA * wave + i) + (lane >> 3);
+      int64_t ra = lrow;
+      ra = A0 + ra < p.rows_a ? ra : p.rows_a - 1 - A0;
+      offa[i] = (uint32_t)(ra * lda) + 16u * (uint32_t)((lane & 7) ^ swz(lrow));
+    }
 #pragma unroll
-  for (int i = 0; i < C::DB; ++i) {
-    const int lrow = 8 * (C::DB * wave + i) + (lane >> 3);
-    int64_t rb = lrow;
-    rb = B0 + rb < p.rows_b ? rb : p.rows_b - 1 - B0;
-    offb[i] = (uint32_t)(rb * p.ldb_b) + 16u * (uint32_t)((lane & 7) ^ swz(lrow));
+    for (int i = 0; i < C::DB; ++i) {
+      const int lrow = 8 * (C::DB * wave + i) + (lane >> 3);
+      int64_t rb = lrow;
+      rb = B0 + rb < p.rows_b ? rb : p.rows_b - 1 - B0;
+      offb[i] = (uint32_t)(rb * ldb) + 16u * (uint32_t)((lane & 7) ^ swz(lrow));
+    }
+    gA = a + A0 * lda + (int64_t)kbeg * SBK;
+    gB = b + B0 * ldb + (int64_t)kbeg * SBK;
+  };
+  // Segmented reduction (full-K tiles of EPI_DXLIN only): stage st of segment j reads its operands at stage
+  // st - kbase; seek(st) moves to st's segment.  The stages passed to seek increase by at most one per call
+  // and every segment holds at least one stage, so one step per call reaches it.
+  constexpr bool KSEGS = (MODE == MODE_KSEG);
+  int kseg = 0, kbase = 0, kend = 0x7fffffff;
+  auto bind_seg = [&](int j) {   // j is workgroup-uniform; constant indices keep the fields argument loads
+    const KSeg* sp = &p0.ks[0];
+#pragma unroll
+    for (int i = 1; i < MAX_SEG; ++i) sp = j == i ? &p0.ks[i] : sp;
+    bind(sp->a, sp->b, sp->lda_b, sp->ldb_b);
+    kend = sp->end;
+  };
+  if constexpr (KSEGS) {
+    if (p0.nks > 0) bind_seg(0);
+    else bind(p.a, p.b, p.lda_b, p.ldb_b);
+  } else {
+    bind(p.a, p.b, p.lda_b, p.ldb_b);
   }
-  const uint8_t* gA = p.a + A0 * p.lda_b + (int64_t)kbeg * SBK;
-  const uint8_t* gB = p.b + B0 * p.ldb_b + (int64_t)kbeg * SBK;
+  auto seek = [&](int st) {
+    if constexpr (KSEGS) {
+      if (st >= kend) {
+        kbase = kend;
+        bind_seg(++kseg);
+      }
+    }
+  };
   uint8_t* ldsa = smem + 1024 * C::DA * wave;            // this wave's DMA rows inside a stage
   uint8_t* ldsb = smem + TA * WBK + 1024 * C::DB * wave;
 
   // DMA of stage st (128 reduction bytes) into LDS slot `slot`.
   auto issue = [&](int st, int slot) {
+    const int64_t so = (int64_t)(st - kbase) * WBK;
 #pragma unroll
     for (int i = 0; i < C::DA; ++i)
-      __builtin_amdgcn_global_load_lds(K2Q_GPTR(gA + (int64_t)st * WBK + offa[i]),
+      __builtin_amdgcn_global_load_lds(K2Q_GPTR(gA + so + offa[i]),
                                        K2Q_LPTR(ldsa + slot * C::STAGE + 1024 * i), 16, 0, 0);
 #pragma unroll
     for (int i = 0; i < C::DB; ++i)
-      __builtin_amdgcn_global_load_lds(K2Q_GPTR(gB + (int64_t)st * WBK + offb[i]),
+      __builtin_amdgcn_global_load_lds(K2Q_GPTR(gB + so + offb[i]),
                                        K2Q_LPTR(ldsb + slot * C::STAGE + 1024 * i), 16, 0, 0);
   };
   // Fragments of substep kk (32 reduction bytes) of the stage in LDS slot `slot`.
@@ -484,12 +527,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
       if constexpr (NR > NI) __builtin_amdgcn_sched_group_barrier(0x100, NR - NI, 0);
     };
     issue(0, 0);
+    seek(ns > 1 ? 1 : 0);
     issue(ns > 1 ? 1 : 0, 1);
     wait_vmcnt<G>();           // stage 0 (stage 1 may be in flight)
     lds_barrier();
     read_frags(0, 0, f0a, f0b);
     for (int st = 0; st < ns; ++st) {
       const int sl = st & 1;
+      seek(st + 2 < ns ? st + 2 : ns - 1);   // the segment of the stage this iteration's DMA fetches
       read_frags(sl, 1, f1a, f1b);
       sub(f0a, f0b);
       read_frags(sl, 2, f0a, f0b);
@@ -1044,10 +1089,12 @@ double tile_cost(int64_t rows_a, int64_t rows_b, int nk, int cus, double stage_c
   return (double)full * round(slots) + (rem ? round(rem) : 0.0);
 }
 
-TileChoice choose_tile(int epi, int64_t rows_a, int64_t rows_b, int64_t kbytes, bool grouped, int forced, int cus) {
+// allowed: bit t set = tile shape t may be chosen; can_split: T256 may cut its last round along K.
+TileChoice choose_tile(int epi, int64_t rows_a, int64_t rows_b, int64_t kbytes, unsigned allowed, bool can_split,
+                       int forced, int cus) {
   const int nk = (int)(kbytes / SBK);
   const int64_t tiles256 = ((rows_a + 255) / 256) * ((rows_b + 255) / 256);
-  TileChoice c{TILE_256, grouped ? SplitPlan{tiles256, 0, 1, 0.0} : split_plan(tiles256, nk, cus)};
+  TileChoice c{TILE_256, can_split ? split_plan(tiles256, nk, cus) : SplitPlan{tiles256, 0, 1, 0.0}};
   if (forced >= 0) {
     c.tile = forced;
     if (forced != TILE_256) c.split = SplitPlan{0, 0, 1, 0.0};
@@ -1055,14 +1102,25 @@ TileChoice choose_tile(int epi, int64_t rows_a, int64_t rows_b, int64_t kbytes, 
   }
   if (epi == EPI_DX) return c;
   double best = c.split.s > 1 ? c.split.cost : tile_cost<T256>(rows_a, rows_b, nk, cus, 1.0, 1.0, 8.0);
-  const double t320 = tile_cost<T320>(rows_a, rows_b, nk, cus, 1.25, 1.25, 8.0);
-  const double t192 = grouped ? 1e300 : tile_cost<T192>(rows_a, rows_b, nk, cus, 0.80, 0.80, 7.0);
-  const double t128 = tile_cost<T128>(rows_a, rows_b, nk, cus, 0.60, 0.30, 4.0);
+  const double t320 = allowed >> TILE_320 & 1 ? tile_cost<T320>(rows_a, rows_b, nk, cus, 1.25, 1.25, 8.0) : 1e300;
+  const double t192 = allowed >> TILE_192 & 1 ? tile_cost<T192>(rows_a, rows_b, nk, cus, 0.80, 0.80, 7.0) : 1e300;
+  const double t128 = allowed >> TILE_128 & 1 ? tile_cost<T128>(rows_a, rows_b, nk, cus, 0.60, 0.30, 4.0) : 1e300;
   if (t320 < best) { best = t320; c.tile = TILE_320; }
   if (t192 < best) { best = t192; c.tile = TILE_192; }
   if (t128 < best) { best = t128; c.tile = TILE_128; }
   if (c.tile != TILE_256) c.split = SplitPlan{0, 0, 1, 0.0};
   return c;
+}
+
+// The tile shapes and split a launch may take: grouped forwards (row segments on 256- or 128-row boundaries)
+// no 192-row tiles and no split; segmented reductions no split (a piece would start inside a segment) and no
+// 256 x 320 tiles (that kernel variant spills registers).
+constexpr unsigned ALL_TILES = (1u << TILE_COUNT) - 1;
+unsigned allowed_tiles(bool grouped, bool ksegs) {
+  unsigned m = ALL_TILES;
+  if (grouped) m &= ~(1u << TILE_192);
+  if (ksegs) m &= ~(1u << TILE_320);
+  return m;
 }
 
 // Workspace for any schedule an entry may take: the T256 split plan's pieces (used when the launch runs T256
@@ -1082,21 +1140,32 @@ int set_lds() {
 // Balanced persistent grid: as many rounds as the tiles need on this GPU's workgroup slots, and just enough
 // workgroups for that many rounds, each taking the same number of tiles (3168 T256 tiles on 256 CUs: 244
 // workgroups of 13), instead of a last round that leaves most CUs idle.
-template <int EPI, class C>
+template <int EPI, class C, int MODE = MODE_TILE>
 int launch_tiles(const GemmArgs& p, hipStream_t st) {
-  if (int rc = set_lds<EPI, MODE_TILE, C>()) return rc;
+  if (int rc = set_lds<EPI, MODE, C>()) return rc;
   const int64_t slots = (int64_t)k2q_cu_count() * C::WPC;
   const int64_t rounds = (p.dp_tiles + slots - 1) / slots;
   const int64_t nwg = (p.dp_tiles + rounds - 1) / rounds;
-  hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_TILE, C>), dim3((unsigned)nwg), dim3(GT), C::LDS, st, p);
+  hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE, C>), dim3((unsigned)nwg), dim3(GT), C::LDS, st, p);
   return K2Q_OK;
+}
+
+// Full-K tiles: the segmented-reduction kernel when the launch has reduction segments (EPI_DXLIN only).
+template <int EPI, class C>
+int launch_full(const GemmArgs& p, hipStream_t st) {
+  if constexpr (EPI == EPI_DXLIN) {
+    if (p.nks > 0) return launch_tiles<EPI, C, MODE_KSEG>(p, st);
+  }
+  return launch_tiles<EPI, C>(p, st);
 }
 
 template <int EPI>
 int launch_gemm(GemmArgs p, void* ws, int64_t ws_bytes, hipStream_t st, int forced = TILE_AUTO) {
   if (p.ldr == 0) p.ldr = p.r;
   if (forced >= TILE_COUNT || (EPI == EPI_DX && forced >= 0 && forced != TILE_256)) return K2Q_EINVAL;
-  TileChoice c = choose_tile(EPI, p.rows_a, p.rows_b, p.kbytes, p.nseg > 0, forced, k2q_cu_count());
+  TileChoice c = choose_tile(EPI, p.rows_a, p.rows_b, p.kbytes, allowed_tiles(p.nseg > 0, p.nks > 0),
+                             p.nseg == 0 && p.nks == 0, forced, k2q_cu_count());
+  if (forced >= 0 && !(allowed_tiles(p.nseg > 0, p.nks > 0) >> forced & 1)) return K2Q_EINVAL;
   if (p.nseg > 0) {   // segments start on tile boundaries
     const int ta = c.tile == TILE_192 ? 192 : c.tile == TILE_128 ? 128 : 256;
     for (int i = 0; i < p.nseg; ++i)
@@ -1115,9 +1184,9 @@ int launch_gemm(GemmArgs p, void* ws, int64_t ws_bytes, hipStream_t st, int forc
     if constexpr (EPI == EPI_DX) {
       rc = K2Q_EINVAL;
     } else {
-      if (c.tile == TILE_320) rc = launch_tiles<EPI, T320>(p, st);
-      else if (c.tile == TILE_192) rc = launch_tiles<EPI, T192>(p, st);
-      else rc = launch_tiles<EPI, T128>(p, st);
+      if (c.tile == TILE_320) rc = launch_full<EPI, T320>(p, st);
+      else if (c.tile == TILE_192) rc = launch_full<EPI, T192>(p, st);
+      else rc = launch_full<EPI, T128>(p, st);
     }
     return rc ? rc : k2q_launch_status();
   }
@@ -1136,7 +1205,7 @@ int launch_gemm(GemmArgs p, void* ws, int64_t ws_bytes, hipStream_t st, int forc
     if ((rc = set_lds<EPI, MODE_PIECE, T256>()) || (rc = set_lds<EPI, MODE_FIXUP, T256>())) return rc;
     hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_PIECE, T256>), dim3((unsigned)(q.rem * q.s)), dim3(GT), T256::LDS, st, p);
   }
-  if (q.dp_tiles > 0 && (rc = launch_tiles<EPI, T256>(p, st))) return rc;
+  if (q.dp_tiles > 0 && (rc = launch_full<EPI, T256>(p, st))) return rc;
   if (q.s > 1) hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_FIXUP, T256>), dim3((unsigned)q.rem), dim3(GT), T256::LDS, st, p);
   return k2q_launch_status();
 }
@@ -1208,7 +1277,7 @@ extern "C" int k2q_gemm_w8a8_plan(int64_t M, int64_t N, int64_t K, int cus, int 
     if (split_pieces) *split_pieces = 1;
     return K2Q_TILE_GEMV;
   }
-  const TileChoice c = choose_tile(EPI_W8, N, M, K, grouped != 0, TILE_AUTO, cus);
+  const TileChoice c = choose_tile(EPI_W8, N, M, K, allowed_tiles(grouped != 0, false), grouped == 0, TILE_AUTO, cus);
   if (split_pieces) *split_pieces = c.tile == TILE_256 ? c.split.s : 1;
   return c.tile;
 }
@@ -1326,6 +1395,33 @@ extern "C" int k2q_gemm_dx_lin(const uint16_t* dy, const uint16_t* wt, int64_t M
   p.out = dx; p.ldo = K;
   p.lora_rb = g; p.lora_ra = lora_a; p.r = g ? (int)r : 0; p.lora_scale = 1.f;
   return launch_gemm<EPI_DXLIN>(p, ws, ws_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int k2q_gemm_dx_grouped(const k2q_dx_segment* seg, int64_t nseg, int64_t M, int64_t K, const float* g,
+                                   int64_t ldg, const float* lora_a, int64_t r, uint16_t* dx, void* stream) {
+  if (!seg || nseg < 1 || nseg > MAX_SEG || M < 1 || K < 64 || K % 64 || !dx || !k2q_aligned(dx, 16))
+    return K2Q_EINVAL;
+  GemmArgs p{};
+  int64_t stages = 0;
+  for (int64_t i = 0; i < nseg; ++i) {
+    const k2q_dx_segment& sg = seg[i];
+    if (!sg.dy || !sg.wt || sg.N < 64 || sg.N % 64 || sg.ldy < sg.N || sg.ldy % 8 || !k2q_aligned(sg.dy, 16) ||
+        !k2q_aligned(sg.wt, 16))
+      return K2Q_EINVAL;
+    stages += 2 * sg.N / WBK;
+    if (stages > 0x3fffffff) return K2Q_EUNSUPPORTED;
+    p.ks[i] = KSeg{reinterpret_cast<const uint8_t*>(sg.wt), reinterpret_cast<const uint8_t*>(sg.dy), 2 * sg.N,
+                   2 * sg.ldy, (int)stages};
+  }
+  int rc = check_lora(g, lora_a, r);
+  if (rc) return rc;
+  if (g && (ldg < r || ldg % 4)) return K2Q_EINVAL;
+  p.nks = (int)nseg;
+  p.a = p.ks[0].a; p.b = p.ks[0].b; p.lda_b = p.ks[0].lda_b; p.ldb_b = p.ks[0].ldb_b;
+  p.rows_a = K; p.rows_b = M; p.kbytes = stages * WBK;
+  p.out = dx; p.ldo = K;
+  p.lora_rb = g; p.lora_ra = lora_a; p.r = g ? (int)r : 0; p.ldr = g ? (int)ldg : 0; p.lora_scale = 1.f;
+  return launch_gemm<EPI_DXLIN>(p, nullptr, 0, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int k2q_gemm_w4a8(const int8_t* qx, const float* sx, const uint8_t* qw4, const uint16_t* sw4,

@@ -193,8 +193,10 @@ def _state_key(m):
 class _GroupedFn(torch.autograd.Function):
     """Forward: one LoRA down-projection over the stacked adapters (``u = x [A_0; A_1; ..]^T``) and one grouped
     GEMM (``k2q_gemm_w8a8_grouped``) giving every member's output, each bit-identical to the member's own
-    fused forward.  Backward: per member, the LoRA gradients and ``dX`` as ``_ConvRotLinearFn`` computes them;
-    the members' ``dX`` are added (the accumulation autograd performs at the shared input)."""
+    fused forward.  Backward: per member, the LoRA gradients as ``_ConvRotLinearFn`` computes them; ``dX`` of
+    all members in one GEMM (``k2q_gemm_dx_grouped``) whose reduction runs over every member's output gradient
+    and effective weight, with the members' LoRA terms stacked along the rank: the sum autograd would form at
+    the shared input, in f32 and rounded once."""
 
     @staticmethod
     def forward(ctx, x2, qx, sx, bases, scales, *ab):
@@ -209,6 +211,7 @@ class _GroupedFn(torch.autograd.Function):
                 segs.append((base.qweight, base.weight_scale, base._bias_f32(), Bs[li], li * r, sc))
                 li += 1
         ys = _lib.gemm_w8a8_grouped(qx, sx, segs, u)
+        ctx.set_materialize_grads(False)    # an output nothing used gets no gradient pass (None, not zeros)
         ctx.bases, ctx.scales, ctx.r, ctx.nl = bases, scales, r, len(As)
         ctx.save_for_backward(x2 if As else None, u, *As, *Bs)
         return tuple(ys)
@@ -219,23 +222,28 @@ class _GroupedFn(torch.autograd.Function):
         nl, r = ctx.nl, ctx.r
         As, Bs = ab[:nl], ab[nl:]
         grads = [None] * (2 * nl)
-        dx, li = None, 0
+        segs, gs, ga, li = [], [], [], 0
         for i, (base, sc) in enumerate(zip(ctx.bases, ctx.scales)):
             dy, has = dys[i], sc is not None
             if dy is not None:
                 dy = dy.contiguous()
                 if dy.dtype != torch.bfloat16:
                     dy = dy.to(torch.bfloat16)
-                g = None
                 if has:
                     need_a, need_b = ctx.needs_input_grad[5 + 2 * li], ctx.needs_input_grad[6 + 2 * li]
                     u_i = u[:, li * r:(li + 1) * r].contiguous() if need_b else None
                     g, grads[2 * li], grads[2 * li + 1] = _lib.lora_grads(dy, x2 if need_a else None, u_i, Bs[li], sc)
+                    gs.append(g)
+                    ga.append(As[li])
                 if ctx.needs_input_grad[0]:
-                    d = _lib.gemm_dx(dy, base.qweight, base.weight_scale, w4=False, g=g,
-                                     lora_a=As[li] if has else None, wt=base.cached_dx_weight())
-                    dx = d if dx is None else dx + d
+                    segs.append((dy, base.dx_weight()))
             li += int(has)
+        dx = None
+        if ctx.needs_input_grad[0] and segs:
+            # one GEMM over the members' reductions: the sum autograd would form at the shared input
+            g = torch.cat(gs, dim=1) if len(gs) > 1 else (gs[0] if gs else None)
+            a = torch.cat(ga) if len(ga) > 1 else (ga[0] if ga else None)
+            dx = _lib.gemm_dx_grouped(segs, g, a)
         return (dx, None, None, None, None, *grads)
 
 
@@ -292,11 +300,11 @@ def _groupable(m) -> bool:
     return base is m or hasattr(m, "_kernel_factors")
 
 
-def group_siblings(dit, groups=(("attn", ("wq", "wk", "wv", "gate")),)) -> int:
+def group_siblings(dit, groups=(("attn", ("wq", "wk", "wv", "gate")), ("mlp", ("gate", "up")))) -> int:
     """Make the ConvRot linears that read one tensor run as one grouped launch, in place: for every block of
     ``dit.blocks`` and every ``(parent, names)`` of ``groups`` (default: the attention inputs of
-    ``mmdit.py:199``, where one launch replaces four; ``mlp.gate / up`` already fill the GPU on their own),
-    patch the members' forwards.  Members must be w8a8 ConvRot bases (or adapters over them with the fused
+    ``mmdit.py:199`` and the SwiGLU gate / up of ``mmdit.py:178``: each group's forward is one launch and its
+    input gradient one GEMM), patch the members' forwards.  Members must be w8a8 ConvRot bases (or adapters over them with the fused
     rank rules), ``out_features`` multiples of 256, one adapter rank.  Call after ``quantize_dit_convrot`` and
     ``inject_lora``.  Returns the number of groups formed."""
     n = 0

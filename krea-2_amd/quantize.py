@@ -118,7 +118,7 @@ class _ConvRotLinearFn(torch.autograd.Function):
         dx = None
         if ctx.needs_input_grad[0]:
             dx = _lib.gemm_dx(dy, qweight, wscale, w4=ctx.w4, g=g, lora_a=A if g is not None else None,
-                              wt=ctx.owner.cached_dx_weight())
+                              wt=ctx.owner.dx_weight())
         return dx, dA, dB, None, None, None, None, None, None, None, None, None
 
 
@@ -137,8 +137,8 @@ class ConvRotLinear(nn.Module):
         if mode not in MODES:
             raise ValueError(f"mode must be one of {MODES}, got {mode!r}")
         self.mode = mode
-        self.cache_dx_weight = False   # keep the backward's effective weight between calls (see below)
-        self._dx_cache = None
+        self.keep_dx_weight = True   # keep the backward's effective weight resident (see dx_weight)
+        self.register_parameter("dx_weight_t", None)
         if lin is None:  # filled by from_quantized
             return
         w = lin.weight.data
@@ -195,21 +195,45 @@ class ConvRotLinear(nn.Module):
     def weight(self) -> torch.Tensor:  # device probe for LoRALinear (quantize.py:44-46)
         return self.qweight
 
-    def cached_dx_weight(self) -> torch.Tensor | None:
-        """With ``cache_dx_weight`` on, the effective weight ``bf16(2^-7 W_hat R)^T`` that the input-gradient
-        GEMM reads (K x N bf16, 2 bytes per weight), built once and reused while the codes and scales are the
-        same tensors (pointer, version, device); otherwise None and every backward builds it.  The frozen
-        base never changes during LoRA training, so the cache trades 2 bytes per weight of HBM (24 GB for
-        the 12.2e9 block weights) for the per-call weight pass; it defeats block swap's paging."""
-        if not getattr(self, "cache_dx_weight", False):
-            self._dx_cache = None
-            return None
+    def dx_weight(self) -> torch.Tensor:
+        """The effective weight ``bf16(2^-7 W_hat R)^T`` (K x N bf16) that the input-gradient GEMM reads.
+
+        With ``keep_dx_weight`` on (the default) it is built at the first backward and kept as the frozen
+        parameter ``dx_weight_t`` (2 bytes per weight: 24 GB for the 12.2e9 block weights, beside 12 GB of
+        codes, on a 288 GB GPU): the base is frozen for the whole LoRA run, so one pass per layer replaces a
+        pass per backward.  Being a ``requires_grad=False`` parameter, it pages with the codes under block
+        swap (``mmdit.py:409-414`` moves every such parameter).  It is rebuilt when the codes or scales change
+        in place (their version counters) or move to another device, and is left out of ``state_dict`` (it is
+        derived data); an edit through ``.data`` bumps no version, so turn the cache off and on after one.  Off
+        (:func:`set_dx_weight_cache`), every backward builds it and lets it go."""
         q, s = self.qweight, self.wscale
-        key = (q.data_ptr(), q._version, s.data_ptr(), s._version, q.device)
-        if self._dx_cache is None or self._dx_cache[0] != key:
-            self._dx_cache = None
-            self._dx_cache = (key, _lib.dx_weight(q, self.weight_scale, w4=self.mode == "w4a8"))
-        return self._dx_cache[1]
+        if not getattr(self, "keep_dx_weight", False):
+            self.dx_weight_t = None
+            return _lib.dx_weight(q, self.weight_scale, w4=self.mode == "w4a8")
+        src = (q._version, s._version, q.device, tuple(q.shape))
+        wt = self.dx_weight_t
+        if wt is None or getattr(self, "_dx_src", None) != src or wt.device != q.device:
+            self.dx_weight_t = None
+            self.dx_weight_t = nn.Parameter(_lib.dx_weight(q, self.weight_scale, w4=self.mode == "w4a8"),
+                                            requires_grad=False)
+            self._dx_src = src
+        return self.dx_weight_t
+
+    def _save_to_state_dict(self, destination, prefix, keep_vars):
+        wt = self._parameters.pop("dx_weight_t", None)
+        try:
+            super()._save_to_state_dict(destination, prefix, keep_vars)
+        finally:
+            self.register_parameter("dx_weight_t", wt)
+
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
+                              error_msgs):
+        self._parameters.pop("dx_weight_t", None)      # derived from the codes being loaded: rebuilt on use
+        try:
+            super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys,
+                                          unexpected_keys, error_msgs)
+        finally:
+            self.register_parameter("dx_weight_t", None)
 
     @property
     def weight_scale(self) -> torch.Tensor:
@@ -283,17 +307,16 @@ def quantize_dit_convrot(dit, mode: str = "w8a8") -> int:
 
 
 def set_dx_weight_cache(model: nn.Module, enable: bool = True) -> int:
-    """Turn the input-gradient weight cache of every :class:`ConvRotLinear` in ``model`` on or off (off also
-    frees the cached weights).  On, each layer keeps ``bf16(2^-7 W_hat R)^T`` (2 bytes per weight) after its
-    first backward instead of rebuilding it on every call.  The cache follows the codes' pointer and version:
-    block swap's re-pointering rebuilds it; an edit through ``.data`` does not, so turn it off and on again
-    after one.  Returns the number of layers set."""
+    """Keep (default) or drop the resident input-gradient weight of every :class:`ConvRotLinear` in ``model``
+    (:meth:`ConvRotLinear.dx_weight`).  Off frees the kept weights and makes every backward build its own:
+    1 byte per weight of HBM instead of 3, for one extra weight pass per backward.  Returns the number of
+    layers set."""
     n = 0
     for m in model.modules():
         if isinstance(m, ConvRotLinear):
-            m.cache_dx_weight = bool(enable)
+            m.keep_dx_weight = bool(enable)
             if not enable:
-                m._dx_cache = None
+                m.dx_weight_t = None
             n += 1
     return n
 

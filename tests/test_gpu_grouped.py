@@ -1,12 +1,16 @@
-"""GPU tests of the grouped W8A8 forward (``k2q_gemm_w8a8_grouped``) and of ``group_siblings``.
+"""GPU tests of the grouped W8A8 forward (``k2q_gemm_w8a8_grouped``), the grouped input gradient
+(``k2q_gemm_dx_grouped``) and of ``group_siblings``.
 
-* Kernel: every segment's output is bit-identical to ``k2q_gemm_w8a8`` of that segment alone on the same
-  codes (full-K tiles), with and without bias / adapter per segment, ragged M, and the Krea 2 attention-input
-  shapes (6144 -> 6144 | 1536 | 1536 | 6144).
-* Module: a restated block's attention inputs grouped against the same block ungrouped: forward within one
-  bf16 rounding (the stacked LoRA down-projection may add in another order), gradients within the bars of the
-  per-layer path, one grouped launch per block, a checkpointed backward equal to a plain one, and a member whose
-  adapter changed between the calls running its own forward.
+* Forward kernel: every segment's output is bit-identical to ``k2q_gemm_w8a8`` of that segment alone on the
+  same codes (full-K tiles), with and without bias / adapter per segment, ragged M, and the Krea 2
+  attention-input shapes (6144 -> 6144 | 1536 | 1536 | 6144).
+* Input-gradient kernel: the segmented reduction equals ``k2q_gemm_dx_lin`` over the concatenated operands
+  bit for bit (same stage order, full-K tiles), one-stage segments and row-strided output gradients included,
+  and the float64 sum within bf16 rounding.
+* Module: a restated block's attention inputs and SwiGLU gate / up grouped against the same block ungrouped:
+  forward within one bf16 rounding (the stacked LoRA down-projection may add in another order), gradients
+  within the bars of the per-layer path, one grouped launch per group, a checkpointed backward equal to a
+  plain one, and a member whose adapter changed between the calls running its own forward.
 """
 import copy
 
@@ -67,6 +71,50 @@ def test_grouped_argument_checks(k2, dev):
         L.gemm_w8a8_grouped(qx[:8], sx[:8], [(*ok, 0, 1.0)])  # skinny M runs the GEMV per linear
 
 
+@pytest.mark.parametrize("M,K,Ns,r,strided", [(300, 640, (512, 64, 128, 256), 48, True),
+                                               (1000, 1024, (64, 64), 16, False),
+                                               (4608, 6144, (6144, 1536, 1536, 6144), 64, False),
+                                               (257, 384, (1024,), 0, True)])
+def test_dx_grouped_equals_concatenated(k2, dev, M, K, Ns, r, strided):
+    L = k2._lib
+    g = torch.Generator().manual_seed(M + K + len(Ns))
+    big = (torch.randn(M, sum(Ns) + 64 * strided, generator=g) * 1e-2).to(torch.bfloat16).to(dev)
+    dys, col = [], 0
+    for N in Ns:                                       # strided: every dy a column slice of one wider tensor
+        d = big[:, col:col + N]
+        dys.append(d if strided else d.contiguous())
+        col += N
+    wts = [(torch.randn(K, N, generator=g) * 0.02).to(torch.bfloat16).to(dev) for N in Ns]
+    gg = (torch.randn(M, r, generator=g) * 1e-3).to(dev) if r else None
+    A = (torch.randn(r, K, generator=g) * 0.01).to(dev) if r else None
+    dx = L.gemm_dx_grouped(list(zip(dys, wts)), gg, A)
+    dy_cat = torch.cat([d.contiguous() for d in dys], dim=1)
+    wt_cat = torch.cat(wts, dim=1).contiguous()
+    N = dy_cat.shape[1]
+    dummy_q = torch.zeros(N, K, dtype=torch.int8, device=dev)
+    ref = L.gemm_dx(dy_cat, dummy_q, torch.ones(N, device=dev), g=gg, lora_a=A, wt=wt_cat, split=False)
+    assert torch.equal(dx, ref)
+    ref64 = dy_cat.double() @ wt_cat.double().t()
+    if r:
+        ref64 += gg.double() @ A.double()
+    err = (dx.double() - ref64).norm() / ref64.norm()
+    assert err < 4e-3
+
+
+def test_dx_grouped_argument_checks(k2, dev):
+    L = k2._lib
+    dy = torch.zeros(64, 128, dtype=torch.bfloat16, device=dev)
+    wt = torch.zeros(256, 128, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):
+        L.gemm_dx_grouped([(dy, wt)] * 5)                                   # at most 4 segments
+    with pytest.raises(ValueError):
+        L.gemm_dx_grouped([(dy[:, :96], wt[:, :96])])                      # N % 64
+    with pytest.raises(ValueError):
+        L.gemm_dx_grouped([(dy, wt), (dy[:32], wt)])                       # M differs
+    with pytest.raises(ValueError):
+        L.gemm_dx_grouped([(dy, wt)], torch.zeros(64, 16, device=dev), torch.zeros(16, 100, device=dev))
+
+
 def _build(k2, dev, rank=16):
     g = torch.Generator().manual_seed(3)
     dit = Dit()
@@ -104,7 +152,7 @@ def test_group_siblings_matches_ungrouped(k2, dev, monkeypatch):
     dit, ad = _build(k2, dev)
     gdit = copy.deepcopy(dit)
     gad = {k: gdit.get_submodule(k) for k in ad}
-    assert k2.group_siblings(gdit) == 2           # one group (wq, wk, wv, gate) per block
+    assert k2.group_siblings(gdit) == 4           # (wq, wk, wv, gate) and (gate, up) per block
     calls = []
     real = k2._lib.gemm_w8a8_grouped
     monkeypatch.setattr(k2._lib, "gemm_w8a8_grouped", lambda *a, **kw: calls.append(1) or real(*a, **kw))
@@ -117,7 +165,7 @@ def test_group_siblings_matches_ungrouped(k2, dev, monkeypatch):
     y0, dx0, gr0 = _step(dit, ad, x, vec, dy)
     y1, dx1, gr1 = _step(gdit, gad, x, vec, dy)
     torch.cuda.synchronize()
-    assert len(calls) == 2                        # one grouped launch per block forward
+    assert len(calls) == 4                        # one grouped launch per group and block forward
     # the stacked down-projection may round u differently in the last bit; through attention's backward that
     # moves the upstream gradients, hence the block-level bars (the layer-level test below is tighter)
     assert _rel(y1, y0) < 1e-3
@@ -140,7 +188,7 @@ def test_grouped_layer_gradients(k2, dev, rank):
     the down-projection); rank 24 is padded to 32 per member."""
     dit, ad = _build(k2, dev, rank)
     gdit = copy.deepcopy(dit)
-    assert k2.group_siblings(gdit) == 2
+    assert k2.group_siblings(gdit) == 4
     names = ("wq", "wk", "wv", "gate")
     g = torch.Generator().manual_seed(6)
     x = (torch.randn(2, 192, FEAT, generator=g)).to(torch.bfloat16).to(dev)
@@ -166,9 +214,37 @@ def test_grouped_layer_gradients(k2, dev, rank):
         assert _rel(a1, a0) < 1e-3 and _rel(b1, b0) < 1e-4
 
 
+def test_grouped_unused_outputs_get_no_gradient_pass(k2, dev):
+    """Members whose outputs reach no loss (here wk and wv) get no backward work in the grouped node, as
+    ungrouped autograd would skip their nodes: their adapters get no gradient, and dX and the used members'
+    gradients match the ungrouped block's."""
+    dit, ad = _build(k2, dev)
+    gdit = copy.deepcopy(dit)
+    assert k2.group_siblings(gdit) == 4
+    names = ("wq", "wk", "wv", "gate")
+    g = torch.Generator().manual_seed(16)
+    x = (torch.randn(2, 160, FEAT, generator=g)).to(torch.bfloat16).to(dev)
+    w = (torch.randn(2, 160, FEAT, generator=g) * 1e-2).to(dev)
+    res = []
+    for d in (dit, gdit):
+        mods = [getattr(d.blocks[0].attn, n) for n in names]
+        for m in mods:
+            m.lora_A.grad = m.lora_B.grad = None
+        xr = x.clone().requires_grad_(True)
+        q, _k, _v, gt = (m(xr) for m in mods)
+        ((q.float() * torch.sigmoid(gt.float())) * w).sum().backward()
+        res.append((xr.grad, [(m.lora_A.grad, m.lora_B.grad) for m in mods]))
+    (dx0, g0), (dx1, g1) = res
+    assert _rel(dx1, dx0) < 1e-2
+    for i in (1, 2):
+        assert g0[i] == (None, None) and g1[i] == (None, None), names[i]
+    for i in (0, 3):
+        assert _rel(g1[i][0], g0[i][0]) < 1e-3 and _rel(g1[i][1], g0[i][1]) < 1e-4, names[i]
+
+
 def test_group_member_with_changed_adapter_runs_alone(k2, dev):
     dit, _ = _build(k2, dev)
-    assert k2.group_siblings(dit) == 2
+    assert k2.group_siblings(dit) == 4
     attn = dit.blocks[0].attn
     g = torch.Generator().manual_seed(5)
     x = (torch.randn(2, 64, FEAT, generator=g)).to(torch.bfloat16).to(dev)
@@ -195,7 +271,7 @@ def test_producers_and_grouping_together(k2, dev):
     dit, ad = _build(k2, dev)
     fdit = copy.deepcopy(dit)
     fad = {k: fdit.get_submodule(k) for k in ad}
-    assert k2.fuse_producers(fdit) == 4 and k2.group_siblings(fdit) == 2
+    assert k2.fuse_producers(fdit) == 4 and k2.group_siblings(fdit) == 4
     g = torch.Generator().manual_seed(8)
     B, Lt = 2, 128
     x = (torch.randn(B, Lt, FEAT, generator=g)).to(torch.bfloat16).to(dev)
@@ -234,7 +310,7 @@ def test_fusions_at_krea_width(k2, dev):
             m.lora_B.copy_(torch.randn(m.lora_B.shape, generator=g) * 0.01)
     fdit = copy.deepcopy(dit)
     fad = {k: fdit.get_submodule(k) for k in ad}
-    assert k2.fuse_producers(fdit) == 2 and k2.group_siblings(fdit) == 1
+    assert k2.fuse_producers(fdit) == 2 and k2.group_siblings(fdit) == 2
     B, Lt, D = 2, 256, dims["feat"]
     x = torch.randn(B, Lt, D, generator=g).to(torch.bfloat16).to(dev)
     vec = (torch.randn(B, 1, 6 * D, generator=g) * 0.3).to(torch.bfloat16).to(dev)
@@ -256,7 +332,7 @@ def test_block_forward_replays_in_a_hip_graph(k2, dev):
     kernel) captured once in a HIP graph and replayed three times on new input data, with eager work and
     synchronizations between the replays: every replay equals the eager forward bit for bit."""
     dit, _ = _build(k2, dev)
-    assert k2.fuse_producers(dit) == 4 and k2.group_siblings(dit) == 2
+    assert k2.fuse_producers(dit) == 4 and k2.group_siblings(dit) == 4
     g = torch.Generator().manual_seed(10)
     B, Lt = 2, 128
     vec = (torch.randn(B, 1, 6 * FEAT, generator=g) * 0.3).to(torch.bfloat16).to(dev)

@@ -433,10 +433,11 @@ def test_module_backward_matches_oracle(k2, dev, mode):
 
 
 @pytest.mark.parametrize("mode", ["w8a8", "w4a8"])
-def test_dx_weight_cache(k2, dev, mode):
-    """With the input-gradient weight cache on, dX and the LoRA grads are bit-identical to the uncached
-    backward, the cached weight is reused across calls and rebuilt when the codes are re-pointered (block
-    swap's `p.data = ...`); turning it off frees it."""
+def test_dx_weight_resident(k2, dev, mode):
+    """The input-gradient weight is kept after the first backward (the default) as a frozen parameter that
+    ``state_dict`` leaves out; it is reused, pages with the codes as block swap moves every frozen parameter
+    (``mmdit.py:409-414``), is rebuilt after an in-place change of the codes, and is dropped by
+    ``set_dx_weight_cache(False)``.  dX and the LoRA grads are bit-identical in every case."""
     _, base, lora = _layers(k2, dev, K=512, N=256, r=16, mode=mode)
     x = make_x(160, 512, seed=21).to(dev)
     dy = (torch.randn(160, 256, generator=torch.Generator().manual_seed(5)) * 1e-3).to(torch.bfloat16).to(dev)
@@ -447,20 +448,36 @@ def test_dx_weight_cache(k2, dev, mode):
         lora(xr).backward(dy)
         return xr.grad.clone(), lora.lora_A.grad.clone(), lora.lora_B.grad.clone()
 
+    assert k2.set_dx_weight_cache(lora, False) == 1
     ref = grads()
-    assert base._dx_cache is None
-    assert k2.set_dx_weight_cache(lora, True) == 1
+    assert base.dx_weight_t is None
+    k2.set_dx_weight_cache(lora, True)
     first = grads()
-    w1 = base._dx_cache[1]
+    w1 = base.dx_weight_t
+    assert isinstance(w1, torch.nn.Parameter) and not w1.requires_grad and w1.shape == (512, 256)
+    assert "dx_weight_t" in dict(base.named_parameters())
+    assert not any(k.endswith("dx_weight_t") for k in lora.state_dict())
     second = grads()
-    assert base._dx_cache[1] is w1                               # reused
-    base.qweight.data = base.qweight.data.clone()                # re-pointered as block swap does
+    assert base.dx_weight_t is w1                                  # reused
+    frozen = [p for p in lora.parameters() if not p.requires_grad]
+    for p in frozen:                                               # block swap: page out ...
+        p.data = p.data.to("cpu")
+    assert base.dx_weight_t.device.type == "cpu"
+    for p in frozen:                                               # ... and back in
+        p.data = p.data.to(dev)
     third = grads()
-    assert base._dx_cache[1] is not w1 and torch.equal(base._dx_cache[1], w1)
-    for got in (first, second, third):
+    assert base.dx_weight_t is w1
+    with torch.no_grad():
+        base.qweight.copy_(base.qweight.clone())                   # an in-place write (same values)
+    fourth = grads()
+    assert base.dx_weight_t is not w1 and torch.equal(base.dx_weight_t, w1)
+    for got in (first, second, third, fourth):
         assert all(torch.equal(a, b) for a, b in zip(got, ref))
+    lora.load_state_dict(lora.state_dict())                        # strict load without the derived weight
+    assert base.dx_weight_t is None
+    assert all(torch.equal(a, b) for a, b in zip(grads(), ref))
     k2.set_dx_weight_cache(lora, False)
-    assert base._dx_cache is None and base.cached_dx_weight() is None
+    assert base.dx_weight_t is None
 
 
 def test_deterministic_and_checkpoint_recompute(k2, dev):
