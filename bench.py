@@ -1,12 +1,16 @@
 """Benchmark of the ConvRot QuantLinear + LoRA forward on one MI355X (BASELINE.json metric and configs).
 
-A step is one QuantLinear+LoRA forward over one batch of synthetic input resident in HBM: rotate+quantize
-(kernel 1), LoRA down-projection, int8 MFMA GEMM with the fused dequant/bias/LoRA epilogue (kernels 2+3).
-The default workload is BASELINE.json configs[2] (M=16384+512, K=3072, N=12288, r=32), the configuration the
-north_star's targets are stated on.  ``value`` is the forward's throughput in TOPS (2*M*N*K per step time).
-Rank 0 prints one JSON line; ``roofline`` covers the dominant kernel (the GEMM, int8-MFMA bound) with its
-average duration measured by HIP events around it inside the timed steps, on the stream the kernels run
-on; ``cpu_baseline`` times the CPU oracle (a port of the same arithmetic) on a bounded sample of rows.
+A step is one QuantLinear+LoRA forward over one batch of synthetic input resident in HBM, as the module
+runs it: one library call (k2q_linear_fwd) issuing rotate+quantize (kernel 1), the LoRA down-projection and
+the int8 MFMA GEMM with the fused dequant/bias/LoRA epilogue (kernels 2+3).  The default workload is
+BASELINE.json configs[2] (M=16384+512, K=3072, N=12288, r=32), the configuration the north_star's targets are
+stated on.  ``value`` is the forward's throughput in TOPS (2*M*N*K per step time).  Times are the GPU's: the
+events bracketing each timed region are preceded by untimed device copies long enough for the host to enqueue
+the whole region first (``queue_head``), so the GPU never waits for a launch; the host's issue time per call
+is reported beside (``host_us_per_step``).  Rank 0 prints one JSON line; ``roofline`` covers the dominant
+kernel (the GEMM, int8-MFMA bound) with its average duration measured by HIP events around it in K steps
+that launch the three kernels one by one, on the stream the kernels run on; ``cpu_baseline`` times the CPU
+oracle (a port of the same arithmetic) on a bounded sample of rows.
 Before the W warmup steps, ``--settle`` seconds of untimed steps let the GPU clocks leave their ramp-up
 state (``extra.settle_s`` reports it).
 
@@ -88,11 +92,40 @@ def settle(fn, seconds):
         torch.cuda.synchronize()
 
 
-def time_loop(fn, iters, warm=3):
+_HEAD = {}
+HOST_US = {}   # host issue time per call of the last fn timed by time_loop, keyed by fn's qualified name
+
+
+def queue_head(dev, ms):
+    """Enqueues about ``ms`` of untimed device copies (256 MB each, ~0.1 ms) and returns without waiting, so
+    the host can enqueue a whole timed region before the GPU reaches it: the events around that region then
+    measure the GPU's time per step, with no gaps where the GPU waited for the host to launch the next kernel
+    (as in a training loop, where the host runs ahead during the large GEMMs, or a replayed HIP graph)."""
+    if dev not in _HEAD:
+        src = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
+        _HEAD[dev] = (src, torch.empty_like(src))
+    src, dst = _HEAD[dev]
+    for _ in range(max(1, min(int(ms / 0.1) + 1, 500))):
+        dst.copy_(src)
+
+
+def time_loop(fn, iters, warm=3, dev=None):
+    """GPU ms per call of ``fn`` over ``iters`` calls between two events.  The warm calls also measure the host's
+    issue time per call (``HOST_US``); a queue head of 1.5x the timed region's host time lets the host run ahead
+    (``queue_head``).  ``dev`` None: no head (the host's launch cost is then part of the time when it exceeds
+    the GPU's)."""
     for _ in range(warm):
         fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(warm):
+        fn()
+    host_ms = (time.perf_counter() - t0) * 1e3 / warm
+    HOST_US[getattr(fn, "__qualname__", "fn")] = host_ms * 1e3
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    if dev is not None:
+        queue_head(dev, 1.5 * host_ms * iters + 0.3)
     s.record()
     for _ in range(iters):
         fn()
@@ -219,45 +252,50 @@ def run_config(k2, cfg, steps, warmup, dev, settle_s=0.0):
     x, W, b, A, B = synth(M, K, N, r, cfg["bias"])
     xd, Ad, Bd = x.to(dev), A.to(dev), B.to(dev)
     bd = None if b is None else b.to(dev)
-    if cfg["w4"]:
+    w4 = cfg["w4"]
+    if w4:
         qw, sw = L.quant_weight_i4(W.to(dev))
         gemm = L.gemm_w4a8
     else:
         qw, sw = L.quant_weight_i8(W.to(dev))
         gemm = L.gemm_w8a8
+    qx = torch.empty((M, K), dtype=torch.int8, device=dev)
+    sx = torch.empty((M,), dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
 
-    def step(ev=None):
-        if ev is not None:
-            ev[0].record()
-        qx, sx, _ = L.rotquant(xd)
-        if ev is not None:
-            ev[1].record()
-        u = L.lora_down(xd, Ad)
-        if ev is not None:
-            ev[2].record()
-        y = gemm(qx, sx, qw, sw, bd, u, Bd, 1.0)
-        if ev is not None:
-            ev[3].record()
-        return y
+    def step():
+        """The module's inference path: one library call (k2q_linear_fwd) issues rotate/quant, the LoRA
+        down-projection and the GEMM with its fused epilogue (which adds the down-projection's K-slices)."""
+        return L.linear_fwd(xd, qx, sx, False, Ad, Bd, 1.0, qw, sw, bd, w4, need_u=False)[0]
 
     settle(step, settle_s)
     for _ in range(warmup):
         step()
-    # Timed region: K steps between two events; inside each step, events on the same stream (torch's
-    # current stream, where the kernels run) bracket rotate/quant, the LoRA down-projection and the GEMM,
-    # so the per-kernel averages come from the timed steps themselves.
+    # Timed region: K steps between two events on the stream the kernels run on (the GPU's time per step).
+    ms_step = time_loop(step, steps, dev=dev)
+    host_us = HOST_US[step.__qualname__]
+
+    # Per-kernel breakdown over K more steps: the same three launches issued one by one, events between them
+    # on that stream, so the GEMM's average launch duration comes from timed steps.
+    def step_events(ev):
+        ev[0].record()
+        q_, s_, _ = L.rotquant(xd)
+        ev[1].record()
+        u = L.lora_down(xd, Ad)
+        ev[2].record()
+        gemm(q_, s_, qw, sw, bd, u, Bd, 1.0)
+        ev[3].record()
+
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
-    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for _ in range(3):
+        step_events(evs[0])
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    s_ev.record()
+    queue_head(dev, 0.3 + 1.5 * 0.06 * steps)   # ~60 us of host time per instrumented step
     for i in range(steps):
-        step(evs[i])
-    e_ev.record()
+        step_events(evs[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms_step = s_ev.elapsed_time(e_ev) / steps
     ms_rot = sum(ev[0].elapsed_time(ev[1]) for ev in evs) / steps
     ms_lora = sum(ev[1].elapsed_time(ev[2]) for ev in evs) / steps
     ms_gemm = sum(ev[2].elapsed_time(ev[3]) for ev in evs) / steps
@@ -272,13 +310,13 @@ def run_config(k2, cfg, steps, warmup, dev, settle_s=0.0):
 
     # Median of 7 timed batches of 40 passes (~35 ms of streaming at cfg2): one short batch right after the
     # GEMM loop has read anywhere from 5.0 to 5.9 TB/s on the same build.
-    batches = sorted(time_loop(rot4, 40) for _ in range(7))
+    batches = sorted(time_loop(rot4, 40, dev=dev) for _ in range(7))
     ms_rot_stream = batches[len(batches) // 2] / len(xs)
     del xs
     ops = 2.0 * M * N * K
     rot_bytes = 2 * M * K + M * K + 4 * M
-    return dict(ms_step=ms_step, wall=wall, ms_rot=ms_rot, ms_rot_stream=ms_rot_stream, ms_lora=ms_lora,
-                ms_gemm=ms_gemm, ops=ops,
+    return dict(ms_step=ms_step, wall=wall, host_us=host_us, ms_rot=ms_rot, ms_rot_stream=ms_rot_stream,
+                ms_lora=ms_lora, ms_gemm=ms_gemm, ops=ops,
                 rot_bytes=rot_bytes, tops=ops / (ms_step * 1e-3) / 1e12, x=x, W=W, b=b, A=A, B=B)
 
 
@@ -323,11 +361,11 @@ def run_cfg3(k2, steps, dev, settle_s=0.0, cpu=False):
     prev = _no_input_reuse(k2)
     try:
         settle(step, settle_s)
-        ms = time_loop(step, steps)             # the frozen base's effective weight resident (the default)
+        ms = time_loop(step, steps, dev=dev)    # the frozen base's effective weight resident (the default)
         with torch.no_grad():
-            ms_fwd = time_loop(lambda: layer(x), steps)
+            ms_fwd = time_loop(lambda: layer(x), steps, dev=dev)
         k2.set_dx_weight_cache(layer, False)    # every backward builds its effective weight
-        ms_per_call = time_loop(step, steps)
+        ms_per_call = time_loop(step, steps, dev=dev)
         k2.set_dx_weight_cache(layer, True)
     finally:
         k2.quantize.shared_input_quant.enabled = prev
@@ -348,7 +386,7 @@ def run_cfg3(k2, steps, dev, settle_s=0.0, cpu=False):
         out = out + ((x.to(A.dtype) @ A.t()) @ B.t()).to(out.dtype)
         out.backward(dy)
 
-    ms_ref = time_loop(ref_step, steps)
+    ms_ref = time_loop(ref_step, steps, dev=dev)
     # The backward's kernels alone: the input-gradient GEMM (bf16 MFMA, with its LoRA term) on the layer's
     # effective weight, and the per-call pass that builds that weight (HBM: N K int8 in, 2 N K bf16 out).
     L = k2._lib
@@ -356,9 +394,9 @@ def run_cfg3(k2, steps, dev, settle_s=0.0, cpu=False):
     wt = L.dx_weight(base.qweight, base.weight_scale)
     gg = (torch.randn(c["M"], c["r"], generator=g) * 1e-3).to(dev)
     A_ = layer.lora_A.detach()
-    ms_dx = sorted(time_loop(lambda: L.gemm_dx(dy, base.qweight, base.weight_scale, g=gg, lora_a=A_, wt=wt), steps)
+    ms_dx = sorted(time_loop(lambda: L.gemm_dx(dy, base.qweight, base.weight_scale, g=gg, lora_a=A_, wt=wt), steps, dev=dev)
                    for _ in range(3))[1]
-    ms_prep = sorted(time_loop(lambda: L.dx_weight(base.qweight, base.weight_scale), steps) for _ in range(3))[1]
+    ms_prep = sorted(time_loop(lambda: L.dx_weight(base.qweight, base.weight_scale), steps, dev=dev) for _ in range(3))[1]
     del wt
     ops_fwd = 2.0 * c["M"] * c["N"] * c["K"]
     dx_tflops = ops_fwd / (ms_dx * 1e-3) / 1e12
@@ -420,8 +458,8 @@ def run_producers(k2, steps, dev):
     out = {}
     for name, fused, ref, nbytes in (("rmsnorm_mod", rms_fused, rms_ref, 5 * M * K + 4 * M),
                                      ("swiglu", swi_fused, swi_ref, 7 * M * KH + 4 * M)):
-        tf = sorted(time_loop(fused, steps) for _ in range(5))[2] / 4
-        tr = sorted(time_loop(ref, steps) for _ in range(5))[2] / 4
+        tf = sorted(time_loop(fused, steps, dev=dev) for _ in range(5))[2] / 4
+        tr = sorted(time_loop(ref, steps, dev=dev) for _ in range(5))[2] / 4
         gbs = nbytes / (tf * 1e-3) / 1e9
         out[name] = {"M": M, "K": K if name == "rmsnorm_mod" else KH, "fused_ms": round(tf, 4),
                      "unfused_ms": round(tr, 4), "fused_GBps": round(gbs, 1),
@@ -452,9 +490,9 @@ def run_grouped(k2, steps, dev):
                 m(x)
 
         with torch.no_grad():
-            t_sep = sorted(time_loop(calls, steps) for _ in range(5))[2]
+            t_sep = sorted(time_loop(calls, steps, dev=dev) for _ in range(5))[2]
             assert fused.group_siblings(types.SimpleNamespace(blocks=[types.SimpleNamespace(attn=attn)])) == 1
-            t_grp = sorted(time_loop(calls, steps) for _ in range(5))[2]
+            t_grp = sorted(time_loop(calls, steps, dev=dev) for _ in range(5))[2]
         ops = 2.0 * M * K * sum(Ns)
         out[f"M{M}"] = {"separate_ms": round(t_sep, 4), "grouped_ms": round(t_grp, 4),
                         "separate_tops": round(ops / (t_sep * 1e-3) / 1e12, 1),
@@ -518,8 +556,8 @@ def run_krea_block(k2, steps, dev):
         if fuse:
             fused.group_siblings(types.SimpleNamespace(blocks=[types.SimpleNamespace(attn=attn, mlp=mlp)]))
         with torch.no_grad():
-            t_f = sorted(time_loop(lambda: block(x0, fuse), steps) for _ in range(3))[1]
-        t_fb = sorted(time_loop(lambda: fwd_bwd(fuse), max(3, steps // 2)) for _ in range(3))[1]
+            t_f = sorted(time_loop(lambda: block(x0, fuse), steps, dev=dev) for _ in range(3))[1]
+        t_fb = sorted(time_loop(lambda: fwd_bwd(fuse), max(3, steps // 2), dev=dev) for _ in range(3))[1]
         out["fused" if fuse else "reference_ops"] = {"fwd_ms": round(t_f, 4), "fwd_bwd_ms": round(t_fb, 4)}
     out["shape"] = f"M={M} width={D} kv={KV} hidden={HID} r={r}; attention excluded"
     return out
@@ -554,8 +592,8 @@ def run_reference_gpu(k2, res, steps, dev):
     with torch.no_grad():
         fp8.lora_A.copy_(A)
         fp8.lora_B.copy_(B)
-        t_ref = sorted(time_loop(ref, steps) for _ in range(3))[1]
-        t_fp8 = sorted(time_loop(lambda: fp8(x), steps) for _ in range(3))[1]
+        t_ref = sorted(time_loop(ref, steps, dev=dev) for _ in range(3))[1]
+        t_fp8 = sorted(time_loop(lambda: fp8(x), steps, dev=dev) for _ in range(3))[1]
     ops = 2.0 * M * N * K
     return {"reference_fp8_path": {"ms": round(t_ref, 4), "tops": round(ops / (t_ref * 1e-3) / 1e12, 1),
                                    "path": "Fp8Linear.forward + LoRALinear.forward restated with torch ops on the GPU"},
@@ -592,10 +630,10 @@ def run_cfg4(k2, steps, dev, settle_s=0.0, cpu=False):
     try:
         with torch.no_grad():
             settle(block, settle_s)
-            ms = time_loop(block, steps)
+            ms = time_loop(block, steps, dev=dev)
             per = {}
             for name, layer, M, K, N in layers:
-                per[name] = round(time_loop(lambda: layer(xs[name]), max(3, steps // 2)), 4)
+                per[name] = round(time_loop(lambda: layer(xs[name]), max(3, steps // 2), dev=dev), 4)
     finally:
         k2.quantize.shared_input_quant.enabled = prev
     tops = total_ops / (ms * 1e-3) / 1e12
@@ -960,6 +998,7 @@ def forward_record(cfg, res, cpu=None, cpu_ref=None):
     rot_gbs = res["rot_bytes"] / (res["ms_rot_stream"] * 1e-3) / 1e9
     rec = {"workload": cfg["name"], "ms": round(res["ms_step"], 4), "tops": round(res["tops"], 1),
            "pct_int8_peak": round(100 * res["tops"] / INT8_PEAK_TOPS, 2),
+           "host_us_per_step": round(res["host_us"], 1),
            "gemm_ms": round(res["ms_gemm"], 4), "lora_down_ms": round(res["ms_lora"], 4),
            "rotquant_ms_in_step": round(res["ms_rot"], 4),
            "roofline": roofline_entry("gemm_w4_kernel" if cfg["w4"] else "gemm_nt_kernel<EPI_W8>", "mfma", gemm_tops,

@@ -147,8 +147,10 @@ int k2q_gemm_w8a8_grouped(const int8_t* qx, const float* sx, int64_t M, int64_t 
  * k2q_gemm_w8a8 / k2q_gemm_w4a8 issued from one call.  wmode K2Q_WMODE_W8: qw int8 N x K, sw f32 N;
  * K2Q_WMODE_W4: qw packed int4 N x K/2, sw bf16 K/64 x N.  x: M rows of ldx bf16; qx (M x K int8), sx (M f32)
  * and u (M x r f32, the LoRA factors the backward reuses) are caller buffers the call fills; y M x N bf16.
- * M <= 8: one launch computes the codes and u, then the GEMV (two launches for the linear).
- * ws: k2q_linear_fwd_ws_bytes bytes, used by the down-projection and the GEMM one after the other. */
+ * u may be NULL when nothing needs the factors afterwards (inference) and M > 8: then, for W8 and r <= 128,
+ * the GEMM epilogue adds the down-projection's K-slice partials itself (no reduce launch; y is bit-identical).
+ * M <= 8: one launch computes the codes and u, then the GEMV (two launches for the linear; u required).
+ * ws: k2q_linear_fwd_ws_bytes bytes (256-byte aligned): factors, their partials and the GEMM's split pieces. */
 #define K2Q_WMODE_W8 0
 #define K2Q_WMODE_W4 1
 int64_t k2q_linear_fwd_ws_bytes(int wmode, int64_t M, int64_t N, int64_t K, int64_t r);

@@ -511,12 +511,15 @@ def gemm_w8a8(qx, sx, qw, sw, bias=None, u=None, lora_b=None, lora_scale: float 
 WMODE_W8, WMODE_W4 = 0, 1
 
 
-def linear_fwd(x2, qx, sx, codes_ready: bool, A, B, lora_scale: float, qw, sw, bias, w4: bool):
+def linear_fwd(x2, qx, sx, codes_ready: bool, A, B, lora_scale: float, qw, sw, bias, w4: bool,
+               need_u: bool = True):
     """One quantized linear + LoRA forward in one library call (``k2q_linear_fwd``): rotate/quant of ``x2`` into
     ``qx`` / ``sx`` (unless ``codes_ready``), ``u = x2 A^T`` (when ``A``), the GEMM with the fused epilogue.
-    Returns ``(y, u | None)``.  The module's per-call entry: the weights and factors come from the module (their
-    shapes fixed when it was built), so only the relations a foreign call needs are checked here, cheaply; the
-    library checks pointers and alignment again.  ``x2`` (M,K) bf16 rows of stride ``x2.stride(0)``."""
+    Returns ``(y, u | None)``; ``need_u=False`` (inference: no backward will read the factors) lets the library
+    keep u internal (for M > 8 the GEMM epilogue then adds the down-projection's slices itself) and returns
+    ``(y, None)``.  The module's per-call entry: the weights and factors come from the module (their shapes
+    fixed when it was built), so only the relations a foreign call needs are checked here, cheaply; the library
+    checks pointers and alignment again.  ``x2`` (M,K) bf16 rows of stride ``x2.stride(0)``."""
     M, K = x2.shape
     N = qw.shape[0]
     dev = x2.device
@@ -535,13 +538,13 @@ def linear_fwd(x2, qx, sx, codes_ready: bool, A, B, lora_scale: float, qw, sw, b
     lib = load()
     wmode = WMODE_W4 if w4 else WMODE_W8
     y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-    u = torch.empty((M, r), dtype=torch.float32, device=dev) if r else None
+    u = torch.empty((M, r), dtype=torch.float32, device=dev) if r and (need_u or M <= 8) else None
     nws = lib.k2q_linear_fwd_ws_bytes(wmode, M, N, K, r)
     ws = torch.empty((nws,), dtype=torch.uint8, device=dev) if nws > 0 else None
     _check(lib.k2q_linear_fwd(x2.data_ptr(), x2.stride(0), M, K, qx.data_ptr(), sx.data_ptr(), int(codes_ready),
                               _ptr(A), _ptr(B), r, float(lora_scale), _ptr(u), wmode, qw.data_ptr(), sw.data_ptr(),
                               _ptr(bias), N, y.data_ptr(), _ptr(ws), nws, _stream(dev)), "k2q_linear_fwd")
-    return y, u
+    return y, (u if need_u else None)
 
 
 def gemm_w8a8_grouped(qx, sx, segments, u=None):

@@ -69,6 +69,8 @@ struct GemmArgs {
                          // LoRA A itself (r x rows_a f32, so column a holds row a's factors) for EPI_DX/DXLIN
   int r;
   int ldr;            // row stride of lora_rb in elements (r unless the factors of several segments share rows)
+  int rb_parts;       // > 1: lora_rb holds that many K-slice partials of the factors, rb_pstride elements apart,
+  int64_t rb_pstride; //      added in slice order as they are read (the down-projection's reduce, folded in)
   float lora_scale;
   int nseg;           // 0: one linear; else rows_a stacks nseg segments (EPI_W8)
   GemmSeg seg[MAX_SEG];
@@ -630,6 +632,15 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
       for (int i = 0; i < NBR; ++i) {
         lfb[i][0] = *reinterpret_cast<const v4f*>(prb[i] + c0);
         lfb[i][1] = *reinterpret_cast<const v4f*>(prb[i] + c0 + 4);
+      }
+      if constexpr (EPI == EPI_W8) {
+        for (int q = 1; q < p.rb_parts; ++q) {   // ((part 0 + part 1) + part 2) ..., as lora_reduce_kernel adds
+#pragma unroll
+          for (int i = 0; i < NBR; ++i) {
+            lfb[i][0] += *reinterpret_cast<const v4f*>(prb[i] + q * p.rb_pstride + c0);
+            lfb[i][1] += *reinterpret_cast<const v4f*>(prb[i] + q * p.rb_pstride + c0 + 4);
+          }
+        }
       }
     };
     if (lora) {
@@ -1249,6 +1260,14 @@ extern "C" int k2q_gemm_w8a8_tile(const int8_t* qx, const float* sx, const int8_
                                   const float* bias, const float* u, const float* lora_b, int64_t r,
                                   float lora_scale, int64_t M, int64_t N, int64_t K, uint16_t* y,
                                   void* ws, int64_t ws_bytes, int tile, void* stream) {
+  return gemm_w8a8_impl(qx, sx, qw, sw, bias, u, 1, 0, lora_b, r, lora_scale, M, N, K, y, ws, ws_bytes, tile,
+                        static_cast<hipStream_t>(stream));
+}
+
+int gemm_w8a8_impl(const int8_t* qx, const float* sx, const int8_t* qw, const float* sw, const float* bias,
+                   const float* u, int u_parts, int64_t u_pstride, const float* lora_b, int64_t r, float lora_scale,
+                   int64_t M, int64_t N, int64_t K, uint16_t* y, void* ws, int64_t ws_bytes, int tile,
+                   hipStream_t st) {
   int rc = check_common(M, N, K);
   if (rc) return rc;
   if (!k2q_aligned(y, 16)) return K2Q_EINVAL;
@@ -1257,9 +1276,9 @@ extern "C" int k2q_gemm_w8a8_tile(const int8_t* qx, const float* sx, const int8_
     return K2Q_EINVAL;
   if (bias && !k2q_aligned(bias, 16)) return K2Q_EINVAL;
   if ((rc = check_lora(u, lora_b, r))) return rc;
+  if (u_parts < 1 || (u_parts > 1 && (M <= K2Q_GEMV_MAX_M || u_pstride < M * r || u_pstride % 4))) return K2Q_EINVAL;
   if (M <= K2Q_GEMV_MAX_M)
-    return k2q_launch_gemv_w8a8(qx, sx, qw, sw, bias, u, lora_b, (int)r, lora_scale, M, N, K, y,
-                                static_cast<hipStream_t>(stream));
+    return k2q_launch_gemv_w8a8(qx, sx, qw, sw, bias, u, lora_b, (int)r, lora_scale, M, N, K, y, st);
   GemmArgs p{};
   p.a = reinterpret_cast<const uint8_t*>(qw);
   p.b = reinterpret_cast<const uint8_t*>(qx);
@@ -1267,7 +1286,8 @@ extern "C" int k2q_gemm_w8a8_tile(const int8_t* qx, const float* sx, const int8_
   p.out = y; p.ldo = N;
   p.sx = sx; p.sw = sw; p.bias = bias;
   p.lora_rb = u; p.lora_ra = lora_b; p.r = u ? (int)r : 0; p.lora_scale = lora_scale;
-  return launch_gemm<EPI_W8>(p, ws, ws_bytes, static_cast<hipStream_t>(stream), tile);
+  p.rb_parts = u_parts; p.rb_pstride = u_pstride;
+  return launch_gemm<EPI_W8>(p, ws, ws_bytes, st, tile);
 }
 
 extern "C" int k2q_gemm_w8a8_plan(int64_t M, int64_t N, int64_t K, int cus, int grouped, int* split_pieces) {

@@ -119,15 +119,52 @@ int launch_skinny(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, const fl
 
 }  // namespace
 
+namespace {
+
+int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
+
+// Workspace layout of the forward (M > K2Q_GEMV_MAX_M): [u: M x r f32 when the caller passes no u]
+// [the down-projection's K-slice partials] [the GEMM's split-K pieces].
+struct FwdLayout {
+  int64_t u_off, parts_off, gemm_off, total;
+};
+
+FwdLayout fwd_layout(int wmode, int64_t M, int64_t N, int64_t K, int64_t r) {
+  FwdLayout L{};
+  int64_t off = 0;
+  if (r > 0 && M > K2Q_GEMV_MAX_M) {
+    L.u_off = off;
+    off += align256(M * r * 4);
+    L.parts_off = off;
+    const int64_t a = k2q_lora_down_ws_bytes(M, K, r), b = lora_down_parts_floats(M, K, r) * 4;
+    off += align256(a > b ? a : b);
+  }
+  L.gemm_off = off;
+  if (wmode == K2Q_WMODE_W8) off += align256(k2q_gemm_w8a8_ws_bytes(M, N, K));
+  L.total = off;
+  return L;
+}
+
+// Whether the GEMM epilogue should add the down-projection's K-slice partials itself instead of a reduce
+// launch: every output-column tile reads the factor rows of its tokens, so the partials cost (slices - 1) x
+// M x r x 4 bytes of extra reads per column of tiles.  Measured on MI355X: at cfg0 (M = 4096, N = K = 3072,
+// r = 16; ~8 MB extra) the one-call forward gains ~9 us over the separate launches; at cfg2 (M = 16896,
+// N = 12288; ~210 MB extra) it loses ~20 us.  The fold is taken up to 16 MB of extra reads.
+bool fold_pays(int64_t M, int64_t N, int64_t K, int64_t r) {
+  const int64_t parts = r > 0 ? lora_down_parts_floats(M, K, r) / (M * r) : 1;
+  if (parts <= 1) return true;
+  int pieces = 1;
+  const int tile = k2q_gemm_w8a8_plan(M, N, K, k2q_cu_count(), 0, &pieces);
+  const int64_t ta = tile == K2Q_TILE_192x256 ? 192 : tile == K2Q_TILE_128x128 ? 128 : 256;
+  const int64_t extra = (parts - 1) * M * r * 4 * ((N + ta - 1) / ta);
+  return extra <= ((int64_t)16 << 20);
+}
+
+}  // namespace
+
 extern "C" int64_t k2q_linear_fwd_ws_bytes(int wmode, int64_t M, int64_t N, int64_t K, int64_t r) {
   if (M < 1 || N < 1 || K < K2Q_HADAMARD || K % K2Q_HADAMARD) return 0;
-  int64_t b = 0;
-  if (r > 0 && M > K2Q_GEMV_MAX_M) b = k2q_lora_down_ws_bytes(M, K, r);
-  if (wmode == K2Q_WMODE_W8) {
-    const int64_t g = k2q_gemm_w8a8_ws_bytes(M, N, K);
-    b = g > b ? g : b;
-  }
-  return b;
+  return fwd_layout(wmode, M, N, K, r).total;
 }
 
 extern "C" int k2q_linear_fwd(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, int8_t* qx, float* sx,
@@ -138,24 +175,45 @@ extern "C" int k2q_linear_fwd(const uint16_t* x, int64_t ldx, int64_t M, int64_t
   if (K > 16384) return K2Q_EUNSUPPORTED;
   if (ldx < K || ldx % 8 || !k2q_aligned(x, 16) || !k2q_aligned(qx, 16)) return K2Q_EINVAL;
   if (wmode != K2Q_WMODE_W8 && wmode != K2Q_WMODE_W4) return K2Q_EINVAL;
-  if (lora_a && (!lora_b || !u || r < 16 || r > K2Q_MAX_RANK || r % 16 || !k2q_aligned(lora_a, 16) ||
-                 !k2q_aligned(u, 16)))
+  if (lora_a && (!lora_b || r < 16 || r > K2Q_MAX_RANK || r % 16 || !k2q_aligned(lora_a, 16) ||
+                 (u && !k2q_aligned(u, 16))))
     return K2Q_EINVAL;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t rr = lora_a ? r : 0;
+  const bool skinny = M <= K2Q_GEMV_MAX_M;
+  const FwdLayout lay = fwd_layout(wmode, M, N, K, rr);
+  if (!skinny && rr > 0 && (!ws || ws_bytes < lay.total || !k2q_aligned(ws, 256))) return K2Q_EINVAL;
+  if (skinny && lora_a && !u) return K2Q_EINVAL;      // the prologue writes u
+  uint8_t* w = static_cast<uint8_t*>(ws);
+  void* gws = ws ? static_cast<void*>(w + lay.gemm_off) : nullptr;
+  const int64_t gws_bytes = ws ? ws_bytes - lay.gemm_off : 0;
   int rc = K2Q_OK;
-  if (M <= K2Q_GEMV_MAX_M) {
+  const float* uu = nullptr;   // the factors the GEMM reads: u, or the down-projection's slice partials
+  int parts = 1;
+  if (skinny) {
     if (lora_a || !codes_ready)
       rc = launch_skinny(x, ldx, M, K, lora_a, rr, u, codes_ready ? nullptr : qx, sx, st);
+    uu = lora_a ? u : nullptr;
   } else {
     if (!codes_ready) rc = k2q_rotquant(x, K2Q_DTYPE_BF16, M, K, ldx, qx, sx, nullptr, stream);
-    if (!rc && lora_a) rc = lora_down_impl(x, M, K, ldx, lora_a, 1, 1.f, rr, ws, ws_bytes, u, st);
+    if (!rc && lora_a) {
+      if (!u && wmode == K2Q_WMODE_W8 && rr <= 128 && fold_pays(M, N, K, rr)) {
+        // nobody needs u itself: the GEMM epilogue adds the K-slice partials (no reduce launch)
+        float* dst = reinterpret_cast<float*>(w + lay.parts_off);
+        rc = lora_down_parts(x, M, K, ldx, lora_a, rr, dst, &parts, st);
+        uu = dst;
+      } else {
+        float* ut = u ? u : reinterpret_cast<float*>(w + lay.u_off);
+        rc = lora_down_impl(x, M, K, ldx, lora_a, 1, 1.f, rr, w + lay.parts_off, lay.gemm_off - lay.parts_off, ut,
+                            st);
+        uu = ut;
+      }
+    }
   }
   if (rc) return rc;
-  const float* uu = lora_a ? u : nullptr;
   if (wmode == K2Q_WMODE_W8)
-    return k2q_gemm_w8a8(qx, sx, static_cast<const int8_t*>(qw), static_cast<const float*>(sw), bias, uu,
-                         lora_a ? lora_b : nullptr, rr, lora_scale, M, N, K, y, ws, ws_bytes, stream);
+    return gemm_w8a8_impl(qx, sx, static_cast<const int8_t*>(qw), static_cast<const float*>(sw), bias, uu, parts,
+                          M * rr, lora_a ? lora_b : nullptr, rr, lora_scale, M, N, K, y, gws, gws_bytes, -1, st);
   return k2q_gemm_w4a8(qx, sx, static_cast<const uint8_t*>(qw), static_cast<const uint16_t*>(sw), bias, uu,
                        lora_a ? lora_b : nullptr, rr, lora_scale, M, N, K, y, stream);
 }

@@ -277,9 +277,9 @@ class ConvRotLinear(nn.Module):
         if grad:
             y = _ConvRotLinearFn.apply(x2, lora_A, lora_B, self.qweight, self.weight_scale, self._bias_f32(), w4,
                                        float(lora_scale), qx, sx, ready, self)
-        else:   # nothing to differentiate: no autograd node, the one library call
+        else:   # nothing to differentiate: no autograd node, the one library call (u stays internal)
             y, _ = _lib.linear_fwd(x2, qx, sx, ready, lora_A, lora_B, float(lora_scale), self.qweight,
-                                   self.weight_scale, self._bias_f32(), w4)
+                                   self.weight_scale, self._bias_f32(), w4, need_u=False)
         if not ready:
             shared_input_quant.keep(x, key, qx, sx)
         return y.reshape(*lead, self.out_features)

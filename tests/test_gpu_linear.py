@@ -6,6 +6,8 @@
   per rank: within f32 rounding of the down-projection kernel and of the float64 product), then the GEMV;
   y within the forward bar of the oracle.
 * ``codes_ready``: codes computed elsewhere (a producer kernel) are used as given.
+* No factors requested (inference): the GEMM epilogue adds the down-projection's K-slice partials itself
+  (W8, r <= 128) or u stays in the workspace; y is bit-identical to the separate launches either way.
 * W4A8 through the same call.
 """
 import numpy as np
@@ -36,7 +38,10 @@ def _case(M, K, N, r, seed, dev, w4=False, bias=True):
 
 
 @pytest.mark.parametrize("M,K,N,r,w4", [(512, 3072, 1024, 32, False), (300, 640, 384, 0, False),
-                                        (1024, 12288, 3072, 16, False), (256, 512, 384, 48, True)])
+                                        (1024, 12288, 3072, 16, False), (256, 512, 384, 48, True),
+                                        (4096, 3072, 3072, 16, False), (700, 1024, 512, 128, False),
+                                        (200, 2048, 256, 256, False), (64, 16384, 512, 64, False),
+                                        (8192, 3072, 12288, 16, False)])
 def test_one_call_equals_separate_launches(k2, dev, M, K, N, r, w4):
     L = k2._lib
     x, w, b, A, B = _case(M, K, N, r, M + K, dev, w4)
@@ -58,6 +63,10 @@ def test_one_call_equals_separate_launches(k2, dev, M, K, N, r, w4):
     # codes given (as a producer kernel leaves them): the call uses them as they are
     y1, _ = L.linear_fwd(xd, q0, s0, True, Ad, Bd, 0.75, qw, sw, bd, w4)
     assert torch.equal(y1, y0)
+    # no factors requested (inference): W8 with r <= 128 folds the down-projection's reduce into the GEMM
+    # epilogue, the other cases keep u in the workspace; y is the same bits either way
+    y2, u2 = L.linear_fwd(xd, qx, sx, False, Ad, Bd, 0.75, qw, sw, bd, w4, need_u=False)
+    assert u2 is None and torch.equal(y2, y0)
 
 
 @pytest.mark.parametrize("M,K,N,r", [(1, 3072, 18432, 16), (2, 3072, 18432, 16), (5, 12288, 3072, 64),
