@@ -13,55 +13,85 @@
 // through a transposing split first (R x M rows of hi and lo) and reaches LDS the same way.  Each workgroup
 // owns 256 columns and one slice of M; the slices' partials are added in slice order by a second kernel
 // (deterministic).
+//
+// Launches per rank chunk (at most 128 ranks): the down-projection of dY (its K-slice partials), one prep
+// kernel (the partials' sum g, and the hi/lo rows of g^T and u^T), one wgrad launch holding both dA and dB,
+// and one reduce for both when M is sliced.
+#include <algorithm>
 #include <mutex>
 
 #include "k2q_common.h"
 
 namespace {
 
-// out = transposed in (rows x cols f32, row-major): f32 out[c][r] = scale * in[r][c] (row stride ldo), or
-// (SPLIT) bf16 hi/lo rows out_hi[c][r], out_lo[c][r]; columns r in [rows, ldo) of the output are zeroed.
-template <bool SPLIT>
-__global__ __launch_bounds__(256) void transpose_kernel(const float* __restrict__ in, int64_t rows, int64_t cols,
-                                                        int64_t ldo, float scale, float* __restrict__ out,
-                                                        uint16_t* __restrict__ out_hi, uint16_t* __restrict__ out_lo) {
+// The wgrad operands of one rank chunk (rc ranks, a multiple of 16), in one launch; blockIdx.z picks the factor:
+//   z == 0: g = the sum of the down-projection's ns K-slice partials gp (slice s at gp + s M rc, rows of rc
+//           floats; added in slice order, as the down-projection's own reduce adds them) -> g (row stride ldg;
+//           null when gp is g itself) and, when gh is set, the bf16 hi/lo rows gh/gl of g^T (rc x Mp);
+//   z == 1: the hi/lo rows uh/ul of u^T, from u (row stride ldu).
+// Tiles of 32 m x 32 ranks pass through LDS (read as float4s along the ranks, written as 32 m per rank row);
+// columns m in [M, Mp) of the transposes are zero.
+__global__ __launch_bounds__(256) void grad_prep_kernel(const float* __restrict__ gp, int ns,
+                                                        const float* __restrict__ u, int64_t ldu, int64_t M,
+                                                        int64_t rc, int64_t Mp, float* __restrict__ g, int64_t ldg,
+                                                        uint16_t* __restrict__ gh, uint16_t* __restrict__ gl,
+                                                        uint16_t* __restrict__ uh, uint16_t* __restrict__ ul) {
   __shared__ float tile[32][33];
-  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;   // 32 x 8
-  const int64_t r0 = (int64_t)blockIdx.x * 32, c0 = (int64_t)blockIdx.y * 32;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t r = r0 + ty + 8 * i, c = c0 + tx;
-    tile[ty + 8 * i][tx] = (r < rows && c < cols) ? in[r * cols + c] : 0.f;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t c = c0 + ty + 8 * i, r = r0 + tx;
-    if (c >= cols || r >= ldo) continue;
-    const float v = tile[tx][ty + 8 * i];
-    if constexpr (SPLIT) {
-      const uint32_t h = f32_to_bf16_bits(v);
-      out_hi[c * ldo + r] = (uint16_t)h;
-      out_lo[c * ldo + r] = (uint16_t)f32_to_bf16_bits(v - bf16_bits_to_f32(h));
-    } else {
-      out[c * ldo + r] = scale * v;
+  const int64_t m0 = (int64_t)blockIdx.x * 32, j0 = (int64_t)blockIdx.y * 32;
+  const bool isg = blockIdx.z == 0;
+  {
+    const int lm = threadIdx.x >> 3, lj = 4 * (threadIdx.x & 7);   // 32 rows x 8 float4s
+    const int64_t m = m0 + lm, j = j0 + lj;
+    v4f v = {0.f, 0.f, 0.f, 0.f};
+    if (m < M && j < rc) {   // rc % 16 == 0: the float4 lies inside the chunk
+      if (isg) {
+        const v4f* p = reinterpret_cast<const v4f*>(gp + m * rc + j);
+        const int64_t step = M * rc / 4;
+        v = p[0];
+#pragma unroll 4
+        for (int s = 1; s < ns; ++s) v += p[s * step];
+        if (g) *reinterpret_cast<v4f*>(g + m * ldg + j) = v;
+      } else {
+        v = *reinterpret_cast<const v4f*>(u + m * ldu + j);
+      }
     }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tile[lm][lj + e] = v[e];
+  }
+  uint16_t* hi = isg ? gh : uh;
+  uint16_t* lo = isg ? gl : ul;
+  if (!hi) return;   // the same for the whole workgroup
+  __syncthreads();
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;   // 32 m x 8 rank rows
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t jj = j0 + ty + 8 * i, m = m0 + tx;
+    if (jj >= rc || m >= Mp) continue;
+    const float v = tile[tx][ty + 8 * i];
+    const uint32_t h = f32_to_bf16_bits(v);
+    hi[jj * Mp + m] = (uint16_t)h;
+    lo[jj * Mp + m] = (uint16_t)f32_to_bf16_bits(v - bf16_bits_to_f32(h));
   }
 }
 
 constexpr int WG_KB = 256;              // Q columns per workgroup (64 per wave)
 constexpr int WG_MS = 32;               // m rows per stage
-constexpr int WG_NST = 4;               // LDS ring depth (stages in flight: WG_NST - 1)
 constexpr int WG_QBYTES = WG_MS * 2 * WG_KB;   // 16 KB of Q per stage: 32 rows of 512 B
 constexpr int WG_QG = WG_QBYTES / 1024 / 4;    // Q DMA instructions per wave per stage
 
 // Per stage, P^T arrives as 2 RT blocks of 16 rows x 32 m (1 KB: hi blocks 0 .. RT-1, lo blocks RT ..), one DMA
-// instruction each, dealt PI per wave (padding instructions re-load block 0 into spare blocks).
+// instruction each, dealt PI per wave (padding instructions re-load block 0 into spare blocks).  Two workgroups
+// share a CU where two rings of at least 3 slots fit its 160 KB of LDS (RT <= 4): a workgroup streams at the
+// pace of its per-stage work (LDS gathers, MFMAs, one barrier), not of the memory latency (measured: 5 stages
+// in flight run no faster than 3), so a second workgroup adds more than deeper rings do.
 template <int RT>
 struct WgShape {
   static constexpr int PI = (2 * RT + 3) / 4;              // P DMA instructions per wave per stage
   static constexpr int G = WG_QG + PI;                     // all DMA instructions per wave per stage
   static constexpr int STAGE = WG_QBYTES + 4 * PI * 1024;  // bytes per ring slot
+  static constexpr int WPC = 2 * 3 * STAGE <= 160 * 1024 ? 2 : 1;   // workgroups per CU
+  static constexpr int NST = 160 * 1024 / (WPC * STAGE);            // ring depth
+  static_assert(NST >= 3 && (NST - 2) * G <= 63, "vmcnt counts at most 63 outstanding loads");
 };
 
 // Q: the 16-byte chunk c of row r sits at chunk c ^ wg_swz(r), so the four lane groups of a fragment
@@ -74,24 +104,48 @@ __device__ __forceinline__ void wg_wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// out (+ slice offset) = scale * P^T Q over the rows [mchunk*blockIdx.y, +mchunk) of M.
+// One product out = scale * P^T Q of the LoRA gradients (dA: P = g, Q = x; dB: P = u, Q = dY, transposed out).
 //   pth/ptl: R x Mp bf16 (P^T hi and lo, zero past M, Mp a multiple of 32); q: M x C bf16, row stride ldq.
-//   trans == 0: out[j][c] (R x C); trans == 1: out[c][j] (C rows of stride ldt).  With gridDim.y > 1 the partial of slice
-//   blockIdx.y goes to out + blockIdx.y * R * C in the [j][c] layout, unscaled (wgrad_reduce finishes it).
-// Both operands arrive by LDS-DMA (global_load_lds_dwordx4) through a WG_NST-slot ring, one s_waitcnt and
-// one s_barrier per stage (no __syncthreads: its fence would drain the prefetches).  Q rows past M are read
+//   The product runs as kblocks x slices workgroups: 256 columns each, over the rows [mchunk s, +mchunk) of M.
+//   slices == 1: out[j][c] (trans == 0, row stride C) or out[c][j] (trans == 1, row stride ldt), scaled.
+//   slices > 1: slice s's unscaled partial at out + s R C, [j][c] (row stride C) or [c][j] (row stride R);
+//   wgrad_reduce_kernel finishes it.
+struct WgJob {
+  const uint16_t* pth;
+  const uint16_t* ptl;
+  const uint16_t* q;
+  float* out;
+  int64_t C, ldq, ldt, kblocks, slices, mchunk, blocks;   // blocks = kblocks * slices (0: no product)
+  float scale;
+  int trans;
+};
+
+// Both products of a rank chunk in one launch: workgroups [0, ja.blocks) compute ja, the rest jb.
+// Both operands arrive by LDS-DMA (global_load_lds_dwordx4) through an NST-slot ring, one s_waitcnt and one
+// s_barrier per stage (no __syncthreads: its fence would drain the prefetches).  Q rows past M are read
 // clamped (finite values) and meet the zero padding of P^T, so they add nothing.
 template <int RT>
-__global__ __launch_bounds__(256) void wgrad_kernel(const uint16_t* __restrict__ pth, const uint16_t* __restrict__ ptl,
-                                                    int64_t M, int64_t Mp, const uint16_t* __restrict__ q, int64_t C,
-                                                    int64_t ldq, int64_t mchunk, float scale, int trans,
-                                                    int64_t ldt, float* __restrict__ out) {
+__global__ __launch_bounds__(256) void wgrad_kernel(WgJob ja, WgJob jb, int64_t M, int64_t Mp) {
   using S = WgShape<RT>;
   constexpr int R = 16 * RT;
-  __shared__ __attribute__((aligned(16))) uint8_t ring[WG_NST * S::STAGE];
+  constexpr int NST = S::NST;
+  __shared__ __attribute__((aligned(16))) uint8_t ring[NST * S::STAGE];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const int64_t kb = (int64_t)blockIdx.x * WG_KB;
-  const int64_t mb = (int64_t)blockIdx.y * mchunk;
+  // Field-wise selects keep the job in scalar registers.
+  const bool second = (int64_t)blockIdx.x >= ja.blocks;
+  const int64_t wi = second ? (int64_t)blockIdx.x - ja.blocks : (int64_t)blockIdx.x;
+  const uint16_t* pth = second ? jb.pth : ja.pth;
+  const uint16_t* ptl = second ? jb.ptl : ja.ptl;
+  const uint16_t* q = second ? jb.q : ja.q;
+  float* out = second ? jb.out : ja.out;
+  const int64_t C = second ? jb.C : ja.C, ldq = second ? jb.ldq : ja.ldq, ldt = second ? jb.ldt : ja.ldt;
+  const int64_t kblocks = second ? jb.kblocks : ja.kblocks, slices = second ? jb.slices : ja.slices;
+  const int64_t mchunk = second ? jb.mchunk : ja.mchunk;
+  const float scale = second ? jb.scale : ja.scale;
+  const int trans = second ? jb.trans : ja.trans;
+  const int64_t slice = wi / kblocks;
+  const int64_t kb = (wi - slice * kblocks) * WG_KB;
+  const int64_t mb = slice * mchunk;
   const int64_t me = M < mb + mchunk ? M : mb + mchunk;
   const int nsteps = (int)((me - mb + WG_MS - 1) / WG_MS);
 
@@ -143,14 +197,14 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const uint16_t* __restrict__
   // Past the last stage the DMA re-loads stage nsteps-1 into the freed slot (never one in use), which keeps
   // the count of outstanding instructions at the wait fixed.
 #pragma unroll
-  for (int st = 0; st < WG_NST - 1; ++st) issue(st < nsteps ? st : nsteps - 1, st);
+  for (int st = 0; st < NST - 1; ++st) issue(st < nsteps ? st : nsteps - 1, st);
   const int jr = lane & 15, g = lane >> 4;
   for (int s = 0; s < nsteps; ++s) {
-    wg_wait_vmcnt<(WG_NST - 2) * S::G>();
+    wg_wait_vmcnt<(NST - 2) * S::G>();
     asm volatile("s_barrier" ::: "memory");   // stage s landed for every wave; stage s-1's slot is free
-    const int nx = s + WG_NST - 1;
-    issue(nx < nsteps ? nx : nsteps - 1, nx % WG_NST);
-    const uint8_t* stg = ring + (s % WG_NST) * S::STAGE;
+    const int nx = s + NST - 1;
+    issue(nx < nsteps ? nx : nsteps - 1, nx % NST);
+    const uint8_t* stg = ring + (s % NST) * S::STAGE;
     v8bf ph[RT], pl[RT];
 #pragma unroll
     for (int jt = 0; jt < RT; ++jt) {
@@ -179,8 +233,10 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const uint16_t* __restrict__
   wg_wait_vmcnt<0>();   // no LDS-DMA in flight when the workgroup ends
 
   // C layout (16x16): lane l holds rows j = 4 (l/16) + i and column c = l%16 of tile (jt, kt).
-  const bool partial = gridDim.y > 1;
-  float* o = partial ? out + (int64_t)blockIdx.y * R * C : out;
+  const bool partial = slices > 1;
+  float* o = partial ? out + slice * R * C : out;
+  const float f = partial ? 1.f : scale;
+  const int64_t ldc = partial ? R : ldt;   // row stride of the [c][j] layout
 #pragma unroll
   for (int kt = 0; kt < 4; ++kt) {
     const int64_t c = kb + 64 * w + 16 * kt + (lane & 15);
@@ -188,49 +244,43 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const uint16_t* __restrict__
 #pragma unroll
     for (int jt = 0; jt < RT; ++jt) {
       const int j = 16 * jt + 4 * (lane >> 4);
-      if (partial || !trans) {
-        const float f = partial ? 1.f : scale;
+      if (trans) {
+        *reinterpret_cast<v4f*>(o + c * ldc + j) = f * acc[jt][kt];
+      } else {
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[(int64_t)(j + i) * C + c] = f * acc[jt][kt][i];
-      } else {
-        *reinterpret_cast<v4f*>(o + c * ldt + j) = scale * acc[jt][kt];
       }
     }
   }
 }
 
-// out = scale * sum over slices (slice order) of part[s][j][c]; layout [j][c] or (trans) [c][j] with row stride ldt.
-__global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restrict__ part, int S, int64_t R, int64_t C,
-                                                           float scale, int trans, int64_t ldt, float* __restrict__ out) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;   // index into [j][c]
-  if (i >= R * C) return;
-  float v = part[i];
-  for (int s = 1; s < S; ++s) v += part[s * R * C + i];
-  v *= scale;
-  if (trans) {
-    const int64_t j = i / C, c = i % C;
-    out[c * ldt + j] = v;
-  } else {
-    out[i] = v;
-  }
-}
-
-struct WgradPlan {
-  int64_t kblocks, slices, mchunk;
+// The slice sum of one product: out[row][col] = scale * sum over slices (slice order) of part[s][row][col]
+// (rows x cols, row stride cols, n4 = rows cols / 4 float4s per slice) with out rows of stride ldo.
+struct RedJob {
+  const float* part;
+  float* out;
+  int64_t cols, ldo, n4, blocks;   // blocks of 256 float4s (0: nothing to add)
+  int slices;
+  float scale;
 };
 
-WgradPlan wgrad_plan(int64_t M, int64_t C) {
-  WgradPlan p{};
-  p.kblocks = (C + WG_KB - 1) / WG_KB;
-  const int cus = k2q_cu_count();
-  int64_t s = cus / p.kblocks;
-  s = s < 1 ? 1 : s;
-  p.mchunk = ((M + s - 1) / s + WG_MS - 1) / WG_MS * WG_MS;
-  p.slices = (M + p.mchunk - 1) / p.mchunk;
-  return p;
+// Both products' slice sums in one launch: workgroups [0, ra.blocks) finish ra, the rest rb.
+__global__ __launch_bounds__(256) void wgrad_reduce_kernel(RedJob ra, RedJob rb) {
+  const bool second = (int64_t)blockIdx.x >= ra.blocks;
+  const int64_t wi = second ? (int64_t)blockIdx.x - ra.blocks : (int64_t)blockIdx.x;
+  const v4f* part = reinterpret_cast<const v4f*>(second ? rb.part : ra.part);
+  float* out = second ? rb.out : ra.out;
+  const int64_t cols = second ? rb.cols : ra.cols, ldo = second ? rb.ldo : ra.ldo, n4 = second ? rb.n4 : ra.n4;
+  const int slices = second ? rb.slices : ra.slices;
+  const float scale = second ? rb.scale : ra.scale;
+  const int64_t i = wi * 256 + threadIdx.x;
+  if (i >= n4) return;
+  v4f v = part[i];
+  for (int s = 1; s < slices; ++s) v += part[s * n4 + i];
+  v *= scale;
+  const int64_t e = 4 * i, row = e / cols;
+  *reinterpret_cast<v4f*>(out + row * ldo + (e - row * cols)) = v;
 }
-
-int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
 
 // Ranks run in chunks of at most GRAD_CHUNK (the wgrad kernel's largest rank tile), one after another on the
 // stream; dA's chunk c is rows [c GRAD_CHUNK, ..) of dA, dB's chunk c columns [c GRAD_CHUNK, ..) of dB.
@@ -242,46 +292,70 @@ bool grad_shape_ok(int64_t M, int64_t N, int64_t K, int64_t r) {
          r % 16 == 0;
 }
 
-struct GradLayout {
-  int64_t ld, pt, part_a, part_b, total;   // byte offsets into the workspace
-  int64_t mp;
-  WgradPlan pa, pb;
+// Slices of M shared by the two products (ca, cb: their column counts, 0 for a product not requested) for a
+// chunk of RT rank tiles: one round of workgroups that fills every workgroup slot (WPC per CU), with at least
+// 384 rows per workgroup (a workgroup's pipeline fill is ~3 stages of 32 rows) -- down to 128 rows when that
+// leaves fewer than half the CUs busy.  Measured on MI355X (M = 4096-4608, columns 3072-16384, ranks 16-64,
+// slice counts 1-16): the rule's count is within 3% of the fastest.
+struct GradPlan {
+  int64_t slices, mchunk;
 };
+
+GradPlan grad_plan(int64_t M, int64_t ca, int64_t cb, int rt) {
+  const int64_t cus = k2q_cu_count();
+  const int64_t wpc = rt <= 2 ? WgShape<2>::WPC : rt <= 4 ? WgShape<4>::WPC : WgShape<8>::WPC;
+  const int64_t kbs = (ca + WG_KB - 1) / WG_KB + (cb + WG_KB - 1) / WG_KB;
+  const int64_t fill = std::max<int64_t>(1, wpc * cus / std::max<int64_t>(kbs, 1));
+  int64_t s = std::min(fill, std::max<int64_t>(1, M / 384));
+  if (kbs * s < cus / 2) s = std::min(fill, std::max<int64_t>(1, M / 128));
+  const int64_t mchunk = ((M + s - 1) / s + WG_MS - 1) / WG_MS * WG_MS;
+  return GradPlan{(M + mchunk - 1) / mchunk, mchunk};
+}
+
+int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
+
+// Workspace: the hi/lo rows of g^T and u^T (all ranks), then one region that holds, in turn, the
+// down-projection's slice partials of g (read by grad_prep_kernel) and the two products' slice partials (dA's,
+// then dB's; written after the prep has run), sized for the largest chunk and any subset of {dA, dB}.
+struct GradLayout {
+  int64_t pt, parts, total;   // byte offsets into the workspace
+  int64_t mp;
+};
+
+int64_t chunk_ranks(int64_t r, int64_t c0) { return r - c0 < GRAD_CHUNK ? r - c0 : GRAD_CHUNK; }
+
+// Bytes of a product's slice partials (0 without slices).
+int64_t part_bytes(const GradPlan& p, int64_t rc, int64_t C) {
+  return p.slices > 1 ? align256(p.slices * rc * C * 4) : 0;
+}
 
 GradLayout grad_layout(int64_t M, int64_t N, int64_t K, int64_t r) {
   GradLayout L{};
   L.mp = (M + 31) / 32 * 32;
-  L.pa = wgrad_plan(M, K);
-  L.pb = wgrad_plan(M, N);
-  int64_t off = 0;
-  const int64_t rc = r < GRAD_CHUNK ? r : GRAD_CHUNK;   // ranks of the largest chunk (chunks share the partials)
-  L.ld = off;     off += align256(k2q_lora_down_ws_bytes(M, N, r));
-  L.pt = off;     off += 4 * align256(r * L.mp * 2);
-  L.part_a = off; off += L.pa.slices > 1 ? align256(L.pa.slices * rc * K * 4) : 0;
-  L.part_b = off; off += L.pb.slices > 1 ? align256(L.pb.slices * rc * N * 4) : 0;
-  L.total = off;
+  int64_t parts = 0;
+  for (int64_t c0 = 0; c0 < r; c0 += GRAD_CHUNK) {
+    const int64_t rc = chunk_ranks(r, c0);
+    const int rt = (int)(rc / 16);
+    parts = std::max(parts, align256(lora_down_parts_floats(M, N, rc) * 4));
+    const GradPlan both = grad_plan(M, K, N, rt), a = grad_plan(M, K, 0, rt), b = grad_plan(M, 0, N, rt);
+    parts = std::max({parts, part_bytes(both, rc, K) + part_bytes(both, rc, N), part_bytes(a, rc, K),
+                      part_bytes(b, rc, N)});
+  }
+  L.pt = 0;
+  L.parts = 4 * align256(r * L.mp * 2);
+  L.total = L.parts + parts;
   return L;
 }
 
 template <int RT>
-void launch_wgrad(const WgradPlan& p, hipStream_t st, const uint16_t* pth, const uint16_t* ptl, int64_t M, int64_t Mp,
-                  const uint16_t* q, int64_t C, float scale, int trans, int64_t ldt, float* part, float* out) {
-  const dim3 grid((unsigned)p.kblocks, (unsigned)p.slices);
-  float* o = p.slices > 1 ? part : out;
-  hipLaunchKernelGGL(wgrad_kernel<RT>, grid, dim3(256), 0, st, pth, ptl, M, Mp, q, C, C, p.mchunk, scale, trans, ldt,
-                     o);
-  if (p.slices > 1) {
-    const int64_t n = (int64_t)16 * RT * C;
-    hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, part,
-                       (int)p.slices, (int64_t)16 * RT, C, scale, trans, ldt, out);
-  }
+void launch_wgrad(const WgJob& ja, const WgJob& jb, int64_t M, int64_t Mp, hipStream_t st) {
+  hipLaunchKernelGGL(wgrad_kernel<RT>, dim3((unsigned)(ja.blocks + jb.blocks)), dim3(256), 0, st, ja, jb, M, Mp);
 }
 
-void wgrad(int rt, const WgradPlan& p, hipStream_t st, const uint16_t* pth, const uint16_t* ptl, int64_t M,
-           int64_t Mp, const uint16_t* q, int64_t C, float scale, int trans, int64_t ldt, float* part, float* out) {
+void wgrad(int rt, const WgJob& ja, const WgJob& jb, int64_t M, int64_t Mp, hipStream_t st) {
   switch (rt) {
 #define K2Q_WG_CASE(RT) \
-  case RT: launch_wgrad<RT>(p, st, pth, ptl, M, Mp, q, C, scale, trans, ldt, part, out); break;
+  case RT: launch_wgrad<RT>(ja, jb, M, Mp, st); break;
     K2Q_WG_CASE(1) K2Q_WG_CASE(2) K2Q_WG_CASE(3) K2Q_WG_CASE(4)
     K2Q_WG_CASE(5) K2Q_WG_CASE(6) K2Q_WG_CASE(7) K2Q_WG_CASE(8)
 #undef K2Q_WG_CASE
@@ -289,10 +363,35 @@ void wgrad(int rt, const WgradPlan& p, hipStream_t st, const uint16_t* pth, cons
   }
 }
 
-// P (M x r f32) -> hi/lo rows of P^T (r x Mp bf16).
-void split_t(hipStream_t st, const float* P, int64_t M, int64_t r, int64_t Mp, uint16_t* hi, uint16_t* lo) {
-  const dim3 grid((unsigned)((Mp + 31) / 32), (unsigned)((r + 31) / 32));
-  hipLaunchKernelGGL(transpose_kernel<true>, grid, dim3(256), 0, st, P, M, r, Mp, 1.f, nullptr, hi, lo);
+// The product of one rank chunk: its job for wgrad_kernel and, with slices, the reduce that finishes it.
+void make_job(const GradPlan& p, bool on, const uint16_t* pth, const uint16_t* ptl, const uint16_t* q, int64_t C,
+              int64_t R, float scale, int trans, int64_t ldt, float* part, float* out, WgJob& job, RedJob& red) {
+  job = WgJob{};
+  red = RedJob{};
+  if (!on) return;
+  job.pth = pth;
+  job.ptl = ptl;
+  job.q = q;
+  job.C = C;
+  job.ldq = C;
+  job.ldt = ldt;
+  job.kblocks = (C + WG_KB - 1) / WG_KB;
+  job.slices = p.slices;
+  job.mchunk = p.mchunk;
+  job.blocks = job.kblocks * p.slices;
+  job.scale = scale;
+  job.trans = trans;
+  job.out = p.slices > 1 ? part : out;
+  if (p.slices > 1) {
+    red.part = part;
+    red.out = out;
+    red.cols = trans ? R : C;
+    red.ldo = trans ? ldt : C;
+    red.n4 = R * C / 4;
+    red.blocks = (red.n4 + 255) / 256;
+    red.slices = (int)p.slices;
+    red.scale = scale;
+  }
 }
 
 }  // namespace
@@ -313,28 +412,43 @@ extern "C" int k2q_lora_grads(const uint16_t* dy, const uint16_t* x, const float
     return K2Q_EINVAL;
   const GradLayout L = grad_layout(M, N, K, r);
   if (ws_bytes < L.total) return K2Q_EINVAL;
-  if (L.pa.kblocks > 0xffff || L.pa.slices > 0xffff || L.pb.slices > 0xffff) return K2Q_EUNSUPPORTED;
+  if ((L.mp / 32) > 0x7fffffff) return K2Q_EUNSUPPORTED;
   hipStream_t st = static_cast<hipStream_t>(stream);
   uint8_t* w = static_cast<uint8_t*>(ws);
   const int64_t pt_bytes = align256(r * L.mp * 2);
   uint16_t* pt[4];
   for (int i = 0; i < 4; ++i) pt[i] = reinterpret_cast<uint16_t*>(w + L.pt + i * pt_bytes);
 
-  // g = dY (scale B^T)^T: the down-projection kernel with dY as the activation and scale * B^T as the factor,
-  // read from B (N x r) directly.
-  const int64_t ld_bytes = k2q_lora_down_ws_bytes(M, N, r);
-  int rc = lora_down_impl(dy, M, N, N, lora_b, r, scale, r, ld_bytes ? w + L.ld : nullptr, ld_bytes, g, st);
-  if (rc) return rc;
-  if (dA) split_t(st, g, M, r, L.mp, pt[0], pt[1]);
-  if (dB) split_t(st, u, M, r, L.mp, pt[2], pt[3]);
   for (int64_t c0 = 0; c0 < r; c0 += GRAD_CHUNK) {
-    const int rt = (int)((r - c0 < GRAD_CHUNK ? r - c0 : GRAD_CHUNK) / 16);
-    if (dA)
-      wgrad(rt, L.pa, st, pt[0] + c0 * L.mp, pt[1] + c0 * L.mp, M, L.mp, x, K, 1.f, 0, 0,
-            reinterpret_cast<float*>(w + L.part_a), dA + c0 * K);
-    if (dB)
-      wgrad(rt, L.pb, st, pt[2] + c0 * L.mp, pt[3] + c0 * L.mp, M, L.mp, dy, N, scale, 1, r,
-            reinterpret_cast<float*>(w + L.part_b), dB + c0);
+    const int64_t rc = chunk_ranks(r, c0);
+    // g = dY (scale B^T)^T: the down-projection kernel with dY as the activation and scale * B^T as the
+    // factor, read from B (N x r) directly; its K-slice partials are added by grad_prep_kernel.  With one
+    // slice and one chunk the partial is g itself (same row stride), written in place.
+    const bool direct = r <= GRAD_CHUNK && lora_down_parts_floats(M, N, rc) == M * rc;
+    float* gp = direct ? g : reinterpret_cast<float*>(w + L.parts);
+    int ns = 0;
+    int rcode = lora_down_parts(dy, M, N, N, lora_b + c0, r, scale, rc, gp, &ns, st);
+    if (rcode) return rcode;
+    if (direct && !dA && !dB) continue;
+    const dim3 pgrid((unsigned)(L.mp / 32), (unsigned)((rc + 31) / 32), dB ? 2u : 1u);
+    hipLaunchKernelGGL(grad_prep_kernel, pgrid, dim3(256), 0, st, gp, ns, dB ? u + c0 : nullptr, r, M, rc, L.mp,
+                       direct ? nullptr : g + c0, r, dA ? pt[0] + c0 * L.mp : nullptr,
+                       dA ? pt[1] + c0 * L.mp : nullptr, dB ? pt[2] + c0 * L.mp : nullptr,
+                       dB ? pt[3] + c0 * L.mp : nullptr);
+    if (!dA && !dB) continue;
+    const GradPlan p = grad_plan(M, dA ? K : 0, dB ? N : 0, (int)(rc / 16));
+    WgJob ja, jb;
+    RedJob ra, rb;
+    float* part_a = reinterpret_cast<float*>(w + L.parts);
+    float* part_b = reinterpret_cast<float*>(w + L.parts + (dA ? part_bytes(p, rc, K) : 0));
+    make_job(p, dA != nullptr, pt[0] + c0 * L.mp, pt[1] + c0 * L.mp, x, K, rc, 1.f, 0, 0, part_a,
+             dA ? dA + c0 * K : nullptr, ja, ra);
+    make_job(p, dB != nullptr, pt[2] + c0 * L.mp, pt[3] + c0 * L.mp, dy, N, rc, scale, 1, r, part_b,
+             dB ? dB + c0 : nullptr, jb, rb);
+    if (ja.blocks + jb.blocks > 0x7fffffff) return K2Q_EUNSUPPORTED;
+    wgrad((int)(rc / 16), ja, jb, M, L.mp, st);
+    if (ra.blocks + rb.blocks > 0)
+      hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((unsigned)(ra.blocks + rb.blocks)), dim3(256), 0, st, ra, rb);
   }
   return k2q_launch_status();
 }
