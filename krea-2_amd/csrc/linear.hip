@@ -4,32 +4,65 @@
 // issued from here, so a caller pays one foreign call per linear.
 //
 // Skinny M (M <= K2Q_GEMV_MAX_M: the adaLN modulation linears run at M = batch) has one more fusion: a prologue
-// kernel computes a row's int8 codes and its LoRA factors u = x A^T in one launch (one workgroup per row), and
-// the GEMV follows, so the linear is two launches.  Its codes are bit-identical to k2q_rotquant (same butterfly
-// per 128-block, same quantizer); u is an f32 dot product per rank in a fixed order (x is bf16, so every product
-// is exact in f32; the sums differ from the MFMA down-projection only by f32 rounding).
+// kernel computes the rows' int8 codes (one workgroup per row) and the LoRA factors u = x A^T (one workgroup
+// per rank, its factor row kept in registers while the M rows stream past) in one launch, and the GEMV follows,
+// so the linear is two launches.  Its codes are bit-identical to k2q_rotquant (same butterfly per 128-block,
+// same quantizer); u is an f32 dot product per rank in a fixed order (x is bf16, so every product is exact in
+// f32; the sums differ from the MFMA down-projection only by f32 rounding).
 #include "rotation.h"
 
 namespace {
 
 using namespace k2q_rot;
 
-constexpr int SK_T = 256;       // lanes per row (four waves)
+constexpr int SK_T = 256;       // lanes per workgroup (four waves)
 constexpr int SK_CW = SK_T * 16;   // elements per chunk
-constexpr int SK_JB = 16;       // ranks per reduction batch
 
-// Row blockIdx.x of x: u[row, :] = x[row, :] A^T (when a != nullptr), then (when q != nullptr) the codes and scale
-// of the rotated row.  kNCH chunks of 4096 elements cover K.
+// Workgroups [0, ncode): row blockIdx.x's codes and scale (the row rotated in registers, one amax).
+// Workgroups [ncode, ncode + r): rank j = blockIdx.x - ncode: u[m, j] = x[m, :] . A[j, :] for the M rows, each
+// lane's 16 columns per chunk summed in column order, then the wave's lanes (shuffle tree), then the four
+// waves in order.  kNCH chunks of 4096 elements cover K.
 template <int kNCH>
 __global__ __launch_bounds__(SK_T) void skinny_prologue_kernel(const __bf16* __restrict__ x, int64_t ldx, int K,
-                                                               const float* __restrict__ a, int r,
-                                                               float* __restrict__ u, int8_t* __restrict__ q,
-                                                               float* __restrict__ s) {
-  __shared__ float red[4][SK_JB];
+                                                               int M, const float* __restrict__ a, int r,
+                                                               float* __restrict__ u, int ncode,
+                                                               int8_t* __restrict__ q, float* __restrict__ s) {
+  __shared__ float red[2][4];
   __shared__ float smax[4];
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-  const int64_t row = blockIdx.x;
   const int off = lane_offset(t);
+
+  if ((int)blockIdx.x >= ncode) {
+    const int j = (int)blockIdx.x - ncode;
+    float w[kNCH][16];
+#pragma unroll
+    for (int c = 0; c < kNCH; ++c) {
+      const int col = c * SK_CW + off;
+      load16<float>(a + (int64_t)j * K + col, col < K, w[c]);
+    }
+    for (int m = 0; m < M; ++m) {
+      float v[kNCH][16];
+#pragma unroll
+      for (int c = 0; c < kNCH; ++c) {
+        const int col = c * SK_CW + off;
+        load16<__bf16>(x + m * ldx + col, col < K, v[c]);
+      }
+      float p = 0.f;
+#pragma unroll
+      for (int c = 0; c < kNCH; ++c) {
+        if (c * SK_CW + off >= K) continue;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) p = __builtin_fmaf(v[c][e], w[c][e], p);
+      }
+      p = wave_sum(p);
+      if (lane == 0) red[m & 1][wave] = p;
+      __syncthreads();   // red[m & 1] is rewritten two rows later, after the next row's barrier
+      if (t == 0) u[(int64_t)m * r + j] = ((red[m & 1][0] + red[m & 1][1]) + red[m & 1][2]) + red[m & 1][3];
+    }
+    return;
+  }
+
+  const int64_t row = blockIdx.x;
   const __bf16* xr = x + row * ldx;
   float v[kNCH][16];
 #pragma unroll
@@ -37,42 +70,6 @@ __global__ __launch_bounds__(SK_T) void skinny_prologue_kernel(const __bf16* __r
     const int col = c * SK_CW + off;
     load16<__bf16>(xr + col, col < K, v[c]);
   }
-
-  if (a) {
-    for (int j0 = 0; j0 < r; j0 += SK_JB) {
-      float p[SK_JB];
-#pragma unroll
-      for (int j = 0; j < SK_JB; ++j) p[j] = 0.f;
-#pragma unroll
-      for (int c = 0; c < kNCH; ++c) {
-        const int col = c * SK_CW + off;
-        if (col >= K) continue;
-#pragma unroll
-        for (int j = 0; j < SK_JB; ++j) {
-          const float4* ap = reinterpret_cast<const float4*>(a + (int64_t)(j0 + j) * K + col);
-#pragma unroll
-          for (int e4 = 0; e4 < 4; ++e4) {
-            const float4 w = ap[e4];
-            p[j] = __builtin_fmaf(v[c][4 * e4], w.x, p[j]);
-            p[j] = __builtin_fmaf(v[c][4 * e4 + 1], w.y, p[j]);
-            p[j] = __builtin_fmaf(v[c][4 * e4 + 2], w.z, p[j]);
-            p[j] = __builtin_fmaf(v[c][4 * e4 + 3], w.w, p[j]);
-          }
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < SK_JB; ++j) p[j] = wave_sum(p[j]);
-      if (lane == 0) {
-#pragma unroll
-        for (int j = 0; j < SK_JB; ++j) red[wave][j] = p[j];
-      }
-      __syncthreads();
-      if (t < SK_JB) u[row * r + j0 + t] = ((red[0][t] + red[1][t]) + red[2][t]) + red[3][t];
-      __syncthreads();
-    }
-  }
-  if (!q) return;
-
   const int l = t & 15;
   const float c1 = (l & 1) ? -1.f : 1.f;
   const float c2 = (l & 2) ? -1.f : 1.f;
@@ -106,12 +103,17 @@ int launch_skinny(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, const fl
                   float* s, hipStream_t st) {
   const __bf16* xp = reinterpret_cast<const __bf16*>(x);
   const int nch = (int)((K + SK_CW - 1) / SK_CW);
-  const dim3 grid((unsigned)M);
+  const int ncode = q ? (int)M : 0;
+  const dim3 grid((unsigned)(ncode + (a ? r : 0)));
+  if (grid.x == 0) return K2Q_OK;
   switch (nch) {
-    case 1: hipLaunchKernelGGL(skinny_prologue_kernel<1>, grid, dim3(SK_T), 0, st, xp, ldx, (int)K, a, (int)r, u, q, s); break;
-    case 2: hipLaunchKernelGGL(skinny_prologue_kernel<2>, grid, dim3(SK_T), 0, st, xp, ldx, (int)K, a, (int)r, u, q, s); break;
-    case 3: hipLaunchKernelGGL(skinny_prologue_kernel<3>, grid, dim3(SK_T), 0, st, xp, ldx, (int)K, a, (int)r, u, q, s); break;
-    case 4: hipLaunchKernelGGL(skinny_prologue_kernel<4>, grid, dim3(SK_T), 0, st, xp, ldx, (int)K, a, (int)r, u, q, s); break;
+#define K2Q_SK_CASE(NCH)                                                                                          \
+  case NCH:                                                                                                      \
+    hipLaunchKernelGGL(skinny_prologue_kernel<NCH>, grid, dim3(SK_T), 0, st, xp, ldx, (int)K, (int)M, a, (int)r, u, \
+                       ncode, q, s);                                                                             \
+    break;
+    K2Q_SK_CASE(1) K2Q_SK_CASE(2) K2Q_SK_CASE(3) K2Q_SK_CASE(4)
+#undef K2Q_SK_CASE
     default: return K2Q_EUNSUPPORTED;
   }
   return k2q_launch_status();
