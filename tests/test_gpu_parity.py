@@ -233,6 +233,30 @@ def test_lora_grads(k2, dev, M, N, K, r):
     assert dA2 is None and dB2 is None and torch.equal(g2, g)      # deterministic; optional outputs
 
 
+@pytest.mark.parametrize("M,N,K,r", [(777, 640, 1280, 48), (64, 4096, 256, 16), (2048, 256, 4096, 32),
+                                     (1000, 1024, 768, 144), (33, 512, 640, 96)])
+def test_lora_grads_single_products(k2, dev, M, N, K, r):
+    """dA alone and dB alone (the other gradient not requested) against float64: the workgroups of the shared
+    wgrad launch and the slice count are planned for the products requested, so each subset runs its own
+    schedule; g is the same bits in every mode."""
+    gen = torch.Generator().manual_seed(3 * M + N + r)
+    dy = (torch.randn(M, N, generator=gen) * 1e-3).to(torch.bfloat16)
+    x = make_x(M, K, seed=r + 1)
+    u = torch.randn(M, r, generator=gen)
+    B = torch.randn(N, r, generator=gen) * 0.01
+    s = 1.25
+    g64 = s * (dy.double() @ B.double())
+    dA64 = g64.t() @ x.double()
+    dB64 = s * (dy.double().t() @ u.double())
+    g, dA, dB = k2._lib.lora_grads(dy.to(dev), x.to(dev), u.to(dev), B.to(dev), s)
+    ga, dAa, dBa = k2._lib.lora_grads(dy.to(dev), x.to(dev), None, B.to(dev), s)
+    gb, dAb, dBb = k2._lib.lora_grads(dy.to(dev), None, u.to(dev), B.to(dev), s)
+    assert dBa is None and dAb is None
+    assert torch.equal(ga, g) and torch.equal(gb, g)
+    for got, want in ((dA, dA64), (dAa, dA64), (dB, dB64), (dBb, dB64)):
+        assert rel_frob(got.cpu().numpy(), want.numpy()) < 2e-5
+
+
 # Skinny M (1 <= M <= 8: the adaLN modulation linears run at M = batch) takes the GEMV path.
 @pytest.mark.parametrize("Ms,K,N,bias", [(1, 128, 4, False), (2, 3072, 1000, True), (5, 640, 260, False),
                                          (8, 12288, 256, True), (3, 16384, 36, False)])
