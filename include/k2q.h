@@ -96,11 +96,34 @@ int k2q_lora_grads(const uint16_t* dy, const uint16_t* x, const float* u, const 
                    float scale, int64_t M, int64_t N, int64_t K, float* g, float* dA, float* dB, void* ws,
                    int64_t ws_bytes, void* stream);
 
+/* One member of k2q_lora_grads_grouped: a linear that reads the group's shared input. */
+typedef struct {
+  const uint16_t* dy;    /* M x N bf16 output gradient, row stride ldy (a multiple of 8) */
+  int64_t ldy;
+  int64_t N;             /* out_features, a multiple of 128 */
+  const float* lora_b;   /* N x r f32 */
+  float scale;           /* the member's LoRA scale s_i */
+  float* dB;             /* N x r f32 out (s_i dy_i^T u_i), or NULL */
+} k2q_lora_member;
+
+/* The LoRA gradients of n <= 8 linears with one rank r <= 128 that read one input x (M x K bf16): the
+ * autograd of lora.py:47-48 for every member of a grouped node (the linears of Attention.forward that read
+ * one tensor, mmdit.py:199; SwiGLU's gate and up, mmdit.py:178).  Member i: g_i = s_i dy_i B_i into columns
+ * [i r, (i+1) r) of g (M x n r, row stride n r: the stacked layout k2q_gemm_dx_grouped reads); dA_i = g_i^T x
+ * into rows [i r, (i+1) r) of dA (n r x K; NULL: none), computed over the stacked ranks in one pass over x per
+ * 128 of them; dB_i from u_i = columns [i r, (i+1) r) of u (M x n r, the grouped forward's stacked factors).
+ * Same arithmetic as k2q_lora_grads per member.  ws: k2q_lora_grads_grouped_ws_bytes bytes, 256-aligned. */
+int64_t k2q_lora_grads_grouped_ws_bytes(const k2q_lora_member* members, int64_t n, int64_t M, int64_t K,
+                                        int64_t r);
+int k2q_lora_grads_grouped(const k2q_lora_member* members, int64_t n, const uint16_t* x, const float* u,
+                           int64_t r, int64_t M, int64_t K, float* g, float* dA, void* ws, int64_t ws_bytes,
+                           void* stream);
+
 /* k2q_lora_grads without a workspace argument; allocates nothing.  No counterpart in the reference: it is for
  * callers that cannot allocate device memory (code under HIP graph capture, tight serving or training loops,
  * harnesses that forbid it).  The workspace comes from a device array inside the library, K2Q_SCRATCH_BYTES per
  * GPU, held until the process ends; a shape whose k2q_lora_grads_ws_bytes exceeds it returns K2Q_ESCRATCH
- * before any launch (cfg3's M = 4608, N = 3072, K = 12288, r = 64 needs ~38 MB).  Every call on one GPU shares
+ * before any launch (cfg3's M = 4608, N = 3072, K = 12288, r = 64 needs ~34 MB).  Every call on one GPU shares
  * that GPU's scratch: calls that overlap on one GPU (two streams, two threads) race.  Results are bit-identical
  * to k2q_lora_grads. */
 #define K2Q_SCRATCH_BYTES ((int64_t)64 << 20)

@@ -38,6 +38,12 @@ class DxSegment(ctypes.Structure):
     _fields_ = [("dy", ctypes.c_void_p), ("ldy", ctypes.c_int64), ("wt", ctypes.c_void_p), ("N", ctypes.c_int64)]
 
 
+class LoraMember(ctypes.Structure):
+    """``k2q_lora_member`` of ``include/k2q.h``: one linear of a grouped LoRA-gradient call."""
+    _fields_ = [("dy", ctypes.c_void_p), ("ldy", ctypes.c_int64), ("N", ctypes.c_int64), ("lora_b", ctypes.c_void_p),
+                ("scale", ctypes.c_float), ("dB", ctypes.c_void_p)]
+
+
 class W8A8Segment(ctypes.Structure):
     """``k2q_w8a8_segment`` of ``include/k2q.h``: one linear of a grouped forward."""
     _fields_ = [("qw", ctypes.c_void_p), ("sw", ctypes.c_void_p), ("bias", ctypes.c_void_p),
@@ -61,6 +67,8 @@ _SIGNATURES = {
     "k2q_lora_down": ([_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _p, _p], _int),
     "k2q_lora_grads_ws_bytes": ([_i64, _i64, _i64, _i64], _i64),
     "k2q_lora_grads": ([_p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p], _int),
+    "k2q_lora_grads_grouped_ws_bytes": ([_p, _i64, _i64, _i64, _i64], _i64),
+    "k2q_lora_grads_grouped": ([_p, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _p, _i64, _p], _int),
     "k2q_lora_grads_noalloc": ([_p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p, _p, _p], _int),
     "k2q_gemm_w8a8_ws_bytes": ([_i64, _i64, _i64], _i64),
     "k2q_gemm_w8a8": ([_p, _p, _p, _p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p, _i64, _p], _int),
@@ -391,6 +399,64 @@ def lora_grads(dy, x, u, lora_b, lora_scale: float):
     _check(lib.k2q_lora_grads(_ptr(dy), _ptr(x), _ptr(u), _ptr(lora_b), r, float(lora_scale), M, N, K, _ptr(g),
                               _ptr(dA), _ptr(dB), _ptr(ws), nws, _stream(dev)), "k2q_lora_grads")
     return g, dA, dB
+
+
+LORA_GROUP_MAX = 8     # members per k2q_lora_grads_grouped call
+
+
+def lora_grads_grouped(dys, x, u, lora_bs, scales, want_db=None):
+    """LoRA gradients of linears that read one input (``k2q_lora_grads_grouped``; the autograd of ``lora.py:47-48``
+    for every member of a grouped node).  Member i: output gradient ``dys[i]`` (M,N_i) bf16, ``lora_bs[i]``
+    (N_i,r) f32 (one rank r <= 128 for all), scale ``scales[i]``.  ``x`` (M,K) bf16 or None (no dA); ``u`` (M, n r)
+    f32, the grouped forward's stacked factors (needed when any dB is wanted).  Returns ``(g, dA | None, dBs)``:
+    ``g`` (M, n r) f32 with member i's ``s_i dy_i B_i`` in columns ``[i r, (i+1) r)``; ``dA`` (n r, K) f32, member
+    i's rows ``[i r, (i+1) r)``; ``dBs[i]`` (N_i, r) f32 where ``want_db[i]`` (default: every member), else None."""
+    n = len(dys)
+    if n < 1 or n > LORA_GROUP_MAX or len(lora_bs) != n or len(scales) != n:
+        raise ValueError(f"lora_grads_grouped takes 1..{LORA_GROUP_MAX} members with one B and scale each")
+    want_db = [True] * n if want_db is None else list(want_db)
+    dev = dys[0].device
+    M = dys[0].shape[0]
+    r = lora_bs[0].shape[1]
+    _check_rank(r)
+    if r > 128:
+        raise ValueError(f"lora_grads_grouped: rank {r} above 128 (use lora_grads per member)")
+    arr = (LoraMember * n)()
+    dBs = []
+    for i, (dy, B) in enumerate(zip(dys, lora_bs)):
+        if dy.dtype != torch.bfloat16 or dy.dim() != 2 or dy.device != dev or dy.shape[0] != M or dy.stride(1) != 1 \
+                or dy.stride(0) % 8 or dy.data_ptr() % 16:
+            raise ValueError(f"dy[{i}] must be ({M}, N) bf16 on {dev} with unit column stride and 16-byte rows")
+        N = dy.shape[1]
+        if N % HADAMARD_BLOCK:
+            raise ValueError(f"member {i}: out_features={N} must be a multiple of {HADAMARD_BLOCK}")
+        _need(B, f"lora_B[{i}]", torch.float32, 2, dev)
+        if B.shape != (N, r):
+            raise ValueError(f"member {i}: lora_B must be {(N, r)}, got {tuple(B.shape)}")
+        dB = torch.empty((N, r), dtype=torch.float32, device=dev) if want_db[i] else None
+        dBs.append(dB)
+        arr[i] = LoraMember(dy.data_ptr(), dy.stride(0), N, B.data_ptr(), float(scales[i]), _ptr(dB))
+    K = HADAMARD_BLOCK
+    if x is not None:
+        _need(x, "x", torch.bfloat16, 2, dev)
+        if x.shape[0] != M:
+            raise ValueError("x rows != dy rows")
+        K = x.shape[1]
+        _check_k(K)
+    if any(want_db):
+        _need(u, "u", torch.float32, 2, dev)
+        if u.shape != (M, n * r):
+            raise ValueError(f"u must be {(M, n * r)} (the stacked factors), got {tuple(u.shape)}")
+    _device_check(dev)
+    lib = load()
+    nws = lib.k2q_lora_grads_grouped_ws_bytes(ctypes.addressof(arr), n, M, K, r)
+    ws = torch.empty((nws,), dtype=torch.uint8, device=dev)
+    g = torch.empty((M, n * r), dtype=torch.float32, device=dev)
+    dA = torch.empty((n * r, K), dtype=torch.float32, device=dev) if x is not None else None
+    _check(lib.k2q_lora_grads_grouped(ctypes.addressof(arr), n, _ptr(x), _ptr(u) if any(want_db) else None, r, M, K,
+                                      g.data_ptr(), _ptr(dA), ws.data_ptr(), nws, _stream(dev)),
+           "k2q_lora_grads_grouped")
+    return g, dA, dBs
 
 
 SCRATCH_BYTES = 64 << 20     # K2Q_SCRATCH_BYTES: the library's own device scratch per GPU

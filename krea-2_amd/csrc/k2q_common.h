@@ -42,11 +42,11 @@ int lora_down_impl(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const f
                    float a_scale, int64_t r, void* ws, int64_t ws_bytes, float* u, hipStream_t st);
 
 // The down-projection's K-slice partials without the reduce, for a consumer that adds them as it reads them
-// (r <= 128; factor as for lora_down_impl): dst receives lora_down_parts_floats(M, K, r) floats, *parts slices
-// of M x r (row stride r, M * r floats apart; one slice is u itself).
+// (r <= 128; factor as for lora_down_impl): *parts slices of M x r, rows of stride ldo, M * ldo floats apart
+// (one slice is u itself); with ldo = r, dst receives lora_down_parts_floats(M, K, r) floats.
 int64_t lora_down_parts_floats(int64_t M, int64_t K, int64_t r);
 int lora_down_parts(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const float* a, int64_t a_kstride,
-                    float a_scale, int64_t r, float* dst, int* parts, hipStream_t st);
+                    float a_scale, int64_t r, float* dst, int64_t ldo, int* parts, hipStream_t st);
 
 // k2q_gemm_w8a8 with the factors u given as u_parts K-slice partials u_pstride floats apart (added in slice
 // order in the epilogue, exactly as the down-projection's reduce adds them) and a tile shape (-1: automatic).

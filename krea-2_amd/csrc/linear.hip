@@ -202,7 +202,7 @@ extern "C" int k2q_linear_fwd(const uint16_t* x, int64_t ldx, int64_t M, int64_t
       if (!u && wmode == K2Q_WMODE_W8 && rr <= 128 && fold_pays(M, N, K, rr)) {
         // nobody needs u itself: the GEMM epilogue adds the K-slice partials (no reduce launch)
         float* dst = reinterpret_cast<float*>(w + lay.parts_off);
-        rc = lora_down_parts(x, M, K, ldx, lora_a, 1, 1.f, rr, dst, &parts, st);
+        rc = lora_down_parts(x, M, K, ldx, lora_a, 1, 1.f, rr, dst, rr, &parts, st);
         uu = dst;
       } else {
         float* ut = u ? u : reinterpret_cast<float*>(w + lay.u_off);

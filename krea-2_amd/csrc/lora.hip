@@ -516,15 +516,15 @@ int64_t lora_down_parts_floats(int64_t M, int64_t K, int64_t r) {
 }
 
 int lora_down_parts(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const float* lora_a, int64_t a_kstride,
-                    float a_scale, int64_t r, float* dst, int* parts, hipStream_t st) {
+                    float a_scale, int64_t r, float* dst, int64_t ldo, int* parts, hipStream_t st) {
   if (!x || !lora_a || !dst || !parts || M < 1 || K < 128 || K % 128 || ldx < K || ldx % 8) return K2Q_EINVAL;
-  if (!rank_ok(r) || r > LORA_CHUNK || a_kstride < 1) return K2Q_EINVAL;
+  if (!rank_ok(r) || r > LORA_CHUNK || a_kstride < 1 || ldo < r || ldo % 4) return K2Q_EINVAL;
   if (!k2q_aligned(x, 16) || !k2q_aligned(lora_a, 16) || !k2q_aligned(dst, 16)) return K2Q_EINVAL;
   const AsPlan q = as_plan(M, K, r);
   if (q.groups > 0x7fffffff || q.slices > 0xffff) return K2Q_EUNSUPPORTED;
   switch (r / 16) {
 #define K2Q_AS_CASE(RT) \
-  case RT: launch_as<RT>(q, st, x, M, ldx, lora_a, K, a_kstride, a_scale, r, dst); break;
+  case RT: launch_as<RT>(q, st, x, M, ldx, lora_a, K, a_kstride, a_scale, ldo, dst); break;
     K2Q_AS_CASE(1) K2Q_AS_CASE(2) K2Q_AS_CASE(3) K2Q_AS_CASE(4)
     K2Q_AS_CASE(5) K2Q_AS_CASE(6) K2Q_AS_CASE(7) K2Q_AS_CASE(8)
 #undef K2Q_AS_CASE

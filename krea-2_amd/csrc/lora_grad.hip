@@ -25,13 +25,13 @@
 namespace {
 
 // The wgrad operands of one rank chunk (rc ranks, a multiple of 16), in one launch; blockIdx.z picks the factor:
-//   z == 0: g = the sum of the down-projection's ns K-slice partials gp (slice s at gp + s M rc, rows of rc
-//           floats; added in slice order, as the down-projection's own reduce adds them) -> g (row stride ldg;
-//           null when gp is g itself) and, when gh is set, the bf16 hi/lo rows gh/gl of g^T (rc x Mp);
+//   z == 0: g = the sum of the down-projection's ns K-slice partials gp (rows of stride ldp, slice s at
+//           gp + s M ldp; added in slice order, as the down-projection's own reduce adds them) -> g (row stride
+//           ldg; null when gp is g itself) and, when gh is set, the bf16 hi/lo rows gh/gl of g^T (rc x Mp);
 //   z == 1: the hi/lo rows uh/ul of u^T, from u (row stride ldu).
 // Tiles of 32 m x 32 ranks pass through LDS (read as float4s along the ranks, written as 32 m per rank row);
 // columns m in [M, Mp) of the transposes are zero.
-__global__ __launch_bounds__(256) void grad_prep_kernel(const float* __restrict__ gp, int ns,
+__global__ __launch_bounds__(256) void grad_prep_kernel(const float* __restrict__ gp, int64_t ldp, int ns,
                                                         const float* __restrict__ u, int64_t ldu, int64_t M,
                                                         int64_t rc, int64_t Mp, float* __restrict__ g, int64_t ldg,
                                                         uint16_t* __restrict__ gh, uint16_t* __restrict__ gl,
@@ -43,10 +43,10 @@ __global__ __launch_bounds__(256) void grad_prep_kernel(const float* __restrict_
     const int lm = threadIdx.x >> 3, lj = 4 * (threadIdx.x & 7);   // 32 rows x 8 float4s
     const int64_t m = m0 + lm, j = j0 + lj;
     v4f v = {0.f, 0.f, 0.f, 0.f};
-    if (m < M && j < rc) {   // rc % 16 == 0: the float4 lies inside the chunk
+    if (m < M && j < rc) {   // rc, ldp, ldu, ldg multiples of 4: the float4 lies inside the chunk, aligned
       if (isg) {
-        const v4f* p = reinterpret_cast<const v4f*>(gp + m * rc + j);
-        const int64_t step = M * rc / 4;
+        const v4f* p = reinterpret_cast<const v4f*>(gp + m * ldp + j);
+        const int64_t step = M * ldp / 4;
         v = p[0];
 #pragma unroll 4
         for (int s = 1; s < ns; ++s) v += p[s * step];
@@ -120,29 +120,51 @@ struct WgJob {
   int trans;
 };
 
-// Both products of a rank chunk in one launch: workgroups [0, ja.blocks) compute ja, the rest jb.
+// Up to WG_MAXJ products of one rank tile count in one launch, their workgroups laid out product after product.
+constexpr int WG_MAXJ = 8;
+struct WgJobs {
+  WgJob j[WG_MAXJ];
+  int n;
+};
+
+// The product workgroup b belongs to, and b's index inside it.  Constant-index copies keep the selected
+// product's fields in scalar registers.
+__device__ __forceinline__ WgJob pick_job(const WgJobs& js, int64_t b, int64_t& wi) {
+  int sel = 0;
+  wi = b;
+#pragma unroll
+  for (int i = 0; i < WG_MAXJ - 1; ++i)
+    if (sel == i && i + 1 < js.n && wi >= js.j[i].blocks) {
+      wi -= js.j[i].blocks;
+      sel = i + 1;
+    }
+  WgJob job = js.j[0];
+#pragma unroll
+  for (int i = 1; i < WG_MAXJ; ++i)
+    if (sel == i) job = js.j[i];
+  return job;
+}
+
 // Both operands arrive by LDS-DMA (global_load_lds_dwordx4) through an NST-slot ring, one s_waitcnt and one
 // s_barrier per stage (no __syncthreads: its fence would drain the prefetches).  Q rows past M are read
 // clamped (finite values) and meet the zero padding of P^T, so they add nothing.
 template <int RT>
-__global__ __launch_bounds__(256) void wgrad_kernel(WgJob ja, WgJob jb, int64_t M, int64_t Mp) {
+__global__ __launch_bounds__(256) void wgrad_kernel(WgJobs jobs, int64_t M, int64_t Mp) {
   using S = WgShape<RT>;
   constexpr int R = 16 * RT;
   constexpr int NST = S::NST;
   __shared__ __attribute__((aligned(16))) uint8_t ring[NST * S::STAGE];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  // Field-wise selects keep the job in scalar registers.
-  const bool second = (int64_t)blockIdx.x >= ja.blocks;
-  const int64_t wi = second ? (int64_t)blockIdx.x - ja.blocks : (int64_t)blockIdx.x;
-  const uint16_t* pth = second ? jb.pth : ja.pth;
-  const uint16_t* ptl = second ? jb.ptl : ja.ptl;
-  const uint16_t* q = second ? jb.q : ja.q;
-  float* out = second ? jb.out : ja.out;
-  const int64_t C = second ? jb.C : ja.C, ldq = second ? jb.ldq : ja.ldq, ldt = second ? jb.ldt : ja.ldt;
-  const int64_t kblocks = second ? jb.kblocks : ja.kblocks, slices = second ? jb.slices : ja.slices;
-  const int64_t mchunk = second ? jb.mchunk : ja.mchunk;
-  const float scale = second ? jb.scale : ja.scale;
-  const int trans = second ? jb.trans : ja.trans;
+  int64_t wi;
+  const WgJob job = pick_job(jobs, (int64_t)blockIdx.x, wi);
+  const uint16_t* pth = job.pth;
+  const uint16_t* ptl = job.ptl;
+  const uint16_t* q = job.q;
+  float* out = job.out;
+  const int64_t C = job.C, ldq = job.ldq, ldt = job.ldt, kblocks = job.kblocks, slices = job.slices;
+  const int64_t mchunk = job.mchunk;
+  const float scale = job.scale;
+  const int trans = job.trans;
   const int64_t slice = wi / kblocks;
   const int64_t kb = (wi - slice * kblocks) * WG_KB;
   const int64_t mb = slice * mchunk;
@@ -264,22 +286,145 @@ struct RedJob {
   float scale;
 };
 
-// Both products' slice sums in one launch: workgroups [0, ra.blocks) finish ra, the rest rb.
-__global__ __launch_bounds__(256) void wgrad_reduce_kernel(RedJob ra, RedJob rb) {
-  const bool second = (int64_t)blockIdx.x >= ra.blocks;
-  const int64_t wi = second ? (int64_t)blockIdx.x - ra.blocks : (int64_t)blockIdx.x;
-  const v4f* part = reinterpret_cast<const v4f*>(second ? rb.part : ra.part);
-  float* out = second ? rb.out : ra.out;
-  const int64_t cols = second ? rb.cols : ra.cols, ldo = second ? rb.ldo : ra.ldo, n4 = second ? rb.n4 : ra.n4;
-  const int slices = second ? rb.slices : ra.slices;
-  const float scale = second ? rb.scale : ra.scale;
+struct RedJobs {
+  RedJob j[WG_MAXJ];
+  int n;
+};
+
+// The slice sums of a launch's products: workgroups laid out product after product (those without slices
+// have none).
+__global__ __launch_bounds__(256) void wgrad_reduce_kernel(RedJobs reds) {
+  int sel = 0;
+  int64_t wi = blockIdx.x;
+#pragma unroll
+  for (int k = 0; k < WG_MAXJ - 1; ++k)
+    if (sel == k && k + 1 < reds.n && wi >= reds.j[k].blocks) {
+      wi -= reds.j[k].blocks;
+      sel = k + 1;
+    }
+  RedJob rj = reds.j[0];
+#pragma unroll
+  for (int k = 1; k < WG_MAXJ; ++k)
+    if (sel == k) rj = reds.j[k];
+  const v4f* part = reinterpret_cast<const v4f*>(rj.part);
   const int64_t i = wi * 256 + threadIdx.x;
-  if (i >= n4) return;
+  if (i >= rj.n4) return;
   v4f v = part[i];
-  for (int s = 1; s < slices; ++s) v += part[s * n4 + i];
-  v *= scale;
-  const int64_t e = 4 * i, row = e / cols;
-  *reinterpret_cast<v4f*>(out + row * ldo + (e - row * cols)) = v;
+  for (int s = 1; s < rj.slices; ++s) v += part[s * rj.n4 + i];
+  v *= rj.scale;
+  const int64_t e = 4 * i, row = e / rj.cols;
+  *reinterpret_cast<v4f*>(rj.out + row * rj.ldo + (e - row * rj.cols)) = v;
+}
+
+// Slices of M shared by the products of one wgrad launch (kbs: their 256-column blocks in total) for RT rank
+// tiles: one round of workgroups that fills every workgroup slot (WPC per CU), with at least 384 rows per
+// workgroup (a workgroup's pipeline fill is ~3 stages of 32 rows) -- down to 128 rows when that leaves fewer
+// than half the CUs busy.  Measured on MI355X (M = 4096-4608, columns 3072-16384, ranks 16-64, slice counts
+// 1-16): the rule's count is within 3% of the fastest.
+struct GradPlan {
+  int64_t slices, mchunk;
+};
+
+int64_t col_blocks(int64_t C) { return (C + WG_KB - 1) / WG_KB; }
+
+GradPlan grad_plan(int64_t M, int64_t kbs, int rt) {
+  const int64_t cus = k2q_cu_count();
+  const int64_t wpc = rt <= 2 ? WgShape<2>::WPC : rt <= 4 ? WgShape<4>::WPC : WgShape<8>::WPC;
+  const int64_t fill = std::max<int64_t>(1, wpc * cus / std::max<int64_t>(kbs, 1));
+  int64_t s = std::min(fill, std::max<int64_t>(1, M / 384));
+  if (kbs * s < cus / 2) s = std::min(fill, std::max<int64_t>(1, M / 128));
+  const int64_t mchunk = ((M + s - 1) / s + WG_MS - 1) / WG_MS * WG_MS;
+  return GradPlan{(M + mchunk - 1) / mchunk, mchunk};
+}
+
+int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
+
+// Bytes of a product's slice partials (0 without slices).
+int64_t part_bytes(const GradPlan& p, int64_t rc, int64_t C) {
+  return p.slices > 1 ? align256(p.slices * rc * C * 4) : 0;
+}
+
+template <int RT>
+void launch_wgrad(const WgJobs& jobs, int64_t blocks, int64_t M, int64_t Mp, hipStream_t st) {
+  hipLaunchKernelGGL(wgrad_kernel<RT>, dim3((unsigned)blocks), dim3(256), 0, st, jobs, M, Mp);
+}
+
+// The products collected for one wgrad launch (one rank tile count) and the reduce that finishes the sliced ones.
+struct ProductSet {
+  WgJobs jobs{};
+  RedJobs reds{};
+  int64_t blocks = 0, red_blocks = 0;
+
+  // Adds out = scale * P^T Q (P^T rows pth/ptl of R ranks; Q: M x C, row stride ldq; trans: out[c][j] with
+  // row stride ldt) under plan p, its slice partials (when p slices M) at part.
+  void add(const GradPlan& p, const uint16_t* pth, const uint16_t* ptl, const uint16_t* q, int64_t C, int64_t ldq,
+           int64_t R, float scale, int trans, int64_t ldt, float* part, float* out) {
+    WgJob& job = jobs.j[jobs.n++];
+    job = WgJob{};
+    job.pth = pth;
+    job.ptl = ptl;
+    job.q = q;
+    job.C = C;
+    job.ldq = ldq;
+    job.ldt = ldt;
+    job.kblocks = col_blocks(C);
+    job.slices = p.slices;
+    job.mchunk = p.mchunk;
+    job.blocks = job.kblocks * p.slices;
+    job.scale = scale;
+    job.trans = trans;
+    job.out = p.slices > 1 ? part : out;
+    blocks += job.blocks;
+    if (p.slices > 1) {
+      RedJob& red = reds.j[reds.n++];
+      red = RedJob{};
+      red.part = part;
+      red.out = out;
+      red.cols = trans ? R : C;
+      red.ldo = trans ? ldt : C;
+      red.n4 = R * C / 4;
+      red.blocks = (red.n4 + 255) / 256;
+      red.slices = (int)p.slices;
+      red.scale = scale;
+      red_blocks += red.blocks;
+    }
+  }
+
+  int run(int rt, int64_t M, int64_t Mp, hipStream_t st) const {
+    if (jobs.n == 0) return K2Q_OK;
+    if (blocks > 0x7fffffff || red_blocks > 0x7fffffff) return K2Q_EUNSUPPORTED;
+    switch (rt) {
+#define K2Q_WG_CASE(RT) \
+  case RT: launch_wgrad<RT>(jobs, blocks, M, Mp, st); break;
+      K2Q_WG_CASE(1) K2Q_WG_CASE(2) K2Q_WG_CASE(3) K2Q_WG_CASE(4)
+      K2Q_WG_CASE(5) K2Q_WG_CASE(6) K2Q_WG_CASE(7) K2Q_WG_CASE(8)
+#undef K2Q_WG_CASE
+      default: return K2Q_EINVAL;
+    }
+    if (red_blocks > 0)
+      hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((unsigned)red_blocks), dim3(256), 0, st, reds);
+    return K2Q_OK;
+  }
+};
+
+// The wgrad operands of one rank chunk: g from dY (the down-projection with the factor s B^T read from B's
+// columns, its K-slice partials at gp with rows of stride ldp, or written straight into g when it has one
+// slice and direct is set) and grad_prep_kernel's g (row stride ldg), g^T hi/lo rows (gh/gl) and u^T hi/lo rows
+// (uh/ul, from u with row stride ldu); null outputs are skipped.
+int prep_chunk(const uint16_t* dy, int64_t ldy, int64_t M, int64_t N, const float* b, int64_t ldb, float scale,
+               int64_t rc, int64_t Mp, bool direct, float* gp, const float* u, int64_t ldu, float* g, int64_t ldg,
+               uint16_t* gh, uint16_t* gl, uint16_t* uh, uint16_t* ul, hipStream_t st) {
+  direct = direct && lora_down_parts_floats(M, N, rc) == M * rc;
+  float* dst = direct ? g : gp;
+  const int64_t ldp = direct ? ldg : rc;
+  int ns = 0;
+  const int rcode = lora_down_parts(dy, M, N, ldy, b, ldb, scale, rc, dst, ldp, &ns, st);
+  if (rcode) return rcode;
+  if (direct && !gh && !uh) return K2Q_OK;
+  const dim3 grid((unsigned)(Mp / 32), (unsigned)((rc + 31) / 32), uh ? 2u : 1u);
+  hipLaunchKernelGGL(grad_prep_kernel, grid, dim3(256), 0, st, dst, ldp, ns, u, ldu, M, rc, Mp,
+                     direct ? nullptr : g, ldg, gh, gl, uh, ul);
+  return K2Q_OK;
 }
 
 // Ranks run in chunks of at most GRAD_CHUNK (the wgrad kernel's largest rank tile), one after another on the
@@ -292,42 +437,15 @@ bool grad_shape_ok(int64_t M, int64_t N, int64_t K, int64_t r) {
          r % 16 == 0;
 }
 
-// Slices of M shared by the two products (ca, cb: their column counts, 0 for a product not requested) for a
-// chunk of RT rank tiles: one round of workgroups that fills every workgroup slot (WPC per CU), with at least
-// 384 rows per workgroup (a workgroup's pipeline fill is ~3 stages of 32 rows) -- down to 128 rows when that
-// leaves fewer than half the CUs busy.  Measured on MI355X (M = 4096-4608, columns 3072-16384, ranks 16-64,
-// slice counts 1-16): the rule's count is within 3% of the fastest.
-struct GradPlan {
-  int64_t slices, mchunk;
-};
-
-GradPlan grad_plan(int64_t M, int64_t ca, int64_t cb, int rt) {
-  const int64_t cus = k2q_cu_count();
-  const int64_t wpc = rt <= 2 ? WgShape<2>::WPC : rt <= 4 ? WgShape<4>::WPC : WgShape<8>::WPC;
-  const int64_t kbs = (ca + WG_KB - 1) / WG_KB + (cb + WG_KB - 1) / WG_KB;
-  const int64_t fill = std::max<int64_t>(1, wpc * cus / std::max<int64_t>(kbs, 1));
-  int64_t s = std::min(fill, std::max<int64_t>(1, M / 384));
-  if (kbs * s < cus / 2) s = std::min(fill, std::max<int64_t>(1, M / 128));
-  const int64_t mchunk = ((M + s - 1) / s + WG_MS - 1) / WG_MS * WG_MS;
-  return GradPlan{(M + mchunk - 1) / mchunk, mchunk};
-}
-
-int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
+int64_t chunk_ranks(int64_t r, int64_t c0) { return r - c0 < GRAD_CHUNK ? r - c0 : GRAD_CHUNK; }
 
 // Workspace: the hi/lo rows of g^T and u^T (all ranks), then one region that holds, in turn, the
-// down-projection's slice partials of g (read by grad_prep_kernel) and the two products' slice partials (dA's,
+// down-projection's slice partials of g (read by grad_prep_kernel) and the products' slice partials (dA's,
 // then dB's; written after the prep has run), sized for the largest chunk and any subset of {dA, dB}.
 struct GradLayout {
   int64_t pt, parts, total;   // byte offsets into the workspace
   int64_t mp;
 };
-
-int64_t chunk_ranks(int64_t r, int64_t c0) { return r - c0 < GRAD_CHUNK ? r - c0 : GRAD_CHUNK; }
-
-// Bytes of a product's slice partials (0 without slices).
-int64_t part_bytes(const GradPlan& p, int64_t rc, int64_t C) {
-  return p.slices > 1 ? align256(p.slices * rc * C * 4) : 0;
-}
 
 GradLayout grad_layout(int64_t M, int64_t N, int64_t K, int64_t r) {
   GradLayout L{};
@@ -337,7 +455,8 @@ GradLayout grad_layout(int64_t M, int64_t N, int64_t K, int64_t r) {
     const int64_t rc = chunk_ranks(r, c0);
     const int rt = (int)(rc / 16);
     parts = std::max(parts, align256(lora_down_parts_floats(M, N, rc) * 4));
-    const GradPlan both = grad_plan(M, K, N, rt), a = grad_plan(M, K, 0, rt), b = grad_plan(M, 0, N, rt);
+    const GradPlan both = grad_plan(M, col_blocks(K) + col_blocks(N), rt), a = grad_plan(M, col_blocks(K), rt),
+                   b = grad_plan(M, col_blocks(N), rt);
     parts = std::max({parts, part_bytes(both, rc, K) + part_bytes(both, rc, N), part_bytes(a, rc, K),
                       part_bytes(b, rc, N)});
   }
@@ -345,53 +464,6 @@ GradLayout grad_layout(int64_t M, int64_t N, int64_t K, int64_t r) {
   L.parts = 4 * align256(r * L.mp * 2);
   L.total = L.parts + parts;
   return L;
-}
-
-template <int RT>
-void launch_wgrad(const WgJob& ja, const WgJob& jb, int64_t M, int64_t Mp, hipStream_t st) {
-  hipLaunchKernelGGL(wgrad_kernel<RT>, dim3((unsigned)(ja.blocks + jb.blocks)), dim3(256), 0, st, ja, jb, M, Mp);
-}
-
-void wgrad(int rt, const WgJob& ja, const WgJob& jb, int64_t M, int64_t Mp, hipStream_t st) {
-  switch (rt) {
-#define K2Q_WG_CASE(RT) \
-  case RT: launch_wgrad<RT>(ja, jb, M, Mp, st); break;
-    K2Q_WG_CASE(1) K2Q_WG_CASE(2) K2Q_WG_CASE(3) K2Q_WG_CASE(4)
-    K2Q_WG_CASE(5) K2Q_WG_CASE(6) K2Q_WG_CASE(7) K2Q_WG_CASE(8)
-#undef K2Q_WG_CASE
-    default: break;
-  }
-}
-
-// The product of one rank chunk: its job for wgrad_kernel and, with slices, the reduce that finishes it.
-void make_job(const GradPlan& p, bool on, const uint16_t* pth, const uint16_t* ptl, const uint16_t* q, int64_t C,
-              int64_t R, float scale, int trans, int64_t ldt, float* part, float* out, WgJob& job, RedJob& red) {
-  job = WgJob{};
-  red = RedJob{};
-  if (!on) return;
-  job.pth = pth;
-  job.ptl = ptl;
-  job.q = q;
-  job.C = C;
-  job.ldq = C;
-  job.ldt = ldt;
-  job.kblocks = (C + WG_KB - 1) / WG_KB;
-  job.slices = p.slices;
-  job.mchunk = p.mchunk;
-  job.blocks = job.kblocks * p.slices;
-  job.scale = scale;
-  job.trans = trans;
-  job.out = p.slices > 1 ? part : out;
-  if (p.slices > 1) {
-    red.part = part;
-    red.out = out;
-    red.cols = trans ? R : C;
-    red.ldo = trans ? ldt : C;
-    red.n4 = R * C / 4;
-    red.blocks = (red.n4 + 255) / 256;
-    red.slices = (int)p.slices;
-    red.scale = scale;
-  }
 }
 
 }  // namespace
@@ -418,37 +490,164 @@ extern "C" int k2q_lora_grads(const uint16_t* dy, const uint16_t* x, const float
   const int64_t pt_bytes = align256(r * L.mp * 2);
   uint16_t* pt[4];
   for (int i = 0; i < 4; ++i) pt[i] = reinterpret_cast<uint16_t*>(w + L.pt + i * pt_bytes);
+  float* parts = reinterpret_cast<float*>(w + L.parts);
 
   for (int64_t c0 = 0; c0 < r; c0 += GRAD_CHUNK) {
     const int64_t rc = chunk_ranks(r, c0);
-    // g = dY (scale B^T)^T: the down-projection kernel with dY as the activation and scale * B^T as the
-    // factor, read from B (N x r) directly; its K-slice partials are added by grad_prep_kernel.  With one
-    // slice and one chunk the partial is g itself (same row stride), written in place.
-    const bool direct = r <= GRAD_CHUNK && lora_down_parts_floats(M, N, rc) == M * rc;
-    float* gp = direct ? g : reinterpret_cast<float*>(w + L.parts);
-    int ns = 0;
-    int rcode = lora_down_parts(dy, M, N, N, lora_b + c0, r, scale, rc, gp, &ns, st);
+    const int rt = (int)(rc / 16);
+    int rcode = prep_chunk(dy, N, M, N, lora_b + c0, r, scale, rc, L.mp, r <= GRAD_CHUNK, parts, dB ? u + c0 : nullptr,
+                           r, g + c0, r, dA ? pt[0] + c0 * L.mp : nullptr, dA ? pt[1] + c0 * L.mp : nullptr,
+                           dB ? pt[2] + c0 * L.mp : nullptr, dB ? pt[3] + c0 * L.mp : nullptr, st);
     if (rcode) return rcode;
-    if (direct && !dA && !dB) continue;
-    const dim3 pgrid((unsigned)(L.mp / 32), (unsigned)((rc + 31) / 32), dB ? 2u : 1u);
-    hipLaunchKernelGGL(grad_prep_kernel, pgrid, dim3(256), 0, st, gp, ns, dB ? u + c0 : nullptr, r, M, rc, L.mp,
-                       direct ? nullptr : g + c0, r, dA ? pt[0] + c0 * L.mp : nullptr,
-                       dA ? pt[1] + c0 * L.mp : nullptr, dB ? pt[2] + c0 * L.mp : nullptr,
-                       dB ? pt[3] + c0 * L.mp : nullptr);
     if (!dA && !dB) continue;
-    const GradPlan p = grad_plan(M, dA ? K : 0, dB ? N : 0, (int)(rc / 16));
-    WgJob ja, jb;
-    RedJob ra, rb;
-    float* part_a = reinterpret_cast<float*>(w + L.parts);
-    float* part_b = reinterpret_cast<float*>(w + L.parts + (dA ? part_bytes(p, rc, K) : 0));
-    make_job(p, dA != nullptr, pt[0] + c0 * L.mp, pt[1] + c0 * L.mp, x, K, rc, 1.f, 0, 0, part_a,
-             dA ? dA + c0 * K : nullptr, ja, ra);
-    make_job(p, dB != nullptr, pt[2] + c0 * L.mp, pt[3] + c0 * L.mp, dy, N, rc, scale, 1, r, part_b,
-             dB ? dB + c0 : nullptr, jb, rb);
-    if (ja.blocks + jb.blocks > 0x7fffffff) return K2Q_EUNSUPPORTED;
-    wgrad((int)(rc / 16), ja, jb, M, L.mp, st);
-    if (ra.blocks + rb.blocks > 0)
-      hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((unsigned)(ra.blocks + rb.blocks)), dim3(256), 0, st, ra, rb);
+    // dA and dB in one launch, sharing the slice count; their partials follow one another in the region
+    const GradPlan p = grad_plan(M, (dA ? col_blocks(K) : 0) + (dB ? col_blocks(N) : 0), rt);
+    ProductSet set;
+    if (dA) set.add(p, pt[0] + c0 * L.mp, pt[1] + c0 * L.mp, x, K, K, rc, 1.f, 0, 0, parts, dA + c0 * K);
+    if (dB)
+      set.add(p, pt[2] + c0 * L.mp, pt[3] + c0 * L.mp, dy, N, N, rc, scale, 1, r,
+              reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(parts) + (dA ? part_bytes(p, rc, K) : 0)),
+              dB + c0);
+    rcode = set.run(rt, M, L.mp, st);
+    if (rcode) return rcode;
+  }
+  return k2q_launch_status();
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// k2q_lora_grads_grouped: the LoRA gradients of n linears that read one input (a grouped node's backward).
+// Member i's g goes straight into columns [i r, (i+1) r) of the stacked g, which the grouped input gradient
+// reads; dA of every member comes from one wgrad pass over x per 128 stacked ranks (rows of the stacked dA);
+// the members' dB products share one launch.  Per member: the down-projection of dY_i and one prep launch.
+namespace {
+
+constexpr int64_t GROUP_MAX = WG_MAXJ;
+
+bool group_ok(const k2q_lora_member* m, int64_t n, int64_t M, int64_t K, int64_t r) {
+  if (!m || n < 1 || n > GROUP_MAX || M < 1 || K < 128 || K % 128 || r < 16 || r > GRAD_CHUNK || r % 16) return false;
+  for (int64_t i = 0; i < n; ++i)
+    if (m[i].N < 128 || m[i].N % 128 || m[i].ldy < m[i].N || m[i].ldy % 8) return false;
+  return true;
+}
+
+struct GroupLayout {
+  int64_t pt, parts, total;
+  int64_t mp;
+};
+
+// The stacked ranks' dA launches: full 128-rank chunks share one launch, a shorter last chunk has its own.
+int64_t group_da_chunks(int64_t R) { return (R + GRAD_CHUNK - 1) / GRAD_CHUNK; }
+
+GroupLayout group_layout(const k2q_lora_member* m, int64_t n, int64_t M, int64_t K, int64_t r) {
+  GroupLayout L{};
+  L.mp = (M + 31) / 32 * 32;
+  const int64_t R = n * r;
+  int64_t parts = 0, nb = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    parts = std::max(parts, align256(lora_down_parts_floats(M, m[i].N, r) * 4));
+    nb += col_blocks(m[i].N);
+  }
+  // dA: the full chunks' launch, then the tail's
+  const int64_t full = R / GRAD_CHUNK, tail = R % GRAD_CHUNK;
+  if (full > 0) {
+    const GradPlan p = grad_plan(M, full * col_blocks(K), 8);
+    parts = std::max(parts, full * part_bytes(p, GRAD_CHUNK, K));
+  }
+  if (tail > 0) parts = std::max(parts, part_bytes(grad_plan(M, col_blocks(K), (int)(tail / 16)), tail, K));
+  // dB: every member in one launch (any subset fits: fewer members plan more slices, but never more bytes than
+  // the whole set at its own plan is guaranteed, so size for each subset size's worst case)
+  for (int64_t kbs = 1; kbs <= nb; ++kbs) {
+    const GradPlan p = grad_plan(M, kbs, (int)(r / 16));
+    int64_t b = 0;
+    for (int64_t i = 0; i < n; ++i) b += part_bytes(p, r, m[i].N);
+    parts = std::max(parts, b);
+  }
+  L.pt = 0;
+  L.parts = 4 * align256(R * L.mp * 2);
+  L.total = L.parts + parts;
+  return L;
+}
+
+}  // namespace
+
+extern "C" int64_t k2q_lora_grads_grouped_ws_bytes(const k2q_lora_member* m, int64_t n, int64_t M, int64_t K,
+                                                   int64_t r) {
+  if (!group_ok(m, n, M, K, r)) return 0;
+  return group_layout(m, n, M, K, r).total;
+}
+
+extern "C" int k2q_lora_grads_grouped(const k2q_lora_member* m, int64_t n, const uint16_t* x, const float* u,
+                                      int64_t r, int64_t M, int64_t K, float* g, float* dA, void* ws,
+                                      int64_t ws_bytes, void* stream) {
+  if (!group_ok(m, n, M, K, r)) return K2Q_EINVAL;
+  bool any_db = false;
+  for (int64_t i = 0; i < n; ++i) {
+    if (!m[i].dy || !m[i].lora_b || !k2q_aligned(m[i].dy, 16) || !k2q_aligned(m[i].lora_b, 16) ||
+        (m[i].dB && !k2q_aligned(m[i].dB, 16)))
+      return K2Q_EINVAL;
+    any_db = any_db || m[i].dB;
+  }
+  if (!g || !ws || !k2q_aligned(g, 16) || !k2q_aligned(ws, 256) || (dA && (!x || !k2q_aligned(x, 16) ||
+      !k2q_aligned(dA, 16))) || (any_db && (!u || !k2q_aligned(u, 16))))
+    return K2Q_EINVAL;
+  const GroupLayout L = group_layout(m, n, M, K, r);
+  if (ws_bytes < L.total) return K2Q_EINVAL;
+  if ((L.mp / 32) > 0x7fffffff) return K2Q_EUNSUPPORTED;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  uint8_t* w = static_cast<uint8_t*>(ws);
+  const int64_t R = n * r;
+  const int64_t pt_bytes = align256(R * L.mp * 2);
+  uint16_t* pt[4];
+  for (int i = 0; i < 4; ++i) pt[i] = reinterpret_cast<uint16_t*>(w + L.pt + i * pt_bytes);
+  float* parts = reinterpret_cast<float*>(w + L.parts);
+
+  for (int64_t i = 0; i < n; ++i) {
+    const k2q_lora_member& mi = m[i];
+    const int64_t c0 = i * r;
+    const int rcode = prep_chunk(mi.dy, mi.ldy, M, mi.N, mi.lora_b, r, mi.scale, r, L.mp, true, parts,
+                                 mi.dB ? u + c0 : nullptr, R, g + c0, R, dA ? pt[0] + c0 * L.mp : nullptr,
+                                 dA ? pt[1] + c0 * L.mp : nullptr, mi.dB ? pt[2] + c0 * L.mp : nullptr,
+                                 mi.dB ? pt[3] + c0 * L.mp : nullptr, st);
+    if (rcode) return rcode;
+  }
+  if (dA) {
+    // the full 128-rank chunks of the stacked g in one launch, the tail in another
+    const int64_t full = R / GRAD_CHUNK, tail = R % GRAD_CHUNK;
+    if (full > 0) {
+      const GradPlan p = grad_plan(M, full * col_blocks(K), 8);
+      ProductSet set;
+      for (int64_t c = 0; c < full; ++c)
+        set.add(p, pt[0] + c * GRAD_CHUNK * L.mp, pt[1] + c * GRAD_CHUNK * L.mp, x, K, K, GRAD_CHUNK, 1.f, 0, 0,
+                reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(parts) + c * part_bytes(p, GRAD_CHUNK, K)),
+                dA + c * GRAD_CHUNK * K);
+      const int rcode = set.run(8, M, L.mp, st);
+      if (rcode) return rcode;
+    }
+    if (tail > 0) {
+      const int64_t c0 = full * GRAD_CHUNK;
+      const GradPlan p = grad_plan(M, col_blocks(K), (int)(tail / 16));
+      ProductSet set;
+      set.add(p, pt[0] + c0 * L.mp, pt[1] + c0 * L.mp, x, K, K, tail, 1.f, 0, 0, parts, dA + c0 * K);
+      const int rcode = set.run((int)(tail / 16), M, L.mp, st);
+      if (rcode) return rcode;
+    }
+  }
+  if (any_db) {
+    int64_t kbs = 0;
+    for (int64_t i = 0; i < n; ++i)
+      if (m[i].dB) kbs += col_blocks(m[i].N);
+    const GradPlan p = grad_plan(M, kbs, (int)(r / 16));
+    ProductSet set;
+    int64_t off = 0;
+    for (int64_t i = 0; i < n; ++i) {
+      if (!m[i].dB) continue;
+      const int64_t c0 = i * r;
+      set.add(p, pt[2] + c0 * L.mp, pt[3] + c0 * L.mp, m[i].dy, m[i].N, m[i].ldy, r, m[i].scale, 1, r,
+              reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(parts) + off), m[i].dB);
+      off += part_bytes(p, r, m[i].N);
+    }
+    const int rcode = set.run((int)(r / 16), M, L.mp, st);
+    if (rcode) return rcode;
   }
   return k2q_launch_status();
 }

@@ -193,15 +193,18 @@ def _state_key(m):
 class _GroupedFn(torch.autograd.Function):
     """Forward: one LoRA down-projection over the stacked adapters (``u = x [A_0; A_1; ..]^T``) and one grouped
     GEMM (``k2q_gemm_w8a8_grouped``) giving every member's output, each bit-identical to the member's own
-    fused forward.  Backward: per member, the LoRA gradients as ``_ConvRotLinearFn`` computes them; ``dX`` of
-    all members in one GEMM (``k2q_gemm_dx_grouped``) whose reduction runs over every member's output gradient
-    and effective weight, with the members' LoRA terms stacked along the rank: the sum autograd would form at
-    the shared input, in f32 and rounded once."""
+    fused forward.  Backward: the members' LoRA gradients in one call (``k2q_lora_grads_grouped``: the same
+    arithmetic as ``_ConvRotLinearFn``'s per member, dA of every member from one pass over x per 128 stacked
+    ranks, g written in the stacked layout; per member when an output got no gradient or the rank is above 128);
+    ``dX`` of all members in one GEMM (``k2q_gemm_dx_grouped``) whose reduction runs over every member's output
+    gradient and effective weight, with the members' LoRA terms stacked along the rank: the sum autograd would
+    form at the shared input, in f32 and rounded once."""
 
     @staticmethod
     def forward(ctx, x2, qx, sx, bases, scales, *ab):
         As, Bs = ab[0::2], ab[1::2]
-        u = _lib.lora_down(x2, torch.cat(As) if len(As) > 1 else As[0]) if As else None
+        a_stack = (torch.cat(As) if len(As) > 1 else As[0]) if As else None
+        u = _lib.lora_down(x2, a_stack) if As else None
         r = As[0].shape[0] if As else 0
         segs, li = [], 0
         for base, sc in zip(bases, scales):
@@ -213,36 +216,49 @@ class _GroupedFn(torch.autograd.Function):
         ys = _lib.gemm_w8a8_grouped(qx, sx, segs, u)
         ctx.set_materialize_grads(False)    # an output nothing used gets no gradient pass (None, not zeros)
         ctx.bases, ctx.scales, ctx.r, ctx.nl = bases, scales, r, len(As)
-        ctx.save_for_backward(x2 if As else None, u, *As, *Bs)
+        ctx.save_for_backward(x2 if As else None, u, a_stack, *As, *Bs)
         return tuple(ys)
 
     @staticmethod
     def backward(ctx, *dys):
-        x2, u, *ab = ctx.saved_tensors
+        x2, u, a_stack, *ab = ctx.saved_tensors
         nl, r = ctx.nl, ctx.r
         As, Bs = ab[:nl], ab[nl:]
         grads = [None] * (2 * nl)
-        segs, gs, ga, li = [], [], [], 0
-        for i, (base, sc) in enumerate(zip(ctx.bases, ctx.scales)):
-            dy, has = dys[i], sc is not None
-            if dy is not None:
-                dy = dy.contiguous()
-                if dy.dtype != torch.bfloat16:
-                    dy = dy.to(torch.bfloat16)
-                if has:
-                    need_a, need_b = ctx.needs_input_grad[5 + 2 * li], ctx.needs_input_grad[6 + 2 * li]
-                    u_i = u[:, li * r:(li + 1) * r].contiguous() if need_b else None
-                    g, grads[2 * li], grads[2 * li + 1] = _lib.lora_grads(dy, x2 if need_a else None, u_i, Bs[li], sc)
-                    gs.append(g)
+        dys = [None if dy is None else (dy.contiguous() if dy.dtype == torch.bfloat16
+                                        else dy.to(torch.bfloat16).contiguous()) for dy in dys]
+        adapted = [i for i, sc in enumerate(ctx.scales) if sc is not None]
+        need_a = [ctx.needs_input_grad[5 + 2 * li] for li in range(nl)]
+        need_b = [ctx.needs_input_grad[6 + 2 * li] for li in range(nl)]
+        g = a = None
+        if nl and r <= 128 and all(dys[i] is not None for i in adapted):
+            # every adapter's gradients in one call: dA of all members from one pass over x per 128 stacked
+            # ranks, g already in the stacked layout the grouped input gradient reads
+            g, dA, dBs = _lib.lora_grads_grouped([dys[i] for i in adapted], x2 if any(need_a) else None, u, Bs,
+                                                 [ctx.scales[i] for i in adapted], need_b)
+            for li in range(nl):
+                grads[2 * li] = dA[li * r:(li + 1) * r] if need_a[li] else None
+                grads[2 * li + 1] = dBs[li]
+            a = a_stack
+        elif nl:
+            gs, ga, li = [], [], 0
+            for i, sc in enumerate(ctx.scales):
+                if sc is None:
+                    continue
+                if dys[i] is not None:
+                    u_i = u[:, li * r:(li + 1) * r].contiguous() if need_b[li] else None
+                    gi, grads[2 * li], grads[2 * li + 1] = _lib.lora_grads(dys[i], x2 if need_a[li] else None, u_i,
+                                                                           Bs[li], sc)
+                    gs.append(gi)
                     ga.append(As[li])
-                if ctx.needs_input_grad[0]:
-                    segs.append((dy, base.dx_weight()))
-            li += int(has)
-        dx = None
-        if ctx.needs_input_grad[0] and segs:
-            # one GEMM over the members' reductions: the sum autograd would form at the shared input
+                li += 1
             g = torch.cat(gs, dim=1) if len(gs) > 1 else (gs[0] if gs else None)
             a = torch.cat(ga) if len(ga) > 1 else (ga[0] if ga else None)
+        dx = None
+        segs = [(dys[i], base.dx_weight()) for i, base in enumerate(ctx.bases) if dys[i] is not None] \
+            if ctx.needs_input_grad[0] else []
+        if segs:
+            # one GEMM over the members' reductions: the sum autograd would form at the shared input
             dx = _lib.gemm_dx_grouped(segs, g, a)
         return (dx, None, None, None, None, *grads)
 

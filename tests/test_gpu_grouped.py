@@ -7,6 +7,10 @@
 * Input-gradient kernel: the segmented reduction equals ``k2q_gemm_dx_lin`` over the concatenated operands
   bit for bit (same stage order, full-K tiles), one-stage segments and row-strided output gradients included,
   and the float64 sum within bf16 rounding.
+* LoRA gradients (``k2q_lora_grads_grouped``): every member's g bit-identical to ``k2q_lora_grads`` of that
+  member alone, written in the stacked layout; the stacked dA (one pass over x per 128 stacked ranks, a shorter
+  last chunk in its own launch) and each member's dB against float64, with ragged widths, row-strided output
+  gradients, eight members and dB requested for some members only.
 * Module: a restated block's attention inputs and SwiGLU gate / up grouped against the same block ungrouped:
   forward within one bf16 rounding (the stacked LoRA down-projection may add in another order), gradients
   within the bars of the per-layer path, one grouped launch per group, a checkpointed backward equal to a
@@ -99,6 +103,70 @@ def test_dx_grouped_equals_concatenated(k2, dev, M, K, Ns, r, strided):
         ref64 += gg.double() @ A.double()
     err = (dx.double() - ref64).norm() / ref64.norm()
     assert err < 4e-3
+
+
+@pytest.mark.parametrize("M,K,Ns,r,want", [(700, 1024, (512, 256, 256, 512), 16, None),
+                                           (333, 768, (384, 640), 64, None),
+                                           (64, 512, (128,) * 8, 16, None),
+                                           (1024, 640, (256, 384, 128), 128, (True, False, True)),
+                                           (200, 512, (256, 256, 256), 48, (False, True, False)),
+                                           (4608, 6144, (6144, 1536, 1536, 6144), 16, None)])
+def test_lora_grads_grouped_matches_members(k2, dev, M, K, Ns, r, want):
+    """g_i = s_i dY_i B_i, dA_i = g_i^T x, dB_i = s_i dY_i^T u_i for linears sharing x, in one grouped call:
+    g bit-identical to each member's own ``k2q_lora_grads`` (same down-projection and slice sums), dA and dB
+    within 2e-5 of float64 (their slice plans differ from the single calls').  The last case is the Krea 2
+    attention-input group at full size (dA and dB checked against the single calls there)."""
+    g = torch.Generator().manual_seed(M + K + r)
+    n = len(Ns)
+    x = (torch.randn(M, K, generator=g)).to(torch.bfloat16)
+    u = torch.randn(M, n * r, generator=g)
+    # the members' output gradients as column blocks of one wider tensor: rows of stride sum(Ns) + 128
+    wide = (torch.randn(M, sum(Ns) + 128, generator=g) * 1e-3).to(torch.bfloat16).to(dev)
+    offs = [sum(Ns[:i]) for i in range(n)]
+    dys = [wide[:, o:o + N] for o, N in zip(offs, Ns)]
+    Bs = [torch.randn(N, r, generator=g).mul(0.01).to(dev) for N in Ns]
+    scales = [0.5 + 0.25 * i for i in range(n)]
+    xd, ud = x.to(dev), u.to(dev)
+    gst, dA, dBs = k2._lib.lora_grads_grouped(dys, xd, ud, Bs, scales, want)
+    big = M * K > 10 ** 7
+    for i in range(n):
+        gi, dAi, dBi = k2._lib.lora_grads(dys[i].contiguous(), xd, ud[:, i * r:(i + 1) * r].contiguous(), Bs[i],
+                                          scales[i])
+        assert torch.equal(gst[:, i * r:(i + 1) * r], gi), i
+        if want is not None and not want[i]:
+            assert dBs[i] is None
+        if big:
+            assert _rel(dA[i * r:(i + 1) * r], dAi) < 1e-5 and _rel(dBs[i], dBi) < 1e-5, i
+            continue
+        dy64 = dys[i].double().cpu()
+        g64 = scales[i] * (dy64 @ Bs[i].double().cpu())
+        assert _rel(dA[i * r:(i + 1) * r].cpu(), g64.t() @ x.double()) < 2e-5, i
+        if dBs[i] is not None:
+            assert _rel(dBs[i].cpu(), scales[i] * (dy64.t() @ u[:, i * r:(i + 1) * r].double())) < 2e-5, i
+    # without x: no dA, the same g
+    g2, dA2, _ = k2._lib.lora_grads_grouped(dys, None, ud, Bs, scales, want)
+    assert dA2 is None and torch.equal(g2, gst)
+
+
+def test_lora_grads_grouped_argument_checks(k2, dev):
+    M, K, r = 64, 256, 16
+    x = torch.zeros(M, K, dtype=torch.bfloat16, device=dev)
+    u = torch.zeros(M, 2 * r, device=dev)
+    dys = [torch.zeros(M, 128, dtype=torch.bfloat16, device=dev)] * 2
+    Bs = [torch.zeros(128, r, device=dev)] * 2
+    with pytest.raises(ValueError, match="members"):
+        k2._lib.lora_grads_grouped(dys * 5, x, torch.zeros(M, 10 * r, device=dev), Bs * 5, [1.0] * 10)
+    with pytest.raises(ValueError, match="rank"):
+        k2._lib.lora_grads_grouped(dys, x, torch.zeros(M, 2 * 256, device=dev),
+                                   [torch.zeros(128, 256, device=dev)] * 2, [1.0] * 2)
+    with pytest.raises(ValueError, match="lora_B"):
+        k2._lib.lora_grads_grouped(dys, x, u, [Bs[0], torch.zeros(128, 32, device=dev)], [1.0] * 2)
+    with pytest.raises(ValueError, match="stacked"):
+        k2._lib.lora_grads_grouped(dys, x, torch.zeros(M, r, device=dev), Bs, [1.0] * 2)
+    lib = k2._lib.load()
+    assert lib.k2q_lora_grads_grouped_ws_bytes(None, 2, M, K, r) == 0
+    assert lib.k2q_lora_grads_grouped(None, 2, x.data_ptr(), u.data_ptr(), r, M, K, u.data_ptr(), None, None, 0,
+                                      torch.cuda.current_stream(dev).cuda_stream) == -1
 
 
 def test_dx_grouped_argument_checks(k2, dev):
