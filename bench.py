@@ -655,7 +655,7 @@ def run_cfg4(k2, steps, dev, settle_s=0.0, cpu=False):
 
 def profile_pass(k2, dev):
     """Fixed launches for rocprofv3 counter passes: cfg2 rotate/quant, LoRA down, GEMM, 3 times each; the cfg3
-    input-gradient GEMM (with its LoRA term) 3 times; the two producer kernels at cfg4's image-stream shapes
+    input-gradient GEMM (with its LoRA term) and the cfg3 LoRA gradients 3 times each; the two producer kernels at cfg4's image-stream shapes
     and the grouped attention-input GEMM (M = 4608, 6144 -> 6144 | 1536 | 1536 | 6144, r = 16) 3 times each;
     then a plain 256 MiB device copy (Tensor.copy_) 3 times, the calibration point for FETCH/WRITE_SIZE."""
     L = k2._lib
@@ -675,7 +675,13 @@ def profile_pass(k2, dev):
     g = (torch.randn(c3["M"], c3["r"], generator=g3) * 1e-3).to(dev)
     for _ in range(3):
         L.gemm_dx(dy, qw3, sw3, g=g, lora_a=A3)
-    del qw3, dy, A3, g
+    # cfg3's LoRA gradients: dA and dB in one wgrad launch
+    x3 = torch.randn(c3["M"], c3["K"], generator=g3).to(torch.bfloat16).to(dev)
+    u3 = torch.randn(c3["M"], c3["r"], generator=g3).to(dev)
+    B3 = (torch.randn(c3["N"], c3["r"], generator=g3) * 0.01).to(dev)
+    for _ in range(3):
+        L.lora_grads(dy, x3, u3, B3, 0.5)
+    del qw3, dy, A3, g, x3, u3, B3
     # the producer kernels at cfg4's image-stream shapes and the grouped attention-input GEMM at M = 4608
     Mi, Ki, Kh = 8192, 3072, 12288
     xi = torch.randn(Mi, Ki, generator=g3).to(torch.bfloat16).to(dev)
@@ -839,6 +845,9 @@ def _profiled_kernels(L):
          2 * M3 * N3 + 2 * K3 * N3 + 4 * M3 * r3 + 4 * r3 * K3, 2 * M3 * K3),
         ("rot_dequant_t_kernel cfg3 (effective weight)", "rot_dequant_t_kernel<false>", 1179648, N3 * K3 + 4 * N3,
          2 * K3 * N3),
+        # x and dY once, the hi/lo rows of g^T and u^T; writes: the two gradients (slice partials come on top)
+        ("wgrad_kernel<4> cfg3 (LoRA dA and dB, one launch)", "wgrad_kernel<4>", None,
+         2 * M3 * K3 + 2 * M3 * N3 + 8 * r3 * M3, 4 * r3 * (K3 + N3)),
         ("prodquant_kernel<RMSMOD> cfg4 image (M=8192, K=3072)", "prodquant_kernel<1, 1, 3, false>", 524288,
          2 * Mi * Ki, 2 * Mi * Ki + Mi * Ki + 4 * Mi),
         ("prodquant_kernel<SWIGLU> cfg4 image (M=8192, K=12288)", "prodquant_kernel<0, 4, 3, false>", 2097152,
