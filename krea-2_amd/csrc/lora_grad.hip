@@ -355,10 +355,16 @@ struct ProductSet {
   RedJobs reds{};
   int64_t blocks = 0, red_blocks = 0;
 
+  bool full = false;   // a product past WG_MAXJ was refused (run() then fails)
+
   // Adds out = scale * P^T Q (P^T rows pth/ptl of R ranks; Q: M x C, row stride ldq; trans: out[c][j] with
   // row stride ldt) under plan p, its slice partials (when p slices M) at part.
   void add(const GradPlan& p, const uint16_t* pth, const uint16_t* ptl, const uint16_t* q, int64_t C, int64_t ldq,
            int64_t R, float scale, int trans, int64_t ldt, float* part, float* out) {
+    if (jobs.n == WG_MAXJ) {
+      full = true;
+      return;
+    }
     WgJob& job = jobs.j[jobs.n++];
     job = WgJob{};
     job.pth = pth;
@@ -391,6 +397,7 @@ struct ProductSet {
   }
 
   int run(int rt, int64_t M, int64_t Mp, hipStream_t st) const {
+    if (full) return K2Q_EUNSUPPORTED;
     if (jobs.n == 0) return K2Q_OK;
     if (blocks > 0x7fffffff || red_blocks > 0x7fffffff) return K2Q_EUNSUPPORTED;
     switch (rt) {
