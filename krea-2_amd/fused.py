@@ -76,8 +76,7 @@ class _RmsModQuantFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x2, norm_scale, mod_scale, mod_shift, eps, rows_per_batch):
-        h, q, s = _lib.rmsmod_rotquant(x2, norm_scale.float().contiguous(), eps, mod_scale, mod_shift,
-                                       rows_per_batch)
+        h, q, s = _lib.rmsmod_rotquant(x2, norm_scale, eps, mod_scale, mod_shift, rows_per_batch)
         ctx.eps, ctx.rpb = eps, rows_per_batch
         ctx.save_for_backward(x2, norm_scale, mod_scale, mod_shift)
         ctx.mark_non_differentiable(q, s)
@@ -93,8 +92,20 @@ class _RmsModQuantFn(torch.autograd.Function):
         dh = dh.contiguous()
         if dh.dtype != torch.bfloat16:
             dh = dh.to(torch.bfloat16)
-        dx = _lib.rmsmod_bwd(dh, x2.contiguous(), ns.float().contiguous(), ctx.eps, ms, rpb)
+        dx = _lib.rmsmod_bwd(dh, x2.contiguous(), ns, ctx.eps, ms, rpb)
         return dx, None, None, None, None, None
+
+
+def _norm_scale_f32(norm: nn.Module) -> torch.Tensor:
+    """The norm's (frozen) scale as the kernels take it, f32 and contiguous, kept on the module and rebuilt when
+    the scale changes (in place: version; re-pointed, e.g. paged by block swap: pointer or device)."""
+    t = norm.scale
+    key = (t._version, t.data_ptr(), t.device, t.dtype, tuple(t.shape))
+    kept = norm.__dict__.get("_k2q_scale_f32")
+    if kept is None or kept[0] != key:
+        kept = (key, t.detach().float().contiguous())
+        norm.__dict__["_k2q_scale_f32"] = kept
+    return kept[1]
 
 
 def modulated_rmsnorm(norm: nn.Module, x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor) -> torch.Tensor:
@@ -123,7 +134,7 @@ def modulated_rmsnorm(norm: nn.Module, x: torch.Tensor, scale: torch.Tensor, shi
     if not (ms.stride(1) == 1 and mb.stride(1) == 1 and ms.stride(0) == mb.stride(0) and ms.stride(0) % 8 == 0
             and ms.data_ptr() % 16 == 0 and mb.data_ptr() % 16 == 0):
         ms, mb = ms.contiguous(), mb.contiguous()
-    h, q, s = _RmsModQuantFn.apply(x2, norm.scale, ms, mb, float(norm.eps), M // B)
+    h, q, s = _RmsModQuantFn.apply(x2, _norm_scale_f32(norm), ms, mb, float(norm.eps), M // B)
     h = h.reshape(x.shape)
     shared_input_quant.seed(h, q, s)
     return h
