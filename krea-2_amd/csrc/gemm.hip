@@ -1075,17 +1075,48 @@ SplitPlan split_plan(int64_t tiles, int nk, int cus) {
   return q;
 }
 
+// Split plan for a launch of 128 x 128 tiles (two workgroups per CU) that fits one round of workgroup slots:
+// every tile cut along K into s pieces (whole stage pairs), then one fixup launch, when that is estimated at
+// least 5 % faster.  Estimates in microseconds, fitted to MI355X timings of 11 launch shapes (M 256-2048,
+// N 1024-6144, K 3072-16384; split or not, the plan's pick is within 6 % of the fastest measured): a full-K tile
+// 0.62 per 128-byte stage + 6; s pieces 0.62 per stage of the longest piece, x 1.25 once pieces outnumber the
+// CUs, + 10 + 0.035 per piece (piece stores and the fixup).  Long reductions over few tiles gain most: M = 1024,
+// N = 3072, K = 12288 (cfg4's text-stream down projection) 70.5 -> 62.8 us with s = 2.
+SplitPlan split_plan128(int64_t tiles, int nk, int cus) {
+  SplitPlan q{tiles, 0, 1, 0.0};
+  const int64_t slots = 2 * (int64_t)cus;
+  if (tiles > slots) return q;
+  const int np = nk / 2;   // 128-byte stages
+  auto stages_us = [&](int stages, int64_t wgs) { return 0.62 * stages * (wgs > cus ? 1.25 : 1.0); };
+  q.cost = stages_us(np, tiles) + 6.0;
+  double best = 0.95 * q.cost;
+  for (int s = 2; s <= 8 && tiles * s <= slots && np / s >= 4; ++s) {
+    const double t = stages_us((np + s - 1) / s, tiles * s) + 10.0 + 0.035 * (double)(tiles * s);
+    if (t < best) {
+      best = t;
+      q.s = s;
+    }
+  }
+  if (q.s > 1) {
+    q.dp_tiles = 0;
+    q.rem = (int)tiles;
+    q.cost = best;
+  }
+  return q;
+}
+
 // Tile shape of a launch: the one with the lowest estimated time, in units of one reduction stage of a T256 tile.
 // A round of `active` tiles over `slots` = CUs x workgroups-per-CU costs nk x c x (0.7 + 0.3 active / slots) +
 // epilogue: a partly filled round runs its stages faster (less HBM and L2 contention).  Per-stage costs relative
 // to T256, fitted to the MI355X timings of 17 launch shapes (M 1024..16896, N 1536..16384, K 3072..16384; the
 // fitted model picks the fastest measured shape on each): T320 1.25, T192 0.80, T128 0.60 with two workgroups
 // sharing a CU and 0.30 with a CU to itself; epilogues 8 (T256, T320), 7 (T192), 4 (T128).  T256 may instead cut
-// its last round's tiles along K (split_plan).  The rotating input-gradient epilogue runs 128 A-rows per wave
-// (T256 only); grouped launches need segments on tile boundaries (TA = 256 or 128).
+// its last round's tiles along K (split_plan), and a launch of T128 tiles its one round (split_plan128).  The
+// rotating input-gradient epilogue runs 128 A-rows per wave (T256 only); grouped launches need segments on tile
+// boundaries (TA = 256 or 128).
 struct TileChoice {
   int tile;
-  SplitPlan split;   // T256 only
+  SplitPlan split;   // T256 and T128
 };
 
 template <class C>
@@ -1106,9 +1137,11 @@ TileChoice choose_tile(int epi, int64_t rows_a, int64_t rows_b, int64_t kbytes, 
   const int nk = (int)(kbytes / SBK);
   const int64_t tiles256 = ((rows_a + 255) / 256) * ((rows_b + 255) / 256);
   TileChoice c{TILE_256, can_split ? split_plan(tiles256, nk, cus) : SplitPlan{tiles256, 0, 1, 0.0}};
+  const int64_t tiles128 = ((rows_a + 127) / 128) * ((rows_b + 127) / 128);
   if (forced >= 0) {
     c.tile = forced;
     if (forced != TILE_256) c.split = SplitPlan{0, 0, 1, 0.0};
+    if (forced == TILE_128 && can_split) c.split = split_plan128(tiles128, nk, cus);
     return c;
   }
   if (epi == EPI_DX) return c;
@@ -1120,6 +1153,7 @@ TileChoice choose_tile(int epi, int64_t rows_a, int64_t rows_b, int64_t kbytes, 
   if (t192 < best) { best = t192; c.tile = TILE_192; }
   if (t128 < best) { best = t128; c.tile = TILE_128; }
   if (c.tile != TILE_256) c.split = SplitPlan{0, 0, 1, 0.0};
+  if (c.tile == TILE_128 && can_split) c.split = split_plan128(tiles128, nk, cus);
   return c;
 }
 
@@ -1134,12 +1168,16 @@ unsigned allowed_tiles(bool grouped, bool ksegs) {
   return m;
 }
 
-// Workspace for any schedule an entry may take: the T256 split plan's pieces (used when the launch runs T256
-// tiles, chosen or forced; other tile shapes leave it untouched).
+// Workspace for any schedule an entry may take: the larger of the T256 and T128 split plans' pieces (used when
+// the launch runs that tile shape, chosen or forced; other shapes leave it untouched).
 int64_t split_ws_bytes(int64_t rows_a, int64_t rows_b, int64_t kbytes) {
-  const int64_t tiles = ((rows_a + 255) / 256) * ((rows_b + 255) / 256);
-  const SplitPlan q = split_plan(tiles, (int)(kbytes / SBK), k2q_cu_count());
-  return q.s > 1 ? (int64_t)q.rem * q.s * 256 * 256 * 4 : 0;
+  const int cus = k2q_cu_count();
+  const int nk = (int)(kbytes / SBK);
+  const SplitPlan q = split_plan(((rows_a + 255) / 256) * ((rows_b + 255) / 256), nk, cus);
+  const SplitPlan q128 = split_plan128(((rows_a + 127) / 128) * ((rows_b + 127) / 128), nk, cus);
+  const int64_t b256 = q.s > 1 ? (int64_t)q.rem * q.s * 256 * 256 * 4 : 0;
+  const int64_t b128 = q128.s > 1 ? (int64_t)q128.rem * q128.s * 128 * 128 * 4 : 0;
+  return b256 > b128 ? b256 : b128;
 }
 
 template <int EPI, int MODE, class C>
@@ -1170,6 +1208,17 @@ int launch_full(const GemmArgs& p, hipStream_t st) {
   return launch_tiles<EPI, C>(p, st);
 }
 
+// A split schedule: the pieces first (they fill the GPU for a short round), then the full tiles, then the fixup.
+template <int EPI, class C>
+int launch_split(const GemmArgs& p, const SplitPlan& q, hipStream_t st) {
+  int rc;
+  if ((rc = set_lds<EPI, MODE_PIECE, C>()) || (rc = set_lds<EPI, MODE_FIXUP, C>())) return rc;
+  hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_PIECE, C>), dim3((unsigned)(q.rem * q.s)), dim3(GT), C::LDS, st, p);
+  if (q.dp_tiles > 0 && (rc = launch_full<EPI, C>(p, st))) return rc;
+  hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_FIXUP, C>), dim3((unsigned)q.rem), dim3(GT), C::LDS, st, p);
+  return K2Q_OK;
+}
+
 template <int EPI>
 int launch_gemm(GemmArgs p, void* ws, int64_t ws_bytes, hipStream_t st, int forced = TILE_AUTO) {
   if (p.ldr == 0) p.ldr = p.r;
@@ -1191,13 +1240,27 @@ int launch_gemm(GemmArgs p, void* ws, int64_t ws_bytes, hipStream_t st, int forc
     p.dp_tiles = tiles;
     p.sk_rem = 0;
     p.sk_s = 1;
+    SplitPlan q = c.split;
+    if (c.tile != TILE_128 || (q.s > 1 && (!ws || ws_bytes < (int64_t)q.rem * q.s * 128 * 128 * 4 ||
+                                           !k2q_aligned(ws, 16))))
+      q = SplitPlan{tiles, 0, 1, 0.0};   // no split, or no room for the pieces: full-K tiles only
     int rc;
     if constexpr (EPI == EPI_DX) {
       rc = K2Q_EINVAL;
     } else {
-      if (c.tile == TILE_320) rc = launch_full<EPI, T320>(p, st);
-      else if (c.tile == TILE_192) rc = launch_full<EPI, T192>(p, st);
-      else rc = launch_full<EPI, T128>(p, st);
+      if (c.tile == TILE_320) {
+        rc = launch_full<EPI, T320>(p, st);
+      } else if (c.tile == TILE_192) {
+        rc = launch_full<EPI, T192>(p, st);
+      } else if (q.s > 1) {
+        p.dp_tiles = q.dp_tiles;
+        p.sk_rem = q.rem;
+        p.sk_s = q.s;
+        p.part = static_cast<int32_t*>(ws);
+        rc = launch_split<EPI, T128>(p, q, st);
+      } else {
+        rc = launch_full<EPI, T128>(p, st);
+      }
     }
     return rc ? rc : k2q_launch_status();
   }
@@ -1210,15 +1273,8 @@ int launch_gemm(GemmArgs p, void* ws, int64_t ws_bytes, hipStream_t st, int forc
   p.sk_rem = q.rem;
   p.sk_s = q.s;
   p.part = static_cast<int32_t*>(ws);
-  int rc = K2Q_OK;
-  // Pieces first: they fill the GPU for a short round, then the full tiles, then the fixup.
-  if (q.s > 1) {
-    if ((rc = set_lds<EPI, MODE_PIECE, T256>()) || (rc = set_lds<EPI, MODE_FIXUP, T256>())) return rc;
-    hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_PIECE, T256>), dim3((unsigned)(q.rem * q.s)), dim3(GT), T256::LDS, st, p);
-  }
-  if (q.dp_tiles > 0 && (rc = launch_full<EPI, T256>(p, st))) return rc;
-  if (q.s > 1) hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_FIXUP, T256>), dim3((unsigned)q.rem), dim3(GT), T256::LDS, st, p);
-  return k2q_launch_status();
+  int rc = q.s > 1 ? launch_split<EPI, T256>(p, q, st) : launch_full<EPI, T256>(p, st);
+  return rc ? rc : k2q_launch_status();
 }
 
 int check_common(int64_t M, int64_t N, int64_t K) {
@@ -1298,7 +1354,7 @@ extern "C" int k2q_gemm_w8a8_plan(int64_t M, int64_t N, int64_t K, int cus, int 
     return K2Q_TILE_GEMV;
   }
   const TileChoice c = choose_tile(EPI_W8, N, M, K, allowed_tiles(grouped != 0, false), grouped == 0, TILE_AUTO, cus);
-  if (split_pieces) *split_pieces = c.tile == TILE_256 ? c.split.s : 1;
+  if (split_pieces) *split_pieces = c.tile == TILE_256 || c.tile == TILE_128 ? c.split.s : 1;
   return c.tile;
 }
 

@@ -368,6 +368,33 @@ def test_gemm_split_schedule_bit_exact(k2, dev, M, N, K):
     assert torch.equal(k2._lib.gemm_w8a8(qx, sx, qw, sw, bias, u, B, 0.5), y0)   # whatever tile is chosen
 
 
+@pytest.mark.parametrize("M,N,K", [(1024, 3072, 12288), (512, 1536, 12288), (256, 6144, 6144), (1024, 2048, 12288)])
+def test_gemm_split_schedule_128_bit_exact(k2, dev, M, N, K):
+    """One round of 128 x 128 tiles over a long reduction (cfg4's text-stream down projection first): every
+    tile cut along K into pieces (2 to 5 here) whose int32 sums a fixup launch adds in order.  Accumulators
+    equal the exact product and the full-K schedule's, and the bf16 outputs (bias, LoRA) equal the full-K
+    schedule's bit for bit."""
+    tile, pieces = k2._lib.gemm_w8a8_plan(M, N, K)
+    assert tile == "128x128" and pieces > 1                     # the split schedule is taken
+    rng = np.random.default_rng(M + N + K + 1)
+    qx_h = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    qw_h = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    qx, qw = torch.from_numpy(qx_h).to(dev), torch.from_numpy(qw_h).to(dev)
+    acc = k2._lib.gemm_w8a8_acc(qx, qw, tile="128x128")
+    assert torch.equal(acc, k2._lib.gemm_w8a8_acc(qx, qw, split=False, tile="128x128"))
+    rows = np.array([0, 1, 127, 128, M // 2, M - 129, M - 1])
+    assert np.array_equal(acc.cpu().numpy()[rows], orc.gemm_acc_fast(qx_h[rows], qw_h))
+    g = torch.Generator().manual_seed(2)
+    sx = (torch.rand(M, generator=g) * 0.01 + 1e-3).to(dev)
+    sw = (torch.rand(N, generator=g) * 0.01 + 1e-3).to(dev)
+    bias = (torch.randn(N, generator=g) * 0.02).to(dev)
+    u = torch.randn(M, 16, generator=g).to(dev)
+    B = (torch.randn(N, 16, generator=g) * 0.01).to(dev)
+    y = k2._lib.gemm_w8a8(qx, sx, qw, sw, bias, u, B, 0.5)
+    y0 = k2._lib.gemm_w8a8(qx, sx, qw, sw, bias, u, B, 0.5, split=False)
+    assert torch.equal(y.view(torch.int16), y0.view(torch.int16))
+
+
 def test_input_gradient_split_schedule(k2, dev):
     """dX with the remainder tiles cut along N (f32 pieces added in slice order): against the oracle, and
     within f32 summation-order noise of the full-N schedule; repeated calls are bit-identical."""

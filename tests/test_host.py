@@ -93,6 +93,11 @@ def test_gemm_plan_edges(k2):
     assert L.gemm_w8a8_plan(9, 512, 128)[0] in L.TILES
     # a last round of 256x256 tiles that is cut along K: a GPU whose CUs the tiles fill a little over once
     assert L.gemm_w8a8_plan(1024, 4608, 16384, 256) == ("256x256", 3)
+    # one round of 128x128 tiles over a long reduction is cut along K (measured 70.5 -> 62.8 us for cfg4's
+    # text-stream down projection, 66.9 -> 46.9 us at N = 2048); a short one is not (text out: 23.6 -> 28.6)
+    assert L.gemm_w8a8_plan(1024, 3072, 12288, 256) == ("128x128", 2)
+    assert L.gemm_w8a8_plan(1024, 2048, 12288, 256) == ("128x128", 4)
+    assert L.gemm_w8a8_plan(1024, 3072, 3072, 256) == ("128x128", 1)
     # grouped launches take no 192-row tiles (segments start on 256- or 128-row boundaries)
     assert L.gemm_w8a8_plan(4096, 3072, 3072) == ("192x256", 1)
     assert L.gemm_w8a8_plan(4096, 3072, 3072, grouped=True)[0] != "192x256"
