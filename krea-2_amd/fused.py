@@ -212,9 +212,8 @@ class _GroupedFn(torch.autograd.Function):
     form at the shared input, in f32 and rounded once."""
 
     @staticmethod
-    def forward(ctx, x2, qx, sx, bases, scales, *ab):
+    def forward(ctx, x2, qx, sx, bases, scales, a_stack, *ab):
         As, Bs = ab[0::2], ab[1::2]
-        a_stack = (torch.cat(As) if len(As) > 1 else As[0]) if As else None
         u = _lib.lora_down(x2, a_stack) if As else None
         r = As[0].shape[0] if As else 0
         segs, li = [], 0
@@ -239,8 +238,8 @@ class _GroupedFn(torch.autograd.Function):
         dys = [None if dy is None else (dy.contiguous() if dy.dtype == torch.bfloat16
                                         else dy.to(torch.bfloat16).contiguous()) for dy in dys]
         adapted = [i for i, sc in enumerate(ctx.scales) if sc is not None]
-        need_a = [ctx.needs_input_grad[5 + 2 * li] for li in range(nl)]
-        need_b = [ctx.needs_input_grad[6 + 2 * li] for li in range(nl)]
+        need_a = [ctx.needs_input_grad[6 + 2 * li] for li in range(nl)]
+        need_b = [ctx.needs_input_grad[7 + 2 * li] for li in range(nl)]
         g = a = None
         if nl and r <= 128 and all(dys[i] is not None for i in adapted):
             # every adapter's gradients in one call: dA of all members from one pass over x per 128 stacked
@@ -271,7 +270,7 @@ class _GroupedFn(torch.autograd.Function):
         if segs:
             # one GEMM over the members' reductions: the sum autograd would form at the shared input
             dx = _lib.gemm_dx_grouped(segs, g, a)
-        return (dx, None, None, None, None, *grads)
+        return (dx, None, None, None, None, None, *grads)
 
 
 class _SiblingGroup:
@@ -285,6 +284,23 @@ class _SiblingGroup:
         self.members = list(members)
         self.ref = self.key = None
         self.kept = {}
+        self.stack = None   # (key, the adapted members' stacked LoRA A rows)
+
+    def _a_stack(self, As):
+        """The members' A factors stacked along the rank.  Kept while every factor is the adapter's own
+        parameter (a leaf the module holds, so its object, version and pointer identify its values: an optimizer
+        step or a re-pointed parameter rebuilds the stack); padded or converted factors are new tensors every
+        call and are stacked every call."""
+        if not As:
+            return None
+        if not all(a.is_leaf for a in As):
+            with torch.no_grad():
+                return torch.cat(As) if len(As) > 1 else As[0].detach()
+        key = tuple((id(a), a._version, a.data_ptr(), a.device) for a in As)
+        if self.stack is None or self.stack[0] != key:
+            with torch.no_grad():
+                self.stack = (key, torch.cat(As) if len(As) > 1 else As[0].detach())
+        return self.stack[1]
 
     @staticmethod
     def _key(x):
@@ -306,7 +322,8 @@ class _SiblingGroup:
         states = [_lora_state(m) for m in self.members]
         bases = tuple(m if isinstance(m, ConvRotLinear) else m.base for m in self.members)
         ab = [t for st in states if st is not None for t in st[:2]]
-        ys = _GroupedFn.apply(x2, qx, sx, bases, tuple(None if st is None else st[2] for st in states), *ab)
+        ys = _GroupedFn.apply(x2, qx, sx, bases, tuple(None if st is None else st[2] for st in states),
+                              self._a_stack(ab[0::2]), *ab)
         lead = x.shape[:-1]
         outs = [y.reshape(*lead, b.out_features) for y, b in zip(ys, bases)]
         self.ref, self.key = weakref.ref(x), key

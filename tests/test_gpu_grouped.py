@@ -282,6 +282,35 @@ def test_grouped_layer_gradients(k2, dev, rank):
         assert _rel(a1, a0) < 1e-3 and _rel(b1, b0) < 1e-4
 
 
+def test_grouped_forward_follows_adapter_updates(k2, dev):
+    """The group keeps its members' stacked LoRA A rows between launches; an in-place update of the adapters
+    (what an optimizer step does) must reach the next grouped forward: after the same update on both models,
+    grouped outputs match the ungrouped ones again, and differ from the pre-update outputs."""
+    dit, _ = _build(k2, dev)
+    gdit = copy.deepcopy(dit)
+    assert k2.group_siblings(gdit) == 4
+    names = ("wq", "wk", "wv", "gate")
+    g = torch.Generator().manual_seed(17)
+    xs = [(torch.randn(2, 96, FEAT, generator=g)).to(torch.bfloat16).to(dev) for _ in range(3)]
+    outs = []
+    for step, x in enumerate(xs):
+        if step:
+            for d in (dit, gdit):
+                for n in names:
+                    m = getattr(d.blocks[0].attn, n)
+                    with torch.no_grad():
+                        m.lora_A.add_(0.01 * step)
+                        m.lora_B.add_(0.002 * step)
+        with torch.no_grad():
+            y0 = [getattr(dit.blocks[0].attn, n)(x) for n in names]
+            y1 = [getattr(gdit.blocks[0].attn, n)(x) for n in names]
+        for a, b in zip(y1, y0):
+            assert (a.float() - b.float()).abs().max() <= b.float().abs().max() * 2 ** -7
+        outs.append(y1)
+    # the updates changed what the adapters add
+    assert not torch.equal(outs[2][0], getattr(gdit.blocks[0].attn, "wq").base(xs[2]))
+
+
 def test_grouped_unused_outputs_get_no_gradient_pass(k2, dev):
     """Members whose outputs reach no loss (here wk and wv) get no backward work in the grouped node, as
     ungrouped autograd would skip their nodes: their adapters get no gradient, and dX and the used members'
