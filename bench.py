@@ -511,6 +511,37 @@ def run_krea_block(k2, steps, dev):
     computes the producers (torch eager ops, every linear quantizing its own input or hitting the
     shared-input cache) against fuse_producers' kernels plus group_siblings' groups (attention inputs and
     SwiGLU gate / up: one grouped forward launch and one input-gradient GEMM each)."""
+    block, fwd_bwd, group, x0, shape = _krea_block(k2, dev)
+    out = {}
+    for fuse in (False, True):
+        if fuse:
+            group()
+        with torch.no_grad():
+            t_f = sorted(time_loop(lambda: block(x0, fuse), steps, dev=dev) for _ in range(3))[1]
+        t_fb = sorted(time_loop(lambda: fwd_bwd(fuse), max(3, steps // 2), dev=dev) for _ in range(3))[1]
+        out["fused" if fuse else "reference_ops"] = {"fwd_ms": round(t_f, 4), "fwd_bwd_ms": round(t_fb, 4)}
+    out["shape"] = shape
+    return out
+
+
+def krea_block_pass(k2, dev, iters):
+    """Fixed launches for a kernel trace of the Krea 2 block leg: ``iters`` fused forward + backward passes
+    (producers fused, both sibling groups), after 3 untimed ones that build the resident effective weights."""
+    block, fwd_bwd, group, _, shape = _krea_block(k2, dev)
+    group()
+    for _ in range(3):
+        fwd_bwd(True)
+    torch.cuda.synchronize()
+    progress("krea block pass: warm")
+    for _ in range(iters):
+        fwd_bwd(True)
+    torch.cuda.synchronize()
+    print(json.dumps({"krea_block_pass": shape, "fused_fwd_bwd_iterations": iters}), flush=True)
+
+
+def _krea_block(k2, dev):
+    """The Krea 2 block leg's layers, inputs and callables: ``block(x, fuse)``, ``fwd_bwd(fuse)``, ``group()``
+    (group_siblings on both groups), the input and a shape string."""
     import types
 
     from krea2_amd import fused
@@ -551,16 +582,10 @@ def run_krea_block(k2, steps, dev):
         x = x0.clone().requires_grad_(True)
         block(x, fuse).backward(dy)
 
-    out = {}
-    for fuse in (False, True):
-        if fuse:
-            fused.group_siblings(types.SimpleNamespace(blocks=[types.SimpleNamespace(attn=attn, mlp=mlp)]))
-        with torch.no_grad():
-            t_f = sorted(time_loop(lambda: block(x0, fuse), steps, dev=dev) for _ in range(3))[1]
-        t_fb = sorted(time_loop(lambda: fwd_bwd(fuse), max(3, steps // 2), dev=dev) for _ in range(3))[1]
-        out["fused" if fuse else "reference_ops"] = {"fwd_ms": round(t_f, 4), "fwd_bwd_ms": round(t_fb, 4)}
-    out["shape"] = f"M={M} width={D} kv={KV} hidden={HID} r={r}; attention excluded"
-    return out
+    def group():
+        fused.group_siblings(types.SimpleNamespace(blocks=[types.SimpleNamespace(attn=attn, mlp=mlp)]))
+
+    return block, fwd_bwd, group, x0, f"M={M} width={D} kv={KV} hidden={HID} r={r}; attention excluded"
 
 
 def run_reference_gpu(k2, res, steps, dev):
@@ -1041,6 +1066,8 @@ def main():
     ap.add_argument("--profile-pass", action="store_true", help="fixed launches for rocprofv3 counter runs")
     ap.add_argument("--power", action="store_true",
                     help="GEMM vs hipBLASLt int8 vs bf16 at the cfg2 shape with board power / clock samples")
+    ap.add_argument("--krea-block-pass", type=int, default=0, metavar="N",
+                    help="N fused forward + backward passes of the Krea 2 block leg (for kernel traces)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write profiles/traffic_cfg2.json from two rocprofv3 --pmc runs over --profile-pass")
     a = ap.parse_args()
@@ -1065,6 +1092,9 @@ def main():
         return
     if a.power:
         power_pass(k2, dev)
+        return
+    if a.krea_block_pass:
+        krea_block_pass(k2, dev, a.krea_block_pass)
         return
     cfg = CONFIGS[a.config]
     res = run_config(k2, cfg, a.steps, a.warmup, dev, a.settle)
