@@ -58,6 +58,19 @@ def test_status_codes_for_bad_arguments_without_gpu(k2):
     assert lib.k2q_lora_down_ws_bytes(4096, 3072, 256) == lib.k2q_lora_down_ws_bytes(4096, 3072, 128) > 0
     assert lib.k2q_lora_grads_ws_bytes(4096, 3072, 3072, 256) > lib.k2q_lora_grads_ws_bytes(4096, 3072, 3072, 128)
     assert lib.k2q_lora_grads_ws_bytes(4096, 3072, 3072, 8192) == 0
+    # grouped LoRA gradients: members, ranks and widths are checked before any launch
+    mem = (k2._lib.LoraMember * 2)(k2._lib.LoraMember(p, 3072, 3072, p, 1.0, None),
+                                   k2._lib.LoraMember(p, 1536, 1536, p, 1.0, None))
+    addr = ctypes.addressof(mem)
+    assert lib.k2q_lora_grads_grouped_ws_bytes(addr, 2, 4608, 6144, 64) > 0
+    assert lib.k2q_lora_grads_grouped_ws_bytes(addr, 2, 4608, 6144, 256) == 0     # rank above 128
+    assert lib.k2q_lora_grads_grouped_ws_bytes(addr, 9, 4608, 6144, 64) == 0      # more than 8 members
+    assert lib.k2q_lora_grads_grouped_ws_bytes(addr, 2, 4608, 100, 64) == 0       # K % 128
+    mem[1].N = 1000                                                               # out_features % 128
+    assert lib.k2q_lora_grads_grouped_ws_bytes(addr, 2, 4608, 6144, 64) == 0
+    mem[1].N, mem[1].ldy = 1536, 1000                                             # row stride below N
+    assert lib.k2q_lora_grads_grouped_ws_bytes(addr, 2, 4608, 6144, 64) == 0
+    assert lib.k2q_lora_grads_grouped(addr, 2, p, p, 64, 4608, 6144, p, p, p, 0, None) == -1
 
 
 # MI355X timings (us, one GEMM launch incl. epilogue) of each output tile shape on the shapes the chooser was
@@ -107,6 +120,14 @@ def test_gemm_plan_edges(k2):
 
 def test_wrappers_validate_before_launch(k2):
     L = k2._lib
+    # grouped LoRA gradients: member count and rank before anything touches a device
+    dy = torch.zeros(4, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="members"):
+        L.lora_grads_grouped([dy] * 9, None, None, [torch.zeros(128, 16)] * 9, [1.0] * 9)
+    with pytest.raises(ValueError, match="above 128"):
+        L.lora_grads_grouped([dy], None, None, [torch.zeros(128, 256)], [1.0])
+    with pytest.raises(ValueError):
+        L.lora_grads_grouped([dy], None, None, [torch.zeros(128, 24)], [1.0])       # rank % 16
     with pytest.raises(ValueError):
         L.rotquant(torch.zeros(4, 100, dtype=torch.bfloat16))
     with pytest.raises(ValueError):
