@@ -276,6 +276,18 @@ __device__ __forceinline__ v8bf f32x8_to_bf16v(v4f a, v4f b, float s) {
   return __builtin_bit_cast(v8bf, w);
 }
 
+// Raw byte buffer over [base, base + bytes) for the workgroup-uniform base and extent.  The pieces go
+// through readfirstlane so the descriptor is built in SGPRs (a descriptor the compiler cannot prove
+// uniform is used through a per-lane loop).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t k2q_rsrc(const void* base, int64_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  const int n = __builtin_amdgcn_readfirstlane((int)bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0, n,
+                                          0x00020000);
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
@@ -395,10 +407,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
   }
 
   // Per-lane source offsets (bytes from the tile's first row) of the DMA instructions: LDS rows
-  // 8 (D wave + i) + lane/8; rows past the matrix end are clamped onto its last row (never stored).
+  // 8 (D wave + i) + lane/8; rows past the matrix end are clamped onto its last row (never stored).  The
+  // copies go through buffer resources over the tile's rows (SGPR base, per-lane offset, the stage as a
+  // scalar offset): as MUBUF instructions they count in vmcnt only, so the compiler's waits for the
+  // fragment reads stay exact (lgkmcnt(n)) instead of draining every outstanding LDS read.
   uint32_t offa[C::DA], offb[C::DB];
-  const uint8_t* gA;
-  const uint8_t* gB;
+  __amdgpu_buffer_rsrc_t rsa, rsb;
   auto bind = [&](const uint8_t* a, const uint8_t* b, int64_t lda, int64_t ldb) {
 #pragma unroll
     for (int i = 0; i < C::DA; ++i) {
@@ -414,8 +428,10 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
       rb = B0 + rb < p.rows_b ? rb : p.rows_b - 1 - B0;
       offb[i] = (uint32_t)(rb * ldb) + 16u * (uint32_t)((lane & 7) ^ swz(lrow));
     }
-    gA = a + A0 * lda + (int64_t)kbeg * SBK;
-    gB = b + B0 * ldb + (int64_t)kbeg * SBK;
+    const int64_t na = p.rows_a - A0 < TA ? p.rows_a - A0 : TA;
+    const int64_t nb = p.rows_b - B0 < TB ? p.rows_b - B0 : TB;
+    rsa = k2q_rsrc(a + A0 * lda + (int64_t)kbeg * SBK, na * lda - (int64_t)kbeg * SBK);
+    rsb = k2q_rsrc(b + B0 * ldb + (int64_t)kbeg * SBK, nb * ldb - (int64_t)kbeg * SBK);
   };
   // Segmented reduction (full-K tiles of EPI_DXLIN only): stage st of segment j reads its operands at stage
   // st - kbase; seek(st) moves to st's segment.  The stages passed to seek increase by at most one per call
@@ -443,20 +459,21 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
       }
     }
   };
-  uint8_t* ldsa = smem + 1024 * C::DA * wave;            // this wave's DMA rows inside a stage
-  uint8_t* ldsb = smem + TA * WBK + 1024 * C::DB * wave;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);   // the LDS destinations (M0) in scalar registers
+  uint8_t* ldsa = smem + 1024 * C::DA * wave_s;            // this wave's DMA rows inside a stage
+  uint8_t* ldsb = smem + TA * WBK + 1024 * C::DB * wave_s;
 
   // DMA of stage st (128 reduction bytes) into LDS slot `slot`.
   auto issue = [&](int st, int slot) {
-    const int64_t so = (int64_t)(st - kbase) * WBK;
+    const int so = (st - kbase) * WBK;
 #pragma unroll
     for (int i = 0; i < C::DA; ++i)
-      __builtin_amdgcn_global_load_lds(K2Q_GPTR(gA + so + offa[i]),
-                                       K2Q_LPTR(ldsa + slot * C::STAGE + 1024 * i), 16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, K2Q_LPTR(ldsa + slot * C::STAGE + 1024 * i), 16, (int)offa[i],
+                                               so, 0, 0);
 #pragma unroll
     for (int i = 0; i < C::DB; ++i)
-      __builtin_amdgcn_global_load_lds(K2Q_GPTR(gB + so + offb[i]),
-                                       K2Q_LPTR(ldsb + slot * C::STAGE + 1024 * i), 16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, K2Q_LPTR(ldsb + slot * C::STAGE + 1024 * i), 16, (int)offb[i],
+                                               so, 0, 0);
   };
   // Fragments of substep kk (32 reduction bytes) of the stage in LDS slot `slot`.
   auto read_frags = [&](int slot, int kk, v4i (&fa)[NA], v4i (&fb)[NB]) {
@@ -829,18 +846,6 @@ struct W4Args {
 };
 
 __device__ __forceinline__ int swz4(int row) { return (row >> 2) & 3; }
-
-// Raw byte buffer over [base, base + bytes) for the workgroup-uniform base and extent.  The pieces go
-// through readfirstlane so the descriptor is built in SGPRs (a descriptor the compiler cannot prove
-// uniform is used through a per-lane loop).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t k2q_rsrc(const void* base, int64_t bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
-  const int n = __builtin_amdgcn_readfirstlane((int)bytes);
-  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0, n,
-                                          0x00020000);
-}
 
 template <int EPI>
 __global__ __launch_bounds__(256, 3) __attribute__((amdgpu_waves_per_eu(3, 3))) void gemm_w4_kernel(W4Args p) {
