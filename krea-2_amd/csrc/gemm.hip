@@ -200,8 +200,9 @@ __device__ __forceinline__ void fwht128_rows(v16f (&f)[4], int h) {
 }
 
 // ---------------------------------------------------------------------------------------------------------
-// Main-loop data movement: global -> LDS by the gfx950 LDS-DMA path (global_load_lds_dwordx4), no VGPR
-// staging.  A stage is 128 bytes of the reduction axis for the tile's TA A-rows and TB B-rows (the
+// Main-loop data movement: global -> LDS by the gfx950 LDS-DMA path (buffer_load_dwordx4 ... lds), no VGPR
+// staging.  The FLAT form (global_load_lds_dwordx4) measured 4-6 % slower on every GEMM shape: the compiler
+// counts a FLAT LDS write against lgkmcnt too, so each wait for a fragment read became lgkmcnt(0).  A stage is 128 bytes of the reduction axis for the tile's TA A-rows and TB B-rows (the
 // frag()/swz() layout above); two stages alternate in LDS.  One DMA wave instruction fills 8 consecutive LDS
 // rows (1 KB: lane l -> row l/8, physical chunk l%8) and each lane fetches the logical chunk (l%8) ^ swz(row)
 // of its row, so every instruction reads 8 whole 128-byte lines.  Measured on MI355X (same box, random data)
@@ -213,7 +214,6 @@ __device__ __forceinline__ void fwht128_rows(v16f (&f)[4], int h) {
 constexpr int SBK = 64;                   // unit of reduction lengths in the split plan (half a stage)
 constexpr int WBK = 128;                  // reduction bytes per stage
 
-#define K2Q_GPTR(p) ((__attribute__((address_space(1))) void*)(p))
 #define K2Q_LPTR(p) ((__attribute__((address_space(3))) void*)(p))
 
 constexpr int GW = 8;                     // waves per workgroup (two per SIMD)
@@ -274,18 +274,6 @@ __device__ __forceinline__ v8bf f32x8_to_bf16v(v4f a, v4f b, float s) {
   const v4u w = v4u{pack_bf16x2(a[0] * s, a[1] * s), pack_bf16x2(a[2] * s, a[3] * s), pack_bf16x2(b[0] * s, b[1] * s),
                     pack_bf16x2(b[2] * s, b[3] * s)};
   return __builtin_bit_cast(v8bf, w);
-}
-
-// Raw byte buffer over [base, base + bytes) for the workgroup-uniform base and extent.  The pieces go
-// through readfirstlane so the descriptor is built in SGPRs (a descriptor the compiler cannot prove
-// uniform is used through a per-lane loop).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t k2q_rsrc(const void* base, int64_t bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
-  const int n = __builtin_amdgcn_readfirstlane((int)bytes);
-  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0, n,
-                                          0x00020000);
 }
 
 template <int N>

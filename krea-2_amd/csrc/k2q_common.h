@@ -30,6 +30,20 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) { return pack_bf16
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
+// Raw byte buffer over [base, base + bytes) for the workgroup-uniform base and extent (bytes < 2^31); reads
+// past the extent return zero.  LDS-DMA through it (buffer_load ... lds) is a MUBUF instruction, counted in
+// vmcnt only, so the compiler keeps exact lgkmcnt waits for the LDS reads around it.  The pieces go
+// through readfirstlane so the descriptor is built in SGPRs (a descriptor the compiler cannot prove
+// uniform is used through a per-lane loop).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t k2q_rsrc(const void* base, int64_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  const int n = __builtin_amdgcn_readfirstlane((int)bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0, n,
+                                          0x00020000);
+}
+
 // Skinny-M forward (gemv.hip), used by k2q_gemm_w8a8 for 1 <= M <= K2Q_GEMV_MAX_M.
 #define K2Q_GEMV_MAX_M 8
 int k2q_launch_gemv_w8a8(const int8_t* qx, const float* sx, const int8_t* qw, const float* sw, const float* bias,

@@ -145,16 +145,18 @@ __device__ __forceinline__ WgJob pick_job(const WgJobs& js, int64_t b, int64_t& 
   return job;
 }
 
-// Both operands arrive by LDS-DMA (global_load_lds_dwordx4) through an NST-slot ring, one s_waitcnt and one
-// s_barrier per stage (no __syncthreads: its fence would drain the prefetches).  Q rows past M are read
-// clamped (finite values) and meet the zero padding of P^T, so they add nothing.
+// Both operands arrive by LDS-DMA (buffer_load ... lds through buffer resources, so the compiler's waits for the
+// LDS reads stay exact) through an NST-slot ring, one s_waitcnt and one s_barrier per stage (no __syncthreads:
+// its fence would drain the prefetches).  Q rows past M lie past the resource's range and read as zero; they
+// meet the zero padding of P^T.
 template <int RT>
 __global__ __launch_bounds__(256) void wgrad_kernel(WgJobs jobs, int64_t M, int64_t Mp) {
   using S = WgShape<RT>;
   constexpr int R = 16 * RT;
   constexpr int NST = S::NST;
   __shared__ __attribute__((aligned(16))) uint8_t ring[NST * S::STAGE];
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
   int64_t wi;
   const WgJob job = pick_job(jobs, (int64_t)blockIdx.x, wi);
   const uint16_t* pth = job.pth;
@@ -172,42 +174,43 @@ __global__ __launch_bounds__(256) void wgrad_kernel(WgJobs jobs, int64_t M, int6
   const int nsteps = (int)((me - mb + WG_MS - 1) / WG_MS);
 
   // Q sources: wave w's instruction i fills stage rows 2(WG_QG w + i) + lane/32, LDS chunk lane%32, which
-  // holds the row's logical chunk (lane%32) ^ wg_swz(row).  Columns past C read the last valid chunk.
-  uint32_t qrow[WG_QG];
-  int64_t qcol[WG_QG];
+  // holds the row's logical chunk (lane%32) ^ wg_swz(row).  Columns past C read the last valid chunk.  The
+  // resource covers this workgroup's rows mb .. me-1 (mchunk is a multiple of the stage's WG_MS rows); the
+  // stage is a scalar offset.
+  const __amdgpu_buffer_rsrc_t rq = k2q_rsrc(q + mb * ldq, (me - mb) * ldq * 2);
+  const int qstage = __builtin_amdgcn_readfirstlane((int)(WG_MS * ldq * 2));
+  uint32_t qoff[WG_QG];
 #pragma unroll
   for (int i = 0; i < WG_QG; ++i) {
     const int row = 2 * (WG_QG * w + i) + (lane >> 5);
-    qrow[i] = (uint32_t)row;
     const int64_t c = kb + 8 * ((lane & 31) ^ wg_swz(row));
-    qcol[i] = c + 8 <= C ? c : C - 8;
+    qoff[i] = (uint32_t)((row * ldq + (c + 8 <= C ? c : C - 8)) * 2);
   }
   // P sources: instruction PI w + i loads block b = PI w + i (block 0 again when b >= 2 RT): lane L -> block
   // row L/4, LDS chunk L%4, holding logical chunk (L%4) ^ ((row >> 2) & 3) of that row's 32 m.
-  const uint16_t* prow[S::PI];
+  const __amdgpu_buffer_rsrc_t rph = k2q_rsrc(pth, (int64_t)R * Mp * 2);
+  const __amdgpu_buffer_rsrc_t rpl = k2q_rsrc(ptl, (int64_t)R * Mp * 2);
+  uint32_t poff[S::PI];
 #pragma unroll
   for (int i = 0; i < S::PI; ++i) {
     const int b = S::PI * w + i < 2 * RT ? S::PI * w + i : 0;
     const int jr = lane >> 2;
-    const uint16_t* base = b < RT ? pth : ptl;
-    prow[i] = base + (int64_t)(16 * (b % RT) + jr) * Mp + 8 * ((lane & 3) ^ ((jr >> 2) & 3));
+    poff[i] = (uint32_t)(((int64_t)(16 * (b % RT) + jr) * Mp + 8 * ((lane & 3) ^ ((jr >> 2) & 3))) * 2);
   }
   auto issue = [&](int st, int slot) {
     uint8_t* dst = ring + slot * S::STAGE;
 #pragma unroll
-    for (int i = 0; i < WG_QG; ++i) {
-      int64_t m = mb + (int64_t)WG_MS * st + qrow[i];
-      m = m < M ? m : M - 1;
-      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(q + m * ldq + qcol[i]),
-                                       (__attribute__((address_space(3))) void*)(dst + 1024 * (WG_QG * w + i)), 16,
-                                       0, 0);
-    }
-    const int64_t m0 = mb + (int64_t)WG_MS * st;   // < Mp: stages never pass the 32-padded end of P^T
+    for (int i = 0; i < WG_QG; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (__attribute__((address_space(3))) void*)(dst + 1024 * (WG_QG * w + i)),
+                                               16, (int)qoff[i], st * qstage, 0, 0);
+    const int m0 = (int)((mb + (int64_t)WG_MS * st) * 2);   // < 2 Mp: stages never pass the 32-padded end of P^T
 #pragma unroll
-    for (int i = 0; i < S::PI; ++i)
-      __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(prow[i] + m0),
-                                       (__attribute__((address_space(3))) void*)(dst + WG_QBYTES + 1024 * (S::PI * w + i)),
-                                       16, 0, 0);
+    for (int i = 0; i < S::PI; ++i) {
+      const int b = S::PI * w + i < 2 * RT ? S::PI * w + i : 0;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(b < RT ? rph : rpl,
+                                               (__attribute__((address_space(3))) void*)(dst + WG_QBYTES + 1024 * (S::PI * w + i)),
+                                               16, (int)poff[i], m0, 0, 0);
+    }
   };
 
   v4f acc[RT][4];
@@ -355,13 +358,14 @@ struct ProductSet {
   RedJobs reds{};
   int64_t blocks = 0, red_blocks = 0;
 
-  bool full = false;   // a product past WG_MAXJ was refused (run() then fails)
+  bool full = false;   // a product past WG_MAXJ, or too large to address, was refused (run() then fails)
 
   // Adds out = scale * P^T Q (P^T rows pth/ptl of R ranks; Q: M x C, row stride ldq; trans: out[c][j] with
   // row stride ldt) under plan p, its slice partials (when p slices M) at part.
   void add(const GradPlan& p, const uint16_t* pth, const uint16_t* ptl, const uint16_t* q, int64_t C, int64_t ldq,
            int64_t R, float scale, int trans, int64_t ldt, float* part, float* out) {
-    if (jobs.n == WG_MAXJ) {
+    // the kernel's buffer resources address a slice's rows of Q, and the whole of P^T, in 31-bit byte offsets
+    if (jobs.n == WG_MAXJ || p.mchunk * ldq * 2 >= 0x7fffffffLL || R * (p.slices * p.mchunk + WG_MS) * 2 >= 0x7fffffffLL) {
       full = true;
       return;
     }
