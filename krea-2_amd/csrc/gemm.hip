@@ -394,28 +394,25 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
     if (t < TA) pre_bi = p.bias ? p.bias[ra] : 0.f;
   }
 
-  // Per-lane source offsets (bytes from the tile's first row) of the DMA instructions: LDS rows
-  // 8 (D wave + i) + lane/8; rows past the matrix end are clamped onto its last row (never stored).  The
-  // copies go through buffer resources over the tile's rows (SGPR base, per-lane offset, the stage as a
-  // scalar offset): as MUBUF instructions they count in vmcnt only, so the compiler's waits for the
-  // fragment reads stay exact (lgkmcnt(n)) instead of draining every outstanding LDS read.
-  uint32_t offa[C::DA], offb[C::DB];
+  // DMA sources.  Instruction i of wave w fills LDS rows 8 (D w + i) + lane/8 with the logical chunks
+  // (lane%8) ^ swz(row) of those rows, so its per-lane byte offset from the tile's first row is V[(D w + i) & 1]
+  // + 8 i ld: one vector register per parity of 8-row group (the swizzle flips with bit 3 of the row), the
+  // 8 i ld part scalar, like the stage offset.  The copies go through buffer resources over the tile's rows:
+  // rows past the matrix end lie past the resource's range, read as zero and only feed outputs that are never
+  // stored.
+  uint32_t va[2], vb[2];
+  int lda_s = 0, ldb_s = 0;
   __amdgpu_buffer_rsrc_t rsa, rsb;
   auto bind = [&](const uint8_t* a, const uint8_t* b, int64_t lda, int64_t ldb) {
 #pragma unroll
-    for (int i = 0; i < C::DA; ++i) {
-      const int lrow = 8 * (C::DA * wave + i) + (lane >> 3);
-      int64_t ra = lrow;
-      ra = A0 + ra < p.rows_a ? ra : p.rows_a - 1 - A0;
-      offa[i] = (uint32_t)(ra * lda) + 16u * (uint32_t)((lane & 7) ^ swz(lrow));
+    for (int par = 0; par < 2; ++par) {
+      const int ca = (lane & 7) ^ (lane >> 3) ^ ((C::DA * wave + par) & 1);
+      const int cb = (lane & 7) ^ (lane >> 3) ^ ((C::DB * wave + par) & 1);
+      va[par] = (uint32_t)((8 * C::DA * wave + (lane >> 3)) * lda) + 16u * (uint32_t)ca;
+      vb[par] = (uint32_t)((8 * C::DB * wave + (lane >> 3)) * ldb) + 16u * (uint32_t)cb;
     }
-#pragma unroll
-    for (int i = 0; i < C::DB; ++i) {
-      const int lrow = 8 * (C::DB * wave + i) + (lane >> 3);
-      int64_t rb = lrow;
-      rb = B0 + rb < p.rows_b ? rb : p.rows_b - 1 - B0;
-      offb[i] = (uint32_t)(rb * ldb) + 16u * (uint32_t)((lane & 7) ^ swz(lrow));
-    }
+    lda_s = __builtin_amdgcn_readfirstlane((int)lda);
+    ldb_s = __builtin_amdgcn_readfirstlane((int)ldb);
     const int64_t na = p.rows_a - A0 < TA ? p.rows_a - A0 : TA;
     const int64_t nb = p.rows_b - B0 < TB ? p.rows_b - B0 : TB;
     rsa = k2q_rsrc(a + A0 * lda + (int64_t)kbeg * SBK, na * lda - (int64_t)kbeg * SBK);
@@ -456,12 +453,12 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
     const int so = (st - kbase) * WBK;
 #pragma unroll
     for (int i = 0; i < C::DA; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, K2Q_LPTR(ldsa + slot * C::STAGE + 1024 * i), 16, (int)offa[i],
-                                               so, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, K2Q_LPTR(ldsa + slot * C::STAGE + 1024 * i), 16, (int)va[i & 1],
+                                               so + 8 * i * lda_s, 0, 0);
 #pragma unroll
     for (int i = 0; i < C::DB; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, K2Q_LPTR(ldsb + slot * C::STAGE + 1024 * i), 16, (int)offb[i],
-                                               so, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsb, K2Q_LPTR(ldsb + slot * C::STAGE + 1024 * i), 16, (int)vb[i & 1],
+                                               so + 8 * i * ldb_s, 0, 0);
   };
   // Fragments of substep kk (32 reduction bytes) of the stage in LDS slot `slot`.
   auto read_frags = [&](int slot, int kk, v4i (&fa)[NA], v4i (&fb)[NB]) {
