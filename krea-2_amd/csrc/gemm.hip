@@ -86,15 +86,6 @@ struct GemmArgs {
 
 __device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
-// Compile-time loop: f(std::integral_constant<int, i>) for i = 0 .. N-1 (scheduling hints take constant counts).
-template <int I, int N, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (I < N) {
-    f(std::integral_constant<int, I>{});
-    static_for<I + 1, N>(f);
-  }
-}
-
 // Workgroup ids are dealt round-robin over the 8 XCDs; renumber them so that consecutive ids share an XCD.
 __device__ __forceinline__ int xcd_remap(int bid, int nwg) {
   const int xcd = bid & 7, idx = bid >> 3;

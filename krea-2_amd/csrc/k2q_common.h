@@ -44,6 +44,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t k2q_rsrc(const void* base, int
                                           0x00020000);
 }
 
+// Compile-time loop: f(std::integral_constant<int, i>) for i = 0 .. N-1 (for scheduling hints and register
+// arrays that need constant indices).
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
 // Skinny-M forward (gemv.hip), used by k2q_gemm_w8a8 for 1 <= M <= K2Q_GEMV_MAX_M.
 #define K2Q_GEMV_MAX_M 8
 int k2q_launch_gemv_w8a8(const int8_t* qx, const float* sx, const int8_t* qw, const float* sw, const float* bias,
