@@ -541,7 +541,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
     read_frags(0, 0, f0a, f0b);
     // Unrolled by two stages so that the LDS slot, and with it every fragment address, is a constant.
     auto stage = [&](int st, auto SLC) {
-      constexpr int sl = decltype(SLC)::value;
+      const int sl = static_cast<int>(SLC);
       seek(st + 2 < ns ? st + 2 : ns - 1);   // the segment of the stage this iteration's DMA fetches
       read_frags(sl, 1, f1a, f1b);
       sub(f0a, f0b);
@@ -566,12 +566,16 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
       for (int i = 0; i < NR; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
       if constexpr (NM > GI) __builtin_amdgcn_sched_group_barrier(0x008, NM - GI, 0);
     };
-    int st = 0;
-    for (; st + 1 < ns; st += 2) {
-      stage(st, std::integral_constant<int, 0>{});
-      stage(st + 1, std::integral_constant<int, 1>{});
+    if constexpr (C::TB == 320) {   // the 256 x 320 tile: unrolled, values live across the loop spill
+      for (int st = 0; st < ns; ++st) stage(st, st & 1);
+    } else {
+      int st = 0;
+      for (; st + 1 < ns; st += 2) {
+        stage(st, std::integral_constant<int, 0>{});
+        stage(st + 1, std::integral_constant<int, 1>{});
+      }
+      if (st < ns) stage(st, std::integral_constant<int, 0>{});
     }
-    if (st < ns) stage(st, std::integral_constant<int, 0>{});
     wait_vmcnt<0>();   // no LDS-DMA may still be in flight when the workgroup's LDS is released
   }
   if constexpr (MODE == MODE_PIECE) {   // park the accumulators for the fixup launch
