@@ -1226,6 +1226,13 @@ int launch_split(const GemmArgs& p, const SplitPlan& q, hipStream_t st) {
 template <int EPI>
 int launch_gemm(GemmArgs p, void* ws, int64_t ws_bytes, hipStream_t st, int forced = TILE_AUTO) {
   if (p.ldr == 0) p.ldr = p.r;
+  // A tile's operand rows are read through buffer resources with 31-bit byte offsets: 320 rows of either side
+  int64_t ld_max = p.lda_b > p.ldb_b ? p.lda_b : p.ldb_b;
+  for (int i = 0; i < p.nks; ++i) {
+    ld_max = p.ks[i].lda_b > ld_max ? p.ks[i].lda_b : ld_max;
+    ld_max = p.ks[i].ldb_b > ld_max ? p.ks[i].ldb_b : ld_max;
+  }
+  if (320 * ld_max >= 0x7fffffffLL) return K2Q_EUNSUPPORTED;
   if (forced >= TILE_COUNT || (EPI == EPI_DX && forced >= 0 && forced != TILE_256)) return K2Q_EINVAL;
   TileChoice c = choose_tile(EPI, p.rows_a, p.rows_b, p.kbytes, allowed_tiles(p.nseg > 0, p.nks > 0),
                              p.nseg == 0 && p.nks == 0, forced, k2q_cu_count());

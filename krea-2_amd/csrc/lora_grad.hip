@@ -174,11 +174,9 @@ __global__ __launch_bounds__(256) void wgrad_kernel(WgJobs jobs, int64_t M, int6
   const int nsteps = (int)((me - mb + WG_MS - 1) / WG_MS);
 
   // Q sources: wave w's instruction i fills stage rows 2(WG_QG w + i) + lane/32, LDS chunk lane%32, which
-  // holds the row's logical chunk (lane%32) ^ wg_swz(row).  Columns past C read the last valid chunk.  The
-  // resource covers this workgroup's rows mb .. me-1 (mchunk is a multiple of the stage's WG_MS rows); the
-  // stage is a scalar offset.
-  const __amdgpu_buffer_rsrc_t rq = k2q_rsrc(q + mb * ldq, (me - mb) * ldq * 2);
-  const int qstage = __builtin_amdgcn_readfirstlane((int)(WG_MS * ldq * 2));
+  // holds the row's logical chunk (lane%32) ^ wg_swz(row).  Columns past C read the last valid chunk.  Each
+  // stage reads through a resource over its own rows (at most WG_MS, up to this workgroup's last row me - 1;
+  // mchunk is a multiple of WG_MS), so the per-lane offsets stay small whatever M and the row stride.
   uint32_t qoff[WG_QG];
 #pragma unroll
   for (int i = 0; i < WG_QG; ++i) {
@@ -199,10 +197,12 @@ __global__ __launch_bounds__(256) void wgrad_kernel(WgJobs jobs, int64_t M, int6
   }
   auto issue = [&](int st, int slot) {
     uint8_t* dst = ring + slot * S::STAGE;
+    const int64_t r0 = mb + (int64_t)WG_MS * st;
+    const __amdgpu_buffer_rsrc_t rq = k2q_rsrc(q + r0 * ldq, (me - r0 < WG_MS ? me - r0 : WG_MS) * ldq * 2);
 #pragma unroll
     for (int i = 0; i < WG_QG; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (__attribute__((address_space(3))) void*)(dst + 1024 * (WG_QG * w + i)),
-                                               16, (int)qoff[i], st * qstage, 0, 0);
+                                               16, (int)qoff[i], 0, 0, 0);
     const int m0 = (int)((mb + (int64_t)WG_MS * st) * 2);   // < 2 Mp: stages never pass the 32-padded end of P^T
 #pragma unroll
     for (int i = 0; i < S::PI; ++i) {
@@ -364,8 +364,8 @@ struct ProductSet {
   // row stride ldt) under plan p, its slice partials (when p slices M) at part.
   void add(const GradPlan& p, const uint16_t* pth, const uint16_t* ptl, const uint16_t* q, int64_t C, int64_t ldq,
            int64_t R, float scale, int trans, int64_t ldt, float* part, float* out) {
-    // the kernel's buffer resources address a slice's rows of Q, and the whole of P^T, in 31-bit byte offsets
-    if (jobs.n == WG_MAXJ || p.mchunk * ldq * 2 >= 0x7fffffffLL || R * (p.slices * p.mchunk + WG_MS) * 2 >= 0x7fffffffLL) {
+    // the kernel addresses P^T (R rows of the padded M) through one buffer resource: 31-bit byte offsets
+    if (jobs.n == WG_MAXJ || R * (p.slices * p.mchunk + WG_MS) * 2 >= 0x7fffffffLL) {
       full = true;
       return;
     }

@@ -71,6 +71,9 @@ def test_status_codes_for_bad_arguments_without_gpu(k2):
     mem[1].N, mem[1].ldy = 1536, 1000                                             # row stride below N
     assert lib.k2q_lora_grads_grouped_ws_bytes(addr, 2, 4608, 6144, 64) == 0
     assert lib.k2q_lora_grads_grouped(addr, 2, p, p, 64, 4608, 6144, p, p, p, 0, None) == -1
+    # a GEMM operand whose 320-row tile spans 2 GiB or more (the copies' buffer offsets are 31-bit): refused
+    seg = k2._lib.DxSegment(p, 1 << 23, p, 64)        # dy rows 16 MiB apart
+    assert lib.k2q_gemm_dx_grouped(ctypes.addressof(seg), 1, 4608, 6144, None, 0, None, 0, p, None) == -4
 
 
 # MI355X timings (us, one GEMM launch incl. epilogue) of each output tile shape on the shapes the chooser was
