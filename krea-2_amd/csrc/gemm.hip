@@ -11,8 +11,9 @@
 // double-buffered (2 x 64 KB) and filled by LDS-DMA.  LDS rows are 128 B; the 16-byte chunk c of row r
 // lives at chunk c ^ f(r) with f(r) = (r & 7) ^ ((r >> 3) & 1), which keeps the 16-byte MFMA fragment
 // reads free of bank conflicts.  Workgroup ids are remapped so that consecutive tiles land on the same
-// XCD (ids are dealt round-robin over the 8 XCDs), then grouped 8 B-tiles at a time so concurrently
-// running tiles share operand strips in that XCD's L2.
+// XCD (ids are dealt round-robin over the 8 XCDs), then grouped GB B-tiles at a time (8 for launches of
+// several rounds; 8, 4 or 2 by operand footprint for one-round launches) so concurrently running tiles share
+// operand strips in that XCD's L2.
 //
 // Epilogues (in registers, MFMA C layout: lane l owns output column l%32 and rows 8j+4(l/32)+i):
 //   EPI_W8   y = bf16(2^-7 s_x[m] s_w[n] acc + bias[n] + LoRA), LoRA = one bf16 MFMA per 16 of rank
@@ -82,6 +83,7 @@ struct GemmArgs {
   int64_t dp_tiles;
   int sk_rem, sk_s;
   int32_t* part;
+  int gb;             // B-tiles per group of the tile order (group_coords), set by launch_gemm
 };
 
 __device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
@@ -93,9 +95,10 @@ __device__ __forceinline__ int xcd_remap(int bid, int nwg) {
   return (rem == 0 || xcd < rem) ? xcd * per + idx : rem * per + (xcd - rem) * (per - 1) + idx;
 }
 
-// Linear tile id -> (A tile, B tile), 8 B-tiles per group so tiles running together share operand strips.
-__device__ __forceinline__ void group_coords(int64_t lid, int64_t tiles_a, int64_t tiles_b, int64_t& ta, int64_t& tb) {
-  constexpr int GB = 8;
+// Linear tile id -> (A tile, B tile), GB B-tiles per group so tiles running together share operand strips
+// (GB chosen per launch by the host: group_width).
+__host__ __device__ __forceinline__ void group_coords(int64_t lid, int64_t tiles_a, int64_t tiles_b, int GB,
+                                                      int64_t& ta, int64_t& tb) {
   const int64_t in_group = (int64_t)GB * tiles_a;
   const int64_t g = lid / in_group;
   const int64_t first_b = g * GB;
@@ -336,7 +339,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
   const int64_t tiles_a = (p0.rows_a + TA - 1) / TA;
   const int64_t tiles_b = (p0.rows_b + TB - 1) / TB;
   int64_t ta, tb;
-  group_coords(lid, tiles_a, tiles_b, ta, tb);
+  group_coords(lid, tiles_a, tiles_b, p0.gb > 0 ? p0.gb : 8, ta, tb);
   int64_t A0 = ta * TA;
   const int64_t B0 = tb * TB;
   // A grouped forward: the tile's segment supplies the operands (workgroup-uniform, scalar registers); A0
@@ -1231,6 +1234,45 @@ int launch_split(const GemmArgs& p, const SplitPlan& q, hipStream_t st) {
   return K2Q_OK;
 }
 
+// B-tiles per group of the tile order.  A launch whose tiles all run at once (one round of full-K tiles, or a
+// split with pieces only) takes the width, of 8, 4 and 2, whose tiles on one XCD span the fewest operand rows
+// (8 on a tie): an XCD holds the workgroups of consecutive remapped ids in the tile kernel, every 8th hardware
+// id in the pieces kernel.  Those launches are short and feed on their operand strips: measured -5 to -21% on
+// 1024-token shapes (128 x 128 tiles), no change on the others.  Launches of several rounds keep 8.
+int group_width(int64_t rows_a, int64_t rows_b, int ta_rows, int tb_rows, int64_t dp_tiles, int64_t pieces,
+                int64_t piece_tiles, int64_t slots) {
+  const int64_t tiles_a = (rows_a + ta_rows - 1) / ta_rows, tiles_b = (rows_b + tb_rows - 1) / tb_rows;
+  int64_t lids[64];
+  int n = 0;
+  if (pieces > 0) {
+    if (dp_tiles > 0) return 8;
+    const int64_t live = pieces < slots ? pieces : slots;
+    for (int64_t b = 0; b < live && n < 64; b += 8) lids[n++] = b % piece_tiles;
+  } else {
+    if (dp_tiles > slots) return 8;
+    const int64_t per = (dp_tiles + 7) / 8;
+    for (int64_t i = 0; i < per && n < 64; ++i) lids[n++] = i;
+  }
+  int best = 8;
+  int64_t best_rows = -1;
+  for (int gb : {8, 4, 2}) {
+    uint64_t seen_a[4] = {0, 0, 0, 0}, seen_b[4] = {0, 0, 0, 0};   // tile indices < 256 on the launches this applies to
+    int na = 0, nb = 0;
+    bool fits = true;
+    for (int i = 0; i < n; ++i) {
+      int64_t ta, tb;
+      group_coords(lids[i], tiles_a, tiles_b, gb, ta, tb);
+      if (ta >= 256 || tb >= 256) { fits = false; break; }
+      if (!(seen_a[ta >> 6] >> (ta & 63) & 1)) { seen_a[ta >> 6] |= 1ull << (ta & 63); ++na; }
+      if (!(seen_b[tb >> 6] >> (tb & 63) & 1)) { seen_b[tb >> 6] |= 1ull << (tb & 63); ++nb; }
+    }
+    if (!fits) return 8;
+    const int64_t rows = (int64_t)na * ta_rows + (int64_t)nb * tb_rows;
+    if (best_rows < 0 || rows < best_rows) { best_rows = rows; best = gb; }
+  }
+  return best;
+}
+
 template <int EPI>
 int launch_gemm(GemmArgs p, void* ws, int64_t ws_bytes, hipStream_t st, int forced = TILE_AUTO) {
   if (p.ldr == 0) p.ldr = p.r;
@@ -1263,6 +1305,14 @@ int launch_gemm(GemmArgs p, void* ws, int64_t ws_bytes, hipStream_t st, int forc
     if (c.tile != TILE_128 || (q.s > 1 && (!ws || ws_bytes < (int64_t)q.rem * q.s * 128 * 128 * 4 ||
                                            !k2q_aligned(ws, 16))))
       q = SplitPlan{tiles, 0, 1, 0.0};   // no split, or no room for the pieces: full-K tiles only
+    {
+      const int tar = c.tile == TILE_320 ? 256 : c.tile == TILE_192 ? 192 : 128;
+      const int tbr = c.tile == TILE_320 ? 320 : c.tile == TILE_192 ? 256 : 128;
+      const int wpc = c.tile == TILE_128 ? T128::WPC : c.tile == TILE_192 ? T192::WPC : T320::WPC;
+      p.gb = q.s > 1 ? group_width(p.rows_a, p.rows_b, tar, tbr, q.dp_tiles, q.rem * q.s, q.rem,
+                                   (int64_t)k2q_cu_count() * wpc)
+                     : group_width(p.rows_a, p.rows_b, tar, tbr, tiles, 0, 1, (int64_t)k2q_cu_count() * wpc);
+    }
     int rc;
     if constexpr (EPI == EPI_DX) {
       rc = K2Q_EINVAL;
@@ -1292,6 +1342,8 @@ int launch_gemm(GemmArgs p, void* ws, int64_t ws_bytes, hipStream_t st, int forc
   p.sk_rem = q.rem;
   p.sk_s = q.s;
   p.part = static_cast<int32_t*>(ws);
+  p.gb = group_width(p.rows_a, p.rows_b, 256, 256, q.dp_tiles, q.s > 1 ? q.rem * q.s : 0, q.rem > 0 ? q.rem : 1,
+                     (int64_t)k2q_cu_count() * T256::WPC);
   int rc = q.s > 1 ? launch_split<EPI, T256>(p, q, st) : launch_full<EPI, T256>(p, st);
   return rc ? rc : k2q_launch_status();
 }
