@@ -543,9 +543,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
     lds_barrier();
     read_frags(0, 0, f0a, f0b);
     // Unrolled by two stages so that the LDS slot, and with it every fragment address, is a constant.
-    // Wave priority (below) splits the scheduling region; on the bf16 256 x 320 tiles that made the compiler
-    // spill ~100 bytes per lane, so those keep the default priority.
-    constexpr bool PRIO = !(C::TB == 320 && (EPI == EPI_LIN || EPI == EPI_DXLIN));
+    // Wave priority (below): the builtin bounds the compiler's scheduling region, which on the bf16 256 x 320
+    // tiles made it spill ~100 bytes per lane; those raise it inside the barrier's own asm statement instead
+    // (no new region boundary; the drop at the end of the stage sits on the rolled loop's latch).
+    constexpr bool PRIO_ASM = C::TB == 320 && (EPI == EPI_LIN || EPI == EPI_DXLIN);
+    constexpr bool PRIO = !PRIO_ASM;
     auto stage = [&](int st, auto SLC) {
       const int sl = static_cast<int>(SLC);
       seek(st + 2 < ns ? st + 2 : ns - 1);   // the segment of the stage this iteration's DMA fetches
@@ -557,7 +559,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
       sub(f0a, f0b);
       wait_vmcnt<0>();                                      // stage st+1
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this wave's reads of slot sl have landed
-      lds_barrier();
+      if constexpr (PRIO_ASM) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier\n\ts_setprio 2" ::: "memory");
+      else lds_barrier();
       // Raised wave priority from the barrier to the end of the stage: the waves past the barrier issue
       // their DMA and MFMAs ahead of waves still in the pre-barrier substeps (0.3-2.3 % faster on the 8
       // large shapes; raising it for the pre-barrier substeps instead measured 0.7-2.4 % slower).
@@ -576,6 +579,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
       for (int i = 0; i < NR; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
       if constexpr (NM > GI) __builtin_amdgcn_sched_group_barrier(0x008, NM - GI, 0);
       if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
+      if constexpr (PRIO_ASM) asm volatile("s_setprio 0");
     };
     if constexpr (C::TB == 320) {   // the 256 x 320 tile keeps the rolled loop (unrolled, it spills registers)
       for (int st = 0; st < ns; ++st) stage(st, st & 1);
