@@ -361,12 +361,12 @@ def run_cfg3(k2, steps, dev, settle_s=0.0, cpu=False):
     prev = _no_input_reuse(k2)
     try:
         settle(step, settle_s)
-        ms = time_loop(step, steps, dev=dev)    # the frozen base's effective weight resident (the default)
+        ms = time_loop(step, steps, dev=dev)    # every backward builds its effective weight (the default)
         with torch.no_grad():
             ms_fwd = time_loop(lambda: layer(x), steps, dev=dev)
-        k2.set_dx_weight_cache(layer, False)    # every backward builds its effective weight
-        ms_per_call = time_loop(step, steps, dev=dev)
-        k2.set_dx_weight_cache(layer, True)
+        k2.set_dx_weight_cache(layer, True)     # the effective weight kept resident (2 more bytes per weight)
+        ms_kept = time_loop(step, steps, dev=dev)
+        k2.set_dx_weight_cache(layer, False)
     finally:
         k2.quantize.shared_input_quant.enabled = prev
 
@@ -413,7 +413,7 @@ def run_cfg3(k2, steps, dev, settle_s=0.0, cpu=False):
                                            INT8_PEAK_TOPS, "TOPS"),
             "dx_weight_roofline": roofline_entry("rot_dequant_t_kernel (effective weight)", "hbm", prep_gbs,
                                                  HBM_PEAK_GBS, "GB/s"),
-            "step_ms_dx_weight_per_call": round(ms_per_call, 4),
+            "step_ms_dx_weight_kept": round(ms_kept, 4),
             "reference_fp8_step_ms_gpu": round(ms_ref, 4),
             **({"cpu": cpu_cfg3(*_layer_tensors(layer, 3, c["K"], c["N"]))} if cpu else {})}
 
@@ -588,6 +588,85 @@ def _krea_block(k2, dev):
     return block, fwd_bwd, group, x0, f"M={M} width={D} kv={KV} hidden={HID} r={r}; attention excluded"
 
 
+def run_vram(k2, dev):
+    """Device memory of one Krea 2 single-stream block's eight linears (width 6144, 48 heads of 128 with 12 KV
+    heads, SwiGLU 16384; mmdit.py:170-175,188-194) under a LoRA step at 1024^2 (M = 4608, r = 16 on every
+    linear), for each frozen base: bf16 ``nn.Linear`` (the reference without quantization), fp8 (the
+    reference's ``Fp8Linear`` storage, quantize.py:33-42, this package's kernels), ConvRot w8a8, and ConvRot
+    w8a8 with the effective input-gradient weight kept.  ``base_GB``: the layers' resident bytes (base
+    parameters + adapters + any kept weight); ``peak_GB``: the most allocated during two gradient-checkpointed
+    forward + backward passes (torch.utils.checkpoint, non-reentrant, as mmdit.py:479-481), measured from the
+    empty state before the layers were built; ``paged_GB``: the bytes block swap moves per page-out (every
+    frozen parameter, mmdit.py:409-414).  The reference's published figures for the whole trainer at 768^2
+    (docs/TRAINING.md:101-107) are 28.8 GB bf16 and 17.5 GB fp8."""
+    import gc
+
+    F_ = torch.nn.functional
+    M, D, KV, HID, r = 4608, 6144, 1536, 16384, 16
+    shapes = {"wq": (D, D), "wk": (D, KV), "wv": (D, KV), "gate": (D, D), "wo": (D, D), "mlp_gate": (D, HID),
+              "mlp_up": (D, HID), "mlp_down": (HID, D)}
+    gen = torch.Generator(device=dev).manual_seed(31)
+
+    def build(kind):
+        layers = {}
+        for name, (K, N) in shapes.items():
+            lin = torch.nn.Linear(K, N, bias=False, dtype=torch.bfloat16, device=dev)
+            with torch.no_grad():
+                lin.weight.normal_(0.0, 0.02, generator=gen)
+            base = lin if kind == "bf16" else k2.Fp8Linear(lin) if kind == "fp8" else k2.ConvRotLinear(lin, "w8a8")
+            del lin
+            layer = k2.LoRALinear(base, r, float(r))
+            with torch.no_grad():
+                layer.lora_B.normal_(0.0, 0.01, generator=gen)
+            if kind == "convrot_w8a8_kept":
+                k2.set_dx_weight_cache(layer, True)
+            layers[name] = layer
+        return layers
+
+    def block(L, x):
+        # the quantized linears of SingleStreamBlock.forward (mmdit.py:310-319) with RMSNorm / modulation /
+        # attention reduced to the ops that keep the linears' shapes (attention: k * v added to the query heads)
+        h = F_.rms_norm(x.float(), (D,), eps=1e-5).to(x.dtype)
+        q, k, v, g = L["wq"](h), L["wk"](h), L["wv"](h), L["gate"](h)
+        o = (q.unflatten(-1, (KV // 128, -1, 128)) + (k * v).unflatten(-1, (KV // 128, 1, 128))).flatten(-3)
+        x = x + L["wo"](o * torch.sigmoid(g))
+        h = F_.rms_norm(x.float(), (D,), eps=1e-5).to(x.dtype)
+        return x + L["mlp_down"](F_.silu(L["mlp_gate"](h)) * L["mlp_up"](h))
+
+    def gb(b):
+        return round(b / 1e9, 3)
+
+    out = {"shape": f"one block, M={M} width={D} kv={KV} hidden={HID} r={r}; checkpointed fwd+bwd"}
+    xg = torch.Generator().manual_seed(32)
+    x0 = torch.randn(1, M, D, generator=xg).to(torch.bfloat16)
+    dy0 = (torch.randn(1, M, D, generator=xg) * 1e-2).to(torch.bfloat16)
+    for kind in ("bf16", "fp8", "convrot_w8a8", "convrot_w8a8_kept"):
+        gc.collect()
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        m0 = torch.cuda.memory_allocated(dev)
+        L = build(kind)
+        x, dy = x0.to(dev), dy0.to(dev)
+        torch.cuda.synchronize()
+        resident = torch.cuda.memory_allocated(dev) - m0 - x.nbytes - dy.nbytes
+        paged = sum(p.nbytes for m in L.values() for p in m.parameters() if not p.requires_grad)
+        torch.cuda.reset_peak_memory_stats(dev)
+        for _ in range(2):
+            xi = x.clone().requires_grad_(True)
+            torch.utils.checkpoint.checkpoint(block, L, xi, use_reentrant=False).backward(dy)
+            del xi
+        torch.cuda.synchronize()
+        peak = torch.cuda.max_memory_allocated(dev) - m0
+        kept = torch.cuda.memory_allocated(dev) - m0 - x.nbytes - dy.nbytes \
+            - sum(p.grad.nbytes for m in L.values() for p in m.parameters() if p.grad is not None)
+        out[kind] = {"base_GB": gb(resident), "base_GB_after_step": gb(kept), "peak_GB": gb(peak),
+                     "paged_GB": gb(paged), "base_GB_28_blocks": gb(28 * kept)}
+        del L, x, dy
+    gc.collect()
+    torch.cuda.empty_cache()
+    return out
+
+
 def run_reference_gpu(k2, res, steps, dev):
     """The reference's own quantized linear + adapter (``Fp8Linear.forward``, quantize.py:48-51: a bf16
     dequantization of the fp8 weight on every call, then ``F.linear``; ``LoRALinear.forward``, lora.py:47-48:
@@ -656,9 +735,12 @@ def run_cfg4(k2, steps, dev, settle_s=0.0, cpu=False):
         with torch.no_grad():
             settle(block, settle_s)
             ms = time_loop(block, steps, dev=dev)
-            per = {}
+            per, host = {}, {}
             for name, layer, M, K, N in layers:
-                per[name] = round(time_loop(lambda: layer(xs[name]), max(3, steps // 2), dev=dev), 4)
+                def call():
+                    layer(xs[name])
+                per[name] = round(time_loop(call, max(3, steps // 2), dev=dev), 4)
+                host[name] = round(HOST_US[call.__qualname__], 1)   # the module call's host issue time
     finally:
         k2.quantize.shared_input_quant.enabled = prev
     tops = total_ops / (ms * 1e-3) / 1e12
@@ -674,12 +756,14 @@ def run_cfg4(k2, steps, dev, settle_s=0.0, cpu=False):
                                              "hbm", adaln_gbs,
                                              HBM_PEAK_GBS, "GB/s"),
             "per_linear_ms": per,
+            "per_linear_host_us": host,
             **({"cpu": cpu_cfg4([(M, K, N, *_layer_tensors(layer, sd, K, N))
                                  for (_, layer, M, K, N), sd in zip(layers, seeds)])} if cpu else {})}
 
 
 def profile_pass(k2, dev):
-    """Fixed launches for rocprofv3 counter passes: cfg2 rotate/quant, LoRA down, GEMM, 3 times each; the cfg3
+    """Fixed launches for rocprofv3 counter passes: cfg2 rotate/quant, LoRA down, GEMM, 3 times each; the W4A8
+    GEMM at cfg1 and at the cfg2 shape, 3 times each; the cfg3
     input-gradient GEMM (with its LoRA term) and the cfg3 LoRA gradients 3 times each; the two producer kernels at cfg4's image-stream shapes
     and the grouped attention-input GEMM (M = 4608, 6144 -> 6144 | 1536 | 1536 | 6144, r = 16) 3 times each;
     then a plain 256 MiB device copy (Tensor.copy_) 3 times, the calibration point for FETCH/WRITE_SIZE."""
@@ -692,6 +776,20 @@ def profile_pass(k2, dev):
         qx, sx, _ = L.rotquant(xd)
         u = L.lora_down(xd, Ad)
         L.gemm_w8a8(qx, sx, qw, sw, None, u, Bd, 1.0)
+    # the W4A8 GEMM at cfg1 (LoRA r = 16, bias) and at the cfg2 shape with int4 weights (LoRA r = 32)
+    c1 = CONFIGS[1]
+    x1, W1, b1, A1, B1 = synth(c1["M"], c1["K"], c1["N"], c1["r"], c1["bias"])
+    x1d = x1.to(dev)
+    qw4, sw4 = L.quant_weight_i4(W1.to(dev))
+    qx1, sx1, _ = L.rotquant(x1d)
+    u1 = L.lora_down(x1d, A1.to(dev))
+    b1d = None if b1 is None else b1.to(dev)
+    qw4b, sw4b = L.quant_weight_i4(W.to(dev))
+    for _ in range(3):
+        L.gemm_w4a8(qx1, sx1, qw4, sw4, b1d, u1, B1.to(dev), 1.0)
+    for _ in range(3):
+        L.gemm_w4a8(qx, sx, qw4b, sw4b, None, u, Bd, 1.0)
+    del x1d, qw4, sw4, qx1, sx1, u1, qw4b, sw4b
     c3 = CFG3
     g3 = torch.Generator().manual_seed(3)
     qw3, sw3 = L.quant_weight_i8((torch.randn(c3["N"], c3["K"], generator=g3) * 0.02).to(torch.bfloat16).to(dev))
@@ -1146,6 +1244,8 @@ def main():
     extra["grouped_attn_inputs"] = run_grouped(k2, max(5, a.steps // 2), dev)
     extra["krea_block_linears"] = run_krea_block(k2, max(5, a.steps // 2), dev)
     progress("producers, grouped attention inputs and the Krea 2 block timed")
+    extra["vram_krea_block"] = run_vram(k2, dev)
+    progress("device memory of the Krea 2 block's linears measured")
     traffic, fresh = measured_traffic("gemm_nt_kernel<EPI_W8> cfg2") if a.config == 2 and not cfg["w4"] else (None, False)
     extra["traffic_profile"] = ("profiles/traffic_cfg2.json, measured on these kernel sources" if fresh else
                                 "no PMC profile of these kernel sources: traffic omitted")

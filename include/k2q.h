@@ -3,8 +3,12 @@
  * Every entry point takes raw device pointers, int64 shapes and a HIP stream passed as `void*`
  * (a hipStream_t; never the null stream in the module), launches asynchronously on that stream and
  * returns an int status (K2Q_OK or a negative K2Q_E* code).  No C++ exception crosses this boundary.
- * The caller (PyTorch's caching allocator) owns every buffer; the library keeps no device memory and
- * no mutable global state between calls, so calls on different streams are re-entrant.
+ * The caller (PyTorch's caching allocator) owns every buffer the other entry points use.  The library
+ * holds one piece of device memory: the static scratch array of k2q_lora_grads_noalloc (K2Q_SCRATCH_BYTES
+ * per GPU), whose per-device address it caches at that entry's first call on a device; that entry is not
+ * re-entrant (overlapping calls on one GPU race for the scratch).  Beside it the library caches each
+ * device's CU count (written once per device, read-only afterwards).  Every other entry point keeps no
+ * state between calls, so its calls on different streams are re-entrant.
  *
  * Layouts (row-major, last index contiguous):
  *   x      M x K   bf16 activations (or f32 / bf16 weights for the weight quantizers)

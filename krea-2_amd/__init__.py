@@ -11,8 +11,8 @@ The directory name is not a Python identifier; load it with ``__graft_entry__.lo
 registers it as ``krea2_amd``.
 """
 from . import _lib
-from .lora import (DEFAULT_TARGETS, LoRALinear, inject_lora, load_lora, load_lora_weights, lora_disabled,
-                   lora_parameters, lora_scaled, save_lora)
+from .lora import (DEFAULT_TARGETS, QWEN_TE_TARGETS, LoRALinear, inject_lora, inject_lora_te, load_lora,
+                   load_lora_weights, lora_disabled, lora_parameters, lora_scaled, save_lora)
 from .checkpoint import load_quantized_base, save_quantized_base
 from .quantize import (MODES, ConvRotLinear, Fp8Linear, quantize_dit_convrot, quantize_dit_fp8,
                        set_dx_weight_cache)
@@ -20,5 +20,5 @@ from .fused import fuse_producers, group_siblings, modulated_rmsnorm, swiglu
 
 __all__ = ["ConvRotLinear", "quantize_dit_convrot", "set_dx_weight_cache", "MODES", "Fp8Linear", "quantize_dit_fp8",
            "save_quantized_base", "load_quantized_base", "fuse_producers", "group_siblings", "modulated_rmsnorm",
-           "swiglu", "LoRALinear", "inject_lora", "lora_scaled", "lora_disabled", "lora_parameters", "save_lora",
-           "load_lora_weights", "load_lora", "DEFAULT_TARGETS", "_lib"]
+           "swiglu", "LoRALinear", "inject_lora", "inject_lora_te", "QWEN_TE_TARGETS", "lora_scaled", "lora_disabled",
+           "lora_parameters", "save_lora", "load_lora_weights", "load_lora", "DEFAULT_TARGETS", "_lib"]

@@ -87,11 +87,6 @@ static inline int k2q_launch_status() {
 
 static inline int k2q_aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
-// Compute units of the current device (launch planning only; 256 on MI355X).
-static inline int k2q_cu_count() {
-  int dev = 0, n = 0;
-  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      n < 1)
-    return 256;
-  return n;
-}
+// Compute units of the current device (launch planning only; 256 on MI355X).  Looked up once per device and
+// cached (api.hip): the attribute query costs more host time than a kernel launch.
+int k2q_cu_count();

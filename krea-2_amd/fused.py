@@ -152,8 +152,22 @@ def _fused_swiglu_forward(self, x):
     return self.down(swiglu(self.gate(x), self.up(x)))
 
 
+def _block_norms_train(blk, vec) -> bool:
+    """Whether the block's forward would need gradients of its norm scales or its modulation (a full fine-tune):
+    the modulation's chunks need one when ``vec`` or the modulation's own parameters do."""
+    if not torch.is_grad_enabled():
+        return False
+    return (blk.prenorm.scale.requires_grad or blk.postnorm.scale.requires_grad
+            or (isinstance(vec, torch.Tensor) and vec.requires_grad)
+            or any(p.requires_grad for p in blk.mod.parameters()))
+
+
 def _fused_block_forward(self, x, vec, freqs, mask=None):
-    # SingleStreamBlock.forward (mmdit.py:310-319) with both modulated norms and their codes from one pass
+    # SingleStreamBlock.forward (mmdit.py:310-319) with both modulated norms and their codes from one pass.  The
+    # fused norm differentiates its input only, so a block whose norm scales or modulation train runs the block
+    # class's own forward (its quantized linears still run on the library's kernels).
+    if _block_norms_train(self, vec):
+        return type(self).forward(self, x, vec, freqs, mask)
     prescale, preshift, pregate, postscale, postshift, postgate = self.mod(vec)
     x = x + pregate * self.attn(modulated_rmsnorm(self.prenorm, x, prescale, preshift), freqs, mask)
     x = x + postgate * self.mlp(modulated_rmsnorm(self.postnorm, x, postscale, postshift))
@@ -164,8 +178,10 @@ def fuse_producers(dit) -> int:
     """Patch the blocks of ``dit.blocks`` in place so their quantized linears' inputs come from the fused
     producers: a block with ``mod / prenorm / postnorm / attn / mlp`` (``SingleStreamBlock``,
     ``mmdit.py:294-319``) whose attention and MLP input linears are ConvRot gets the fused modulated RMSNorm;
-    an MLP with ``gate / up / down`` (``SwiGLU``) whose ``down`` is ConvRot gets the fused product.  Call after
-    ``quantize_dit_convrot`` and ``inject_lora``.  Returns the number of forwards patched."""
+    an MLP with ``gate / up / down`` (``SwiGLU``) whose ``down`` is ConvRot gets the fused product.  A patched
+    block whose norm scales or modulation need gradients when it runs (a full fine-tune rather than LoRA
+    training) runs its class's own forward for that call.  Call after ``quantize_dit_convrot`` and
+    ``inject_lora``.  Returns the number of forwards patched."""
     n = 0
     for blk in dit.blocks:
         mlp = getattr(blk, "mlp", None)

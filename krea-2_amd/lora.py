@@ -8,9 +8,15 @@ Interface kept from the reference (callers and saved files depend on it):
   ``base(x) + (scale * scale_mul) * ((x.f32 @ A^T) @ B^T)`` of ``lora.py:43-48``; ``scale_mul == 0`` returns
   exactly ``base(x)``.
 * ``lora_scaled`` / ``lora_disabled`` (``lora.py:51-70``), ``inject_lora`` with the duck-typed base test
-  (``lora.py:81-116``), ``lora_parameters`` (``:119-123``), ``save_lora`` / ``load_lora_weights`` /
+  (``lora.py:81-116``), ``lora_parameters`` (``:119-123``), ``QWEN_TE_TARGETS`` / ``inject_lora_te`` for the
+  text encoder's language-model projections (``:126-151``), ``save_lora`` / ``load_lora_weights`` /
   ``load_lora`` with the key format ``<prefix>.<module path>.lora_{A,B}.weight`` and metadata
   ``{format: krea2-lora, rank, alpha}`` (``:154-222``).
+
+Every name the reference's trainers import from ``lora`` is here (``train_t2i_lora_cached.py:22``,
+``train_slider.py:28``, ``sample.py:23``), and a trainer must import all of them from this module together:
+``lora_scaled`` / ``lora_disabled`` find adapters by ``isinstance`` against this module's :class:`LoRALinear`,
+so the reference's own context managers do not see adapters injected here (and the reverse).
 
 Over a :class:`~.quantize.ConvRotLinear` or :class:`~.quantize.Fp8Linear` base every rank runs on the library's
 kernels: the down-projection on bf16 MFMA, the up-projection in the GEMM epilogue, the backward in the LoRA
@@ -23,7 +29,8 @@ from __future__ import annotations
 import contextlib
 import math
 import os
-import tempfile
+import stat
+import uuid
 from dataclasses import dataclass
 
 import torch
@@ -180,6 +187,42 @@ def lora_parameters(adapters: dict) -> list:
     return [p for m in adapters.values() for p in (m.lora_A, m.lora_B)]
 
 
+# the language-model projections of the Qwen3-VL text encoder that TE-LoRA adapts (reference ``lora.py:127``)
+QWEN_TE_TARGETS = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+# path components that mark the encoder's vision tower, which TE-LoRA leaves unadapted
+_VISION_MARKS = ("visual", "vision")
+
+
+def inject_lora_te(qwen: nn.Module, rank: int, alpha: float | None = None, *, targets=QWEN_TE_TARGETS) -> dict:
+    """Freeze the text encoder ``qwen`` and put a :class:`LoRALinear` around every ``nn.Linear`` whose own name
+    (the last path component) is one of ``targets``, skipping any whose path mentions the vision tower
+    (reference ``lora.py:130-151``).  Matching by leaf name keeps it independent of how a transformers version
+    nests the decoder layers.  The encoder's linears are plain bf16 ``nn.Linear`` (it is never quantized), so
+    these adapters compute the reference's own torch expression.  Returns ``{module path: adapter}``; raises
+    ``RuntimeError`` when nothing matched.  ``alpha`` defaults to ``rank`` (scale 1)."""
+    alpha = float(rank) if alpha is None else alpha
+    wanted = frozenset(targets)
+    qwen.requires_grad_(False)
+    sites = []
+    for path, mod in qwen.named_modules():
+        owner_path, _, attr = path.rpartition(".")
+        if not isinstance(mod, nn.Linear) or attr not in wanted:
+            continue
+        if any(mark in path for mark in _VISION_MARKS):
+            continue
+        sites.append(_Site(path, qwen.get_submodule(owner_path) if owner_path else qwen, attr, mod))
+    if not sites:
+        raise RuntimeError(f"inject_lora_te: no nn.Linear of {type(qwen).__name__} is named one of {tuple(targets)} "
+                           f"outside the vision tower")
+    adapters = {}
+    for site in sites:
+        adapter = LoRALinear(site.base, rank, alpha)
+        setattr(site.owner, site.attr, adapter)
+        adapters[site.name] = adapter
+    return adapters
+
+
 def _key(prefix: str, name: str, which: str) -> str:
     return f"{prefix}.{name}.lora_{which}.weight"
 
@@ -187,18 +230,25 @@ def _key(prefix: str, name: str, which: str) -> str:
 def save_lora(adapters: dict, path: str, *, rank: int, alpha: float, metadata: dict | None = None,
               key_prefix: str = "diffusion_model") -> None:
     """Write the adapters to ``path`` as safetensors: bf16 ``lora_A`` / ``lora_B`` per adapter under
-    ``<key_prefix>.<name>.lora_{A,B}.weight``, metadata ``format / rank / alpha`` plus ``metadata``.  The file
-    appears atomically (written next to ``path``, then renamed)."""
+    ``<key_prefix>.<name>.lora_{A,B}.weight``, metadata ``format / rank / alpha`` plus ``metadata``.
+    ``key_prefix`` is ``diffusion_model`` for DiT adapters and ``text_encoder`` for TE-LoRA.  The file appears
+    atomically (written next to ``path``, then renamed), with the permissions a plainly created file gets (the
+    process umask applied to 0o666; safetensors alone would leave it readable by its owner only)."""
     from safetensors.torch import save_file
 
     tensors = {_key(key_prefix, name, w): t.detach().to(torch.bfloat16).cpu().contiguous()
                for name, m in adapters.items() for w, t in (("A", m.lora_A), ("B", m.lora_B))}
     meta = {"format": _LORA_FORMAT, "rank": str(rank), "alpha": str(alpha)}
     meta.update({k: str(v) for k, v in (metadata or {}).items()})
-    fd, tmp = tempfile.mkstemp(prefix=os.path.basename(path) + ".", dir=os.path.dirname(os.path.abspath(path)))
-    os.close(fd)
+    # a fresh name beside the target, created the way open() creates files (0o666 less the umask); safetensors
+    # writes its files owner-only, so that mode is put back before the rename and the result is as readable as a
+    # plainly created file
+    tmp = f"{os.path.abspath(path)}.{os.getpid()}.{uuid.uuid4().hex[:12]}.tmp"
+    os.close(os.open(tmp, os.O_WRONLY | os.O_CREAT | os.O_EXCL, 0o666))
     try:
+        mode = stat.S_IMODE(os.stat(tmp).st_mode)
         save_file(tensors, tmp, metadata=meta)
+        os.chmod(tmp, mode)
         os.replace(tmp, path)
     except BaseException:
         if os.path.exists(tmp):

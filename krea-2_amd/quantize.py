@@ -137,8 +137,8 @@ class ConvRotLinear(nn.Module):
         if mode not in MODES:
             raise ValueError(f"mode must be one of {MODES}, got {mode!r}")
         self.mode = mode
-        self.keep_dx_weight = True   # keep the backward's effective weight resident (see dx_weight)
-        self.register_parameter("dx_weight_t", None)
+        self.keep_dx_weight = False   # build the backward's effective weight per call (see dx_weight)
+        self._dx_kept = None          # (source key, effective weight) while the cache is on: not a parameter
         if lin is None:  # filled by from_quantized
             return
         w = lin.weight.data
@@ -198,42 +198,38 @@ class ConvRotLinear(nn.Module):
     def dx_weight(self) -> torch.Tensor:
         """The effective weight ``bf16(2^-7 W_hat R)^T`` (K x N bf16) that the input-gradient GEMM reads.
 
-        With ``keep_dx_weight`` on (the default) it is built at the first backward and kept as the frozen
-        parameter ``dx_weight_t`` (2 bytes per weight: 24 GB for the 12.2e9 block weights, beside 12 GB of
-        codes, on a 288 GB GPU): the base is frozen for the whole LoRA run, so one pass per layer replaces a
-        pass per backward.  Being a ``requires_grad=False`` parameter, it pages with the codes under block
-        swap (``mmdit.py:409-414`` moves every such parameter).  It is rebuilt when the codes or scales change
-        in place (their version counters) or move to another device, and is left out of ``state_dict`` (it is
-        derived data); an edit through ``.data`` bumps no version, so turn the cache off and on after one.  Off
-        (:func:`set_dx_weight_cache`), every backward builds it and lets it go."""
+        By default every backward builds it (one pass over the codes: 1 byte read and 2 written per weight) and
+        lets it go, so the layer holds only its codes and scales: 1 byte per weight resident and paged by block
+        swap, as the reference's fp8 base (``quantize.py:8-11``; ``mmdit.py:409-414``).
+
+        With ``keep_dx_weight`` on (:func:`set_dx_weight_cache`) it is built at the first backward and kept,
+        trading 2 bytes per weight of HBM (24 GB for Krea 2's 12.2e9 block weights) for that pass.  The kept
+        weight is a plain attribute, not a parameter: block swap does not page it and ``state_dict`` does not
+        hold it.  It belongs to the codes' current storage (pointer, version, device), so a layer whose codes
+        were paged out or re-pointed rebuilds it on its next backward, and every build first releases the
+        weights kept for layers whose codes have left the device they were built on (a block paged out by
+        block swap keeps nothing resident past the next backward of any layer).  An edit through ``.data``
+        that keeps the pointer bumps no version: turn the cache off and on after one."""
         q, s = self.qweight, self.wscale
         if not getattr(self, "keep_dx_weight", False):
-            self.dx_weight_t = None
+            self._dx_kept = None
             return _lib.dx_weight(q, self.weight_scale, w4=self.mode == "w4a8")
-        src = (q._version, s._version, q.device, tuple(q.shape))
-        wt = self.dx_weight_t
-        if wt is None or getattr(self, "_dx_src", None) != src or wt.device != q.device:
-            self.dx_weight_t = None
-            self.dx_weight_t = nn.Parameter(_lib.dx_weight(q, self.weight_scale, w4=self.mode == "w4a8"),
-                                            requires_grad=False)
-            self._dx_src = src
-        return self.dx_weight_t
+        key = _dx_key(self)
+        kept = self._dx_kept
+        if kept is not None and kept[0] == key:
+            return kept[1]
+        self._dx_kept = None
+        _release_stale_dx_weights()
+        wt = _lib.dx_weight(q, self.weight_scale, w4=self.mode == "w4a8")
+        self._dx_kept = (key, wt)
+        _dx_holders.add(self)
+        return wt
 
-    def _save_to_state_dict(self, destination, prefix, keep_vars):
-        wt = self._parameters.pop("dx_weight_t", None)
-        try:
-            super()._save_to_state_dict(destination, prefix, keep_vars)
-        finally:
-            self.register_parameter("dx_weight_t", wt)
-
-    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
-                              error_msgs):
-        self._parameters.pop("dx_weight_t", None)      # derived from the codes being loaded: rebuilt on use
-        try:
-            super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys,
-                                          unexpected_keys, error_msgs)
-        finally:
-            self.register_parameter("dx_weight_t", None)
+    @property
+    def dx_weight_kept(self) -> torch.Tensor | None:
+        """The effective weight this layer keeps resident now, or None (cache off, or nothing built yet)."""
+        kept = self.__dict__.get("_dx_kept")
+        return None if kept is None else kept[1]
 
     @property
     def weight_scale(self) -> torch.Tensor:
@@ -306,17 +302,37 @@ def quantize_dit_convrot(dit, mode: str = "w8a8") -> int:
     return len(targets)
 
 
+# layers holding a kept effective weight (weak: a dropped layer takes its weight with it)
+_dx_holders: "weakref.WeakSet[ConvRotLinear]" = weakref.WeakSet()
+
+
+def _dx_key(m: "ConvRotLinear"):
+    """What a kept effective weight was built from: the codes' and scales' storage, versions and device."""
+    q, s = m.qweight, m.wscale
+    return (q.data_ptr(), q._version, s.data_ptr(), s._version, q.device, tuple(q.shape))
+
+
+def _release_stale_dx_weights() -> None:
+    """Drop the effective weights kept for layers whose codes no longer sit where the weight was built (paged
+    to the host by block swap, re-pointed, moved to another device, or rewritten in place)."""
+    for m in list(_dx_holders):
+        kept = m.__dict__.get("_dx_kept")
+        if kept is None or kept[0] != _dx_key(m):
+            m._dx_kept = None
+            _dx_holders.discard(m)
+
+
 def set_dx_weight_cache(model: nn.Module, enable: bool = True) -> int:
-    """Keep (default) or drop the resident input-gradient weight of every :class:`ConvRotLinear` in ``model``
-    (:meth:`ConvRotLinear.dx_weight`).  Off frees the kept weights and makes every backward build its own:
-    1 byte per weight of HBM instead of 3, for one extra weight pass per backward.  Returns the number of
-    layers set."""
+    """Keep or drop (the default) the resident input-gradient weight of every :class:`ConvRotLinear` in
+    ``model`` (:meth:`ConvRotLinear.dx_weight`).  On keeps 2 more bytes per weight of HBM beside the 1-byte codes
+    and saves one weight pass per backward; off frees the kept weights.  Returns the number of layers set."""
     n = 0
     for m in model.modules():
         if isinstance(m, ConvRotLinear):
             m.keep_dx_weight = bool(enable)
             if not enable:
-                m.dx_weight_t = None
+                m._dx_kept = None
+                _dx_holders.discard(m)
             n += 1
     return n
 

@@ -484,51 +484,67 @@ def test_module_backward_matches_oracle(k2, dev, mode):
 
 
 @pytest.mark.parametrize("mode", ["w8a8", "w4a8"])
-def test_dx_weight_resident(k2, dev, mode):
-    """The input-gradient weight is kept after the first backward (the default) as a frozen parameter that
-    ``state_dict`` leaves out; it is reused, pages with the codes as block swap moves every frozen parameter
-    (``mmdit.py:409-414``), is rebuilt after an in-place change of the codes, and is dropped by
-    ``set_dx_weight_cache(False)``.  dX and the LoRA grads are bit-identical in every case."""
+def test_dx_weight_cache_and_block_swap(k2, dev, mode):
+    """By default every backward builds the input-gradient weight and lets it go, so a ConvRot layer's
+    parameters, which block swap pages (``mmdit.py:409-414``), are its codes, scales and bias only: 1 byte per
+    weight resident and paged, as the reference's fp8 base.  With the cache on the weight is kept as a plain
+    attribute (not a parameter, not in ``state_dict``), reused, rebuilt after the codes are paged out and back
+    or written in place, and released when any later backward finds its layer's codes gone from the device.
+    dX and the LoRA grads are bit-identical in every case."""
     _, base, lora = _layers(k2, dev, K=512, N=256, r=16, mode=mode)
+    _, other_base, other = _layers(k2, dev, K=512, N=256, r=16, mode=mode, seed=9)
     x = make_x(160, 512, seed=21).to(dev)
     dy = (torch.randn(160, 256, generator=torch.Generator().manual_seed(5)) * 1e-3).to(torch.bfloat16).to(dev)
 
-    def grads():
-        lora.lora_A.grad = lora.lora_B.grad = None
+    def grads(layer=lora):
+        layer.lora_A.grad = layer.lora_B.grad = None
         xr = x.clone().requires_grad_(True)
-        lora(xr).backward(dy)
-        return xr.grad.clone(), lora.lora_A.grad.clone(), lora.lora_B.grad.clone()
+        layer(xr).backward(dy)
+        return xr.grad.clone(), layer.lora_A.grad.clone(), layer.lora_B.grad.clone()
 
-    assert k2.set_dx_weight_cache(lora, False) == 1
+    paged = {"qweight", "wscale"} | ({"bias"} if base.bias is not None else set())
+    assert base.keep_dx_weight is False                            # the default
     ref = grads()
-    assert base.dx_weight_t is None
-    k2.set_dx_weight_cache(lora, True)
+    assert base.dx_weight_kept is None
+    assert {n for n, _ in base.named_parameters()} == paged
+
+    def swap(layer, device):                                       # mmdit.py:409-414, skip_trainable=True
+        for p in layer.parameters():
+            if not p.requires_grad:
+                p.data = p.data.to(device, non_blocking=True)
+
+    swap(lora, "cpu")                                              # default: block swap moves codes + scales only
+    assert all(p.device.type == "cpu" for p in base.parameters())
+    swap(lora, dev)
+    assert all(torch.equal(a, b) for a, b in zip(grads(), ref))
+
+    assert k2.set_dx_weight_cache(lora, True) == 1
     first = grads()
-    w1 = base.dx_weight_t
-    assert isinstance(w1, torch.nn.Parameter) and not w1.requires_grad and w1.shape == (512, 256)
-    assert "dx_weight_t" in dict(base.named_parameters())
-    assert not any(k.endswith("dx_weight_t") for k in lora.state_dict())
+    w1 = base.dx_weight_kept
+    assert w1 is not None and not isinstance(w1, torch.nn.Parameter) and w1.shape == (512, 256)
+    assert {n for n, _ in base.named_parameters()} == paged        # still only codes, scales, bias
+    assert not any("dx" in k for k in lora.state_dict())
     second = grads()
-    assert base.dx_weight_t is w1                                  # reused
-    frozen = [p for p in lora.parameters() if not p.requires_grad]
-    for p in frozen:                                               # block swap: page out ...
-        p.data = p.data.to("cpu")
-    assert base.dx_weight_t.device.type == "cpu"
-    for p in frozen:                                               # ... and back in
-        p.data = p.data.to(dev)
+    assert base.dx_weight_kept is w1                               # reused
+    swap(lora, "cpu")                                              # paged out: the kept weight stays behind ...
+    assert base.dx_weight_kept is w1 and w1.device.type == "cuda"
+    k2.set_dx_weight_cache(other, True)
+    grads(other)                                                   # ... until any layer's next backward
+    assert base.dx_weight_kept is None and other_base.dx_weight_kept is not None
+    swap(lora, dev)
     third = grads()
-    assert base.dx_weight_t is w1
+    w3 = base.dx_weight_kept
+    assert w3 is not None and w3 is not w1 and torch.equal(w3, w1)
     with torch.no_grad():
         base.qweight.copy_(base.qweight.clone())                   # an in-place write (same values)
     fourth = grads()
-    assert base.dx_weight_t is not w1 and torch.equal(base.dx_weight_t, w1)
+    assert base.dx_weight_kept is not w3 and torch.equal(base.dx_weight_kept, w1)
     for got in (first, second, third, fourth):
         assert all(torch.equal(a, b) for a, b in zip(got, ref))
-    lora.load_state_dict(lora.state_dict())                        # strict load without the derived weight
-    assert base.dx_weight_t is None
+    lora.load_state_dict(lora.state_dict())                        # strict load: no derived weight in it
     assert all(torch.equal(a, b) for a, b in zip(grads(), ref))
     k2.set_dx_weight_cache(lora, False)
-    assert base.dx_weight_t is None
+    assert base.dx_weight_kept is None
 
 
 def test_deterministic_and_checkpoint_recompute(k2, dev):

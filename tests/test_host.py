@@ -290,6 +290,102 @@ def test_save_load_lora_roundtrip(k2, tmp_path):
         assert torch.equal(ad2[n].lora_B, m.lora_B.detach().to(torch.bfloat16).float())
 
 
+def test_trainer_import_lines_resolve_from_the_package(k2):
+    """Every name the reference's trainers and samplers import from ``lora`` (``train_t2i_lora_cached.py:22``,
+    ``train_slider.py:28``, ``sample.py:23``, ``eval_t2i.py:27``) comes from the package, so the whole import line
+    switches at once."""
+    lines = {
+        "train_t2i_lora_cached.py:22": "inject_lora, inject_lora_te, load_lora_weights, lora_parameters, save_lora",
+        "train_slider.py:28": "inject_lora, lora_parameters, lora_scaled, lora_disabled, save_lora",
+        "sample.py:23": "load_lora, lora_scaled",
+    }
+    for where, names in lines.items():
+        ns = {}
+        exec(f"from krea2_amd import {names}", ns)
+        assert all(callable(ns[n.strip()]) for n in names.split(",")), where
+    assert k2.QWEN_TE_TARGETS == ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+
+class _QwenLayer(nn.Module):
+    """A decoder layer with the Qwen3 projection names (what ``inject_lora_te`` matches by leaf name)."""
+
+    def __init__(self, d=32, h=64):
+        super().__init__()
+        self.self_attn = nn.Module()
+        for n in ("q_proj", "k_proj", "v_proj", "o_proj"):
+            setattr(self.self_attn, n, nn.Linear(d, d, bias=False))
+        self.mlp = nn.Module()
+        self.mlp.gate_proj = nn.Linear(d, h, bias=False)
+        self.mlp.up_proj = nn.Linear(d, h, bias=False)
+        self.mlp.down_proj = nn.Linear(h, d, bias=False)
+        self.mlp.act = nn.SiLU()
+
+
+class _ToyQwen(nn.Module):
+    """Language model plus a vision tower that reuses the same projection names (which must stay unadapted)."""
+
+    def __init__(self):
+        super().__init__()
+        self.model = nn.Module()
+        self.model.language_model = nn.Module()
+        self.model.language_model.layers = nn.ModuleList(_QwenLayer() for _ in range(2))
+        self.model.language_model.embed_tokens = nn.Embedding(10, 32)
+        self.model.visual = nn.Module()
+        self.model.visual.blocks = nn.ModuleList(_QwenLayer() for _ in range(1))
+        self.lm_head = nn.Linear(32, 10, bias=False)
+
+
+def test_inject_lora_te_wraps_language_projections_and_skips_vision(k2):
+    torch.manual_seed(0)
+    qwen = _ToyQwen()
+    x = torch.randn(3, 32)
+    before = qwen.model.language_model.layers[0].mlp.down_proj(qwen.model.language_model.layers[0].mlp.up_proj(x))
+    adapters = k2.inject_lora_te(qwen, 4)
+    leaves = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj", "mlp.gate_proj",
+              "mlp.up_proj", "mlp.down_proj")
+    assert set(adapters) == {f"model.language_model.layers.{i}.{leaf}" for i in range(2) for leaf in leaves}
+    for path, m in adapters.items():
+        assert isinstance(m, k2.LoRALinear) and qwen.get_submodule(path) is m
+        assert m.rank == 4 and m.scale == 1.0 and m.lora_A.dtype == torch.float32 and not m.lora_B.any()
+    # the vision tower and the head are left as they were; every base parameter is frozen
+    vis = qwen.model.visual.blocks[0]
+    assert all(type(getattr(vis.self_attn, n)) is nn.Linear for n in ("q_proj", "k_proj", "v_proj", "o_proj"))
+    assert type(vis.mlp.down_proj) is nn.Linear and type(qwen.lm_head) is nn.Linear
+    assert not any(p.requires_grad for n, p in qwen.named_parameters() if "lora_" not in n)
+    assert all(p.requires_grad for p in k2.lora_parameters(adapters))
+    # B = 0: the wrapped layers compute what the plain ones did; then the reference's expression
+    lay = qwen.model.language_model.layers[0].mlp
+    assert torch.equal(lay.down_proj(lay.up_proj(x)), before)
+    nn.init.normal_(lay.up_proj.lora_B)
+    want = lay.up_proj.base(x) + ((x @ lay.up_proj.lora_A.t()) @ lay.up_proj.lora_B.t())
+    torch.testing.assert_close(lay.up_proj(x), want, rtol=0, atol=0)
+    with k2.lora_disabled(qwen):
+        assert torch.equal(lay.up_proj(x), lay.up_proj.base(x))
+    # a custom alpha and target subset; no match at all raises
+    q2 = _ToyQwen()
+    ad2 = k2.inject_lora_te(q2, 8, alpha=4.0, targets=("q_proj",))
+    assert len(ad2) == 2 and all(m.scale == 0.5 for m in ad2.values())
+    with pytest.raises(RuntimeError):
+        k2.inject_lora_te(_ToyQwen(), 4, targets=("no_such_proj",))
+
+
+def test_save_lora_file_gets_the_default_permissions(k2, tmp_path):
+    """The adapter file is renamed into place with the mode a plainly created file gets (umask applied)."""
+    import os
+    import stat
+    dit = _Dit()
+    adapters = k2.inject_lora(dit, 16, include_txtfusion=False, include_txtmlp=False)
+    path = tmp_path / "a.safetensors"
+    k2.save_lora(adapters, str(path), rank=16, alpha=16.0, key_prefix="text_encoder")
+    plain = tmp_path / "plain"
+    plain.write_bytes(b"")
+    assert stat.S_IMODE(os.stat(path).st_mode) == stat.S_IMODE(os.stat(plain).st_mode)
+    assert sorted(p.name for p in tmp_path.iterdir()) == ["a.safetensors", "plain"]    # no temp file left
+    from safetensors import safe_open
+    with safe_open(str(path), "pt") as f:
+        assert "text_encoder.blocks.0.attn.wq.lora_A.weight" in f.keys()
+
+
 def test_walker_requires_gpu_and_says_so(k2):
     if torch.cuda.is_available():
         pytest.skip("GPU present")
@@ -455,6 +551,40 @@ def test_fusion_walkers_leave_unquantized_blocks_alone(k2):
         k2.modulated_rmsnorm(norm, x, sc[:2].requires_grad_(True), sc[:2])
     with torch.no_grad(), pytest.raises(RuntimeError):                   # no autograd: only the CPU refusal
         k2.modulated_rmsnorm(norm, x, sc[:2].requires_grad_(True), sc[:2])
+
+
+def test_fused_block_runs_its_own_forward_when_norms_train(k2):
+    """A block patched by fuse_producers computes the gradients of its input only through the fused norm; when its
+    norm scale or modulation needs a gradient it runs the block class's own forward instead (checked on the CPU,
+    with the block's linears swapped back to plain ones after patching: the class forward then runs entirely
+    here, while the fused forward would reach the library and refuse CPU tensors)."""
+    from tests import restated_block as rb
+    torch.manual_seed(0)
+    blk = rb.Block(feat=256, heads=2, kvheads=1, hid=512)
+    plain = {n: getattr(blk.attn, n) for n in ("wq",)} | {"gate": blk.mlp.gate}
+    blk.attn.wq = _cpu_quantized(N=256, K=256, bias=False)
+    blk.mlp.gate = _cpu_quantized(N=512, K=256, bias=False)
+    blk.mlp.down = _cpu_quantized(N=256, K=512, bias=False)
+    dit = nn.Module()
+    dit.blocks = nn.ModuleList([blk])
+    assert k2.fuse_producers(dit) == 2 and "forward" in vars(blk)
+    blk.attn.wq, blk.mlp.gate = plain["wq"], plain["gate"]
+    blk.mlp.down = nn.Linear(512, 256, bias=False)
+    del blk.mlp.forward                       # the SwiGLU patch is not under test here
+    blk.requires_grad_(False)
+    x = torch.randn(2, 8, 256)
+    vec = torch.randn(2, 1, 6 * 256) * 0.1
+    blk.prenorm.scale.requires_grad_(True)
+    y = blk(x, vec, None)
+    torch.testing.assert_close(y, rb.Block.forward(blk, x, vec, None), rtol=0, atol=0)
+    y.sum().backward()
+    assert blk.prenorm.scale.grad is not None and blk.prenorm.scale.grad.abs().sum() > 0
+    blk.prenorm.scale.requires_grad_(False)
+    blk.mod.lin.requires_grad_(True)          # the modulation trains: the class forward again
+    torch.testing.assert_close(blk(x, vec, None), rb.Block.forward(blk, x, vec, None), rtol=0, atol=0)
+    blk.mod.lin.requires_grad_(False)
+    with pytest.raises(RuntimeError):         # frozen norms: the fused path, which refuses CPU tensors
+        blk(x.bfloat16(), vec.bfloat16(), None)
 
 
 def test_grouped_wrapper_validates_before_launch(k2):
