@@ -277,11 +277,17 @@ def run_config(k2, cfg, steps, warmup, dev, settle_s=0.0):
 
     # Per-kernel breakdown over K more steps: the same three launches issued one by one, events between them
     # on that stream, so the GEMM's average launch duration comes from timed steps.
+    fused_down = L.linear_fwd_fuses_down(M, K, r)
+
     def step_events(ev):
         ev[0].record()
-        q_, s_, _ = L.rotquant(xd)
-        ev[1].record()
-        u = L.lora_down(xd, Ad)
+        if fused_down:     # the one-call forward's route: u from the rotate/quant pass
+            q_, s_, u = L.rotquant_lora(xd, Ad)
+            ev[1].record()
+        else:
+            q_, s_, _ = L.rotquant(xd)
+            ev[1].record()
+            u = L.lora_down(xd, Ad)
         ev[2].record()
         gemm(q_, s_, qw, sw, bd, u, Bd, 1.0)
         ev[3].record()
@@ -316,7 +322,7 @@ def run_config(k2, cfg, steps, warmup, dev, settle_s=0.0):
     ops = 2.0 * M * N * K
     rot_bytes = 2 * M * K + M * K + 4 * M
     return dict(ms_step=ms_step, wall=wall, host_us=host_us, ms_rot=ms_rot, ms_rot_stream=ms_rot_stream,
-                ms_lora=ms_lora, ms_gemm=ms_gemm, ops=ops,
+                ms_lora=ms_lora, ms_gemm=ms_gemm, ops=ops, fused_down=fused_down,
                 rot_bytes=rot_bytes, tops=ops / (ms_step * 1e-3) / 1e12, x=x, W=W, b=b, A=A, B=B)
 
 
@@ -641,6 +647,7 @@ def run_vram(k2, dev):
     x0 = torch.randn(1, M, D, generator=xg).to(torch.bfloat16)
     dy0 = (torch.randn(1, M, D, generator=xg) * 1e-2).to(torch.bfloat16)
     for kind in ("bf16", "fp8", "convrot_w8a8", "convrot_w8a8_kept"):
+        k2.quantize.shared_input_quant.clear()     # codes kept from an earlier leg would leave the baseline
         gc.collect()
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
@@ -1133,6 +1140,7 @@ def forward_record(cfg, res, cpu=None, cpu_ref=None):
            "host_us_per_step": round(res["host_us"], 1),
            "gemm_ms": round(res["ms_gemm"], 4), "lora_down_ms": round(res["ms_lora"], 4),
            "rotquant_ms_in_step": round(res["ms_rot"], 4),
+           "lora_down_in_rotquant_pass": bool(res["fused_down"]),
            "roofline": roofline_entry("gemm_w4_kernel" if cfg["w4"] else "gemm_nt_kernel<EPI_W8>", "mfma", gemm_tops,
                                       INT8_PEAK_TOPS, "TOPS"),
            "rotquant_roofline": roofline_entry("rotquant_kernel (4 inputs streamed from HBM)", "hbm", rot_gbs,

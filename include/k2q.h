@@ -55,6 +55,15 @@ int k2q_check_device(void);
 int k2q_rotquant(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                  int8_t* q, float* s, uint16_t* x_rot, void* stream);
 
+/* (1) + the LoRA down-projection from the same pass over x: the codes and scales of k2q_rotquant (bf16 x,
+ * bit-identical) and u = x lora_a^T (lora_a r x K f32; u M rows of stride ldu f32, ranks 0 .. r-1), the first
+ * product of LoRALinear.forward (reference lora.py:47) computed where Fp8Linear.forward receives x
+ * (quantize.py:48).  One row per wave: K <= 3072 and K % 512 == 0, r in {16, 32, 48, 64}; other shapes return
+ * K2Q_EUNSUPPORTED (k2q_lora_down then computes u in its own launch).  u is f32-accurate (A split into bf16
+ * hi + lo on bf16 MFMA) in a fixed summation order, not bit-identical to k2q_lora_down's. */
+int k2q_rotquant_lora(const void* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, float* s,
+                      const float* lora_a, int64_t r, float* u, int64_t ldu, void* stream);
+
 /* int4 group-64 weight quantizer of W R (counterpart of Fp8Linear.__init__, quantize.py:34-39). */
 int k2q_quant_weight_i4(const void* w, int w_dtype, int64_t N, int64_t K,
                         uint8_t* qw4, uint16_t* sw4, void* stream);
@@ -177,10 +186,16 @@ int k2q_gemm_w8a8_grouped(const int8_t* qx, const float* sx, int64_t M, int64_t 
  * u may be NULL when nothing needs the factors afterwards (inference) and M > 8: then, for W8 and r <= 128,
  * the GEMM epilogue adds the down-projection's K-slice partials itself (no reduce launch; y is bit-identical).
  * M <= 8: one launch computes the codes and u, then the GEMV (two launches for the linear; u required).
+ * Where k2q_linear_fwd_fuses_down(M, K, r) is 1 (codes not given, K <= 3072, a CU's worth or two of 16-row
+ * tiles), the codes and u come from one k2q_rotquant_lora launch instead of k2q_rotquant + k2q_lora_down (u then
+ * carries that kernel's summation order).
  * ws: k2q_linear_fwd_ws_bytes bytes (256-byte aligned): factors, their partials and the GEMM's split pieces. */
 #define K2Q_WMODE_W8 0
 #define K2Q_WMODE_W4 1
 int64_t k2q_linear_fwd_ws_bytes(int wmode, int64_t M, int64_t N, int64_t K, int64_t r);
+/* Host only: 1 when k2q_linear_fwd with LoRA factors and codes not given computes u in the rotate/quant pass
+ * (k2q_rotquant_lora), else 0 (no reference counterpart; lets callers and tests reproduce its launches). */
+int k2q_linear_fwd_fuses_down(int64_t M, int64_t K, int64_t r);
 int k2q_linear_fwd(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, int8_t* qx, float* sx, int codes_ready,
                    const float* lora_a, const float* lora_b, int64_t r, float lora_scale, float* u, int wmode,
                    const void* qw, const void* sw, const float* bias, int64_t N, uint16_t* y, void* ws,

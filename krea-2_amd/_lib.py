@@ -58,6 +58,7 @@ _SIGNATURES = {
     "k2q_version": ([], ctypes.c_char_p),
     "k2q_check_device": ([], _int),
     "k2q_rotquant": ([_p, _int, _i64, _i64, _i64, _p, _p, _p, _p], _int),
+    "k2q_rotquant_lora": ([_p, _i64, _i64, _i64, _p, _p, _p, _i64, _p, _i64, _p], _int),
     "k2q_quant_weight_i4": ([_p, _int, _i64, _i64, _p, _p, _p], _int),
     "k2q_swiglu_rotquant": ([_p, _i64, _p, _i64, _i64, _i64, _p, _p, _p, _p], _int),
     "k2q_rmsmod_rotquant": ([_p, _i64, _i64, _i64, _p, _f32, _p, _p, _i64, _i64, _p, _p, _p, _p], _int),
@@ -75,6 +76,7 @@ _SIGNATURES = {
     "k2q_gemm_w8a8_grouped": ([_p, _p, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _i64, _p], _int),
     "k2q_gemm_w4a8": ([_p, _p, _p, _p, _p, _p, _p, _i64, _f32, _i64, _i64, _i64, _p, _p], _int),
     "k2q_linear_fwd_ws_bytes": ([_int, _i64, _i64, _i64, _i64], _i64),
+    "k2q_linear_fwd_fuses_down": ([_i64, _i64, _i64], _int),
     "k2q_linear_fwd": ([_p, _i64, _i64, _i64, _p, _p, _int, _p, _p, _i64, _f32, _p, _int, _p, _p, _p, _i64, _p, _p,
                         _i64, _p], _int),
     "k2q_gemm_w8a8_acc": ([_p, _p, _i64, _i64, _i64, _p, _p, _i64, _int, _p], _int),
@@ -201,6 +203,35 @@ def rotquant(x: torch.Tensor, want_xrot: bool = False):
     _check(load().k2q_rotquant(_ptr(x), dt, M, K, K, _ptr(q), _ptr(s), _ptr(xr), _stream(x.device)),
            "k2q_rotquant")
     return q, s, xr
+
+
+def rotquant_lora_fits(K: int, r: int) -> bool:
+    """Whether :func:`rotquant_lora` takes the shape (one row per wave: K <= 3072, K % 512 == 0; r 16-64)."""
+    return 512 <= K <= 3072 and K % 512 == 0 and r in (16, 32, 48, 64) and 16 * (r // 16) * 1024 <= 16 * (K + 8) * 2
+
+
+def rotquant_lora(x: torch.Tensor, A: torch.Tensor):
+    """Rotate/quant of ``x`` (M,K) bf16 with the LoRA down-projection ``u = x A^T`` from the same pass
+    (``k2q_rotquant_lora``; ``A`` (r,K) f32).  Returns ``(q int8 (M,K), s f32 (M,), u f32 (M,r))``; the codes
+    equal :func:`rotquant`'s bit for bit."""
+    _need(x, "x", torch.bfloat16, 2)
+    M, K = x.shape
+    _check_k(K)
+    if M < 1:
+        raise ValueError("x has no rows")
+    _need(A, "lora_a", torch.float32, 2, x.device)
+    r = A.shape[0]
+    if A.shape[1] != K:
+        raise ValueError(f"lora_a {tuple(A.shape)} does not match K={K}")
+    if not rotquant_lora_fits(K, r):
+        raise ValueError(f"rotquant_lora takes K <= 3072 with K % 512 == 0 and r in 16..64 by 16, got K={K} r={r}")
+    _device_check(x.device)
+    q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    s = torch.empty((M,), dtype=torch.float32, device=x.device)
+    u = torch.empty((M, r), dtype=torch.float32, device=x.device)
+    _check(load().k2q_rotquant_lora(_ptr(x), M, K, K, _ptr(q), _ptr(s), _ptr(A), r, _ptr(u), r, _stream(x.device)),
+           "k2q_rotquant_lora")
+    return q, s, u
 
 
 def _need_rows(t: torch.Tensor, name: str, dev: torch.device | None = None) -> None:
@@ -575,6 +606,11 @@ def gemm_w8a8(qx, sx, qw, sw, bias=None, u=None, lora_b=None, lora_scale: float 
 
 
 WMODE_W8, WMODE_W4 = 0, 1
+
+
+def linear_fwd_fuses_down(M: int, K: int, r: int) -> bool:
+    """Whether :func:`linear_fwd` (codes not given, rank ``r`` factors) takes u from the rotate/quant pass."""
+    return bool(load().k2q_linear_fwd_fuses_down(M, K, r))
 
 
 def linear_fwd(x2, qx, sx, codes_ready: bool, A, B, lora_scale: float, qw, sw, bias, w4: bool,

@@ -90,3 +90,9 @@ static inline int k2q_aligned(const void* p, uintptr_t a) { return ((uintptr_t)p
 // Compute units of the current device (launch planning only; 256 on MI355X).  Looked up once per device and
 // cached (api.hip): the attribute query costs more host time than a kernel launch.
 int k2q_cu_count();
+
+// Rotate/quant with the LoRA down-projection from the same pass (rotquant.hip): the codes of k2q_rotquant and
+// u = x A^T (A: r x K f32) for K <= 4096, K % 512 == 0, r in {16, 32, 48, 64} (k2q_rotquant_lora_fits).
+int k2q_rotquant_lora_fits(int64_t K, int64_t r);
+int rotquant_lora_impl(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, float* s, const float* a,
+                       int64_t r, float* u, int64_t ldu, hipStream_t st);

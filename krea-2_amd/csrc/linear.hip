@@ -162,7 +162,23 @@ bool fold_pays(int64_t M, int64_t N, int64_t K, int64_t r) {
   return extra <= ((int64_t)16 << 20);
 }
 
+// Whether the forward takes u from the rotate/quant pass (rotquant_lora_kernel) instead of a separate
+// down-projection launch.  That kernel holds one 16-row tile per CU and streams A from L2 for every tile, so it
+// is latency-bound once a CU has several tiles.  Measured on MI355X (K = 3072, 4 rotating inputs, rotate/quant
+// + down-projection against the fused kernel): M = 1024 r = 16 24.7 -> 13.0 us, M = 4096 r = 16 25.5 -> 13.7,
+// M = 8192 r = 16 27.1 -> 25.1, M = 16896 r = 16 46.9 -> 59.4, M = 16896 r = 32 50.7 -> 78.9, M = 4608 r = 64
+// 27.6 -> 51.6.  So: at most one tile per CU for r <= 32, two for r = 16.
+bool fuse_down(int64_t M, int64_t K, int64_t r) {
+  if (r < 16 || r > 32 || !k2q_rotquant_lora_fits(K, r)) return false;
+  const int64_t tiles = (M + 15) / 16, cus = k2q_cu_count();
+  return tiles <= (r == 16 ? 2 * cus : cus);
+}
+
 }  // namespace
+
+extern "C" int k2q_linear_fwd_fuses_down(int64_t M, int64_t K, int64_t r) {
+  return M > K2Q_GEMV_MAX_M && fuse_down(M, K, r) ? 1 : 0;
+}
 
 extern "C" int64_t k2q_linear_fwd_ws_bytes(int wmode, int64_t M, int64_t N, int64_t K, int64_t r) {
   if (M < 1 || N < 1 || K < K2Q_HADAMARD || K % K2Q_HADAMARD) return 0;
@@ -196,6 +212,11 @@ extern "C" int k2q_linear_fwd(const uint16_t* x, int64_t ldx, int64_t M, int64_t
     if (lora_a || !codes_ready)
       rc = launch_skinny(x, ldx, M, K, lora_a, rr, u, codes_ready ? nullptr : qx, sx, st);
     uu = lora_a ? u : nullptr;
+  } else if (!codes_ready && lora_a && fuse_down(M, K, rr)) {
+    // u from the pass that rotates and quantizes x (one launch for both)
+    float* ut = u ? u : reinterpret_cast<float*>(w + lay.u_off);
+    rc = rotquant_lora_impl(x, M, K, ldx, qx, sx, lora_a, rr, ut, rr, st);
+    uu = ut;
   } else {
     if (!codes_ready) rc = k2q_rotquant(x, K2Q_DTYPE_BF16, M, K, ldx, qx, sx, nullptr, stream);
     if (!rc && lora_a) {

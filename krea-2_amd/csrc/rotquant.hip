@@ -127,6 +127,199 @@ __global__ __launch_bounds__(256) void rotquant_kernel(const Tin* __restrict__ x
   }
 }
 
+// ---------------------------------------------------------------------------------------------------------
+// Rotate/quant with the LoRA down-projection u = x A^T from the same pass over x (reference lora.py:47, the
+// first product; kernel (3)'s A.x term).  K <= 3072 (one row per wave), K % 512 == 0, r = 16 RT <= 64.
+//
+// A workgroup of 16 waves owns tiles of 16 rows (the row count of v_mfma_f32_16x16x32_bf16), one row per wave,
+// and walks its tiles persistently with the next tile's row in flight.  Each wave copies its raw bf16 row into
+// LDS (row stride K + 8: rows start 16 bytes apart in the banks), rotates and quantizes it in registers exactly
+// as rotquant_kernel does (the same codes, bit for bit), then the 16 waves split K into 16 column ranges and
+// multiply the tile's rows (from LDS) by A (f32 from L2, split in registers into bf16 hi + lo, as the
+// standalone down-projection does: ~2^-16 relative) on bf16 MFMA with f32 accumulation.  The 16 wave
+// partials meet in LDS and are added in wave order (deterministic).  A is read once per 16-row tile: 4 r K
+// bytes from L2 per 32 K bytes of x.
+// ---------------------------------------------------------------------------------------------------------
+constexpr int RQL_WAVES = 16;
+
+__device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// hi = bf16(v), lo = bf16(v - hi) for 8 consecutive k.
+__device__ __forceinline__ void split8_hilo(v4f p, v4f q, v8bf& hi, v8bf& lo) {
+  const v4u h = v4u{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(q[0], q[1]), pack_bf16x2(q[2], q[3])};
+  const v4u l = v4u{pack_bf16x2(p[0] - __uint_as_float(h[0] << 16), p[1] - __uint_as_float(h[0] & 0xffff0000u)),
+                    pack_bf16x2(p[2] - __uint_as_float(h[1] << 16), p[3] - __uint_as_float(h[1] & 0xffff0000u)),
+                    pack_bf16x2(q[0] - __uint_as_float(h[2] << 16), q[1] - __uint_as_float(h[2] & 0xffff0000u)),
+                    pack_bf16x2(q[2] - __uint_as_float(h[3] << 16), q[3] - __uint_as_float(h[3] & 0xffff0000u))};
+  hi = __builtin_bit_cast(v8bf, h);
+  lo = __builtin_bit_cast(v8bf, l);
+}
+
+template <int kNCH, int RT>
+__global__ __launch_bounds__(64 * RQL_WAVES) void rotquant_lora_kernel(const __bf16* __restrict__ x, int64_t M, int K,
+                                                                      int64_t ldx, int8_t* __restrict__ q,
+                                                                      float* __restrict__ s,
+                                                                      const float* __restrict__ a, int64_t ldu,
+                                                                      float* __restrict__ u) {
+  // Loads complete in issue order as far as the wave's vmcnt wait knows, so the next tile's row (HBM) is issued
+  // only after this tile's A fragments (L2): waiting for a fragment then never waits for the row.
+  constexpr int NB = RT == 1 ? 4 : RT == 2 ? 2 : 1;   // 32-wide steps per A batch (<= 32 VGPRs of fragments)
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs[];   // [16][K + 8] bf16 rows; the u partials
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int l = lane & 15;
+  const int off = lane_offset(lane);
+  const int ldl = K + 8;
+  const int64_t ntiles = (M + RQL_WAVES - 1) / RQL_WAVES;
+  const int kw = K / RQL_WAVES;        // this wave's columns of the u product (a multiple of 32)
+  const int nks = kw / 32;
+  const float c1 = (l & 1) ? -1.f : 1.f;
+  const float c2 = (l & 2) ? -1.f : 1.f;
+  const float c8 = (l & 8) ? -1.f : 1.f;
+  const float sigma = c1 * c2 * c8;
+  const int kb = w * kw + 8 * (lane >> 4);
+  const uint16_t* xl = xs + (lane & 15) * ldl + kb;
+  const float* al = a + (int64_t)(lane & 15) * K + kb;
+
+  uint4 raw[kNCH][2];
+  auto load_row = [&](int64_t tile) {
+    const int64_t row = tile * RQL_WAVES + w;
+    const bool ok = tile < ntiles && row < M;
+    const __bf16* xr = x + (ok ? row : 0) * ldx;
+#pragma unroll
+    for (int c = 0; c < kNCH; ++c) {
+      const int col = c * 1024 + off;
+      raw[c][0] = raw[c][1] = make_uint4(0, 0, 0, 0);
+      if (ok && col < K) {
+        raw[c][0] = *reinterpret_cast<const uint4*>(xr + col);
+        raw[c][1] = *reinterpret_cast<const uint4*>(xr + col + 8);
+      }
+    }
+  };
+
+  load_row(blockIdx.x);
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int64_t row = tile * RQL_WAVES + w;
+    const bool row_ok = row < M;
+    // the raw row into LDS (rows past M are zeros: their u is never stored), then to f32 registers
+    float v[kNCH][16];
+#pragma unroll
+    for (int c = 0; c < kNCH; ++c) {
+      const int col = c * 1024 + off;
+      if (col < K) {
+        *reinterpret_cast<uint4*>(xs + w * ldl + col) = raw[c][0];
+        *reinterpret_cast<uint4*>(xs + w * ldl + col + 8) = raw[c][1];
+      }
+      const uint32_t wd[8] = {raw[c][0].x, raw[c][0].y, raw[c][0].z, raw[c][0].w,
+                              raw[c][1].x, raw[c][1].y, raw[c][1].z, raw[c][1].w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        v[c][2 * j] = __uint_as_float(wd[j] << 16);
+        v[c][2 * j + 1] = __uint_as_float(wd[j] & 0xffff0000u);
+      }
+    }
+
+    // rotate + per-row int8 quantization: rotquant_kernel's arithmetic for one row per wave
+    float amax = 0.f;
+#pragma unroll
+    for (int c = 0; c < kNCH; ++c) {
+      rotate16(v[c], c1, c2, c8);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[c][i]));
+    }
+    amax = fmaxf(wave_max(amax), 1e-8f);
+    if (row_ok) {
+      const float mul = __fdiv_rn(127.f, amax) * sigma;
+      if (lane == 0) s[row] = __fdiv_rn(amax, 127.f);
+      int8_t* qr = q + row * (int64_t)K;
+#pragma unroll
+      for (int c = 0; c < kNCH; ++c) {
+        const int col = c * 1024 + off;
+        if (col < K) store_codes16(qr + col, v[c], mul);
+      }
+    }
+
+    // u partial over columns [w kw, (w + 1) kw): lane l multiplies row l % 16 (8 k at 8 (l / 16) of each 32-wide
+    // step) by rank l % 16 of each 16-rank tile.  A comes in batches of NB steps; the next tile's row is issued
+    // right after the last batch's loads.
+    v4f acc[RT];
+#pragma unroll
+    for (int jt = 0; jt < RT; ++jt) acc[jt] = v4f{0.f, 0.f, 0.f, 0.f};
+    v4f fa[NB][RT][2];
+    bool synced = false;
+    for (int k0 = 0; k0 < nks; k0 += NB) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int ks = k0 + b < nks ? k0 + b : nks - 1;
+#pragma unroll
+        for (int jt = 0; jt < RT; ++jt) {
+          const float* p = al + (int64_t)16 * jt * K + 32 * ks;
+          fa[b][jt][0] = *reinterpret_cast<const v4f*>(p);
+          fa[b][jt][1] = *reinterpret_cast<const v4f*>(p + 4);
+        }
+      }
+      if (k0 + NB >= nks) load_row(tile + gridDim.x);   // the next tile's row streams in behind the last batch
+      if (!synced) {
+        lds_sync();   // the tile's 16 rows are in LDS
+        synced = true;
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        if (k0 + b >= nks) break;
+        const v8bf xa = __builtin_bit_cast(v8bf, *reinterpret_cast<const v4i*>(xl + 32 * (k0 + b)));
+#pragma unroll
+        for (int jt = 0; jt < RT; ++jt) {
+          v8bf hi, lo;
+          split8_hilo(fa[b][jt][0], fa[b][jt][1], hi, lo);
+          acc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, hi, acc[jt], 0, 0, 0);
+          acc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa, lo, acc[jt], 0, 0, 0);
+        }
+      }
+    }
+    lds_sync();   // every wave is done reading the rows
+    float* part = reinterpret_cast<float*>(xs);   // [16 waves][RT][4][64]
+#pragma unroll
+    for (int jt = 0; jt < RT; ++jt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) part[((w * RT + jt) * 4 + i) * 64 + lane] = acc[jt][i];
+    lds_sync();
+    // C layout (16x16): lane ln owns rank 16 jt + ln % 16 and rows 4 (ln / 16) + i of the tile
+    if (threadIdx.x < 256 * RT) {
+      const int ln = threadIdx.x & 63, i = (threadIdx.x >> 6) & 3, jt = threadIdx.x >> 8;
+      float sum = part[(jt * 4 + i) * 64 + ln];
+#pragma unroll
+      for (int ww = 1; ww < RQL_WAVES; ++ww) sum += part[((ww * RT + jt) * 4 + i) * 64 + ln];
+      const int64_t m = tile * RQL_WAVES + 4 * (ln >> 4) + i;
+      if (m < M) u[m * ldu + 16 * jt + (ln & 15)] = sum;
+    }
+    lds_sync();   // the partials are read before the next tile's rows overwrite them
+  }
+}
+
+template <int kNCH, int RT>
+int launch_rql(const __bf16* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, float* s, const float* a, int64_t ldu,
+               float* u, hipStream_t st) {
+  const int lds = RQL_WAVES * (int)(K + 8) * 2;
+  if (hipFuncSetAttribute((const void*)rotquant_lora_kernel<kNCH, RT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          lds) != hipSuccess)
+    return K2Q_ELAUNCH;
+  const int64_t tiles = (M + RQL_WAVES - 1) / RQL_WAVES;
+  const int64_t cus = k2q_cu_count();
+  const unsigned grid = (unsigned)(tiles < cus ? tiles : cus);
+  hipLaunchKernelGGL((rotquant_lora_kernel<kNCH, RT>), dim3(grid), dim3(64 * RQL_WAVES), lds, st, x, M, (int)K, ldx,
+                     q, s, a, ldu, u);
+  return k2q_launch_status();
+}
+
+template <int RT>
+int launch_rql_r(const __bf16* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, float* s, const float* a,
+                 int64_t ldu, float* u, hipStream_t st) {
+  switch ((K + 1023) / 1024) {
+    case 1: return launch_rql<1, RT>(x, M, K, ldx, q, s, a, ldu, u, st);
+    case 2: return launch_rql<2, RT>(x, M, K, ldx, q, s, a, ldu, u, st);
+    default: return launch_rql<3, RT>(x, M, K, ldx, q, s, a, ldu, u, st);
+  }
+}
+
 template <typename Tin, int WPR, int MODE>
 void launch_wpr(const Tin* xp, int64_t M, int64_t K, int64_t ldx, int8_t* q, float* s, uint16_t* xrot, uint8_t* q4,
                 uint16_t* s4, hipStream_t st) {
@@ -181,4 +374,35 @@ extern "C" int k2q_quant_weight_i4(const void* w, int w_dtype, int64_t N, int64_
   if (w_dtype == K2Q_DTYPE_BF16)
     return launch_rotquant<__bf16, MODE_GROUP_I4>(w, N, K, K, nullptr, nullptr, nullptr, qw4, sw4, st);
   return launch_rotquant<float, MODE_GROUP_I4>(w, N, K, K, nullptr, nullptr, nullptr, qw4, sw4, st);
+}
+
+// Shapes rotquant_lora_kernel takes: one row per wave in at most 3 chunks of 1024 (K <= 3072: 4 chunks leave
+// no registers for the A fragments without spilling), 16 column ranges of whole 32-wide steps (K % 512 == 0),
+// and the 16 wave partials of r ranks fitting where the rows sat in LDS.
+int k2q_rotquant_lora_fits(int64_t K, int64_t r) {
+  if (K < 512 || K > 3072 || K % 512 || r < 16 || r % 16 || r > 64) return 0;
+  return (int64_t)RQL_WAVES * (r / 16) * 4 * 64 * 4 <= (int64_t)RQL_WAVES * (K + 8) * 2;
+}
+
+int rotquant_lora_impl(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, float* s, const float* a,
+                       int64_t r, float* u, int64_t ldu, hipStream_t st) {
+  if (!k2q_rotquant_lora_fits(K, r)) return K2Q_EUNSUPPORTED;
+  const __bf16* xp = reinterpret_cast<const __bf16*>(x);
+  switch (r / 16) {
+    case 1: return launch_rql_r<1>(xp, M, K, ldx, q, s, a, ldu, u, st);
+    case 2: return launch_rql_r<2>(xp, M, K, ldx, q, s, a, ldu, u, st);
+    case 3: return launch_rql_r<3>(xp, M, K, ldx, q, s, a, ldu, u, st);
+    default: return launch_rql_r<4>(xp, M, K, ldx, q, s, a, ldu, u, st);
+  }
+}
+
+extern "C" int k2q_rotquant_lora(const void* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, float* s,
+                                 const float* lora_a, int64_t r, float* u, int64_t ldu, void* stream) {
+  int rc = check_rotquant_args(x, K2Q_DTYPE_BF16, M, K, ldx);
+  if (rc) return rc;
+  if (!q || !s || !lora_a || !u || !k2q_aligned(q, 16) || !k2q_aligned(lora_a, 16) || ldu < r || r % 16 != 0 || r < 16)
+    return K2Q_EINVAL;
+  if (!k2q_rotquant_lora_fits(K, r)) return K2Q_EUNSUPPORTED;
+  return rotquant_lora_impl(static_cast<const uint16_t*>(x), M, K, ldx, q, s, lora_a, r, u, ldu,
+                            static_cast<hipStream_t>(stream));
 }

@@ -71,6 +71,10 @@ class _SharedInputQuant:
         if self.enabled:
             self.ref, self.key, self.val = weakref.ref(x), key, (qx, sx)
 
+    def clear(self) -> None:
+        """Forget the kept codes (their memory returns to the allocator)."""
+        self.ref = self.key = self.val = None
+
     def seed(self, x: torch.Tensor, qx: torch.Tensor, sx: torch.Tensor) -> None:
         """Record codes a producer-fused kernel computed for ``x`` (exactly those ``rotquant`` gives), so the
         ConvRot layers that receive ``x`` next skip their own rotate/quant."""

@@ -234,9 +234,12 @@ def test_group_siblings_matches_ungrouped(k2, dev, monkeypatch):
     y1, dx1, gr1 = _step(gdit, gad, x, vec, dy)
     torch.cuda.synchronize()
     assert len(calls) == 4                        # one grouped launch per group and block forward
-    # the stacked down-projection may round u differently in the last bit; through attention's backward that
-    # moves the upstream gradients, hence the block-level bars (the layer-level test below is tighter)
-    assert _rel(y1, y0) < 1e-3
+    # u differs in the last bits between the routes (ungrouped, the first linear on a tensor takes u from the
+    # rotate/quant pass at these sizes, the others from the down-projection; grouped, one stacked
+    # down-projection), which moves a few bf16 outputs by one step; the next layers requantize those outputs, so
+    # a moved element can flip an int8 code, and through attention's backward that moves the upstream gradients:
+    # hence the block-level bars (the layer-level test below is tighter)
+    assert _rel(y1, y0) < 5e-3
     assert _rel(dx1, dx0) < 1e-2
     for k in gr0:
         assert _rel(gr1[k][0], gr0[k][0]) < 2e-2 and _rel(gr1[k][1], gr0[k][1]) < 2e-2, k

@@ -1,7 +1,8 @@
 """GPU tests of ``k2q_linear_fwd``: one library call per quantized linear + LoRA forward (the module's path).
 
 * M > 8: the call issues the same launches as the separate entry points (rotate/quant, LoRA down-projection,
-  GEMM), so codes, scales, u and y are bit-identical to calling them one by one.
+  GEMM; or, where ``k2q_linear_fwd_fuses_down`` says so, rotate/quant with the down-projection in the same pass,
+  then the GEMM), so codes, scales, u and y are bit-identical to calling them one by one.
 * M <= 8: one prologue launch computes the codes (bit-identical to ``k2q_rotquant``) and u (an f32 dot product
   per rank: within f32 rounding of the down-projection kernel and of the float64 product), then the GEMV;
   y within the forward bar of the oracle.
@@ -41,7 +42,8 @@ def _case(M, K, N, r, seed, dev, w4=False, bias=True):
                                         (1024, 12288, 3072, 16, False), (256, 512, 384, 48, True),
                                         (4096, 3072, 3072, 16, False), (700, 1024, 512, 128, False),
                                         (200, 2048, 256, 256, False), (64, 16384, 512, 64, False),
-                                        (8192, 3072, 12288, 16, False)])
+                                        (8192, 3072, 12288, 16, False), (4096, 3072, 3072, 16, True),
+                                        (16896, 3072, 1024, 32, False), (1024, 2048, 512, 32, False)])
 def test_one_call_equals_separate_launches(k2, dev, M, K, N, r, w4):
     L = k2._lib
     x, w, b, A, B = _case(M, K, N, r, M + K, dev, w4)
@@ -53,20 +55,37 @@ def test_one_call_equals_separate_launches(k2, dev, M, K, N, r, w4):
     qx = torch.empty(M, K, dtype=torch.int8, device=dev)
     sx = torch.empty(M, device=dev)
     y, u = L.linear_fwd(xd, qx, sx, False, Ad, Bd, 0.75, qw, sw, bd, w4)
-    q0, s0, _ = L.rotquant(xd)
-    u0 = L.lora_down(xd, Ad) if r else None
+    fused = bool(r) and L.linear_fwd_fuses_down(M, K, r)
+    if fused:
+        q0, s0, u0 = L.rotquant_lora(xd, Ad)
+    else:
+        q0, s0, _ = L.rotquant(xd)
+        u0 = L.lora_down(xd, Ad) if r else None
     gemm = L.gemm_w4a8 if w4 else L.gemm_w8a8
     y0 = gemm(q0, s0, qw, sw, bd, u0, Bd, 0.75)
     assert torch.equal(qx, q0) and torch.equal(sx, s0) and torch.equal(y, y0)
     if r:
         assert torch.equal(u, u0)
-    # codes given (as a producer kernel leaves them): the call uses them as they are
+        ref = orc.lora_down(x.float().numpy(), A.numpy())
+        assert rel_frob(u.cpu().numpy(), ref) < 1e-5
+    # codes given (as a producer kernel leaves them): the call uses them as they are, u from the down-projection
     y1, _ = L.linear_fwd(xd, q0, s0, True, Ad, Bd, 0.75, qw, sw, bd, w4)
-    assert torch.equal(y1, y0)
+    ud = L.lora_down(xd, Ad) if r else None
+    assert torch.equal(y1, gemm(q0, s0, qw, sw, bd, ud, Bd, 0.75))
     # no factors requested (inference): W8 with r <= 128 folds the down-projection's reduce into the GEMM
     # epilogue, the other cases keep u in the workspace; y is the same bits either way
     y2, u2 = L.linear_fwd(xd, qx, sx, False, Ad, Bd, 0.75, qw, sw, bd, w4, need_u=False)
     assert u2 is None and torch.equal(y2, y0)
+
+
+def test_fused_down_plan(k2):
+    """The one-call forward takes u from the rotate/quant pass for K <= 3072 (K % 512 == 0) with r 16 or 32 when
+    the 16-row tiles fit one round of CUs (two for r = 16), and issues the separate down-projection otherwise."""
+    f = k2._lib.linear_fwd_fuses_down
+    assert f(4096, 3072, 16) and f(1024, 3072, 16) and f(8192, 3072, 16) and f(4096, 3072, 32) and f(16, 1024, 32)
+    assert not f(16896, 3072, 32) and not f(8208, 3072, 16) and not f(4112, 3072, 32)
+    assert not f(4096, 6144, 16) and not f(4096, 3072, 64) and not f(4096, 640, 16) and not f(8, 3072, 16)
+    assert not f(16, 512, 32)     # 32 ranks of wave partials do not fit where 16 rows of 512 sat in LDS
 
 
 @pytest.mark.parametrize("M,K,N,r", [(1, 3072, 18432, 16), (2, 3072, 18432, 16), (5, 12288, 3072, 64),

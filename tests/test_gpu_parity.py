@@ -190,6 +190,59 @@ def test_forward_w4a8(k2, dev, M, K, N, r, bias):
     assert rel_frob(y.float().cpu().numpy(), ref["y64"]) < 4e-3
 
 
+@pytest.mark.parametrize("M,K,r", [(1, 512, 16), (15, 1024, 32), (17, 3072, 16), (4096, 3072, 16), (16896, 3072, 32),
+                                   (1000, 3072, 64), (333, 2048, 48), (257, 1536, 32), (4111, 2560, 64), (8192, 3072, 16)])
+def test_rotquant_lora_same_pass(k2, dev, M, K, r):
+    """Rotate/quant with the LoRA down-projection from the same pass over x (``k2q_rotquant_lora``): the codes
+    and scales equal the oracle's (and k2q_rotquant's) bit for bit, u is within 1e-5 of the f64 product, the
+    columns of u past r and the rows of a longer buffer are left alone, and repeated calls are bit-identical."""
+    x = make_x(M, K, seed=M + K + r)
+    A = torch.randn(r, K, generator=torch.Generator().manual_seed(r + 1)) * 0.01
+    xd, Ad = x.to(dev), A.to(dev)
+    q, s, u = k2._lib.rotquant_lora(xd, Ad)
+    q0, s0, _ = orc.rotquant(x.float().numpy())
+    assert np.array_equal(q.cpu().numpy(), q0)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s0.view(np.uint32))
+    ref = orc.lora_down(x.float().numpy(), A.numpy())
+    assert rel_frob(u.cpu().numpy(), ref) < 1e-5
+    q2, s2, u2 = k2._lib.rotquant_lora(xd, Ad)
+    assert torch.equal(q2, q) and torch.equal(s2, s) and torch.equal(u2, u)
+    # through the C ABI with a wider u (ldu = r + 16) inside a larger buffer: only rows < M, columns < r written
+    ub = torch.full((M + 3, r + 16), 7.0, device=dev)
+    qb = torch.empty(M, K, dtype=torch.int8, device=dev)
+    sb = torch.empty(M, device=dev)
+    lib = k2._lib.load()
+    assert lib.k2q_rotquant_lora(xd.data_ptr(), M, K, K, qb.data_ptr(), sb.data_ptr(), Ad.data_ptr(), r,
+                                 ub.data_ptr(), r + 16, torch.cuda.current_stream(dev).cuda_stream) == 0
+    assert torch.equal(qb, q) and torch.equal(sb, s) and torch.equal(ub[:M, :r], u)
+    assert torch.all(ub[:M, r:] == 7.0) and torch.all(ub[M:] == 7.0)
+
+
+def test_rotquant_lora_refuses_other_shapes(k2, dev):
+    """Shapes outside three chunks per lane (K > 3072), K not a multiple of 512, or ranks outside 16..64 are refused
+    before launch (the module then runs the separate down-projection)."""
+    lib = k2._lib.load()
+    x = torch.zeros(4, 6144, dtype=torch.bfloat16, device=dev)
+    A = torch.zeros(16, 6144, device=dev)
+    q = torch.empty(4, 6144, dtype=torch.int8, device=dev)
+    assert lib.k2q_rotquant_lora(x.data_ptr(), 4, 4096, 6144, q.data_ptr(), torch.empty(4, device=dev).data_ptr(),
+                                 A.data_ptr(), 16, torch.empty(4, 16, device=dev).data_ptr(), 16,
+                                 torch.cuda.current_stream(dev).cuda_stream) == -4
+    s = torch.empty(4, device=dev)
+    u = torch.empty(4, 128, device=dev)
+    st = torch.cuda.current_stream(dev).cuda_stream
+    assert lib.k2q_rotquant_lora(x.data_ptr(), 4, 6144, 6144, q.data_ptr(), s.data_ptr(), A.data_ptr(), 16,
+                                 u.data_ptr(), 16, st) == -4
+    assert lib.k2q_rotquant_lora(x.data_ptr(), 4, 640, 6144, q.data_ptr(), s.data_ptr(), A.data_ptr(), 16,
+                                 u.data_ptr(), 16, st) == -4
+    assert lib.k2q_rotquant_lora(x.data_ptr(), 4, 3072, 6144, q.data_ptr(), s.data_ptr(), A.data_ptr(), 128,
+                                 u.data_ptr(), 128, st) == -4
+    assert lib.k2q_rotquant_lora(x.data_ptr(), 4, 3072, 6144, q.data_ptr(), s.data_ptr(), A.data_ptr(), 24,
+                                 u.data_ptr(), 24, st) == -1
+    with pytest.raises(ValueError):
+        k2._lib.rotquant_lora(x, A)
+
+
 @pytest.mark.parametrize("M,K,r", [(2, 3072, 16), (1024, 12288, 16), (4608, 12288, 64), (100, 640, 48),
                                    (33, 1024, 128), (17, 2048, 80), (16896, 3072, 32), (1000, 3072, 256),
                                    (300, 1024, 144), (4608, 6144, 192)])
