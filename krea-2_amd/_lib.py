@@ -132,7 +132,14 @@ def _check(rc: int, name: str) -> None:
         raise RuntimeError(f"{name} failed: {_STATUS.get(rc, rc)}")
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(dev: torch.device) -> int:
+    """The raw ``hipStream_t`` of the current stream of ``dev`` (torch's own getter when it has one: a tenth of
+    the host time of building a ``torch.cuda.Stream`` object per call)."""
+    if _raw_stream is not None:
+        return _raw_stream(dev.index if dev.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(dev).cuda_stream
 
 
@@ -608,6 +615,11 @@ def gemm_w8a8(qx, sx, qw, sw, bias=None, u=None, lora_b=None, lora_scale: float 
 WMODE_W8, WMODE_W4 = 0, 1
 
 
+# workspace bytes of k2q_linear_fwd per (wmode, M, N, K, r): a pure function of the shape and the device's CU
+# count (one GPU model per process here), asked once per shape
+_FWD_WS: dict = {}
+
+
 def linear_fwd_fuses_down(M: int, K: int, r: int) -> bool:
     """Whether :func:`linear_fwd` (codes not given, rank ``r`` factors) takes u from the rotate/quant pass."""
     return bool(load().k2q_linear_fwd_fuses_down(M, K, r))
@@ -641,7 +653,10 @@ def linear_fwd(x2, qx, sx, codes_ready: bool, A, B, lora_scale: float, qw, sw, b
     wmode = WMODE_W4 if w4 else WMODE_W8
     y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     u = torch.empty((M, r), dtype=torch.float32, device=dev) if r and (need_u or M <= 8) else None
-    nws = lib.k2q_linear_fwd_ws_bytes(wmode, M, N, K, r)
+    key = (wmode, M, N, K, r)
+    nws = _FWD_WS.get(key)
+    if nws is None:
+        nws = _FWD_WS.setdefault(key, lib.k2q_linear_fwd_ws_bytes(wmode, M, N, K, r))
     ws = torch.empty((nws,), dtype=torch.uint8, device=dev) if nws > 0 else None
     _check(lib.k2q_linear_fwd(x2.data_ptr(), x2.stride(0), M, K, qx.data_ptr(), sx.data_ptr(), int(codes_ready),
                               _ptr(A), _ptr(B), r, float(lora_scale), _ptr(u), wmode, qw.data_ptr(), sw.data_ptr(),

@@ -1052,9 +1052,8 @@ int launch_w4(const W4Args& p, hipStream_t st) {
   constexpr int lds = 2 * W4_STAGE;
   // Buffer-resource extents are 32-bit: a tile's rows of either operand and the whole scale array.
   if (p.K * W4_BB >= (int64_t(1) << 31) || (p.K / 64) * p.N * 2 >= (int64_t(1) << 31)) return K2Q_EUNSUPPORTED;
-  if (hipFuncSetAttribute((const void*)gemm_w4_kernel<EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          lds) != hipSuccess)
-    return K2Q_ELAUNCH;
+  static std::atomic<uint64_t> lds_set{0};
+  if (k2q_lds_limit_once(gemm_w4_kernel<EPI>, lds, lds_set)) return K2Q_ELAUNCH;
   const int64_t tiles = ((p.N + W4_BA - 1) / W4_BA) * ((p.M + W4_BB - 1) / W4_BB);
   if (tiles > 0x7fffffff) return K2Q_EUNSUPPORTED;
   hipLaunchKernelGGL(gemm_w4_kernel<EPI>, dim3((unsigned)tiles), dim3(256), lds, st, p);
@@ -1201,8 +1200,8 @@ int64_t split_ws_bytes(int64_t rows_a, int64_t rows_b, int64_t kbytes) {
 
 template <int EPI, int MODE, class C>
 int set_lds() {
-  return hipFuncSetAttribute((const void*)gemm_nt_kernel<EPI, MODE, C>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                             C::LDS) == hipSuccess ? K2Q_OK : K2Q_ELAUNCH;
+  static std::atomic<uint64_t> lds_set{0};
+  return k2q_lds_limit_once(gemm_nt_kernel<EPI, MODE, C>, C::LDS, lds_set);
 }
 
 // Balanced persistent grid: as many rounds as the tiles need on this GPU's workgroup slots, and just enough

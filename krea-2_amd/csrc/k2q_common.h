@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "../../include/k2q.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -90,6 +92,22 @@ static inline int k2q_aligned(const void* p, uintptr_t a) { return ((uintptr_t)p
 // Compute units of the current device (launch planning only; 256 on MI355X).  Looked up once per device and
 // cached (api.hip): the attribute query costs more host time than a kernel launch.
 int k2q_cu_count();
+
+// Raises kernel fn's dynamic-LDS limit to `bytes` once per device; `done` (one static per kernel instance, a
+// bit per device) remembers it, so a launch pays for the attribute call only the first time on a device.
+// Callers pass the most the instance can need, so a later launch never needs a higher limit.
+template <class Fn>
+int k2q_lds_limit_once(Fn* fn, int bytes, std::atomic<uint64_t>& done) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return K2Q_ELAUNCH;
+  const uint64_t bit = dev >= 0 && dev < 64 ? (uint64_t(1) << dev) : 0;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return K2Q_OK;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, bytes) !=
+      hipSuccess)
+    return K2Q_ELAUNCH;
+  done.fetch_or(bit, std::memory_order_acq_rel);
+  return K2Q_OK;
+}
 
 // Rotate/quant with the LoRA down-projection from the same pass (rotquant.hip): the codes of k2q_rotquant and
 // u = x A^T (A: r x K f32) for K <= 4096, K % 512 == 0, r in {16, 32, 48, 64} (k2q_rotquant_lora_fits).

@@ -299,8 +299,8 @@ template <int kNCH, int RT>
 int launch_rql(const __bf16* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, float* s, const float* a, int64_t ldu,
                float* u, hipStream_t st) {
   const int lds = RQL_WAVES * (int)(K + 8) * 2;
-  if (hipFuncSetAttribute((const void*)rotquant_lora_kernel<kNCH, RT>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          lds) != hipSuccess)
+  static std::atomic<uint64_t> lds_set{0};   // the limit is set once, for the instance's largest K
+  if (k2q_lds_limit_once(rotquant_lora_kernel<kNCH, RT>, RQL_WAVES * (1024 * kNCH + 8) * 2, lds_set))
     return K2Q_ELAUNCH;
   const int64_t tiles = (M + RQL_WAVES - 1) / RQL_WAVES;
   const int64_t cus = k2q_cu_count();

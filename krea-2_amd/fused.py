@@ -320,8 +320,7 @@ class _SiblingGroup:
 
     @staticmethod
     def _key(x):
-        return (x._version, x.data_ptr(), tuple(x.shape), tuple(x.stride()), x.device,
-                torch.cuda.current_stream(x.device).cuda_stream)
+        return (x._version, x.data_ptr(), tuple(x.shape), tuple(x.stride()), x.device, _lib._stream(x.device))
 
     def call(self, idx: int, x: torch.Tensor):
         key = self._key(x)

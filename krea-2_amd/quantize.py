@@ -45,8 +45,7 @@ class _SharedInputQuant:
 
     @staticmethod
     def _key(x: torch.Tensor):
-        return (x._version, x.data_ptr(), tuple(x.shape), tuple(x.stride()), x.device,
-                torch.cuda.current_stream(x.device).cuda_stream)
+        return (x._version, x.data_ptr(), tuple(x.shape), tuple(x.stride()), x.device, _lib._stream(x.device))
 
     def lookup(self, x: torch.Tensor, x2: torch.Tensor):
         key = self._key(x)
