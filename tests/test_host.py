@@ -121,6 +121,19 @@ def test_gemm_plan_edges(k2):
         L.gemm_w8a8_plan(4, 4, 100)
 
 
+def test_forward_takes_down_projection_from_the_rotquant_pass_where_measured_faster(k2):
+    """The one-call forward's route for u, decided on the host (the CU count is the MI355X's 256 without a GPU):
+    the rotate/quant pass computes it for K <= 3072 (K % 512 == 0), r 16 or 32, while the 16-row tiles fit one
+    round of CUs (two for r = 16); otherwise rotate/quant and the down-projection are separate launches."""
+    f = k2._lib.linear_fwd_fuses_down
+    assert f(4096, 3072, 16) and f(8192, 3072, 16) and f(4096, 3072, 32) and f(9, 1024, 32)   # cfg0/1, cfg4
+    assert not f(16896, 3072, 32)        # cfg2: 1056 tiles, streaming A per tile measured slower
+    assert not f(8193, 3072, 16) and not f(4097, 3072, 32)
+    assert not f(4608, 12288, 64) and not f(4096, 6144, 16) and not f(4096, 3072, 64) and not f(8, 3072, 16)
+    assert k2._lib.rotquant_lora_fits(3072, 64) and not k2._lib.rotquant_lora_fits(4096, 16)
+    assert not k2._lib.rotquant_lora_fits(512, 32)      # 32 ranks of partials exceed 16 rows of 512 in LDS
+
+
 def test_wrappers_validate_before_launch(k2):
     L = k2._lib
     # grouped LoRA gradients: member count and rank before anything touches a device
