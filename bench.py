@@ -1244,6 +1244,12 @@ def main():
         extra[f"cfg{c}"] = forward_record(CONFIGS[c], rc, cc, ccr)
         del rc
         progress(f"cfg{c} timed")
+    # the W4A8 base at the headline shape (not a BASELINE config: cfg2's M, K, N and r with cfg1's int4 weights)
+    w4c = dict(CONFIGS[2], w4=True, name="cfg2 shape with W4A8 (g64) weights, M=16896 K=3072 N=12288 r=32")
+    rw = run_config(k2, w4c, max(5, a.steps // 2), a.warmup, dev, a.settle / 2)
+    extra["cfg2_shape_w4a8"] = forward_record(w4c, rw)
+    del rw
+    progress("cfg2 shape with W4A8 weights timed")
     extra["cfg3"] = run_cfg3(k2, max(5, a.steps // 2), dev, a.settle / 2, cpu=not a.no_cpu)
     progress("cfg3 timed")
     extra["cfg4"] = run_cfg4(k2, max(5, a.steps // 2), dev, a.settle / 2, cpu=not a.no_cpu)
