@@ -770,7 +770,8 @@ def run_cfg4(k2, steps, dev, settle_s=0.0, cpu=False):
 
 def profile_pass(k2, dev):
     """Fixed launches for rocprofv3 counter passes: cfg2 rotate/quant, LoRA down, GEMM, 3 times each; the W4A8
-    GEMM at cfg1 and at the cfg2 shape, 3 times each; the cfg3
+    GEMM at cfg1 and at the cfg2 shape, 3 times each; cfg0's rotate/quant with the LoRA down-projection in the
+    same pass, 3 times; the cfg3
     input-gradient GEMM (with its LoRA term) and the cfg3 LoRA gradients 3 times each; the two producer kernels at cfg4's image-stream shapes
     and the grouped attention-input GEMM (M = 4608, 6144 -> 6144 | 1536 | 1536 | 6144, r = 16) 3 times each;
     then a plain 256 MiB device copy (Tensor.copy_) 3 times, the calibration point for FETCH/WRITE_SIZE."""
@@ -796,7 +797,13 @@ def profile_pass(k2, dev):
         L.gemm_w4a8(qx1, sx1, qw4, sw4, b1d, u1, B1.to(dev), 1.0)
     for _ in range(3):
         L.gemm_w4a8(qx, sx, qw4b, sw4b, None, u, Bd, 1.0)
-    del x1d, qw4, sw4, qx1, sx1, u1, qw4b, sw4b
+    # cfg0: rotate/quant with the LoRA down-projection from the same pass (the one-call forward's route there)
+    c0 = CONFIGS[0]
+    x0, _, _, A0, _ = synth(c0["M"], c0["K"], c0["N"], c0["r"], c0["bias"])
+    x0d, A0d = x0.to(dev), A0.to(dev)
+    for _ in range(3):
+        L.rotquant_lora(x0d, A0d)
+    del x1d, qw4, sw4, qx1, sx1, u1, qw4b, sw4b, x0d, A0d
     c3 = CFG3
     g3 = torch.Generator().manual_seed(3)
     qw3, sw3 = L.quant_weight_i8((torch.randn(c3["N"], c3["K"], generator=g3) * 0.02).to(torch.bfloat16).to(dev))
@@ -961,6 +968,7 @@ def _gemm_kernel(L, epi, M, N, K, grouped=False, cus=256):
 # Kernels of --profile-pass: (label, kernel-name substring(s), grid threads, algorithmic read, algorithmic write).
 def _profiled_kernels(L):
     M2, K2, N2, r2 = 16896, 3072, 12288, 32
+    M0, K0, r0 = 4096, 3072, 16
     M3, K3, N3, r3 = 4608, 12288, 3072, 64
     Mi, Ki, Kh = 8192, 3072, 12288
     Mg, Kg, Ng, rg = 4608, 6144, 15360, 16
@@ -971,6 +979,9 @@ def _profiled_kernels(L):
         ("rotquant_kernel cfg2", "rotquant_kernel", 1081344, 2 * M2 * K2, M2 * K2 + 4 * M2),
         ("lora_down_as_kernel<2> cfg2", "lora_down_as_kernel<2>", None, 2 * M2 * K2 + 4 * r2 * K2, 3 * 4 * M2 * r2),
         ("lora_reduce_kernel cfg2", "lora_reduce_kernel", 135168, 3 * 4 * M2 * r2, 4 * M2 * r2),
+        # x once and A once from HBM (each 16-row tile re-reads A, but from L2); codes, scales and u written
+        ("rotquant_lora_kernel cfg0 (codes and u in one pass)", "rotquant_lora_kernel", 262144,
+         2 * M0 * K0 + 4 * r0 * K0, M0 * K0 + 4 * M0 + 4 * M0 * r0),
         ("gemm_nt_kernel<EPI_DXLIN> cfg3 (input gradient)", *_gemm_kernel(L, 4, M3, K3, 2 * N3),
          2 * M3 * N3 + 2 * K3 * N3 + 4 * M3 * r3 + 4 * r3 * K3, 2 * M3 * K3),
         ("rot_dequant_t_kernel cfg3 (effective weight)", "rot_dequant_t_kernel<false>", 1179648, N3 * K3 + 4 * N3,
