@@ -399,6 +399,43 @@ def test_save_lora_file_gets_the_default_permissions(k2, tmp_path):
         assert "text_encoder.blocks.0.attn.wq.lora_A.weight" in f.keys()
 
 
+def test_effective_weight_cache_logic_on_cpu(k2, monkeypatch):
+    """The effective input-gradient weight's cache, with the library's builder replaced by a CPU stand-in: off by
+    default (built per call, nothing kept); on, kept as a plain attribute keyed to the codes' storage, rebuilt
+    after they move, released by the next build anywhere once its layer's codes have left the device they were
+    built on, and dropped when the cache is switched off.  Parameters are codes, scales and bias only."""
+    builds = []
+
+    def fake_dx_weight(q, s, w4=False):
+        builds.append(q.data_ptr())
+        return torch.zeros(q.shape[1], q.shape[0], dtype=torch.bfloat16, device=q.device)
+
+    monkeypatch.setattr(k2._lib, "dx_weight", fake_dx_weight)
+    a, b = _cpu_quantized(N=128, K=256), _cpu_quantized(N=128, K=256, seed=1)
+    assert a.keep_dx_weight is False
+    a.dx_weight()
+    assert a.dx_weight_kept is None and len(builds) == 1                 # default: per call, nothing kept
+    assert {n for n, _ in a.named_parameters()} == {"qweight", "wscale", "bias"}
+    holder = nn.ModuleList([a, b])
+    assert k2.set_dx_weight_cache(holder, True) == 2
+    w1 = a.dx_weight()
+    assert a.dx_weight() is w1 and len(builds) == 2                      # kept and reused
+    assert not isinstance(w1, nn.Parameter) and not any("dx" in k for k in a.state_dict())
+    assert {n for n, _ in a.named_parameters()} == {"qweight", "wscale", "bias"}
+    for p in a.parameters():                                             # "paged out" (re-pointed elsewhere)
+        p.data = p.data.clone()
+    assert a.dx_weight_kept is w1                                        # stays until some build runs
+    b.dx_weight()                                                        # another layer's build releases it
+    assert a.dx_weight_kept is None and b.dx_weight_kept is not None
+    w2 = a.dx_weight()
+    assert w2 is not w1 and len(builds) == 4
+    with torch.no_grad():
+        a.qweight.add_(0)                                                # in-place write: version bump
+    assert a.dx_weight() is not w2
+    k2.set_dx_weight_cache(holder, False)
+    assert a.dx_weight_kept is None and b.dx_weight_kept is None
+
+
 def test_walker_requires_gpu_and_says_so(k2):
     if torch.cuda.is_available():
         pytest.skip("GPU present")
