@@ -467,13 +467,20 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
                                                so + 8 * i * ldb_s, 0, K2Q_DMA_CPOL);
   };
   // Fragments of substep kk (32 reduction bytes) of the stage in LDS slot `slot`.
+  // A lane's fragment rows are c32 plus multiples of 32, which share the chunk swizzle (swz looks at the row's
+  // low four bits), so each substep's reads take one per-lane address per operand and constant offsets of
+  // 32 rows (immediate ds_read offsets) instead of an address per fragment.
+  const int fsw = swz(c32);
+  const uint8_t* fra = smem + (C::ARW * wa + c32) * BKB;
+  const uint8_t* frb = smem + TA * WBK + (C::BRW * wb + c32) * BKB;
   auto read_frags = [&](int slot, int kk, v4i (&fa)[NA], v4i (&fb)[NB]) {
-    const uint8_t* tA = smem + slot * C::STAGE;
-    const uint8_t* tB = tA + TA * WBK;
+    const int co = slot * C::STAGE + 16 * ((2 * kk + h) ^ fsw);
+    const uint8_t* tA = fra + co;
+    const uint8_t* tB = frb + co;
 #pragma unroll
-    for (int i = 0; i < NA; ++i) fa[i] = frag(tA, C::ARW * wa + 32 * i + c32, 2 * kk + h);
+    for (int i = 0; i < NA; ++i) fa[i] = *reinterpret_cast<const v4i*>(tA + 32 * BKB * i);
 #pragma unroll
-    for (int i = 0; i < NB; ++i) fb[i] = frag(tB, C::BRW * wb + 32 * i + c32, 2 * kk + h);
+    for (int i = 0; i < NB; ++i) fb[i] = *reinterpret_cast<const v4i*>(tB + 32 * BKB * i);
   };
   auto mfmas = [&](const v4i (&fa)[NA], const v4i (&fb)[NB]) {
 #pragma unroll
