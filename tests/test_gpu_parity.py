@@ -216,6 +216,13 @@ def test_rotquant_lora_same_pass(k2, dev, M, K, r):
                                  ub.data_ptr(), r + 16, torch.cuda.current_stream(dev).cuda_stream) == 0
     assert torch.equal(qb, q) and torch.equal(sb, s) and torch.equal(ub[:M, :r], u)
     assert torch.all(ub[:M, r:] == 7.0) and torch.all(ub[M:] == 7.0)
+    # rows of a wider buffer (row stride ldx > K, as a strided view of a larger activation hands them over)
+    xw = torch.zeros(M, K + 64, dtype=torch.bfloat16, device=dev)
+    xw[:, :K] = xd
+    qw_, sw_, uw_ = torch.empty_like(q), torch.empty_like(s), torch.empty_like(u)
+    assert lib.k2q_rotquant_lora(xw.data_ptr(), M, K, K + 64, qw_.data_ptr(), sw_.data_ptr(), Ad.data_ptr(), r,
+                                 uw_.data_ptr(), r, torch.cuda.current_stream(dev).cuda_stream) == 0
+    assert torch.equal(qw_, q) and torch.equal(sw_, s) and torch.equal(uw_, u)
 
 
 def test_rotquant_lora_refuses_other_shapes(k2, dev):
