@@ -118,18 +118,20 @@ __device__ __forceinline__ void rotate16(float (&v)[16], float c1, float c2, flo
     asm volatile("v_fmac_f32_dpp %0, %0, %1 row_ror:8 row_mask:0xf bank_mask:0xf" : "+v"(v[i]) : "v"(c8));
 }
 
-// q = rint(v * mul) for 16 values, stored as one 16-byte vector (|v * mul| <= 127 by construction).
+// q = rint(v * mul) for 16 values, stored as one 16-byte vector (|v * mul| <= 127 by construction).  The
+// product is rounded to f32 first (a multiply of its own: the build does not contract it into an FMA), then
+// 1.5 * 2^23 is added: in [2^23, 2^24) floats are the integers, so the adder rounds t to rint(t) (to nearest,
+// ties to even, like rintf; 2^23 * 1.5 is even) and the sum's bit pattern is 0x4B400000 + rint(t), whose low
+// byte is the two's-complement code.  That replaces the round + convert of each value.
 __device__ __forceinline__ void store_codes16(int8_t* p, const float (&v)[16], float mul) {
   uint32_t w[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    uint32_t pk = 0;
+    uint32_t b[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int qi = (int)__builtin_rintf(v[4 * j + e] * mul);
-      pk |= ((uint32_t)qi & 0xffu) << (8 * e);
-    }
-    w[j] = pk;
+    for (int e = 0; e < 4; ++e) b[e] = __float_as_uint(v[4 * j + e] * mul + 12582912.0f);
+    // bytes 0 of b0, b1, b2, b3 (v_perm_b32 selects bytes of {S0, S1}: 0-3 from S1, 4-7 from S0, 0x0c = 0)
+    w[j] = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u) | __builtin_amdgcn_perm(b[3], b[2], 0x04000c0cu);
   }
   *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
 }
