@@ -123,7 +123,7 @@ __device__ __forceinline__ void rotate16(float (&v)[16], float c1, float c2, flo
 // 1.5 * 2^23 is added: in [2^23, 2^24) floats are the integers, so the adder rounds t to rint(t) (to nearest,
 // ties to even, like rintf; 2^23 * 1.5 is even) and the sum's bit pattern is 0x4B400000 + rint(t), whose low
 // byte is the two's-complement code.  That replaces the round + convert of each value.
-__device__ __forceinline__ void store_codes16(int8_t* p, const float (&v)[16], float mul) {
+__device__ __forceinline__ uint4 pack_codes16(const float (&v)[16], float mul) {
   uint32_t w[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -133,7 +133,11 @@ __device__ __forceinline__ void store_codes16(int8_t* p, const float (&v)[16], f
     // bytes 0 of b0, b1, b2, b3 (v_perm_b32 selects bytes of {S0, S1}: 0-3 from S1, 4-7 from S0, 0x0c = 0)
     w[j] = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u) | __builtin_amdgcn_perm(b[3], b[2], 0x04000c0cu);
   }
-  *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+__device__ __forceinline__ void store_codes16(int8_t* p, const float (&v)[16], float mul) {
+  *reinterpret_cast<uint4*>(p) = pack_codes16(v, mul);
 }
 
 }  // namespace k2q_rot

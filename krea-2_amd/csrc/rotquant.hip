@@ -196,6 +196,21 @@ __global__ __launch_bounds__(64 * RQL_WAVES) void rotquant_lora_kernel(const __b
     }
   };
 
+  v4f fa[NB][RT][2];
+  // one batch of NB 32-wide steps of A from step k0 (steps past the wave's range repeat its last one, unused)
+  auto load_a = [&](int k0) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int ks = k0 + b < nks ? k0 + b : nks - 1;
+#pragma unroll
+      for (int jt = 0; jt < RT; ++jt) {
+        const float* p = al + (int64_t)16 * jt * K + 32 * ks;
+        fa[b][jt][0] = *reinterpret_cast<const v4f*>(p);
+        fa[b][jt][1] = *reinterpret_cast<const v4f*>(p + 4);
+      }
+    }
+  };
+
   load_row(blockIdx.x);
   for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
     const int64_t row = tile * RQL_WAVES + w;
@@ -217,7 +232,6 @@ __global__ __launch_bounds__(64 * RQL_WAVES) void rotquant_lora_kernel(const __b
         v[c][2 * j + 1] = __uint_as_float(wd[j] & 0xffff0000u);
       }
     }
-
     // rotate + per-row int8 quantization: rotquant_kernel's arithmetic for one row per wave
     float amax = 0.f;
 #pragma unroll
@@ -227,40 +241,39 @@ __global__ __launch_bounds__(64 * RQL_WAVES) void rotquant_lora_kernel(const __b
       for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[c][i]));
     }
     amax = fmaxf(wave_max(amax), 1e-8f);
+    const float mul = __fdiv_rn(127.f, amax) * sigma;
+    uint4 codes[kNCH];
+#pragma unroll
+    for (int c = 0; c < kNCH; ++c) {
+      codes[c] = pack_codes16(v[c], mul);
+      // the codes are formed here, before A's loads are issued (the rotated row's registers are then free)
+      asm volatile("" ::"v"(codes[c].x), "v"(codes[c].y), "v"(codes[c].z), "v"(codes[c].w) : "memory");
+    }
+    // A's first batch is issued before the code stores, so waiting for it never waits for a store's completion
+    // (loads and stores retire in issue order for vmcnt); with a single batch the next tile's row follows it.
+    load_a(0);
+    if (NB >= nks) load_row(tile + gridDim.x);
     if (row_ok) {
-      const float mul = __fdiv_rn(127.f, amax) * sigma;
       if (lane == 0) s[row] = __fdiv_rn(amax, 127.f);
       int8_t* qr = q + row * (int64_t)K;
 #pragma unroll
       for (int c = 0; c < kNCH; ++c) {
         const int col = c * 1024 + off;
-        if (col < K) store_codes16(qr + col, v[c], mul);
+        if (col < K) *reinterpret_cast<uint4*>(qr + col) = codes[c];
       }
     }
+    lds_sync();   // the tile's 16 rows are in LDS
 
     // u partial over columns [w kw, (w + 1) kw): lane l multiplies row l % 16 (8 k at 8 (l / 16) of each 32-wide
-    // step) by rank l % 16 of each 16-rank tile.  A comes in batches of NB steps; the next tile's row is issued
-    // right after the last batch's loads.
+    // step) by rank l % 16 of each 16-rank tile.  Later batches of A are issued as the previous one is used up;
+    // the next tile's row is issued right after the last batch's loads.
     v4f acc[RT];
 #pragma unroll
     for (int jt = 0; jt < RT; ++jt) acc[jt] = v4f{0.f, 0.f, 0.f, 0.f};
-    v4f fa[NB][RT][2];
-    bool synced = false;
     for (int k0 = 0; k0 < nks; k0 += NB) {
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        const int ks = k0 + b < nks ? k0 + b : nks - 1;
-#pragma unroll
-        for (int jt = 0; jt < RT; ++jt) {
-          const float* p = al + (int64_t)16 * jt * K + 32 * ks;
-          fa[b][jt][0] = *reinterpret_cast<const v4f*>(p);
-          fa[b][jt][1] = *reinterpret_cast<const v4f*>(p + 4);
-        }
-      }
-      if (k0 + NB >= nks) load_row(tile + gridDim.x);   // the next tile's row streams in behind the last batch
-      if (!synced) {
-        lds_sync();   // the tile's 16 rows are in LDS
-        synced = true;
+      if (k0 > 0) {
+        load_a(k0);
+        if (k0 + NB >= nks) load_row(tile + gridDim.x);
       }
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
