@@ -189,7 +189,9 @@ int k2q_gemm_w8a8_grouped(const int8_t* qx, const float* sx, int64_t M, int64_t 
  * Where k2q_linear_fwd_fuses_down(M, K, r) is 1 (codes not given, K <= 3072, a CU's worth or two of 16-row
  * tiles), the codes and u come from one k2q_rotquant_lora launch instead of k2q_rotquant + k2q_lora_down (u then
  * carries that kernel's summation order).
- * ws: k2q_linear_fwd_ws_bytes bytes (256-byte aligned): factors, their partials and the GEMM's split pieces. */
+ * ws: k2q_linear_fwd_ws_bytes bytes (256-byte aligned): factors, their partials and the GEMM's split pieces.
+ * It may be NULL when u is given and the call takes u from the rotate/quant pass (k2q_linear_fwd_fuses_down)
+ * and, for W8, k2q_gemm_w8a8_ws_bytes(M, N, K) is 0: nothing of it is used then. */
 #define K2Q_WMODE_W8 0
 #define K2Q_WMODE_W4 1
 int64_t k2q_linear_fwd_ws_bytes(int wmode, int64_t M, int64_t N, int64_t K, int64_t r);

@@ -615,8 +615,8 @@ def gemm_w8a8(qx, sx, qw, sw, bias=None, u=None, lora_b=None, lora_scale: float 
 WMODE_W8, WMODE_W4 = 0, 1
 
 
-# workspace bytes of k2q_linear_fwd per (wmode, M, N, K, r): a pure function of the shape and the device's CU
-# count (one GPU model per process here), asked once per shape
+# workspace bytes of k2q_linear_fwd per (wmode, M, N, K, r), as (any call, a call with u given and codes not
+# given): pure functions of the shape and the device's CU count (one GPU model per process here), asked once per shape
 _FWD_WS: dict = {}
 
 
@@ -654,9 +654,14 @@ def linear_fwd(x2, qx, sx, codes_ready: bool, A, B, lora_scale: float, qw, sw, b
     y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     u = torch.empty((M, r), dtype=torch.float32, device=dev) if r and (need_u or M <= 8) else None
     key = (wmode, M, N, K, r)
-    nws = _FWD_WS.get(key)
-    if nws is None:
-        nws = _FWD_WS.setdefault(key, lib.k2q_linear_fwd_ws_bytes(wmode, M, N, K, r))
+    plan = _FWD_WS.get(key)
+    if plan is None:
+        nws = lib.k2q_linear_fwd_ws_bytes(wmode, M, N, K, r)
+        # with u given, a call that takes u from the rotate/quant pass and whose GEMM does not split uses no ws
+        unused = r and M > 8 and lib.k2q_linear_fwd_fuses_down(M, K, r) and \
+            (w4 or lib.k2q_gemm_w8a8_ws_bytes(M, N, K) == 0)
+        plan = _FWD_WS.setdefault(key, (nws, 0 if unused else nws))
+    nws = plan[1] if u is not None and not codes_ready else plan[0]
     ws = torch.empty((nws,), dtype=torch.uint8, device=dev) if nws > 0 else None
     _check(lib.k2q_linear_fwd(x2.data_ptr(), x2.stride(0), M, K, qx.data_ptr(), sx.data_ptr(), int(codes_ready),
                               _ptr(A), _ptr(B), r, float(lora_scale), _ptr(u), wmode, qw.data_ptr(), sw.data_ptr(),

@@ -56,7 +56,7 @@ struct KSeg {
   int end;                 // first stage (WBK reduction bytes) past this segment
 };
 
-struct GemmArgs {
+struct GemmBase {
   const uint8_t* a;   // A operand, rows_a x kbytes, row stride lda_b bytes
   const uint8_t* b;   // B operand, rows_b x kbytes
   int64_t rows_a, rows_b, kbytes, lda_b, ldb_b;
@@ -74,9 +74,9 @@ struct GemmArgs {
   int64_t rb_pstride; //      added in slice order as they are read (the down-projection's reduce, folded in)
   float lora_scale;
   int nseg;           // 0: one linear; else rows_a stacks nseg segments (EPI_W8)
-  GemmSeg seg[MAX_SEG];
   int nks;            // 0: one reduction operand pair; else the reduction runs over nks segments (EPI_DXLIN)
-  KSeg ks[MAX_SEG];
+  int nwg;            // workgroups of a full-K tile launch (the grid size, passed so that the kernel reads no
+                      // hidden launch arguments and its launches write ~256 bytes less)
   // Split schedule for the last, partly filled round of tiles: tiles 0 .. dp_tiles-1 run over the full
   // reduction; each of the sk_rem remainder tiles dp_tiles + i is cut into sk_s pieces (piece q covers
   // reduction slice q / sk_rem) whose accumulators go to part, and a fixup launch adds them.
@@ -85,6 +85,18 @@ struct GemmArgs {
   int32_t* part;
   int gb;             // B-tiles per group of the tile order (group_coords), set by launch_gemm
 };
+
+// The kernel arguments: the base fields, plus the segment tables (seg for nseg, ks for nks) in the kernels of
+// grouped launches only.  The tables are most of the struct's bytes, and a launch's arguments are written out
+// per launch: ~180 bytes instead of ~660 measured ~2 us less host time per launch while the GPU is busy.
+template <int NS>
+struct GemmArgsN : GemmBase {
+  GemmSeg seg[NS];
+  KSeg ks[NS];
+};
+template <>
+struct GemmArgsN<0> : GemmBase {};
+using GemmArgs = GemmArgsN<MAX_SEG>;   // what the host fills; a launch without segments passes its base
 
 __device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
@@ -110,7 +122,7 @@ __host__ __device__ __forceinline__ void group_coords(int64_t lid, int64_t tiles
 
 // The same in 32-bit arithmetic, for the W4 kernel's one tile per workgroup (tile counts < 2^31).
 __device__ __forceinline__ void tile_coords(uint32_t tiles_a, uint32_t tiles_b, uint32_t& ta, uint32_t& tb) {
-  const uint32_t lid = (uint32_t)xcd_remap(blockIdx.x, gridDim.x);
+  const uint32_t lid = (uint32_t)xcd_remap(blockIdx.x, tiles_a * tiles_b);   // the grid is one workgroup per tile
   constexpr uint32_t GB = 8;
   const uint32_t in_group = GB * tiles_a;
   const uint32_t g = lid / in_group;
@@ -292,40 +304,41 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 
 enum { MODE_TILE = 0, MODE_PIECE = 1, MODE_FIXUP = 2, MODE_KSEG = 3 };
 
-// MODE_TILE: full-K tiles 0 .. dp_tiles-1 with their epilogues; workgroup b takes tiles r * gridDim.x + b'
+// MODE_TILE: full-K tiles 0 .. dp_tiles-1 with their epilogues; workgroup b takes tiles r * nwg + b'
 // (b' its XCD-remapped id) for rounds r = 0, 1, ... while they exist, so the launch can use fewer
 // workgroups than CUs and give each the same number of tiles.  MODE_PIECE: one piece of a remainder tile,
 // accumulators parked in part.  MODE_FIXUP: the pieces of remainder tile dp_tiles + blockIdx.x added in
 // slice order, then the epilogue.  MODE_KSEG: MODE_TILE over a segmented reduction (the grouped input
 // gradient: the operand pair changes at segment boundaries).  Separate kernels, so the register allocation of
 // the tile kernel is not shared with the other paths.  The split modes run T256 tiles only.
-template <int EPI, int MODE, class C>
-__device__ __forceinline__ void gemm_tile(const GemmArgs& p, int64_t lid, int kbeg, int nk);
+template <int EPI, int MODE, class C, int NS>
+__device__ __forceinline__ void gemm_tile(const GemmArgsN<NS>& p, int64_t lid, int kbeg, int nk);
 
-template <int EPI, int MODE, class C>
+template <int EPI, int MODE, class C, int NS>
 __global__ __launch_bounds__(GT, C::WPC) __attribute__((amdgpu_waves_per_eu(2 * C::WPC, 2 * C::WPC)))
-void gemm_nt_kernel(GemmArgs p) {
+void gemm_nt_kernel(GemmArgsN<NS> p) {
   const int64_t nk_full = p.kbytes / SBK;
   if constexpr (MODE == MODE_FIXUP) {
-    gemm_tile<EPI, MODE, C>(p, p.dp_tiles + blockIdx.x, 0, (int)nk_full);
+    gemm_tile<EPI, MODE, C, NS>(p, p.dp_tiles + blockIdx.x, 0, (int)nk_full);
   } else if constexpr (MODE == MODE_PIECE) {   // pieces cover whole stage pairs
     const int sl = (int)blockIdx.x / p.sk_rem;
     const int np = (int)(nk_full / 2);
     const int kbeg = 2 * (sl * np / p.sk_s);
-    gemm_tile<EPI, MODE, C>(p, p.dp_tiles + (int)blockIdx.x % p.sk_rem, kbeg, 2 * ((sl + 1) * np / p.sk_s) - kbeg);
+    gemm_tile<EPI, MODE, C, NS>(p, p.dp_tiles + (int)blockIdx.x % p.sk_rem, kbeg,
+                                2 * ((sl + 1) * np / p.sk_s) - kbeg);
   } else {
-    const int64_t me = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-    for (int64_t base = 0; base + me < p.dp_tiles; base += gridDim.x) {
+    const int64_t me = xcd_remap((int)blockIdx.x, p.nwg);
+    for (int64_t base = 0; base + me < p.dp_tiles; base += p.nwg) {
       if (base > 0) lds_barrier();   // every wave is done with the previous tile's LDS
-      gemm_tile<EPI, MODE, C>(p, base + me, 0, (int)nk_full);
+      gemm_tile<EPI, MODE, C, NS>(p, base + me, 0, (int)nk_full);
     }
   }
 }
 
 // One output tile (linear id lid) over reduction stages kbeg .. kbeg+nk-1, then its epilogue (MODE_TILE,
 // MODE_FIXUP) or its parked accumulators (MODE_PIECE).
-template <int EPI, int MODE, class C>
-__device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int kbeg, int nk) {
+template <int EPI, int MODE, class C, int NS>
+__device__ __forceinline__ void gemm_tile(const GemmArgsN<NS>& p0, int64_t lid, int kbeg, int nk) {
   constexpr bool BF16 = (EPI == EPI_DX || EPI == EPI_LIN || EPI == EPI_DXLIN);
   constexpr bool SCALED = (EPI == EPI_W8 || EPI == EPI_LIN);   // per-row scale / bias epilogue
   constexpr int NA = C::NA, NB = C::NB, TA = C::TA, TB = C::TB;
@@ -346,8 +359,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
   // becomes the row within the segment.  Constant segment indices keep every field a plain argument load.
   // Grouped launches run full-K tiles only (no split pieces), so the piece and fixup kernels, at their
   // register limit, carry none of this.  Segments start on multiples of TA (the launch checks it).
-  GemmArgs p = p0;
-  if constexpr (EPI == EPI_W8 && MODE == MODE_TILE) {
+  GemmBase p = p0;
+  if constexpr (EPI == EPI_W8 && MODE == MODE_TILE && NS > 0) {
     if (p0.nseg > 0) {
       int s = 0;
 #pragma unroll
@@ -428,13 +441,15 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& p0, int64_t lid, int k
   constexpr bool KSEGS = (MODE == MODE_KSEG);
   int kseg = 0, kbase = 0, kend = 0x7fffffff;
   auto bind_seg = [&](int j) {   // j is workgroup-uniform; constant indices keep the fields argument loads
-    const KSeg* sp = &p0.ks[0];
+    if constexpr (NS > 0) {
+      const KSeg* sp = &p0.ks[0];
 #pragma unroll
-    for (int i = 1; i < MAX_SEG; ++i) sp = j == i ? &p0.ks[i] : sp;
-    bind(sp->a, sp->b, sp->lda_b, sp->ldb_b);
-    kend = sp->end;
+      for (int i = 1; i < NS; ++i) sp = j == i ? &p0.ks[i] : sp;
+      bind(sp->a, sp->b, sp->lda_b, sp->ldb_b);
+      kend = sp->end;
+    }
   };
-  if constexpr (KSEGS) {
+  if constexpr (KSEGS && NS > 0) {
     if (p0.nks > 0) bind_seg(0);
     else bind(p.a, p.b, p.lda_b, p.ldb_b);
   } else {
@@ -1205,22 +1220,44 @@ int64_t split_ws_bytes(int64_t rows_a, int64_t rows_b, int64_t kbytes) {
   return b256 > b128 ? b256 : b128;
 }
 
-template <int EPI, int MODE, class C>
+template <int EPI, int MODE, class C, int NS>
 int set_lds() {
   static std::atomic<uint64_t> lds_set{0};
-  return k2q_lds_limit_once(gemm_nt_kernel<EPI, MODE, C>, C::LDS, lds_set);
+  return k2q_lds_limit_once(gemm_nt_kernel<EPI, MODE, C, NS>, C::LDS, lds_set);
+}
+
+// The base of a launch's arguments, for the kernels that take no segment tables.
+inline GemmArgsN<0> slim(const GemmArgs& p) {
+  GemmArgsN<0> q;
+  static_cast<GemmBase&>(q) = p;
+  return q;
 }
 
 // Balanced persistent grid: as many rounds as the tiles need on this GPU's workgroup slots, and just enough
 // workgroups for that many rounds, each taking the same number of tiles (3168 T256 tiles on 256 CUs: 244
-// workgroups of 13), instead of a last round that leaves most CUs idle.
+// workgroups of 13), instead of a last round that leaves most CUs idle.  Launches with segments (a grouped
+// forward, a segmented reduction) take the kernel that carries the tables; the others the slim one.
 template <int EPI, class C, int MODE = MODE_TILE>
 int launch_tiles(const GemmArgs& p, hipStream_t st) {
-  if (int rc = set_lds<EPI, MODE, C>()) return rc;
   const int64_t slots = (int64_t)k2q_cu_count() * C::WPC;
   const int64_t rounds = (p.dp_tiles + slots - 1) / slots;
-  const int64_t nwg = (p.dp_tiles + rounds - 1) / rounds;
-  hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE, C>), dim3((unsigned)nwg), dim3(GT), C::LDS, st, p);
+  const dim3 grid((unsigned)((p.dp_tiles + rounds - 1) / rounds));
+  constexpr bool kTables = MODE == MODE_KSEG || (EPI == EPI_W8 && MODE == MODE_TILE);
+  if constexpr (kTables) {
+    if (MODE == MODE_KSEG || p.nseg > 0) {
+      if (int rc = set_lds<EPI, MODE, C, MAX_SEG>()) return rc;
+      GemmArgs pt = p;
+      pt.nwg = (int)grid.x;
+      hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE, C, MAX_SEG>), grid, dim3(GT), C::LDS, st, pt);
+      return K2Q_OK;
+    }
+  }
+  if constexpr (MODE != MODE_KSEG) {
+    if (int rc = set_lds<EPI, MODE, C, 0>()) return rc;
+    GemmArgsN<0> ps = slim(p);
+    ps.nwg = (int)grid.x;
+    hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE, C, 0>), grid, dim3(GT), C::LDS, st, ps);
+  }
   return K2Q_OK;
 }
 
@@ -1234,13 +1271,17 @@ int launch_full(const GemmArgs& p, hipStream_t st) {
 }
 
 // A split schedule: the pieces first (they fill the GPU for a short round), then the full tiles, then the fixup.
+// Split launches carry no segments (the caller runs grouped launches as full-K tiles).
 template <int EPI, class C>
 int launch_split(const GemmArgs& p, const SplitPlan& q, hipStream_t st) {
+  if (p.nseg > 0 || p.nks > 0) return K2Q_EINVAL;
   int rc;
-  if ((rc = set_lds<EPI, MODE_PIECE, C>()) || (rc = set_lds<EPI, MODE_FIXUP, C>())) return rc;
-  hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_PIECE, C>), dim3((unsigned)(q.rem * q.s)), dim3(GT), C::LDS, st, p);
+  if ((rc = set_lds<EPI, MODE_PIECE, C, 0>()) || (rc = set_lds<EPI, MODE_FIXUP, C, 0>())) return rc;
+  const GemmArgsN<0> ps = slim(p);
+  hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_PIECE, C, 0>), dim3((unsigned)(q.rem * q.s)), dim3(GT), C::LDS, st,
+                     ps);
   if (q.dp_tiles > 0 && (rc = launch_full<EPI, C>(p, st))) return rc;
-  hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_FIXUP, C>), dim3((unsigned)q.rem), dim3(GT), C::LDS, st, p);
+  hipLaunchKernelGGL((gemm_nt_kernel<EPI, MODE_FIXUP, C, 0>), dim3((unsigned)q.rem), dim3(GT), C::LDS, st, ps);
   return K2Q_OK;
 }
 

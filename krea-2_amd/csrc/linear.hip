@@ -200,11 +200,16 @@ extern "C" int k2q_linear_fwd(const uint16_t* x, int64_t ldx, int64_t M, int64_t
   const int64_t rr = lora_a ? r : 0;
   const bool skinny = M <= K2Q_GEMV_MAX_M;
   const FwdLayout lay = fwd_layout(wmode, M, N, K, rr);
-  if (!skinny && rr > 0 && (!ws || ws_bytes < lay.total || !k2q_aligned(ws, 256))) return K2Q_EINVAL;
+  // u from the rotate/quant pass straight into the caller's u leaves the factor region of ws unused
+  const bool fused = !skinny && !codes_ready && lora_a && fuse_down(M, K, rr);
+  const bool lora_ws = !skinny && rr > 0 && !(fused && u);
+  if (lora_ws && (!ws || ws_bytes < lay.total)) return K2Q_EINVAL;
+  if (ws && !k2q_aligned(ws, 256)) return K2Q_EINVAL;
   if (skinny && lora_a && !u) return K2Q_EINVAL;      // the prologue writes u
   uint8_t* w = static_cast<uint8_t*>(ws);
-  void* gws = ws ? static_cast<void*>(w + lay.gemm_off) : nullptr;
-  const int64_t gws_bytes = ws ? ws_bytes - lay.gemm_off : 0;
+  // the GEMM's split pieces (without room for them it runs full-K tiles: the same output)
+  void* gws = ws && ws_bytes > lay.gemm_off ? static_cast<void*>(w + lay.gemm_off) : nullptr;
+  const int64_t gws_bytes = gws ? ws_bytes - lay.gemm_off : 0;
   int rc = K2Q_OK;
   const float* uu = nullptr;   // the factors the GEMM reads: u, or the down-projection's slice partials
   int parts = 1;
@@ -212,7 +217,7 @@ extern "C" int k2q_linear_fwd(const uint16_t* x, int64_t ldx, int64_t M, int64_t
     if (lora_a || !codes_ready)
       rc = launch_skinny(x, ldx, M, K, lora_a, rr, u, codes_ready ? nullptr : qx, sx, st);
     uu = lora_a ? u : nullptr;
-  } else if (!codes_ready && lora_a && fuse_down(M, K, rr)) {
+  } else if (fused) {
     // u from the pass that rotates and quantizes x (one launch for both)
     float* ut = u ? u : reinterpret_cast<float*>(w + lay.u_off);
     rc = rotquant_lora_impl(x, M, K, ldx, qx, sx, lora_a, rr, ut, rr, st);

@@ -160,7 +160,7 @@ __global__ __launch_bounds__(64 * RQL_WAVES) void rotquant_lora_kernel(const __b
                                                                       int64_t ldx, int8_t* __restrict__ q,
                                                                       float* __restrict__ s,
                                                                       const float* __restrict__ a, int64_t ldu,
-                                                                      float* __restrict__ u) {
+                                                                      float* __restrict__ u, int nwg) {
   // Loads complete in issue order as far as the wave's vmcnt wait knows, so the next tile's row (HBM) is issued
   // only after this tile's A fragments (L2): waiting for a fragment then never waits for the row.
   constexpr int NB = RT == 1 ? 4 : RT == 2 ? 2 : 1;   // 32-wide steps per A batch (<= 32 VGPRs of fragments)
@@ -212,7 +212,8 @@ __global__ __launch_bounds__(64 * RQL_WAVES) void rotquant_lora_kernel(const __b
   };
 
   load_row(blockIdx.x);
-  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+  // nwg: the grid size, passed so that the kernel reads no hidden launch arguments (smaller launches)
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += nwg) {
     const int64_t row = tile * RQL_WAVES + w;
     const bool row_ok = row < M;
     // the raw row into LDS (rows past M are zeros: their u is never stored), then to f32 registers
@@ -252,7 +253,7 @@ __global__ __launch_bounds__(64 * RQL_WAVES) void rotquant_lora_kernel(const __b
     // A's first batch is issued before the code stores, so waiting for it never waits for a store's completion
     // (loads and stores retire in issue order for vmcnt); with a single batch the next tile's row follows it.
     load_a(0);
-    if (NB >= nks) load_row(tile + gridDim.x);
+    if (NB >= nks) load_row(tile + nwg);
     if (row_ok) {
       if (lane == 0) s[row] = __fdiv_rn(amax, 127.f);
       int8_t* qr = q + row * (int64_t)K;
@@ -273,7 +274,7 @@ __global__ __launch_bounds__(64 * RQL_WAVES) void rotquant_lora_kernel(const __b
     for (int k0 = 0; k0 < nks; k0 += NB) {
       if (k0 > 0) {
         load_a(k0);
-        if (k0 + NB >= nks) load_row(tile + gridDim.x);
+        if (k0 + NB >= nks) load_row(tile + nwg);
       }
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
@@ -319,7 +320,7 @@ int launch_rql(const __bf16* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, fl
   const int64_t cus = k2q_cu_count();
   const unsigned grid = (unsigned)(tiles < cus ? tiles : cus);
   hipLaunchKernelGGL((rotquant_lora_kernel<kNCH, RT>), dim3(grid), dim3(64 * RQL_WAVES), lds, st, x, M, (int)K, ldx,
-                     q, s, a, ldu, u);
+                     q, s, a, ldu, u, (int)grid);
   return k2q_launch_status();
 }
 

@@ -126,3 +126,40 @@ def test_skinny_w4(k2, dev):
     ref = orc.forward(x.float().numpy(), qo, so, w4=True, bias=b.numpy(), lora_A=A.numpy(), lora_B=B.numpy(),
                       lora_scale=1.0)
     assert rel_frob(y.float().cpu().numpy(), ref["y64"]) < 4e-3
+
+
+def test_workspace_only_where_used(k2, dev):
+    """``k2q_linear_fwd`` takes ws = NULL where nothing of it is used (u given, u from the rotate/quant pass, no
+    GEMM split) with the same output as with the full workspace, and refuses NULL where the factors need it."""
+    L = k2._lib
+    lib = L.load()
+    M, K, N, r = 4096, 3072, 3072, 16
+    assert L.linear_fwd_fuses_down(M, K, r) and lib.k2q_gemm_w8a8_ws_bytes(M, N, K) == 0
+    x, w, b, A, B = _case(M, K, N, r, 91, dev)
+    xd, Ad, Bd, bd = x.to(dev), A.to(dev), B.to(dev), b.to(dev)
+    qw, sw = L.quant_weight_i8(w.to(dev))
+    st = L._stream(dev)
+    nws = lib.k2q_linear_fwd_ws_bytes(0, M, N, K, r)
+    ws = torch.empty(nws, dtype=torch.uint8, device=dev)
+    outs = []
+    for wsp, wsb in ((ws.data_ptr(), nws), (None, 0)):
+        qx = torch.empty(M, K, dtype=torch.int8, device=dev)
+        sx = torch.empty(M, device=dev)
+        u = torch.empty(M, r, device=dev)
+        y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        assert lib.k2q_linear_fwd(xd.data_ptr(), K, M, K, qx.data_ptr(), sx.data_ptr(), 0, Ad.data_ptr(),
+                                  Bd.data_ptr(), r, 0.5, u.data_ptr(), 0, qw.data_ptr(), sw.data_ptr(), bd.data_ptr(),
+                                  N, y.data_ptr(), wsp, wsb, st) == 0
+        outs.append((qx, sx, u, y))
+    for a, c in zip(*outs):
+        assert torch.equal(a, c)
+    y2 = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    qx, sx, u = outs[0][:3]
+    # codes given: the down-projection's partials live in ws, so NULL is refused; so is u = NULL without ws
+    assert lib.k2q_linear_fwd(xd.data_ptr(), K, M, K, qx.data_ptr(), sx.data_ptr(), 1, Ad.data_ptr(), Bd.data_ptr(),
+                              r, 0.5, u.data_ptr(), 0, qw.data_ptr(), sw.data_ptr(), bd.data_ptr(), N, y2.data_ptr(),
+                              None, 0, st) == -1
+    assert lib.k2q_linear_fwd(xd.data_ptr(), K, M, K, qx.data_ptr(), sx.data_ptr(), 0, Ad.data_ptr(), Bd.data_ptr(),
+                              r, 0.5, None, 0, qw.data_ptr(), sw.data_ptr(), bd.data_ptr(), N, y2.data_ptr(),
+                              None, 0, st) == -1
+    torch.cuda.synchronize()
