@@ -33,7 +33,6 @@ __global__ __launch_bounds__(256) void lora_down_kernel(const uint16_t* __restri
                                                         const float* __restrict__ a, int64_t K, int kslice,
                                                         int64_t ldo, float* __restrict__ out) {
   constexpr int UNR = RT <= 2 ? 2 : 1;   // 32-wide k steps per load batch
-  constexpr int R = 16 * RT;
   __shared__ float part[3][TT][RT][4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t m0 = (int64_t)blockIdx.x * 16 * TT;
@@ -144,7 +143,6 @@ __global__ __launch_bounds__(64 * LD_NW) void lora_down_as_kernel(const uint16_t
                                                                   int64_t rows_per_wg, int64_t ldo,
                                                                   float* __restrict__ out) {
   constexpr int NS = LdShape<RT>::NS;
-  constexpr int R = 16 * RT;
   __shared__ float red[2][LD_NW][RT][4][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t k0 = (int64_t)blockIdx.y * LdShape<RT>::SPAN + (int64_t)w * 32 * NS;
