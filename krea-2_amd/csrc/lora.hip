@@ -224,16 +224,44 @@ __global__ __launch_bounds__(64 * LD_NW) void lora_down_as_kernel(const uint16_t
 }
 
 // u = sum of the K-slice partials in slice order (deterministic).  part: [ks][M][4 r4] f32; u: M rows of
-// ldu4 float4s, of which the first r4 are written.
+// ldu4 float4s, of which the first r4 are written.  KS > 0: ks == KS, unrolled, so all KS loads are in flight
+// before the first add (a loop over a run-time count waits for each load in turn); KS == 0: any ks.
+template <int KS>
 __global__ __launch_bounds__(256) void lora_reduce_kernel(const v4f* __restrict__ part, int ks, int64_t M, int64_t r4,
                                                           int64_t ldu4, v4f* __restrict__ u) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t n4 = M * r4;
   if (i >= n4) return;
-  v4f s = part[i];
-  for (int p = 1; p < ks; ++p) s += part[p * n4 + i];
+  v4f s;
+  if constexpr (KS > 0) {
+    v4f t[KS];
+#pragma unroll
+    for (int p = 0; p < KS; ++p) t[p] = part[p * n4 + i];
+    s = t[0];
+#pragma unroll
+    for (int p = 1; p < KS; ++p) s += t[p];
+  } else {
+    s = part[i];
+    for (int p = 1; p < ks; ++p) s += part[p * n4 + i];
+  }
   const int64_t m = i / r4;
   u[m * ldu4 + (i - m * r4)] = s;
+}
+
+void launch_reduce(const float* part, int ks, int64_t M, int64_t r, int64_t ldu, float* u, hipStream_t st) {
+  const int64_t n4 = M * r / 4;
+  const dim3 grid((unsigned)((n4 + 255) / 256));
+  const v4f* pp = reinterpret_cast<const v4f*>(part);
+  v4f* uu = reinterpret_cast<v4f*>(u);
+  switch (ks) {
+#define K2Q_RED_CASE(N) \
+  case N: hipLaunchKernelGGL(lora_reduce_kernel<N>, grid, dim3(256), 0, st, pp, ks, M, r / 4, ldu / 4, uu); break;
+    K2Q_RED_CASE(2) K2Q_RED_CASE(3) K2Q_RED_CASE(4) K2Q_RED_CASE(6) K2Q_RED_CASE(8) K2Q_RED_CASE(12)
+    K2Q_RED_CASE(16)
+#undef K2Q_RED_CASE
+    default:
+      hipLaunchKernelGGL(lora_reduce_kernel<0>, grid, dim3(256), 0, st, pp, ks, M, r / 4, ldu / 4, uu);
+  }
 }
 
 // Launch plan: TT row tiles per workgroup (fewer for tiny M), and K cut into ks slices (K % (128 ks) == 0,
@@ -482,11 +510,7 @@ int lora_down_chunk(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, const 
       default:
         return K2Q_EINVAL;
     }
-    if (q.slices > 1) {
-      const int64_t n4 = M * rc / 4;
-      hipLaunchKernelGGL(lora_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st,
-                         static_cast<const v4f*>(ws), (int)q.slices, M, rc / 4, ldu / 4, reinterpret_cast<v4f*>(u));
-    }
+    if (q.slices > 1) launch_reduce(static_cast<const float*>(ws), (int)q.slices, M, rc, ldu, u, st);
     return k2q_launch_status();
   }
   // No room for the slice partials: the row-tiled kernel over the whole of K in one launch.
