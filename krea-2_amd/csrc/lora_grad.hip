@@ -312,8 +312,22 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(RedJobs reds) {
   const v4f* part = reinterpret_cast<const v4f*>(rj.part);
   const int64_t i = wi * 256 + threadIdx.x;
   if (i >= rj.n4) return;
+  // Slices in groups of 8 whose loads are all issued before the adds (indices past the last slice re-read it;
+  // their terms are not added), so the sum keeps slice order: ((p0 + p1) + p2) ...
   v4f v = part[i];
-  for (int s = 1; s < rj.slices; ++s) v += part[s * rj.n4 + i];
+  for (int s0 = 1; s0 < rj.slices; s0 += 8) {
+    v4f t[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int s = s0 + q < rj.slices ? s0 + q : rj.slices - 1;
+      t[q] = part[s * rj.n4 + i];
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const v4f w = v + t[q];
+      v = s0 + q < rj.slices ? w : v;
+    }
+  }
   v *= rj.scale;
   const int64_t e = 4 * i, row = e / rj.cols;
   *reinterpret_cast<v4f*>(rj.out + row * rj.ldo + (e - row * rj.cols)) = v;
