@@ -14,8 +14,6 @@
 
 namespace {
 
-constexpr int kMaxNCH = 4;  // chunks of 16 elements per lane (K <= 1024 * WPR * 4)
-
 enum { MODE_ROW_I8 = 0, MODE_GROUP_I4 = 1 };
 
 using namespace k2q_rot;
