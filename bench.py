@@ -545,6 +545,35 @@ def krea_block_pass(k2, dev, iters):
     print(json.dumps({"krea_block_pass": shape, "fused_fwd_bwd_iterations": iters}), flush=True)
 
 
+def cfg3_pass(k2, dev, iters):
+    """Fixed launches for a kernel trace of the cfg3 leg: ``iters`` training steps (forward, then dX, dA, dB
+    through autograd) of the cfg3 layer, after 5 untimed ones, every call rotating and quantizing its input."""
+    c = CFG3
+    layer = make_layer(k2, c["K"], c["N"], c["r"], dev, seed=3)
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(c["M"], c["K"], generator=g).to(torch.bfloat16).to(dev).requires_grad_(True)
+    dy = (torch.randn(c["M"], c["N"], generator=g) * 1e-3).to(torch.bfloat16).to(dev)
+
+    def step():
+        x.grad = None
+        layer.lora_A.grad = None
+        layer.lora_B.grad = None
+        layer(x).backward(dy)
+
+    prev = _no_input_reuse(k2)
+    try:
+        for _ in range(5):
+            step()
+        torch.cuda.synchronize()
+        progress("cfg3 pass: warm")
+        for _ in range(iters):
+            step()
+        torch.cuda.synchronize()
+    finally:
+        k2.quantize.shared_input_quant.enabled = prev
+    print(json.dumps({"cfg3_pass": c["name"], "training_steps": iters}), flush=True)
+
+
 def _krea_block(k2, dev):
     """The Krea 2 block leg's layers, inputs and callables: ``block(x, fuse)``, ``fwd_bwd(fuse)``, ``group()``
     (group_siblings on both groups), the input and a shape string."""
@@ -1185,6 +1214,8 @@ def main():
                     help="GEMM vs hipBLASLt int8 vs bf16 at the cfg2 shape with board power / clock samples")
     ap.add_argument("--krea-block-pass", type=int, default=0, metavar="N",
                     help="N fused forward + backward passes of the Krea 2 block leg (for kernel traces)")
+    ap.add_argument("--cfg3-pass", type=int, default=0, metavar="N",
+                    help="N cfg3 training steps of one layer (for kernel traces)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write profiles/traffic_cfg2.json from two rocprofv3 --pmc runs over --profile-pass")
     a = ap.parse_args()
@@ -1212,6 +1243,9 @@ def main():
         return
     if a.krea_block_pass:
         krea_block_pass(k2, dev, a.krea_block_pass)
+        return
+    if a.cfg3_pass:
+        cfg3_pass(k2, dev, a.cfg3_pass)
         return
     cfg = CONFIGS[a.config]
     res = run_config(k2, cfg, a.steps, a.warmup, dev, a.settle)
