@@ -1,8 +1,9 @@
-"""Seeded shape sweep of the producer-fused kernels, their backward kernels and the grouped GEMM: ragged M,
-K with and without a partial chunk (K a multiple of 128 that is not a multiple of the 1024 / 2048 / 4096
-chunk width), row strides above K, one to four segments.  The bars are those of the dedicated tests: codes
-and scales bit-exact against rotate/quant of the kernel's own h, h within the stated bf16 steps of the
-oracle, grouped outputs bit-identical to the per-segment GEMM."""
+"""Seeded shape sweep of the producer-fused kernels, their backward kernels, the grouped GEMM and the one-call
+forward: ragged M, K with and without a partial chunk (K a multiple of 128 that is not a multiple of the
+1024 / 2048 / 4096 chunk width), row strides above K, one to four segments, M from 1 to a few thousand with
+every rank the module pads to.  The bars are those of the dedicated tests: codes and scales bit-exact against
+rotate/quant of the kernel's own h (or the oracle's for the forward), h within the stated bf16 steps of the
+oracle, grouped outputs bit-identical to the per-segment GEMM, the forward within the float64 formula's bar."""
 import numpy as np
 import pytest
 import torch
@@ -100,3 +101,57 @@ def test_grouped_sweep(k2, dev, M, K, Ns, r):
     for (qw, sw, b, lb, c, sc), y in zip(segs, ys):
         uc = u[:, c:c + r].contiguous() if lb is not None else None
         assert torch.equal(y, L.gemm_w8a8(qx, sx, qw, sw, b, uc, lb, sc, split=False))
+
+
+def _lin_case(rng):
+    band = int(rng.integers(0, 4))
+    M = int(rng.integers(1, 9)) if band == 0 else int(rng.integers(9, 300)) if band == 1 else \
+        int(rng.integers(300, 1500)) if band == 2 else int(rng.integers(1500, 4200))
+    K = int(rng.choice([128, 384, 1152, 3072, 4992, 6144]))
+    N = 32 * int(rng.integers(1, 48)) + int(rng.choice([0, 4, 12]))
+    r = int(rng.choice([0, 16, 32, 48, 64, 128]))
+    return M, K, N, r, bool(rng.integers(0, 4) == 0), bool(rng.integers(0, 2))
+
+
+_LIN_CASES = [_lin_case(_RNG) for _ in range(14)]
+
+
+@pytest.mark.parametrize("M,K,N,r,w4,bias", _LIN_CASES)
+def test_linear_fwd_sweep(k2, dev, M, K, N, r, w4, bias):
+    """The module's one-call forward (``k2q_linear_fwd``) over seeded random shapes, which take its different
+    routes (GEMV for M <= 8, A.x in the rotate/quant pass or its own launch, each output tile shape and split the
+    chooser picks): codes and scales bit-exact against the oracle, u within 1e-5 and y within the forward bar of
+    the float64 formula, and the inference form (no factors returned) the same bits as the training form."""
+    L = k2._lib
+    g = torch.Generator().manual_seed(M * 31 + K + N + r)
+    x = torch.randn(M, K, generator=g)
+    x[:, torch.randperm(K, generator=g)[: max(1, K // 100)]] *= 20
+    x = x.to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    b = torch.randn(N, generator=g) * 0.02 if bias else None
+    A = torch.randn(r, K, generator=g) * 0.01 if r else None
+    B = torch.randn(N, r, generator=g) * 0.01 if r else None
+    xd = x.to(dev)
+    if w4:
+        qw, sw = L.quant_weight_i4(w.to(dev))
+        qw_o, sw_o = orc.quant_weight_i4(w.float().numpy())
+    else:
+        qw, sw = L.quant_weight_i8(w.to(dev))
+        qw_o, sw_o = orc.quant_weight_i8(w.float().numpy())
+    qx = torch.empty(M, K, dtype=torch.int8, device=dev)
+    sx = torch.empty(M, device=dev)
+    Ad = A.to(dev) if r else None
+    Bd = B.to(dev) if r else None
+    bd = b.to(dev) if bias else None
+    y, u = L.linear_fwd(xd, qx, sx, False, Ad, Bd, 0.75, qw, sw, bd, w4)
+    y2, u2 = L.linear_fwd(xd, qx, sx, False, Ad, Bd, 0.75, qw, sw, bd, w4, need_u=False)
+    torch.cuda.synchronize()
+    ref = orc.forward(x.float().numpy(), qw_o, sw_o, w4=w4, bias=None if b is None else b.numpy(),
+                      lora_A=None if A is None else A.numpy(), lora_B=None if B is None else B.numpy(),
+                      lora_scale=0.75, fast=not w4)
+    assert np.array_equal(qx.cpu().numpy(), ref["qx"]) and np.array_equal(sx.cpu().numpy(), ref["sx"])
+    yk = _np(y).astype(np.float64)
+    assert np.linalg.norm(yk - ref["y64"]) <= 4e-3 * np.linalg.norm(ref["y64"])
+    if r:
+        assert np.linalg.norm(_np(u) - ref["u"]) <= 1e-5 * np.linalg.norm(ref["u"])
+    assert u2 is None and torch.equal(y2, y)
