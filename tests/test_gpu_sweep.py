@@ -1,9 +1,10 @@
-"""Seeded shape sweep of the producer-fused kernels, their backward kernels, the grouped GEMM and the one-call
-forward: ragged M, K with and without a partial chunk (K a multiple of 128 that is not a multiple of the
-1024 / 2048 / 4096 chunk width), row strides above K, one to four segments, M from 1 to a few thousand with
-every rank the module pads to.  The bars are those of the dedicated tests: codes and scales bit-exact against
-rotate/quant of the kernel's own h (or the oracle's for the forward), h within the stated bf16 steps of the
-oracle, grouped outputs bit-identical to the per-segment GEMM, the forward within the float64 formula's bar."""
+"""Seeded shape sweep of the producer-fused kernels, their backward kernels, the grouped GEMM, the one-call
+forward and the backward through the frozen base: ragged M, K with and without a partial chunk (K a multiple
+of 128 that is not a multiple of the 1024 / 2048 / 4096 chunk width), row strides above K, one to four
+segments, M from 1 to a few thousand with every rank the module pads to.  The bars are those of the dedicated
+tests: codes and scales bit-exact against rotate/quant of the kernel's own h (or the oracle's for the
+forward), h within the stated bf16 steps of the oracle, grouped outputs bit-identical to the per-segment GEMM,
+the forward and the backward within the float64 formulas' bars."""
 import numpy as np
 import pytest
 import torch
@@ -155,3 +156,47 @@ def test_linear_fwd_sweep(k2, dev, M, K, N, r, w4, bias):
     if r:
         assert np.linalg.norm(_np(u) - ref["u"]) <= 1e-5 * np.linalg.norm(ref["u"])
     assert u2 is None and torch.equal(y2, y)
+
+
+def _bwd_case(rng):
+    band = int(rng.integers(0, 3))
+    M = int(rng.integers(1, 64)) if band == 0 else int(rng.integers(64, 900)) if band == 1 else \
+        int(rng.integers(900, 4000))
+    return (M, 128 * int(rng.integers(1, 40)), 128 * int(rng.integers(1, 30)), int(rng.choice([0, 16, 32, 48, 64, 128])),
+            bool(rng.integers(0, 4) == 0))
+
+
+_BWD_CASES = [_bwd_case(_RNG) for _ in range(12)]
+
+
+@pytest.mark.parametrize("M,K,N,r,w4", _BWD_CASES)
+def test_backward_sweep(k2, dev, M, K, N, r, w4):
+    """The backward through the frozen base (``gemm_dx``: the effective weight, each tile shape and split, the
+    LoRA term in the epilogue) and the LoRA gradients (``lora_grads``) over seeded random shapes, against the
+    float64 formulas: dx within the forward's bar, g, dA and dB within 2e-5 relative Frobenius."""
+    L = k2._lib
+    gen = torch.Generator().manual_seed(M * 13 + K + N + r)
+    w = (torch.randn(N, K, generator=gen) * 0.02).to(torch.bfloat16)
+    x = torch.randn(M, K, generator=gen).to(torch.bfloat16)
+    dy = (torch.randn(M, N, generator=gen) * 1e-3).to(torch.bfloat16)
+    A = torch.randn(r, K, generator=gen) * 0.01 if r else None
+    B = torch.randn(N, r, generator=gen) * 0.01 if r else None
+    u = (x.float() @ A.t()) if r else None
+    s = 0.75
+    if w4:
+        qw, sw = L.quant_weight_i4(w.to(dev))
+        qo, so = orc.quant_weight_i4(w.float().numpy())
+    else:
+        qw, sw = L.quant_weight_i8(w.to(dev))
+        qo, so = orc.quant_weight_i8(w.float().numpy())
+    g = dA = dB = None
+    if r:
+        g, dA, dB = L.lora_grads(dy.to(dev), x.to(dev), u.to(dev), B.to(dev), s)
+    dx = L.gemm_dx(dy.to(dev), qw, sw, w4=w4, g=g, lora_a=A.to(dev) if r else None)
+    torch.cuda.synchronize()
+    ref = orc.backward(_np(dy), _np(x), qo, so, w4=w4, lora_A=None if A is None else A.numpy(),
+                       lora_B=None if B is None else B.numpy(), lora_scale=s)
+    assert np.linalg.norm(_np(dx) - ref["dx64"]) <= 4e-3 * np.linalg.norm(ref["dx64"])
+    if r:
+        for got, want in ((g, ref["g"]), (dA, ref["dA"]), (dB, ref["dB"])):
+            assert np.linalg.norm(_np(got) - want) <= 2e-5 * np.linalg.norm(want)
