@@ -365,6 +365,15 @@ __global__ __launch_bounds__(256) void dequant_t_kernel(const int8_t* __restrict
 // the input gradient is the plain product dy wt^T.  Thread t holds 32 k of row n = t/4 (k = 32 (t%4) +
 // 0..31 of the 128-wide Hadamard block); the butterflies on k bits 0-4 run in registers, bits 5 and 6
 // between the four threads of a quad (DPP).  Then an LDS transpose, as in dequant_t_kernel.
+//   W8: the rotation runs on the integer codes, exactly, and the row scale (times 2^-7) is applied once
+//   to the result: each output is the exact (c R)[k] rounded once to f32 and once to bf16.  The codes are
+//   offset by 128 (unsigned bytes, unpacked two per 32-bit register with one byte permute) and the block's
+//   first output corrected by 128 * 128 (the rotation of the constant 128 row); every partial sum lies in
+//   [-32640, 32640], so the butterflies run as packed 16-bit integer adds, two elements per instruction.
+//   Register i holds elements i and i + 16, so k bits 0-3 pair registers and bit 4 pairs the two halves.
+//   W4: the two 64-wide groups of a block carry different scales, so the codes are scaled first and the
+//   butterflies run in f32.
+typedef short k2q_v2s __attribute__((ext_vector_type(2)));
 template <bool W4>
 __global__ __launch_bounds__(256) void rot_dequant_t_kernel(const int8_t* __restrict__ qw,
                                                             const float* __restrict__ sw,
@@ -377,8 +386,54 @@ __global__ __launch_bounds__(256) void rot_dequant_t_kernel(const int8_t* __rest
   {
     const int nl = t >> 2, kq = t & 3;
     const int64_t n = n0 + nl < N ? n0 + nl : N - 1;   // rows past N computed on row N-1, never written
-    float v[32];
-    if (W4) {
+    if constexpr (!W4) {
+      const uint4 p0 = *reinterpret_cast<const uint4*>(qw + n * K + k0 + 32 * kq);
+      const uint4 p1 = *reinterpret_cast<const uint4*>(qw + n * K + k0 + 32 * kq + 16);
+      const uint32_t w[8] = {p0.x ^ 0x80808080u, p0.y ^ 0x80808080u, p0.z ^ 0x80808080u, p0.w ^ 0x80808080u,
+                             p1.x ^ 0x80808080u, p1.y ^ 0x80808080u, p1.z ^ 0x80808080u, p1.w ^ 0x80808080u};
+      k2q_v2s r[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {   // halves: code i and code i + 16 (both + 128), zero-extended
+        const uint32_t b = (uint32_t)(i & 3);
+        r[i] = __builtin_bit_cast(k2q_v2s, __builtin_amdgcn_perm(w[(i >> 2) + 4], w[i >> 2],
+                                                                   0x0c000c00u | b | ((4u + b) << 16)));
+      }
+#pragma unroll
+      for (int st = 1; st < 16; st <<= 1)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (!(i & st)) {
+            const k2q_v2s a = r[i], c = r[i + st];
+            r[i] = a + c;
+            r[i + st] = a - c;
+          }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {   // k bit 4: the halves of one register
+        const k2q_v2s sw2 = __builtin_shufflevector(r[i], r[i], 1, 0);
+        r[i] = r[i] * k2q_v2s{1, -1} + sw2;
+      }
+      const k2q_v2s sg1 = (kq & 1) ? k2q_v2s{-1, -1} : k2q_v2s{1, 1};
+      const k2q_v2s sg2 = (kq & 2) ? k2q_v2s{-1, -1} : k2q_v2s{1, 1};
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {   // k bit 5: partner t ^ 1 (quad_perm 1,0,3,2)
+        const k2q_v2s o = __builtin_bit_cast(k2q_v2s, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, r[i]), 0xB1, 0xF, 0xF, false));
+        r[i] = r[i] * sg1 + o;
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {   // k bit 6: partner t ^ 2 (quad_perm 2,3,0,1)
+        const k2q_v2s o = __builtin_bit_cast(k2q_v2s, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, r[i]), 0x4E, 0xF, 0xF, false));
+        r[i] = r[i] * sg2 + o;
+      }
+      if (kq == 0) r[0][0] = (short)(r[0][0] - 16384);   // the block's first output: minus 128 * 128
+      const float s = sw[n] * 0.0078125f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t pk = pack_bf16x2((float)r[i][0] * s, (float)r[i][1] * s);
+        tile[32 * kq + i][nl] = (uint16_t)pk;
+        tile[32 * kq + i + 16][nl] = (uint16_t)(pk >> 16);
+      }
+    } else {
+      float v[32];
       const uint4 p = *reinterpret_cast<const uint4*>(qw4 + n * (K / 2) + (k0 + 32 * kq) / 2);
       const float s = bf16_bits_to_f32(sw4[((k0 + 32 * kq) / 64) * N + n]);
       const uint32_t w[4] = {p.x, p.y, p.z, p.w};
@@ -390,35 +445,28 @@ __global__ __launch_bounds__(256) void rot_dequant_t_kernel(const int8_t* __rest
           v[16 * c + j] = (float)((int)((byte & 0xfu) ^ 8u) - 8) * s;
           v[16 * c + j + 8] = (float)((int)((byte >> 4) ^ 8u) - 8) * s;
         }
-    } else {
-      const uint4 p0 = *reinterpret_cast<const uint4*>(qw + n * K + k0 + 32 * kq);
-      const uint4 p1 = *reinterpret_cast<const uint4*>(qw + n * K + k0 + 32 * kq + 16);
-      const float s = sw[n];
-      const uint32_t w[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
 #pragma unroll
-      for (int j = 0; j < 32; ++j) v[j] = (float)(int8_t)((w[j >> 2] >> (8 * (j & 3))) & 0xffu) * s;
+      for (int st = 1; st < 32; st <<= 1)
+#pragma unroll
+        for (int j = 0; j < 32; ++j)
+          if (!(j & st)) {
+            const float a = v[j], b = v[j + st];
+            v[j] = a + b;
+            v[j + st] = a - b;
+          }
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {   // k bit 5: partner t ^ 1 (quad_perm 1,0,3,2)
+        const float o = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[j]), 0xB1, 0xF, 0xF, false));
+        v[j] = (kq & 1) ? o - v[j] : v[j] + o;
+      }
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {   // k bit 6: partner t ^ 2 (quad_perm 2,3,0,1)
+        const float o = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[j]), 0x4E, 0xF, 0xF, false));
+        v[j] = (kq & 2) ? o - v[j] : v[j] + o;
+      }
+#pragma unroll
+      for (int j = 0; j < 32; ++j) tile[32 * kq + j][nl] = (uint16_t)f32_to_bf16_bits(v[j] * 0.0078125f);
     }
-#pragma unroll
-    for (int st = 1; st < 32; st <<= 1)
-#pragma unroll
-      for (int j = 0; j < 32; ++j)
-        if (!(j & st)) {
-          const float a = v[j], b = v[j + st];
-          v[j] = a + b;
-          v[j + st] = a - b;
-        }
-#pragma unroll
-    for (int j = 0; j < 32; ++j) {   // k bit 5: partner t ^ 1 (quad_perm 1,0,3,2)
-      const float o = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[j]), 0xB1, 0xF, 0xF, false));
-      v[j] = (kq & 1) ? o - v[j] : v[j] + o;
-    }
-#pragma unroll
-    for (int j = 0; j < 32; ++j) {   // k bit 6: partner t ^ 2 (quad_perm 2,3,0,1)
-      const float o = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v[j]), 0x4E, 0xF, 0xF, false));
-      v[j] = (kq & 2) ? o - v[j] : v[j] + o;
-    }
-#pragma unroll
-    for (int j = 0; j < 32; ++j) tile[32 * kq + j][nl] = (uint16_t)f32_to_bf16_bits(v[j] * 0.0078125f);
   }
   __syncthreads();
 #pragma unroll

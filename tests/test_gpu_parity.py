@@ -376,8 +376,11 @@ def test_input_gradient(k2, dev, M, K, N, r, w4, fold):
 
 @pytest.mark.parametrize("N,K,w4", [(64, 128, False), (200, 384, False), (3072, 12288, False), (96, 512, True)])
 def test_effective_weight_prep(k2, dev, N, K, w4):
-    """k2q_dx_prep_eff: wt = bf16(2^-7 W_hat R)^T against the dense block-Hadamard product in float32 (one
-    bf16 rounding apart at most: the butterfly and the matmul add in different orders)."""
+    """k2q_dx_prep_eff: wt = bf16(2^-7 W_hat R)^T.  W8: the rotation of the integer codes is exact, so every
+    element equals the float64 product rounded once to f32 and once to bf16, bit for bit (also with every code
+    at -127, the largest sums).  W4 (a block mixes two group scales, so the codes are scaled first): against
+    the dense block-Hadamard product in float32, one bf16 rounding apart at most (the butterfly and the matmul
+    add in different orders)."""
     w = make_w(N, K, seed=N + K + 1)
     if w4:
         qw, sw = k2._lib.quant_weight_i4(w.to(dev))
@@ -387,14 +390,24 @@ def test_effective_weight_prep(k2, dev, N, K, w4):
         qw, sw = k2._lib.quant_weight_i8(w.to(dev))
         what = qw.float() * sw[:, None]
     lib = k2._lib.load()
-    wt = torch.empty(K, N, dtype=torch.bfloat16, device=dev)
     P = k2._lib._ptr
-    rc = lib.k2q_dx_prep_eff(None if w4 else P(qw), None if w4 else P(sw), P(qw) if w4 else None,
-                             P(sw) if w4 else None, N, K, P(wt), k2._lib._stream(dev))
-    assert rc == 0
-    torch.cuda.synchronize()
-    H = torch.from_numpy(__import__("scipy.linalg").linalg.hadamard(128).astype(np.float32)).to(dev)
-    ref = ((what.view(N, K // 128, 128) @ H).view(N, K) * 0.0078125).t()
+
+    def prep(q, s):
+        wt = torch.empty(K, N, dtype=torch.bfloat16, device=dev)
+        rc = lib.k2q_dx_prep_eff(None if w4 else P(q), None if w4 else P(s), P(q) if w4 else None,
+                                 P(s) if w4 else None, N, K, P(wt), k2._lib._stream(dev))
+        assert rc == 0
+        torch.cuda.synchronize()
+        return wt
+
+    wt = prep(qw, sw)
+    H64 = torch.from_numpy(__import__("scipy.linalg").linalg.hadamard(128).astype(np.float64)).to(dev)
+    if not w4:
+        for q in (qw, torch.full_like(qw, -127)):
+            exact = ((q.double().view(N, K // 128, 128) @ H64).view(N, K) * sw.double()[:, None] * 2.0 ** -7).t()
+            assert torch.equal(prep(q, sw), exact.float().to(torch.bfloat16))
+        return
+    ref = ((what.view(N, K // 128, 128) @ H64.float()).view(N, K) * 0.0078125).t()
     err = (wt.float() - ref).abs()
     tol = ref.abs() * 2 ** -8 + float(ref.abs().max()) * 2 ** -20   # plus f32 order noise near zero
     assert bool((err <= tol).all()), float((err - tol).max())
