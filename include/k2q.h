@@ -242,7 +242,8 @@ int k2q_gemm_w4a8_f32(const int8_t* qx, const uint8_t* qw4, const uint16_t* sw4,
  * Two equivalent routes (same bar, different rounding points):
  * - k2q_dx_prep_eff writes wt = bf16(2^-7 W_hat R)^T (K x N), the effective weight of the straight-through
  *   forward with the rotation folded in, and k2q_gemm_dx_lin(dy, wt, ...) is then the whole gradient
- *   (the route the module's backward takes);
+ *   (the route the module's backward takes); for int8 codes each element is the exact product rounded once
+ *   to f32 and once to bf16;
  * - k2q_dx_prep writes wt = bf16(W_hat)^T and k2q_gemm_dx applies the inverse rotation in its epilogue.
  * g = lora_scale * dy @ lora_b (M x r f32) is supplied by the caller, lora_a is the module's A (r x K
  * f32, lora.py:39); both nullable.  ws: as for k2q_gemm_w8a8 (f32 pieces, added in a fixed order),
