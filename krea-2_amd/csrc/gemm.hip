@@ -26,9 +26,14 @@
 // Every bf16 output is rounded once, after the LoRA term is added in f32.
 #include "k2q_common.h"
 
+#include <type_traits>
+
 namespace {
 
 enum { EPI_W8 = 0, EPI_ACC = 1, EPI_DX = 2, EPI_LIN = 3, EPI_DXLIN = 4 };
+
+typedef short k2q_v4s __attribute__((ext_vector_type(4)));   // 4 bf16 as the 16x16x16 bf16 MFMA's operand
+
 
 constexpr int BKB = 128;    // reduction bytes per stage
 
@@ -99,6 +104,10 @@ struct GemmArgsN<0> : GemmBase {};
 using GemmArgs = GemmArgsN<MAX_SEG>;   // what the host fills; a launch without segments passes its base
 
 __device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+// The 16 x 16 fragment reads (lane l: row l%16 of a 16-row block, chunk 4 w + l/16) take this one instead:
+// measured with the same reads over an LDS-resident buffer, swz conflicts on them (1.3e9 bank-conflict cycles
+// where row & 7 has none, and is the faster of the two), while the 32 x 32 reads are conflict-free under swz.
+__device__ __forceinline__ int swz16(int row) { return row & 7; }
 
 // Workgroup ids are dealt round-robin over the 8 XCDs; renumber them so that consecutive ids share an XCD.
 __device__ __forceinline__ int xcd_remap(int bid, int nwg) {
@@ -137,9 +146,11 @@ __device__ __forceinline__ v4i frag(const uint8_t* s, int row, int chunk) {
   return *reinterpret_cast<const v4i*>(s + row * BKB + 16 * (chunk ^ swz(row)));
 }
 
-template <bool BF16>
-__device__ __forceinline__ void mma(v4i a, v4i b, v16i& c) {
-  if constexpr (BF16) {
+template <bool BF16, class AccT>
+__device__ __forceinline__ void mma(v4i a, v4i b, AccT& c) {
+  if constexpr (std::is_same_v<AccT, v4i>) {   // int8, 16 x 16 blocks
+    c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+  } else if constexpr (BF16) {
     v16f cf = __builtin_bit_cast(v16f, c);
     cf = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b),
                                                 cf, 0, 0, 0);
@@ -286,6 +297,14 @@ __device__ __forceinline__ void ctile_put(uint8_t* ct, int mrow0, int ncol0, int
     *reinterpret_cast<v2u*>(row + 16 * j) = v2u{pack_bf16x2(f[4 * j], f[4 * j + 1]), pack_bf16x2(f[4 * j + 2], f[4 * j + 3])};
 }
 
+// One 16 x 16 block (MFMA C layout) into the LDS tile as bf16: lane l owns tile row mrow0 + l%16 and columns
+// ncol0 + 4(l/16) .. +3.
+template <int CROW>
+__device__ __forceinline__ void ctile_put16(uint8_t* ct, int mrow0, int ncol0, int lane, const v4f& f) {
+  uint8_t* row = ct + (mrow0 + (lane & 15)) * CROW + 2 * (ncol0 + 4 * (lane >> 4));
+  *reinterpret_cast<v2u*>(row) = v2u{pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3])};
+}
+
 __device__ __forceinline__ v8bf f32x8_to_bf16v(v4f a, v4f b, float s) {
   const v4u w = v4u{pack_bf16x2(a[0] * s, a[1] * s), pack_bf16x2(a[2] * s, a[3] * s), pack_bf16x2(b[0] * s, b[1] * s),
                     pack_bf16x2(b[2] * s, b[3] * s)};
@@ -341,7 +360,15 @@ template <int EPI, int MODE, class C, int NS>
 __device__ __forceinline__ void gemm_tile(const GemmArgsN<NS>& p0, int64_t lid, int kbeg, int nk) {
   constexpr bool BF16 = (EPI == EPI_DX || EPI == EPI_LIN || EPI == EPI_DXLIN);
   constexpr bool SCALED = (EPI == EPI_W8 || EPI == EPI_LIN);   // per-row scale / bias epilogue
-  constexpr int NA = C::NA, NB = C::NB, TA = C::TA, TB = C::TB;
+  // MFMA block: 16 x 16 (v_mfma_i32_16x16x64_i8) for the int8 256 x 320 tiles, 32 x 32 (v_mfma_i32_32x32x32_i8,
+  // v_mfma_f32_32x32x16_bf16) for the rest.  Register-only loops of the two int8 forms sustain 4.18 and 3.54
+  // POP/s on this board (the 16 x 16 one moves fewer accumulator bytes per MAC, and the clock is set by
+  // power); inside the GEMM the 16 x 16 main loop below measured faster on the 256 x 320 tiles and slower on
+  // the 256 x 256 and 128 x 128 ones, and the bf16 16 x 16 form gained nothing.  Per wave the output is NA x
+  // NB such blocks.
+  constexpr int MB = (!BF16 && C::TB == 320) ? 16 : 32;
+  constexpr int NA = C::ARW / MB, NB = C::BRW / MB, TA = C::TA, TB = C::TB;
+  using Acc = std::conditional_t<MB == 32, v16i, v4i>;
   static_assert(EPI != EPI_DX || C::ARW == 128, "the rotating epilogue runs a 128-row FWHT per wave");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // [2][A stage | B stage], then epilogue
   // The thread index through an empty asm: values derived from it are then computed per tile, not hoisted
@@ -386,13 +413,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgsN<NS>& p0, int64_t lid, 
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wa = wave % C::WVA, wb = wave / C::WVA;
-  const int h = lane >> 5, c32 = lane & 31;
+  const int h = lane >> 5, c32 = lane & 31;   // 32 x 32 C layout: lane l owns B-row l%32, A-rows 8j+4(l/32)+i
+  const int q4 = lane >> 4, c16 = lane & 15;  // 16 x 16 C layout: lane l owns B-row l%16, A-rows 4(l/16)+i
 
-  v16i acc[NA][NB];
+  Acc acc[NA][NB];
 #pragma unroll
   for (int i = 0; i < NA; ++i)
 #pragma unroll
-    for (int j = 0; j < NB; ++j) acc[i][j] = v16i{0};
+    for (int j = 0; j < NB; ++j) acc[i][j] = Acc{0};
 
   // Epilogue operands of this tile, fetched now so their latency hides under the main loop:
   // thread t < TB holds s_x of B-row B0+t (times 2^-7), thread t < TA s_w and bias of A-row A0+t.
@@ -423,8 +451,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgsN<NS>& p0, int64_t lid, 
   auto bind = [&](const uint8_t* a, const uint8_t* b, int64_t lda, int64_t ldb) {
 #pragma unroll
     for (int par = 0; par < 2; ++par) {
-      const int ca = (lane & 7) ^ (lane >> 3) ^ ((C::DA * wave + par) & 1);
-      const int cb = (lane & 7) ^ (lane >> 3) ^ ((C::DB * wave + par) & 1);
+      // the 16 x 16 main loop's layout swizzles by row & 7 only (see swz16)
+      const int ca = (lane & 7) ^ (lane >> 3) ^ (MB == 16 ? 0 : ((C::DA * wave + par) & 1));
+      const int cb = (lane & 7) ^ (lane >> 3) ^ (MB == 16 ? 0 : ((C::DB * wave + par) & 1));
       va[par] = (uint32_t)((8 * C::DA * wave + (lane >> 3)) * lda) + 16u * (uint32_t)ca;
       vb[par] = (uint32_t)((8 * C::DB * wave + (lane >> 3)) * ldb) + 16u * (uint32_t)cb;
     }
@@ -529,20 +558,129 @@ __device__ __forceinline__ void gemm_tile(const GemmArgsN<NS>& p0, int64_t lid, 
       for (int ia = 0; ia < NA; ++ia)
 #pragma unroll
         for (int ib = 0; ib < NB; ++ib) {
-          const uint8_t* u = pc + (int64_t)(ia * NB + ib) * 4 * GT * 16;
-          const v4i q0 = *reinterpret_cast<const v4i*>(u + toff);
-          const v4i q1 = *reinterpret_cast<const v4i*>(u + GT * 16 + toff);
-          const v4i q2 = *reinterpret_cast<const v4i*>(u + 2 * GT * 16 + toff);
-          const v4i q3 = *reinterpret_cast<const v4i*>(u + 3 * GT * 16 + toff);
-          const v16i v = __builtin_shufflevector(__builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7),
-                                                 __builtin_shufflevector(q2, q3, 0, 1, 2, 3, 4, 5, 6, 7), 0, 1, 2,
-                                                 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
-          if constexpr (BF16)
-            acc[ia][ib] = __builtin_bit_cast(v16i, __builtin_bit_cast(v16f, acc[ia][ib]) + __builtin_bit_cast(v16f, v));
-          else
-            acc[ia][ib] += v;
+          if constexpr (MB == 16) {   // one 16-byte unit per block
+            acc[ia][ib] += *reinterpret_cast<const v4i*>(pc + (int64_t)(ia * NB + ib) * GT * 16 + toff);
+          } else {
+            const uint8_t* u = pc + (int64_t)(ia * NB + ib) * 4 * GT * 16;
+            const v4i q0 = *reinterpret_cast<const v4i*>(u + toff);
+            const v4i q1 = *reinterpret_cast<const v4i*>(u + GT * 16 + toff);
+            const v4i q2 = *reinterpret_cast<const v4i*>(u + 2 * GT * 16 + toff);
+            const v4i q3 = *reinterpret_cast<const v4i*>(u + 3 * GT * 16 + toff);
+            const v16i v = __builtin_shufflevector(__builtin_shufflevector(q0, q1, 0, 1, 2, 3, 4, 5, 6, 7),
+                                                   __builtin_shufflevector(q2, q3, 0, 1, 2, 3, 4, 5, 6, 7), 0, 1,
+                                                   2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
+            if constexpr (BF16)
+              acc[ia][ib] = __builtin_bit_cast(v16i, __builtin_bit_cast(v16f, acc[ia][ib]) + __builtin_bit_cast(v16f, v));
+            else
+              acc[ia][ib] += v;
+          }
         }
     }
+  } else if constexpr (MB == 16) {
+    // int8 main loop on 16 x 16 blocks.  A stage is two 64-byte windows; a window is a grid of NA x NB
+    // v_mfma_i32_16x16x64_i8 (a lane's fragment: 16 bytes of one row, row c16 of the block, chunk 4 w + q4 of
+    // window w).  The operand with fewer blocks per wave is "held" (all NH fragments of a window in
+    // registers); the other is "streamed": one fragment per micro-step, read P micro-steps ahead, and each
+    // micro-step is its NH MFMAs against the held fragments.  The stage barrier sits P micro-steps before
+    // the stage's end: every read of the stage's slot is issued before it (the streamed reads run P ahead)
+    // and every read after it belongs to the next stage (the other slot, whose copies that barrier
+    // publishes), so the MFMAs run on across the barrier.  Live fragments: the two windows' held sets for P
+    // micro-steps, plus P + 1 streamed ones: (2 NH + P + 1) x 4 VGPRs (44 on the 256 x 320 tile, against 56
+    // for the two substep sets of the 32 x 32 loop).
+    constexpr bool STRB = NB >= NA;             // stream the B side (it has more blocks)
+    constexpr int NH = STRB ? NA : NB, NSB = STRB ? NB : NA;
+#ifndef K2Q_MS_P
+#define K2Q_MS_P 4
+#endif
+    constexpr int P = K2Q_MS_P < NSB - 1 ? K2Q_MS_P : NSB - 1;
+    constexpr int NU = 2 * NSB;                  // micro-steps per stage
+    constexpr int RING = (NU % (P + 1) == 0) ? P + 1 : (NU % (P + 2) == 0) ? P + 2 : (NU % (P + 3) == 0) ? P + 3 : NU;
+    static_assert(NSB > P && RING > P && NU % RING == 0, "micro-step pipeline");
+    const int fsw16 = swz16(c16);               // the block's rows are c16 + 16 i: one swizzle per lane
+    const uint8_t* fha = smem + (STRB ? (C::ARW * wa + c16) * BKB : TA * WBK + (C::BRW * wb + c16) * BKB);
+    const uint8_t* fsa = smem + (STRB ? TA * WBK + (C::BRW * wb + c16) * BKB : (C::ARW * wa + c16) * BKB);
+    const int cw0 = 16 * (q4 ^ fsw16), cw1 = 16 * ((4 + q4) ^ fsw16);
+    v4i hf[2][NH];   // held fragments of windows 0 and 1
+    v4i sf[RING];    // streamed fragments, micro-step u in sf[u % RING]
+    auto rd_held = [&](int slot, int w, v4i (&f)[NH]) {
+      const uint8_t* b = fha + slot * C::STAGE + (w ? cw1 : cw0);
+#pragma unroll
+      for (int i = 0; i < NH; ++i) f[i] = *reinterpret_cast<const v4i*>(b + 16 * BKB * i);
+    };
+    auto rd_str = [&](int slot, int w, int j) -> v4i {
+      return *reinterpret_cast<const v4i*>(fsa + slot * C::STAGE + (w ? cw1 : cw0) + 16 * BKB * j);
+    };
+    auto mstep = [&](const v4i (&hv)[NH], v4i sv, auto J) {
+      constexpr int j = decltype(J)::value;
+#pragma unroll
+      for (int i = 0; i < NH; ++i) {
+        if constexpr (STRB) mma<false>(hv[i], sv, acc[i][j]);
+        else mma<false>(sv, hv[i], acc[j][i]);
+      }
+    };
+    const int ns = nk / 2;   // stages
+    issue(0, 0);
+    seek(ns > 1 ? 1 : 0);
+    issue(ns > 1 ? 1 : 0, 1);
+    wait_vmcnt<G>();           // stage 0 (stage 1 may be in flight)
+    lds_barrier();
+    rd_held(0, 0, hf[0]);
+#pragma unroll
+    for (int u = 0; u < P; ++u) sf[u] = rd_str(0, 0, u);
+    // One micro-step u of stage st in LDS slot sl.
+    auto mu = [&](int st, int sl, auto U) {
+      constexpr int u = decltype(U)::value;
+      constexpr int w = u / NSB, j = u % NSB, v = u + P;
+      if constexpr (u == NU - P) {
+        seek(st + 2 < ns ? st + 2 : ns - 1);
+        wait_vmcnt<0>();                                      // stage st+1
+        lds_barrier();                                        // every read of slot sl has landed (lgkmcnt(0))
+        __builtin_amdgcn_s_setprio(2);
+        issue(st + 2 < ns ? st + 2 : ns - 1, sl);
+      }
+      if constexpr (v < NU) sf[v % RING] = rd_str(sl, v / NSB, v % NSB);
+      else sf[v % RING] = rd_str(sl ^ 1, 0, v - NU);       // the next stage's window 0
+      if constexpr (u == NSB - P) rd_held(sl, 1, hf[1]);
+      if constexpr (u == NU - P) rd_held(sl ^ 1, 0, hf[0]);
+      mstep(hf[w], sf[u % RING], std::integral_constant<int, j>{});
+      constexpr int NRD = 1 + ((u == NSB - P || u == NU - P) ? NH : 0);   // reads issued in this micro-step
+      if constexpr (u >= NU - P) {   // after the barrier: the DMA instructions and reads between the MFMAs
+        constexpr int GQ = (G + P - 1) / P;                   // DMA instructions per post-barrier micro-step
+        constexpr int g0 = (u - (NU - P)) * GQ;
+        constexpr int GN = g0 >= G ? 0 : (G - g0 < GQ ? G - g0 : GQ);
+        static_for<0, NH>([&](auto I) {
+          constexpr int i = decltype(I)::value;
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                     // MFMA
+          constexpr int nd = (NRD * (i + 1)) / NH - (NRD * i) / NH;
+          if constexpr (nd > 0) __builtin_amdgcn_sched_group_barrier(0x100, nd, 0);              // DS read
+          constexpr int nv = (GN * (i + 1)) / NH - (GN * i) / NH;
+          if constexpr (nv > 0) __builtin_amdgcn_sched_group_barrier(0x020, nv, 0);              // VMEM
+        });
+      } else {
+        static_for<0, NH>([&](auto I) {
+          constexpr int i = decltype(I)::value;
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                     // MFMA
+          constexpr int nd = (NRD * (i + 1)) / NH - (NRD * i) / NH;
+          if constexpr (nd > 0) __builtin_amdgcn_sched_group_barrier(0x100, nd, 0);              // DS read
+        });
+      }
+    };
+    // The loop is rotated: an iteration runs from one stage barrier to the next (the post-barrier micro-steps of
+    // stage st, then the pre-barrier ones of stage st + 1), so its back-edge sits at the barrier's own
+    // lgkmcnt(0).  Entered anywhere else, the rolled loop made the compiler wait for every fragment read in
+    // flight at the back-edge (unrolled by two stages, the 256 x 320 tile spills ~100 registers).
+    auto pre = [&](int st, int sl) { static_for<0, NU - P>([&](auto U) { mu(st, sl, U); }); };
+    auto post = [&](int st, int sl) {
+      static_for<NU - P, NU>([&](auto U) { mu(st, sl, U); });
+      __builtin_amdgcn_s_setprio(0);
+    };
+    pre(0, 0);
+    for (int st = 0; st + 1 < ns; ++st) {
+      post(st, st & 1);
+      pre(st + 1, (st + 1) & 1);
+    }
+    post(ns - 1, (ns - 1) & 1);
+    wait_vmcnt<0>();   // no LDS-DMA may still be in flight when the workgroup's LDS is released
   } else {
     v4i f0a[NA], f0b[NB], f1a[NA], f1b[NB];
     const int ns = nk / 2;   // stages
@@ -620,11 +758,16 @@ __device__ __forceinline__ void gemm_tile(const GemmArgsN<NS>& p0, int64_t lid, 
 #pragma unroll
     for (int ia = 0; ia < NA; ++ia)
 #pragma unroll
-      for (int ib = 0; ib < NB; ++ib)
+      for (int ib = 0; ib < NB; ++ib) {
+        if constexpr (MB == 16) {
+          *reinterpret_cast<v4i*>(dst + (int64_t)(ia * NB + ib) * GT * 16 + toff) = acc[ia][ib];
+        } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          *reinterpret_cast<v4i*>(dst + (int64_t)((ia * NB + ib) * 4 + q) * GT * 16 + toff) =
-              v4i{acc[ia][ib][4 * q], acc[ia][ib][4 * q + 1], acc[ia][ib][4 * q + 2], acc[ia][ib][4 * q + 3]};
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<v4i*>(dst + (int64_t)((ia * NB + ib) * 4 + q) * GT * 16 + toff) =
+                v4i{acc[ia][ib][4 * q], acc[ia][ib][4 * q + 1], acc[ia][ib][4 * q + 2], acc[ia][ib][4 * q + 3]};
+        }
+      }
     return;
   }
 
@@ -637,15 +780,20 @@ __device__ __forceinline__ void gemm_tile(const GemmArgsN<NS>& p0, int64_t lid, 
     for (int ia = 0; ia < NA; ++ia)
 #pragma unroll
       for (int ib = 0; ib < NB; ++ib) {
-        const int64_t m = b0 + 32 * ib + c32;
-        if (m >= p.rows_b) continue;
+        if constexpr (MB == 16) {
+          const int64_t m = b0 + 16 * ib + c16, n = a0 + 16 * ia + 4 * q4;
+          if (m < p.rows_b && n < p.rows_a) *reinterpret_cast<v4i*>(out + m * p.ldo + n) = acc[ia][ib];
+        } else {
+          const int64_t m = b0 + 32 * ib + c32;
+          if (m >= p.rows_b) continue;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int64_t n = a0 + 32 * ia + 8 * j + 4 * h;
-          if (n >= p.rows_a) continue;
-          int4 v = make_int4(acc[ia][ib][4 * j], acc[ia][ib][4 * j + 1], acc[ia][ib][4 * j + 2],
-                             acc[ia][ib][4 * j + 3]);
-          *reinterpret_cast<int4*>(out + m * p.ldo + n) = v;
+          for (int j = 0; j < 4; ++j) {
+            const int64_t n = a0 + 32 * ia + 8 * j + 4 * h;
+            if (n >= p.rows_a) continue;
+            int4 v = make_int4(acc[ia][ib][4 * j], acc[ia][ib][4 * j + 1], acc[ia][ib][4 * j + 2],
+                               acc[ia][ib][4 * j + 3]);
+            *reinterpret_cast<int4*>(out + m * p.ldo + n) = v;
+          }
         }
       }
     return;
@@ -722,7 +870,23 @@ __device__ __forceinline__ void gemm_tile(const GemmArgsN<NS>& p0, int64_t lid, 
     }
     lds_barrier();
     uint8_t* ctile = smem;
-    if constexpr (SCALED) {
+    if constexpr (SCALED && MB == 16) {   // a lane's 4 values: A-rows 4 q4 .. +3 of one B-row
+#pragma unroll
+      for (int ia = 0; ia < NA; ++ia) {
+        const int nl = C::ARW * wa + 16 * ia + 4 * q4;
+        const v4f sw = *reinterpret_cast<const v4f*>(s_sw + nl);
+        const v4f bi = *reinterpret_cast<const v4f*>(s_bi + nl);
+#pragma unroll
+        for (int ib = 0; ib < NB; ++ib) {
+          const float sxm = s_sx[C::BRW * wb + 16 * ib + c16];
+          const v4f a = __builtin_convertvector(acc[ia][ib], v4f);
+          v4f f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) f[i] = __builtin_fmaf(a[i], sxm * sw[i], bi[i]);
+          acc[ia][ib] = __builtin_bit_cast(v4i, f);
+        }
+      }
+    } else if constexpr (SCALED) {
 #pragma unroll
       for (int ia = 0; ia < NA; ++ia) {
         v4f sw[4], bi[4];
@@ -782,19 +946,37 @@ __device__ __forceinline__ void gemm_tile(const GemmArgsN<NS>& p0, int64_t lid, 
         load_ra(cn);
         load_rb(cn);
         lds_barrier();
-        v8bf fa[NA], fb[NB];
+        if constexpr (MB == 16) {   // v_mfma_f32_16x16x16_bf16: a lane's fragment is ranks 4 q4 .. +3 of row c16
+          // (the 16x16x32 form over the chunk's 16 ranks and 16 zero ranks measured slower: twice the fragment
+          // registers, and the 256 x 320 tile then spills)
+          k2q_v4s fa[NA], fb[NB];
 #pragma unroll
-        for (int i = 0; i < NA; ++i)
-          fa[i] = *reinterpret_cast<const v8bf*>(sla + (C::ARW * wa + 32 * i + c32) * LROW + 16 * h);
+          for (int i = 0; i < NA; ++i)
+            fa[i] = *reinterpret_cast<const k2q_v4s*>(sla + (C::ARW * wa + 16 * i + c16) * LROW + 8 * q4);
 #pragma unroll
-        for (int i = 0; i < NB; ++i)
-          fb[i] = *reinterpret_cast<const v8bf*>(slb + (C::BRW * wb + 32 * i + c32) * LROW + 16 * h);
+          for (int i = 0; i < NB; ++i)
+            fb[i] = *reinterpret_cast<const k2q_v4s*>(slb + (C::BRW * wb + 16 * i + c16) * LROW + 8 * q4);
 #pragma unroll
-        for (int ia = 0; ia < NA; ++ia)
+          for (int ia = 0; ia < NA; ++ia)
 #pragma unroll
-          for (int ib = 0; ib < NB; ++ib)
-            acc[ia][ib] = __builtin_bit_cast(
-                v16i, __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ia], fb[ib], __builtin_bit_cast(v16f, acc[ia][ib]), 0, 0, 0));
+            for (int ib = 0; ib < NB; ++ib)
+              acc[ia][ib] = __builtin_bit_cast(
+                  v4i, __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(fa[ia], fb[ib], __builtin_bit_cast(v4f, acc[ia][ib]), 0, 0, 0));
+        } else {
+          v8bf fa[NA], fb[NB];
+#pragma unroll
+          for (int i = 0; i < NA; ++i)
+            fa[i] = *reinterpret_cast<const v8bf*>(sla + (C::ARW * wa + 32 * i + c32) * LROW + 16 * h);
+#pragma unroll
+          for (int i = 0; i < NB; ++i)
+            fb[i] = *reinterpret_cast<const v8bf*>(slb + (C::BRW * wb + 32 * i + c32) * LROW + 16 * h);
+#pragma unroll
+          for (int ia = 0; ia < NA; ++ia)
+#pragma unroll
+            for (int ib = 0; ib < NB; ++ib)
+              acc[ia][ib] = __builtin_bit_cast(
+                  v16i, __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ia], fb[ib], __builtin_bit_cast(v16f, acc[ia][ib]), 0, 0, 0));
+        }
         lds_barrier();   // every wave has its fragments before the next chunk overwrites them
       }
     }
@@ -815,9 +997,14 @@ __device__ __forceinline__ void gemm_tile(const GemmArgsN<NS>& p0, int64_t lid, 
 #pragma unroll
         for (int ia = 0; ia < NA; ++ia)
 #pragma unroll
-          for (int ib = 0; ib < NB; ++ib)
-            ctile_put<C::CROW>(ctile, C::BRW * wb - rbeg + 32 * ib, C::ARW * wa + 32 * ia, lane,
-                               __builtin_bit_cast(v16f, acc[ia][ib]));
+          for (int ib = 0; ib < NB; ++ib) {
+            if constexpr (MB == 16)
+              ctile_put16<C::CROW>(ctile, C::BRW * wb - rbeg + 16 * ib, C::ARW * wa + 16 * ia, lane,
+                                   __builtin_bit_cast(v4f, acc[ia][ib]));
+            else
+              ctile_put<C::CROW>(ctile, C::BRW * wb - rbeg + 32 * ib, C::ARW * wa + 32 * ia, lane,
+                                 __builtin_bit_cast(v16f, acc[ia][ib]));
+          }
       }
       lds_barrier();
       const int64_t R0 = B0 + rbeg;

@@ -153,26 +153,43 @@ __global__ __launch_bounds__(64 * LD_NW) void lora_down_as_kernel(const uint16_t
   const int ntiles = (int)((m_end - m_beg + 15) / 16);
 
   v8bf ah[RT][NS], al[RT][NS];
+  // The factor fragments, a rank tile at a time: all of a tile's loads are issued before the first of them is
+  // waited for, and the next tile's are in flight while this one is split.
+  v4f fl[2][NS][2];
+  auto fetch = [&](auto ROWS) {
+    constexpr bool kRows = decltype(ROWS)::value;
+    auto load = [&](int jt, v4f (&f)[NS][2]) {
+      const int64_t rank = 16 * jt + (lane & 15);
 #pragma unroll
-  for (int jt = 0; jt < RT; ++jt)
+      for (int s = 0; s < NS; ++s) {
+        const int64_t k = kb + 32 * s;
+        if constexpr (kRows) {   // factor rows (r x K), as nn.Linear stores A
+          const float* pa = a + rank * K + k;
+          f[s][0] = *reinterpret_cast<const v4f*>(pa);
+          f[s][1] = *reinterpret_cast<const v4f*>(pa + 4);
+        } else {                 // factor columns (K x r, e.g. lora_B for g = s dY B), scaled below
+          const float* pa = a + k * a_kstride + rank;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      const int64_t rank = 16 * jt + (lane & 15), k = kb + 32 * s;
-      v4f f0, f1;
-      if (a_kstride == 1) {   // factor rows (r x K), as nn.Linear stores A
-        const float* pa = a + rank * K + k;
-        f0 = *reinterpret_cast<const v4f*>(pa);
-        f1 = *reinterpret_cast<const v4f*>(pa + 4);
-      } else {                // factor columns (K x r, e.g. lora_B for g = s dY B), scaled
-        const float* pa = a + k * a_kstride + rank;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          f0[e] = pa[e * a_kstride] * a_scale;
-          f1[e] = pa[(e + 4) * a_kstride] * a_scale;
+          for (int e = 0; e < 4; ++e) {
+            f[s][0][e] = pa[e * a_kstride];
+            f[s][1][e] = pa[(e + 4) * a_kstride];
+          }
         }
       }
-      split8(f0, f1, ah[jt][s], al[jt][s]);
+    };
+    load(0, fl[0]);
+#pragma unroll
+    for (int jt = 0; jt < RT; ++jt) {
+      if (jt + 1 < RT) load(jt + 1, fl[(jt + 1) & 1]);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        if constexpr (kRows) split8(fl[jt & 1][s][0], fl[jt & 1][s][1], ah[jt][s], al[jt][s]);
+        else split8(fl[jt & 1][s][0] * a_scale, fl[jt & 1][s][1] * a_scale, ah[jt][s], al[jt][s]);
+      }
     }
+  };
+  if (a_kstride == 1) fetch(std::true_type{});
+  else fetch(std::false_type{});
 
   auto load_x = [&](v4i (&f)[NS], int t) {
     int64_t m = m_beg + 16 * (int64_t)t + (lane & 15);
