@@ -144,6 +144,30 @@ def test_gemm_w4_group_partials_exact(k2, dev, M, N, K):
     assert rel_frob(out.cpu().numpy(), ref) < 1e-6
 
 
+@pytest.mark.parametrize("M,N,K", [(256, 256, 3072), (130, 132, 12288)])
+def test_gemm_w4_scale_exponents(k2, dev, M, N, K):
+    """Group scales that exercise the integer chunks: every scale exponent from 2^-24 to 2^6 (windows left
+    in both directions), zero and negative scales, runs of equal exponents longer than a chunk, and codes
+    at -128 / -8 (the largest group sums).  Within the f32 bound of the float64 sum sum_g s_g acc_g."""
+    rng = np.random.default_rng(M + N + K)
+    qx = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    qx[: M // 4] = -128
+    q4 = rng.integers(-8, 8, size=(N, K), dtype=np.int8)
+    q4[: N // 4] = -8
+    G = K // 64
+    e = rng.integers(-24, 7, size=(G, N)).astype(np.float64)
+    e[:, N // 2:] = -7.0                                        # long runs of one exponent
+    s = (1.0 + rng.random((G, N))) * np.exp2(e)
+    s[rng.random((G, N)) < 0.05] = 0.0
+    s[rng.random((G, N)) < 0.2] *= -1.0
+    s4 = torch.from_numpy(s).to(torch.bfloat16)
+    out = k2._lib.gemm_w4a8_f32(torch.from_numpy(qx).to(dev), torch.from_numpy(orc.pack_i4(q4)).to(dev),
+                                s4.to(dev)).double().cpu().numpy()
+    pg = orc.gemm_acc_groups(qx, q4).astype(np.float64) * s4.double().numpy().T[None, :, :]
+    ref, mag = pg.sum(axis=2), np.abs(pg).sum(axis=2)
+    assert np.all(np.abs(out - ref) <= mag * (G * 2.0 ** -24) + 1e-30)
+
+
 # ------------------------------------------------------------------------------------------- kernel (3)
 def _forward_case(k2, dev, M, K, N, r, w4, bias, seed):
     x = make_x(M, K, seed=seed)
