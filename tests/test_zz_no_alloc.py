@@ -3,6 +3,7 @@ scratch) against ``k2q_lora_grads`` (caller workspace): bit-identical outputs on
 with a smaller input (the scratch keeps the first call's contents), called through the C ABI; nothing allocated
 by torch during the calls; a shape beyond the scratch is refused with K2Q_ESCRATCH before any launch."""
 import ctypes
+import gc
 
 import pytest
 import torch
@@ -25,14 +26,22 @@ def _noalloc(lib, dy, x, u, B, s, dev):
     g = torch.empty(M, r, device=dev)
     dA = torch.empty(r, K, device=dev)
     dB = torch.empty(N, r, device=dev)
+    # earlier tests' reference cycles (modules with patched bound methods) are collected now, and the collector
+    # stays off during the call, so that only the call itself can move torch's count
+    gc.collect()
     torch.cuda.synchronize()
-    before = torch.cuda.memory_allocated(dev)
-    rc = lib.k2q_lora_grads_noalloc(dy.data_ptr(), x.data_ptr(), u.data_ptr(), B.data_ptr(), r, s, M, N, K,
-                                    g.data_ptr(), dA.data_ptr(), dB.data_ptr(),
-                                    torch.cuda.current_stream(dev).cuda_stream)
-    torch.cuda.synchronize()
+    gc.disable()
+    try:
+        before = torch.cuda.memory_allocated(dev)
+        rc = lib.k2q_lora_grads_noalloc(dy.data_ptr(), x.data_ptr(), u.data_ptr(), B.data_ptr(), r, s, M, N, K,
+                                        g.data_ptr(), dA.data_ptr(), dB.data_ptr(),
+                                        torch.cuda.current_stream(dev).cuda_stream)
+        torch.cuda.synchronize()
+        after = torch.cuda.memory_allocated(dev)
+    finally:
+        gc.enable()
     assert rc == 0
-    assert torch.cuda.memory_allocated(dev) == before
+    assert after == before
     return g, dA, dB
 
 
