@@ -590,7 +590,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgsN<NS>& p0, int64_t lid, 
     constexpr bool STRB = NB >= NA;             // stream the B side (it has more blocks)
     constexpr int NH = STRB ? NA : NB, NSB = STRB ? NB : NA;
 #ifndef K2Q_MS_P
-#define K2Q_MS_P 4
+#define K2Q_MS_P 5
 #endif
     constexpr int P = K2Q_MS_P < NSB - 1 ? K2Q_MS_P : NSB - 1;
     constexpr int NU = 2 * NSB;                  // micro-steps per stage
